@@ -1,0 +1,200 @@
+/*
+ * ttt_attn.h — C ABI of the MI355X (gfx950) grad-grad-safe attention library.
+ *
+ * libttt_attn.so exports these entry points.  They take raw device pointers,
+ * int64 sizes and element strides, and a HIP stream passed as `void*`.  No
+ * entry point allocates device memory: the caller owns every input, output and
+ * statistics buffer.  Kernels are enqueued asynchronously on `stream`; the
+ * return value is 0 on success or a nonzero ttt_status, with a message
+ * available from ttt_last_error() (thread-local).  No C++ exception crosses
+ * this boundary.
+ *
+ * Layout contract (all entry points):
+ *   - [B,H,T,D] operands (q, k, v, o, dO, cotangents, gradients) are described
+ *     by a ttt_view: base pointer plus element strides for the B, H and T
+ *     dimensions; the D dimension must be contiguous (stride 1).  Base pointers
+ *     and the T stride (in bytes) must be 16-byte aligned.
+ *   - P is a [B,H,T,T] matrix described by a ttt_view whose stride_t is the row
+ *     stride; the column dimension must be contiguous and the row stride (in
+ *     bytes) 16-byte aligned.  With causal=1 only the lower block triangle of
+ *     64x64 tiles (block column <= block row) is written or read; the other
+ *     tiles are never touched.
+ *   - Row statistics (lse, rowsum, E, F) are contiguous fp32 [B*H*T] arrays,
+ *     index (b*H + h)*T + t.  lse is the natural-log log-sum-exp of the scaled
+ *     scores of each row.
+ *   - head_dim must be 64 or 128; dtype is one of ttt_dtype.  Arithmetic is
+ *     fp32-accumulated MFMA on the input dtype.
+ *
+ * The computed quantities (per (b,h) slice, s = scale):
+ *   S = s*Q*K^T (causal: entries with col > row are -inf), P = softmax(S),
+ *   O = P*V;  D = rowsum(dO o O);  dV = P^T*dO;  dP = dO*V^T;
+ *   dS = P o (dP - D);  dQ = s*dS*K;  dK = s*dS^T*Q.
+ *   Double backward with cotangents gQ, gK, gV on (dQ, dK, dV):
+ *   gdS = s*(gQ*K^T + Q*gK^T);  E = rowsum(gdS o P);  gdP = P o (gdS - E);
+ *   gP = dO*gV^T + gdS o (dP - D) - E o dP;  F = rowsum(gP o P);
+ *   gS = P o (gP - F);
+ *   GQ = s*(dS*gK + gS*K);  GK = s*(dS^T*gQ + gS^T*Q);  GV = gdP^T*dO;
+ *   GdO = P*gV + gdP*V.
+ */
+#ifndef TTT_ATTN_H
+#define TTT_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum ttt_dtype {
+  TTT_F16 = 0,
+  TTT_BF16 = 1,
+  TTT_F32 = 2
+} ttt_dtype;
+
+typedef enum ttt_status {
+  TTT_OK = 0,
+  TTT_ERR_INVALID_ARGUMENT = 1, /* null pointer, bad size, misaligned stride */
+  TTT_ERR_UNSUPPORTED = 2,      /* head_dim or dtype outside what is built  */
+  TTT_ERR_LAUNCH = 3            /* HIP reported an error on kernel launch   */
+} ttt_status;
+
+/* Problem description shared by every entry point. */
+typedef struct ttt_problem {
+  int32_t dtype;    /* ttt_dtype                                  */
+  int32_t causal;   /* 0 or 1                                     */
+  int64_t batch;    /* B                                          */
+  int64_t heads;    /* H                                          */
+  int64_t seqlen;   /* T                                          */
+  int64_t head_dim; /* D: 64 or 128                               */
+  float scale;      /* softmax scale s                            */
+} ttt_problem;
+
+/* A strided [B,H,T,X] operand (X = D, or T for P). Strides are in elements. */
+typedef struct ttt_view {
+  void* data;
+  int64_t stride_b;
+  int64_t stride_h;
+  int64_t stride_t;
+} ttt_view;
+
+/* Library version (major*10000 + minor*100 + patch). */
+int ttt_version(void);
+
+/* Message for the most recent nonzero status on the calling thread. */
+const char* ttt_last_error(void);
+
+/*
+ * Forward.  Writes O and lse; if p != NULL (and p->data != NULL) also writes
+ * P = softmax(S) rounded to the input dtype, and computes O from that rounded
+ * P (two passes over K: row statistics, then P and P*V).  With p == NULL it
+ * runs a single online-softmax pass.
+ * Replaces: TritonAttentionFn.forward, ttt_kernels/triton_attention.py:261-337
+ * (the _attention_with_probs P path at :51-59 and :270-273, the Triton
+ * forward kernels _attn_fwd_kernel :87-138, _attn_fwd_kernel_stats :149-206
+ * and _attn_probs_kernel :217-256).
+ */
+int ttt_attn_fwd(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
+                 const ttt_view* v, const ttt_view* o, float* lse,
+                 const ttt_view* p, void* stream);
+
+/*
+ * dQ (row-block kernel).  P is read from p when p != NULL, otherwise it is
+ * recomputed from q, k and lse.  The row statistic D is taken from rowsum_in
+ * when it is not NULL; otherwise it is computed as rowsum(dO o O) from o and,
+ * if rowsum_out != NULL, stored there.
+ * Replaces: _attn_bwd_dq_kernel, ttt_kernels/backward_stubs.py:259-309, and
+ * the dQ half of triton_attn_bwd_dqdk_from_p :362-404; the recompute-mode
+ * stub triton_attn_bwd_dq :529-530.
+ */
+int ttt_attn_bwd_dq(const ttt_problem* pr, const ttt_view* q,
+                    const ttt_view* k, const ttt_view* v, const ttt_view* o,
+                    const ttt_view* dout, const float* lse, const ttt_view* p,
+                    const float* rowsum_in, float* rowsum_out,
+                    const ttt_view* dq, void* stream);
+
+/*
+ * dK and dV (column-block kernel), from P (p != NULL) or recomputed from lse.
+ * dk may be NULL: then only dV = P^T*dO is computed and rowsum is not read.
+ * Replaces: _attn_bwd_dv_from_p_kernel + triton_attn_bwd_dv_from_p,
+ * backward_stubs.py:124-181; _attn_bwd_dk_kernel :313-359 and the dK half of
+ * triton_attn_bwd_dqdk_from_p :406-425; the recompute dV kernel
+ * _attn_bwd_dv_kernel + triton_attn_bwd_dv :22-121; the stub
+ * triton_attn_bwd_dk :533-534.
+ */
+int ttt_attn_bwd_dkdv(const ttt_problem* pr, const ttt_view* q,
+                      const ttt_view* k, const ttt_view* v,
+                      const ttt_view* dout, const float* lse,
+                      const ttt_view* p, const float* rowsum,
+                      const ttt_view* dk, const ttt_view* dv, void* stream);
+
+/*
+ * Full first backward in one call: ttt_attn_bwd_dq (computing D from O into
+ * rowsum_out) followed by ttt_attn_bwd_dkdv on the same stream.
+ * Replaces: the save_p backward of TritonAttentionFn.backward,
+ * triton_attention.py:351-379, and the default recompute backward :416-420.
+ */
+int ttt_attn_bwd(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
+                 const ttt_view* v, const ttt_view* o, const ttt_view* dout,
+                 const float* lse, const ttt_view* p, float* rowsum_out,
+                 const ttt_view* dq, const ttt_view* dk, const ttt_view* dv,
+                 void* stream);
+
+/*
+ * Row statistic from P, with the reference's definition
+ * rowsum[m] = sum_n (dO*V^T)[m,n] * P[m,n].
+ * Replaces: _attn_rowsum_kernel + triton_attn_rowsum_from_p,
+ * backward_stubs.py:184-255.
+ */
+int ttt_attn_bwd_rowsum(const ttt_problem* pr, const ttt_view* p,
+                        const ttt_view* dout, const ttt_view* v,
+                        float* rowsum, void* stream);
+
+/*
+ * Double backward, row-block pass: computes the row statistics E and F
+ * (stored for the column pass), GQ, and, when gdout != NULL, GdO.
+ * Replaces: the stubs triton_attn_bwd2_dq, backward_stubs.py:539-540, and the
+ * torch double-backward of TritonDqDkFn / TritonRowSumFn / TritonDvFn,
+ * backward_stubs.py:434-514 (corrected: full softmax-Jacobian terms).
+ */
+int ttt_attn_gg_row(const ttt_problem* pr, const ttt_view* q,
+                    const ttt_view* k, const ttt_view* v,
+                    const ttt_view* dout, const float* lse, const ttt_view* p,
+                    const float* rowsum, const ttt_view* gq,
+                    const ttt_view* gk, const ttt_view* gv,
+                    const ttt_view* gq_out, const ttt_view* gdout,
+                    float* e_out, float* f_out, void* stream);
+
+/*
+ * Double backward, column-block pass: GK and GV, reading E and F from
+ * ttt_attn_gg_row.
+ * Replaces: the stubs triton_attn_bwd2_dk and triton_attn_bwd2_dv,
+ * backward_stubs.py:543-548.
+ */
+int ttt_attn_gg_col(const ttt_problem* pr, const ttt_view* q,
+                    const ttt_view* k, const ttt_view* v,
+                    const ttt_view* dout, const float* lse, const ttt_view* p,
+                    const float* rowsum, const float* e_in, const float* f_in,
+                    const ttt_view* gq, const ttt_view* gk,
+                    const ttt_view* gv, const ttt_view* gk_out,
+                    const ttt_view* gv_out, void* stream);
+
+/*
+ * Full double backward in one call: ttt_attn_gg_row then ttt_attn_gg_col on
+ * the same stream.  e_buf and f_buf are caller-owned fp32 [B*H*T] buffers.
+ * Replaces: TritonDqDkFn.backward + TritonRowSumFn.backward +
+ * TritonDvFn.backward, backward_stubs.py:434-514, as reached from
+ * TritonAttentionFn.backward with create_graph=True, triton_attention.py:354-358.
+ */
+int ttt_attn_gg(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
+                const ttt_view* v, const ttt_view* dout, const float* lse,
+                const ttt_view* p, const float* rowsum, const ttt_view* gq,
+                const ttt_view* gk, const ttt_view* gv, const ttt_view* gq_out,
+                const ttt_view* gk_out, const ttt_view* gv_out,
+                const ttt_view* gdout, float* e_buf, float* f_buf,
+                void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TTT_ATTN_H */

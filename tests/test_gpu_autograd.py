@@ -1,0 +1,148 @@
+"""End-to-end parity of the reference-compatible API on the GPU:
+``triton_attention`` forward, ``autograd.grad(create_graph=True)`` and the
+grad-grad, for every ``bwd_mode``, against the math path restated in
+``oracle.math_path`` (run on the CPU in float64 on the same rounded inputs).
+
+Tolerances: fp16/bf16 relative Frobenius <= 2e-2; fp32 max-abs <= 1e-5.
+"""
+import math
+
+import pytest
+import torch
+
+import ttt_kernels
+from oracle import math_path
+from tests._util import check
+from ttt_kernels.triton_attention import BWD_MODES, TritonAttentionFn, triton_attention
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(b, h, t, d, dtype, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(b, h, t, d, generator=g).to(dtype) for _ in range(7)]
+
+
+def _gpu_step(xs, causal, scale, mode, do_requires_grad=False):
+    q, k, v, do, rq, rk, rv = (x.cuda() for x in xs)
+    q, k, v = (t.requires_grad_(True) for t in (q, k, v))
+    do = do.requires_grad_(do_requires_grad)
+    o = triton_attention(q, k, v, causal=causal, scale=scale, bwd_mode=mode)
+    dq, dk, dv = torch.autograd.grad(o, (q, k, v), do, create_graph=True)
+    s = (dq * rq).sum() + (dk * rk).sum() + (dv * rv).sum()
+    wrt = (q, k, v, do) if do_requires_grad else (q, k, v)
+    g = torch.autograd.grad(s, wrt)
+    torch.cuda.synchronize()
+    out = dict(o=o, dq=dq, dk=dk, dv=dv, gq=g[0], gk=g[1], gv=g[2])
+    if do_requires_grad:
+        out["gdo"] = g[3]
+    return out
+
+
+def _cpu_ref(xs, causal, scale, do_requires_grad=False):
+    return math_path.gradgrad_step(*(x.double() for x in xs), causal, scale, do_requires_grad=do_requires_grad)
+
+
+@pytest.mark.parametrize("mode", [m for m in BWD_MODES if m != "custom"] + ["some_unknown_mode"])
+@pytest.mark.parametrize("causal", [False, True])
+def test_modes_gradgrad(mode, causal):
+    xs = _inputs(1, 2, 128, 64, torch.float16, seed=11)
+    print(f"[case] mode={mode} causal={causal}", flush=True)
+    got = _gpu_step(xs, causal, 0.125, mode)
+    ref = _cpu_ref(xs, causal, 0.125)
+    for n in ("o", "dq", "dk", "dv", "gq", "gk", "gv"):
+        check(n, got[n], ref[n], torch.float16)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("mode", ["save_p_triton_full", "recompute"])
+def test_gdo_when_do_requires_grad(dtype, mode):
+    xs = _inputs(2, 1, 96, 64, dtype, seed=12)
+    print(f"[case] gdo dtype={dtype} mode={mode}", flush=True)
+    got = _gpu_step(xs, True, 0.125, mode, do_requires_grad=True)
+    ref = _cpu_ref(xs, True, 0.125, do_requires_grad=True)
+    for n in ("o", "dq", "dk", "dv", "gq", "gk", "gv", "gdo"):
+        check(n, got[n], ref[n], dtype)
+
+
+@pytest.mark.parametrize("d", [32, 80, 64, 128])
+def test_head_dims(d):
+    xs = _inputs(1, 2, 64, d, torch.float32, seed=13)
+    print(f"[case] head_dim={d}", flush=True)
+    scale = 1.0 / math.sqrt(d)
+    got = _gpu_step(xs, False, None, "save_p_triton_full")
+    ref = _cpu_ref(xs, False, scale)
+    for n in ("o", "dq", "dk", "dv", "gq", "gk", "gv"):
+        assert got[n].shape == xs[0].shape
+        check(n, got[n], ref[n], torch.float32)
+
+
+def test_reference_harness_form_fp32():
+    """The reference's own harness (mean loss, sum of g.pow(2).mean()) in fp32,
+    b2 h2 T64 d64 causal (tests/test_gradgrad.py:12-25)."""
+    xs = _inputs(2, 2, 64, 64, torch.float32, seed=0)
+    print("[case] harness fp32", flush=True)
+    q, k, v = (x.cuda().requires_grad_(True) for x in xs[:3])
+    out = triton_attention(q, k, v, causal=True)
+    loss = out.float().mean()
+    grads = torch.autograd.grad(loss, (q, k, v), create_graph=True)
+    s = sum(g.pow(2).mean() for g in grads)
+    gg = torch.autograd.grad(s, (q, k, v))
+    ref = math_path.harness_step(*(x.double() for x in xs[:3]), True, 0.125)
+    for n, x in zip(("dq", "dk", "dv"), grads):
+        check(n, x, ref[n], torch.float32)
+    # The mean-loss grad-grad values are ~1e-10; compare relative to their scale.
+    for n, x in zip(("gq", "gk", "gv"), gg):
+        r = ref[n]
+        err = (x.double().cpu() - r).abs().max().item() / max(r.abs().max().item(), 1e-30)
+        assert err < 1e-4, (n, err)
+
+
+def test_custom_mode_first_order_without_graph():
+    xs = _inputs(1, 1, 64, 64, torch.float16, seed=14)
+    print("[case] custom", flush=True)
+    q, k, v, do = (x.cuda() for x in xs[:4])
+    q, k, v = (t.requires_grad_(True) for t in (q, k, v))
+    o = triton_attention(q, k, v, causal=True, bwd_mode="custom")
+    dq, dk, dv = torch.autograd.grad(o, (q, k, v), do, create_graph=True)
+    assert dq.grad_fn is None and dk.grad_fn is None and dv.grad_fn is None
+    ref = _cpu_ref(xs, True, 0.125)
+    for n, x in zip(("dq", "dk", "dv"), (dq, dk, dv)):
+        check(n, x, ref[n], torch.float16)
+
+
+def test_saved_probs_exposed_for_save_p():
+    xs = _inputs(1, 1, 64, 64, torch.float16, seed=15)
+    q, k, v = (x.cuda().requires_grad_(True) for x in xs[:3])
+    print("[case] saved_probs", flush=True)
+    o = triton_attention(q, k, v, bwd_mode="save_p")
+    p = o.grad_fn.saved_probs[0]
+    _, pref = math_path.attention_with_probs(*(x.double() for x in xs[:3]), False, 0.125)
+    check("p", p, pref, torch.float16)
+
+
+def test_no_create_graph_first_order():
+    xs = _inputs(2, 2, 100, 64, torch.bfloat16, seed=16)
+    print("[case] first-order only", flush=True)
+    q, k, v, do = (x.cuda() for x in xs[:4])
+    q, k, v = (t.requires_grad_(True) for t in (q, k, v))
+    o = triton_attention(q, k, v, causal=True, bwd_mode="save_p_triton_full")
+    o.backward(do)
+    ref = _cpu_ref(xs, True, 0.125)
+    for n, t in zip(("dq", "dk", "dv"), (q, k, v)):
+        check(n, t.grad, ref[n], torch.bfloat16)
+
+
+def test_empty_inputs():
+    q = torch.zeros(0, 2, 16, 64, device="cuda", dtype=torch.float16, requires_grad=True)
+    o = triton_attention(q, q, q)
+    assert o.shape == q.shape
+
+
+def test_alias_package_identity():
+    import importlib
+    impl = importlib.import_module("testtimeideas_amd.ttt_kernels.triton_attention")
+    alias = importlib.import_module("ttt_kernels.triton_attention")
+    # as in the reference package, the attribute ttt_kernels.triton_attention is the function
+    assert ttt_kernels.triton_attention is impl.triton_attention
+    assert alias.TritonAttentionFn is impl.TritonAttentionFn is TritonAttentionFn

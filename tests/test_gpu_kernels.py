@@ -1,0 +1,159 @@
+"""GPU parity of every kernel entry point, called through the C ABI, against the
+float64 closed-form oracle on the same (dtype-rounded) inputs.
+
+Tolerances: fp16/bf16 relative Frobenius <= 2e-2; fp32 max-abs <= 1e-5.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import closed_form as cf
+from tests._util import check, rel_fro, max_abs
+from testtimeideas_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+DT = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}
+
+
+def _inputs(b, h, t, d, dtype, seed=0, qkv_scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    xs = [torch.randn(b, h, t, d, generator=g) for _ in range(7)]
+    for i in range(3):
+        xs[i] = xs[i] * qkv_scale
+    return [x.to(dtype) for x in xs]
+
+
+def _ref(xs, causal, scale):
+    return cf.double_backward(*(x.double().numpy() for x in xs), causal, scale)
+
+
+def _run(xs, causal, scale, save_p, want_gdo=True):
+    q, k, v, do, gq, gk, gv = (x.cuda() for x in xs)
+    o, lse, p = _lib.fwd(q, k, v, causal, scale, save_p)
+    dq, dk, dv, rowsum = _lib.bwd(q, k, v, o, do, lse, p, causal, scale)
+    GQ, GK, GV, GdO = _lib.gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, causal, scale, want_gdo)
+    torch.cuda.synchronize()
+    return dict(o=o, lse=lse, p=p, dq=dq, dk=dk, dv=dv, rowsum=rowsum, gq=GQ, gk=GK, gv=GV, gdo=GdO)
+
+
+def _active_mask(t, causal):
+    """Elements of P that the kernels write: all, or the lower 64x64 block triangle."""
+    if not causal:
+        return np.ones((t, t), dtype=bool)
+    bi = np.arange(t) // 64
+    return bi[None, :] <= bi[:, None]
+
+
+def _compare(out, ref, dtype, causal, t, names=("o", "dq", "dk", "dv", "gq", "gk", "gv", "gdo")):
+    errs = {}
+    for n in names:
+        if out.get(n) is None:
+            continue
+        errs[n] = check(n, out[n], ref[n], dtype)
+    # row statistics: LSE (natural log) and D
+    errs["lse"] = check("lse", out["lse"], ref["lse"], torch.float32, abs_tol=2e-5 if dtype == torch.float32 else 2e-3)
+    errs["rowsum"] = check("rowsum", out["rowsum"], ref["rowsum"], dtype)
+    if out["p"] is not None:
+        m = _active_mask(t, causal)
+        got = out["p"].double().cpu().numpy()[..., m]
+        errs["p"] = check("p", got, ref["p"][..., m], dtype)
+    return errs
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "fp16", "bf16"])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("save_p", [True, False])
+def test_all_kernels_small(dtype, d, causal, save_p):
+    t = 128
+    dt = DT[dtype]
+    xs = _inputs(1, 2, t, d, dt, seed=1)
+    scale = 1.0 / math.sqrt(d)
+    print(f"[case] small dtype={dtype} d={d} causal={causal} save_p={save_p} t={t}", flush=True)
+    out = _run(xs, causal, scale, save_p)
+    _compare(out, _ref(xs, causal, scale), dt, causal, t)
+
+
+@pytest.mark.parametrize("t", [1, 37, 64, 100, 191, 257])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("save_p", [True, False])
+def test_ragged_lengths(t, causal, save_p):
+    dt = torch.float16
+    xs = _inputs(2, 1, t, 64, dt, seed=t)
+    scale = 0.125
+    print(f"[case] ragged t={t} causal={causal} save_p={save_p}", flush=True)
+    out = _run(xs, causal, scale, save_p)
+    _compare(out, _ref(xs, causal, scale), dt, causal, t)
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "fp16"])
+def test_c1_shape_fp32_parity(dtype):
+    """C1 shape (b1 h1 T64 d64, non-causal) on the GPU kernels."""
+    dt = DT[dtype]
+    xs = _inputs(1, 1, 64, 64, dt, seed=0)
+    print(f"[case] c1 dtype={dtype}", flush=True)
+    for save_p in (True, False):
+        out = _run(xs, False, 0.125, save_p)
+        _compare(out, _ref(xs, False, 0.125), dt, False, 64)
+
+
+def test_per_kernel_entry_points_match_fused():
+    """The per-kernel entry points (used under timing) give the fused results."""
+    xs = _inputs(1, 2, 192, 64, torch.float16, seed=3)
+    print("[case] per-kernel vs fused", flush=True)
+    a = _run(xs, True, 0.125, True)
+    with _lib.kernel_timing() as rec:
+        b = _run(xs, True, 0.125, True)
+    for n in ("o", "dq", "dk", "dv", "gq", "gk", "gv", "gdo", "rowsum", "lse"):
+        assert torch.equal(a[n], b[n]), n
+    assert set(rec) >= {"ttt_attn_fwd", "ttt_attn_bwd_dq", "ttt_attn_bwd_dkdv", "ttt_attn_gg_row",
+                        "ttt_attn_gg_col"}
+
+
+def test_deterministic():
+    """Two runs give bitwise identical outputs (no atomics anywhere)."""
+    xs = _inputs(1, 1, 320, 64, torch.bfloat16, seed=4)
+    print("[case] determinism", flush=True)
+    a = _run(xs, True, 0.125, True)
+    b = _run(xs, True, 0.125, True)
+    for n in ("o", "dq", "dk", "dv", "gq", "gk", "gv", "gdo", "lse", "rowsum"):
+        assert torch.equal(a[n], b[n]), n
+    # causal P: only the lower block triangle is written (the rest is never touched)
+    m = torch.from_numpy(_active_mask(320, True)).cuda()
+    assert torch.equal(a["p"][..., m], b["p"][..., m])
+
+
+def test_rowsum_from_p_and_dv_from_p():
+    """Reference-definition launchers: rowsum = sum P o (dO V^T); dV = P^T dO."""
+    xs = _inputs(2, 2, 130, 64, torch.float16, seed=5)
+    q, k, v, do = (x.cuda() for x in xs[:4])
+    print("[case] rowsum/dv from P", flush=True)
+    ref = _ref(xs, False, 0.125)
+    _, _, p = _lib.fwd(q, k, v, False, 0.125, True)
+    rs = _lib.rowsum_from_p(p, do, v, False)
+    _, dv = _lib.bwd_dkdv(None, None, None, do, p, None, None, False, 1.0, want_dk=False)
+    torch.cuda.synchronize()
+    check("rowsum", rs, ref["rowsum"], torch.float16)
+    check("dv", dv, ref["dv"], torch.float16)
+
+
+def test_strided_inputs():
+    """Operands that are transposed views of [B,T,H,D] storage run without copies."""
+    g = torch.Generator().manual_seed(6)
+    b, h, t, d = 2, 3, 96, 64
+    base = [torch.randn(b, t, h, d, generator=g).to(torch.float16) for _ in range(7)]
+    xs = [x.transpose(1, 2) for x in base]  # [B,H,T,D] views, stride_t = H*D
+    print("[case] strided", flush=True)
+    dev = [y.cuda().transpose(1, 2) for y in base]
+    assert not dev[0].is_contiguous()
+    q, k, v, do, gq, gk, gv = dev
+    o, lse, p = _lib.fwd(q, k, v, True, 0.125, True)
+    dq, dk, dv, rowsum = _lib.bwd(q, k, v, o, do, lse, p, True, 0.125)
+    GQ, GK, GV, GdO = _lib.gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, True, 0.125, True)
+    torch.cuda.synchronize()
+    ref = _ref([x.contiguous() for x in xs], True, 0.125)
+    for n, x in dict(o=o, dq=dq, dk=dk, dv=dv, gq=GQ, gk=GK, gv=GV, gdo=GdO).items():
+        check(n, x, ref[n], torch.float16)

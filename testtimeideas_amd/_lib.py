@@ -1,0 +1,345 @@
+"""ctypes binding of ``libttt_attn.so`` (the C ABI in ``include/ttt_attn.h``).
+
+This module is the thin layer between torch tensors and the HIP kernels:
+it checks devices, dtypes and shapes, makes operands kernel-compatible
+(unit stride in the last dimension, 16-byte aligned rows, head dim padded to
+64 or 128), allocates outputs with torch's caching allocator, and calls the
+C entry points on torch's current HIP stream.  There is no fallback: if the
+library is missing or an operand is not on a ROCm device, it raises.
+
+Every public function mirrors a launcher of the reference
+(``ttt_kernels/backward_stubs.py`` and the forward in
+``ttt_kernels/triton_attention.py``); see the docstrings for the lines.
+"""
+from __future__ import annotations
+
+import contextlib
+import ctypes
+import os
+from typing import Dict, List, Optional, Tuple
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libttt_attn.so")
+
+_DTYPE_CODE = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+
+
+class ExtensionMissingError(RuntimeError):
+    """libttt_attn.so has not been built (run ``__graft_entry__.build()``)."""
+
+
+class _Problem(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32),
+        ("causal", ctypes.c_int32),
+        ("batch", ctypes.c_int64),
+        ("heads", ctypes.c_int64),
+        ("seqlen", ctypes.c_int64),
+        ("head_dim", ctypes.c_int64),
+        ("scale", ctypes.c_float),
+    ]
+
+
+class _View(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("stride_b", ctypes.c_int64),
+        ("stride_h", ctypes.c_int64),
+        ("stride_t", ctypes.c_int64),
+    ]
+
+
+_P = ctypes.POINTER
+_VP = _P(_View)
+_FP = ctypes.c_void_p  # float* passed as an address
+_SIGS = {
+    "ttt_attn_fwd": [_P(_Problem), _VP, _VP, _VP, _VP, _FP, _VP, ctypes.c_void_p],
+    "ttt_attn_bwd_dq": [_P(_Problem), _VP, _VP, _VP, _VP, _VP, _FP, _VP, _FP, _FP, _VP, ctypes.c_void_p],
+    "ttt_attn_bwd_dkdv": [_P(_Problem), _VP, _VP, _VP, _VP, _FP, _VP, _FP, _VP, _VP, ctypes.c_void_p],
+    "ttt_attn_bwd": [_P(_Problem), _VP, _VP, _VP, _VP, _VP, _FP, _VP, _FP, _VP, _VP, _VP, ctypes.c_void_p],
+    "ttt_attn_bwd_rowsum": [_P(_Problem), _VP, _VP, _VP, _FP, ctypes.c_void_p],
+    "ttt_attn_gg_row": [_P(_Problem), _VP, _VP, _VP, _VP, _FP, _VP, _FP, _VP, _VP, _VP, _VP, _VP, _FP, _FP,
+                        ctypes.c_void_p],
+    "ttt_attn_gg_col": [_P(_Problem), _VP, _VP, _VP, _VP, _FP, _VP, _FP, _FP, _FP, _VP, _VP, _VP, _VP, _VP,
+                        ctypes.c_void_p],
+    "ttt_attn_gg": [_P(_Problem), _VP, _VP, _VP, _VP, _FP, _VP, _FP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _FP,
+                    _FP, ctypes.c_void_p],
+}
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load() -> ctypes.CDLL:
+    """Load libttt_attn.so once and bind the entry points' signatures."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ExtensionMissingError(
+            f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'` "
+            "(or `make -C testtimeideas_amd/csrc`)")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, args in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = ctypes.c_int
+    lib.ttt_last_error.argtypes = []
+    lib.ttt_last_error.restype = ctypes.c_char_p
+    lib.ttt_version.argtypes = []
+    lib.ttt_version.restype = ctypes.c_int
+    _lib = lib
+    return lib
+
+
+def _call(name: str, *args) -> None:
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.ttt_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name} failed (status {rc}): {msg}")
+
+
+# ---------------------------------------------------------------------------
+# Optional per-kernel timing with HIP events on the launch stream.
+# ---------------------------------------------------------------------------
+_timing: Optional[Dict[str, List[Tuple[torch.cuda.Event, torch.cuda.Event]]]] = None
+
+
+@contextlib.contextmanager
+def kernel_timing():
+    """Record a (start, end) HIP event pair around every launch while active.
+
+    Yields a dict ``name -> [(start, end), ...]``; call
+    ``torch.cuda.synchronize()`` before reading elapsed times.  While timing
+    is active, the fused entry points are issued as their per-kernel entry
+    points so that each kernel is bracketed on its own.
+    """
+    global _timing
+    prev = _timing
+    _timing = {}
+    try:
+        yield _timing
+    finally:
+        _timing = prev
+
+
+def _timed(name: str, *args) -> None:
+    if _timing is None:
+        _call(name, *args)
+        return
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record()
+    _call(name, *args)
+    e.record()
+    _timing.setdefault(name, []).append((s, e))
+
+
+def mean_ms(rec: Dict[str, List[Tuple[torch.cuda.Event, torch.cuda.Event]]]) -> Dict[str, float]:
+    return {k: sum(a.elapsed_time(b) for a, b in v) / len(v) for k, v in rec.items() if v}
+
+
+# ---------------------------------------------------------------------------
+# Operand preparation.
+# ---------------------------------------------------------------------------
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _view(t: Optional[torch.Tensor]):
+    if t is None:
+        return None
+    s = t.stride()
+    return ctypes.byref(_View(t.data_ptr(), s[0], s[1], s[2]))
+
+
+def _fptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def padded_head_dim(d: int) -> int:
+    if d <= 64:
+        return 64
+    if d <= 128:
+        return 128
+    raise NotImplementedError(f"head_dim {d} > 128 is not supported (the reference's kernels stop at 128 too)")
+
+
+def _kernel_ok(t: torch.Tensor) -> bool:
+    if t.stride(-1) != 1 and t.size(-1) > 1:
+        return False
+    eb = t.element_size()
+    if t.data_ptr() % 16:
+        return False
+    return all((s * eb) % 16 == 0 for s in t.stride()[:-1])
+
+
+def prep(t: torch.Tensor, d_pad: int) -> torch.Tensor:
+    """Return a [B,H,T,d_pad] tensor the kernels accept (copy only if needed)."""
+    d = t.size(-1)
+    if d != d_pad:
+        out = t.new_zeros(t.shape[:-1] + (d_pad,))
+        out[..., :d] = t
+        return out
+    if _kernel_ok(t):
+        return t
+    return t.contiguous()
+
+
+def check_inputs(*ts: torch.Tensor) -> None:
+    ref = ts[0]
+    if ref.dim() != 4:
+        raise ValueError(f"expected [B, H, T, D] tensors, got shape {tuple(ref.shape)}")
+    if ref.device.type != "cuda":
+        raise RuntimeError(
+            "ttt_kernels runs on a ROCm GPU; got a tensor on device "
+            f"'{ref.device}' (there is no CPU path)")
+    if ref.dtype not in _DTYPE_CODE:
+        raise TypeError(f"unsupported dtype {ref.dtype}; expected float16, bfloat16 or float32")
+    for t in ts[1:]:
+        if t.shape != ref.shape:
+            raise ValueError(f"shape mismatch: {tuple(t.shape)} vs {tuple(ref.shape)}")
+        if t.dtype != ref.dtype or t.device != ref.device:
+            raise ValueError("all operands must share dtype and device")
+
+
+def _problem(x: torch.Tensor, causal: bool, scale: float) -> _Problem:
+    b, h, t, d = x.shape
+    return _Problem(_DTYPE_CODE[x.dtype], 1 if causal else 0, b, h, t, d, float(scale))
+
+
+def alloc_p(like: torch.Tensor) -> torch.Tensor:
+    """[B,H,T,T] P buffer whose rows start on 16-byte boundaries."""
+    b, h, t, _ = like.shape
+    per = 16 // like.element_size()
+    tp = (t + per - 1) // per * per
+    buf = torch.empty((b, h, t, tp), dtype=like.dtype, device=like.device)
+    return buf if tp == t else buf[..., :t]
+
+
+def _stats(like: torch.Tensor) -> torch.Tensor:
+    b, h, t, _ = like.shape
+    return torch.empty((b, h, t), dtype=torch.float32, device=like.device)
+
+
+def prep_p(p: torch.Tensor) -> torch.Tensor:
+    if p.stride(-1) == 1 and p.data_ptr() % 16 == 0 and all(
+            (s * p.element_size()) % 16 == 0 for s in p.stride()[:-1]):
+        return p
+    out = alloc_p(p)
+    out.copy_(p)
+    return out
+
+
+def _empty_like_out(x: torch.Tensor) -> torch.Tensor:
+    return torch.empty(x.shape, dtype=x.dtype, device=x.device)
+
+
+# ---------------------------------------------------------------------------
+# Tensor-level entry points (inputs already padded and validated).
+# ---------------------------------------------------------------------------
+def fwd(q, k, v, causal: bool, scale: float, want_p: bool):
+    """Forward: O, LSE and (save_p) P.  Reference: TritonAttentionFn.forward,
+    ttt_kernels/triton_attention.py:261-337 (P path :51-59, :270-273)."""
+    o = _empty_like_out(q)
+    lse = _stats(q)
+    p = alloc_p(q) if want_p else None
+    if q.numel() == 0:
+        return o, lse, p
+    pr = _problem(q, causal, scale)
+    _timed("ttt_attn_fwd", ctypes.byref(pr), _view(q), _view(k), _view(v), _view(o), lse.data_ptr(),
+           _view(p), _stream())
+    return o, lse, p
+
+
+def bwd(q, k, v, o, do, lse, p, causal: bool, scale: float):
+    """First backward: dQ, dK, dV and the row statistic D = rowsum(dO o O).
+    Reference: TritonAttentionFn.backward, triton_attention.py:351-379 and
+    :416-420; launchers backward_stubs.py:154-181, 224-255, 362-425."""
+    dq = _empty_like_out(q)
+    dk = _empty_like_out(k)
+    dv = _empty_like_out(v)
+    rowsum = _stats(q)
+    if q.numel() == 0:
+        return dq, dk, dv, rowsum
+    pr = ctypes.byref(_problem(q, causal, scale))
+    st = _stream()
+    lse_p = _fptr(lse)
+    if _timing is None:
+        _call("ttt_attn_bwd", pr, _view(q), _view(k), _view(v), _view(o), _view(do), lse_p, _view(p),
+              rowsum.data_ptr(), _view(dq), _view(dk), _view(dv), st)
+    else:
+        _timed("ttt_attn_bwd_dq", pr, _view(q), _view(k), _view(v), _view(o), _view(do), lse_p, _view(p),
+               None, rowsum.data_ptr(), _view(dq), st)
+        _timed("ttt_attn_bwd_dkdv", pr, _view(q), _view(k), _view(v), _view(do), lse_p, _view(p),
+               rowsum.data_ptr(), _view(dk), _view(dv), st)
+    return dq, dk, dv, rowsum
+
+
+def bwd_dq(q, k, v, do, p, lse, rowsum, causal: bool, scale: float, o=None):
+    """dQ alone (D from rowsum, or formed from O).  Reference: _attn_bwd_dq_kernel,
+    backward_stubs.py:259-309."""
+    dq = _empty_like_out(q)
+    if q.numel() == 0:
+        return dq
+    pr = ctypes.byref(_problem(q, causal, scale))
+    _timed("ttt_attn_bwd_dq", pr, _view(q), _view(k), _view(v), _view(o), _view(do), _fptr(lse), _view(p),
+           _fptr(rowsum), None, _view(dq), _stream())
+    return dq
+
+
+def bwd_dkdv(q, k, v, do, p, lse, rowsum, causal: bool, scale: float, want_dk: bool = True):
+    """dK and dV (or dV alone).  Reference: backward_stubs.py:22-181, 313-359."""
+    dk = _empty_like_out(do) if want_dk else None
+    dv = _empty_like_out(do)
+    if do.numel() == 0:
+        return dk, dv
+    pr = ctypes.byref(_problem(do, causal, scale))
+    _timed("ttt_attn_bwd_dkdv", pr, _view(q), _view(k), _view(v), _view(do), _fptr(lse), _view(p),
+           _fptr(rowsum), _view(dk), _view(dv), _stream())
+    return dk, dv
+
+
+def rowsum_from_p(p, do, v, causal: bool):
+    """rowsum = sum_n P o (dO V^T).  Reference: backward_stubs.py:184-255."""
+    rs = _stats(do)
+    if do.numel() == 0:
+        return rs
+    pr = ctypes.byref(_problem(do, causal, 1.0))
+    _timed("ttt_attn_bwd_rowsum", pr, _view(p), _view(do), _view(v), rs.data_ptr(), _stream())
+    return rs
+
+
+def gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, causal: bool, scale: float, want_gdo: bool):
+    """Double backward: (GQ, GK, GV, GdO or None).  Reference stubs
+    backward_stubs.py:539-548; torch version :434-514 (corrected)."""
+    gq_out = _empty_like_out(q)
+    gk_out = _empty_like_out(k)
+    gv_out = _empty_like_out(v)
+    gdo = _empty_like_out(do) if want_gdo else None
+    e = _stats(q)
+    f = _stats(q)
+    if q.numel() == 0:
+        return gq_out, gk_out, gv_out, gdo
+    pr = ctypes.byref(_problem(q, causal, scale))
+    st = _stream()
+    lse_p = _fptr(lse)
+    if _timing is None:
+        _call("ttt_attn_gg", pr, _view(q), _view(k), _view(v), _view(do), lse_p, _view(p), rowsum.data_ptr(),
+              _view(gq), _view(gk), _view(gv), _view(gq_out), _view(gk_out), _view(gv_out), _view(gdo),
+              e.data_ptr(), f.data_ptr(), st)
+    else:
+        _timed("ttt_attn_gg_row", pr, _view(q), _view(k), _view(v), _view(do), lse_p, _view(p),
+               rowsum.data_ptr(), _view(gq), _view(gk), _view(gv), _view(gq_out), _view(gdo), e.data_ptr(),
+               f.data_ptr(), st)
+        _timed("ttt_attn_gg_col", pr, _view(q), _view(k), _view(v), _view(do), lse_p, _view(p),
+               rowsum.data_ptr(), e.data_ptr(), f.data_ptr(), _view(gq), _view(gk), _view(gv), _view(gk_out),
+               _view(gv_out), st)
+    return gq_out, gk_out, gv_out, gdo
+
+
+def exported_symbols() -> List[str]:
+    """Names of the C entry points this binding uses (for ABI checks)."""
+    return list(_SIGS) + ["ttt_last_error", "ttt_version"]

@@ -1,0 +1,406 @@
+// ttt_common.h — device-side building blocks shared by the gfx950 attention
+// kernels: element traits over the MFMA instructions, the fragment layout,
+// global->LDS tile staging in row-major and transposed form, and the two
+// tile products every kernel is made of.
+//
+// Work decomposition used by every kernel.  A workgroup has 256 threads (four
+// wave64s) and owns 64 "stationary" rows (query rows m for row-block kernels,
+// key rows n for column-block kernels); wave w owns stationary rows 16w..16w+15
+// and lane (c = lane%16, g = lane/16) owns stationary row 16w+c.  The kernel
+// streams 64-row tiles of the other index through LDS.
+//
+// A 64(streamed) x 16(stationary) score-like tile lives in the MFMA
+// accumulator layout of four 16x16 subtiles.  The streamed rows fed to the
+// A operand of subtile a are permuted so that lane (c,g) ends up holding, for
+// k-block kb in {0,1} and slot j in 0..7, the value at streamed index
+//     32*kb + 8*g + j            (see stream_index()).
+// Those eight values per k-block are exactly the B-operand fragment a
+// following MFMA needs when it contracts over the streamed index, so score
+// tiles chain into the next product straight from registers, and per-row
+// statistics of the stationary row stay inside one lane plus two cross-lane
+// steps (xor 16, xor 32).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ttt {
+
+constexpr int kThreads = 256;  // four wave64s per workgroup
+constexpr int kBlk = 64;       // stationary rows per workgroup == streamed tile rows
+
+constexpr float kLog2e = 1.4426950408889634f;  // 1/ln(2)
+constexpr float kLn2 = 0.6931471805599453f;    // ln(2)
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Kernel argument block (passed by value).  [B,H,T,*] operands are base
+// pointers plus element strides; the last dimension is contiguous.
+struct View {
+  void* p;
+  int64_t sb, sh, st;
+};
+
+struct Params {
+  int B, H, T;
+  int causal;
+  float scale;       // s
+  float scale_log2;  // s * log2(e): scores are kept in base-2 units
+  View q, k, v, o, dout;
+  View gq, gk, gv;           // cotangents on (dQ, dK, dV)
+  View dq, dk, dv;           // first-backward outputs
+  View gq_out, gk_out, gv_out, gdout;  // double-backward outputs
+  View p;                    // P, [B,H,T,T], st = row stride
+  float* lse;                // [B*H*T]
+  const float* rowsum_in;    // D (read), or nullptr
+  float* rowsum_out;         // D (written), or nullptr
+  float* e;                  // E row statistic
+  float* f;                  // F row statistic
+};
+
+template <typename T>
+__device__ __forceinline__ T* at(const View& v, int b, int h) {
+  return reinterpret_cast<T*>(v.p) + (int64_t)b * v.sb + (int64_t)h * v.sh;
+}
+
+// ---------------------------------------------------------------------------
+// Element traits.  A fragment is eight consecutive k-slots of one lane for a
+// 32-wide k-block: one v_mfma_f32_16x16x32_{f16,bf16}, or eight
+// v_mfma_f32_16x16x4_f32 whose k-slot t of lane group g is k = 8g + t.
+// ---------------------------------------------------------------------------
+template <typename T>
+struct Elem;
+
+template <>
+struct Elem<_Float16> {
+  typedef f16x8 frag;
+  static constexpr int kChunk = 8;  // elements per 16-byte chunk
+  static __device__ __forceinline__ f32x4 mma(f32x4 c, frag a, frag b) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ _Float16 cvt(float x) { return (_Float16)x; }
+  static __device__ __forceinline__ float f32(_Float16 x) { return (float)x; }
+};
+
+template <>
+struct Elem<__bf16> {
+  typedef bf16x8 frag;
+  static constexpr int kChunk = 8;
+  static __device__ __forceinline__ f32x4 mma(f32x4 c, frag a, frag b) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ __bf16 cvt(float x) { return (__bf16)x; }
+  static __device__ __forceinline__ float f32(__bf16 x) { return (float)x; }
+};
+
+template <>
+struct Elem<float> {
+  typedef f32x8 frag;
+  static constexpr int kChunk = 4;
+  static __device__ __forceinline__ f32x4 mma(f32x4 c, frag a, frag b) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t], b[t], c, 0, 0, 0);
+    return c;
+  }
+  static __device__ __forceinline__ float cvt(float x) { return x; }
+  static __device__ __forceinline__ float f32(float x) { return x; }
+};
+
+// ---------------------------------------------------------------------------
+// Fragment loads (eight consecutive elements; 16 B for 16-bit types, 32 B
+// for fp32).  Addresses are 16-byte aligned.
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::frag load_frag(const T* p) {
+  typedef typename Elem<T>::frag F;
+  if constexpr (sizeof(T) == 2) {
+    return *reinterpret_cast<const F*>(p);
+  } else {
+    const f32x4 lo = *reinterpret_cast<const f32x4*>(p);
+    const f32x4 hi = *reinterpret_cast<const f32x4*>(p + 4);
+    F r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { r[j] = lo[j]; r[4 + j] = hi[j]; }
+    return r;
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::frag zero_frag() {
+  typename Elem<T>::frag r;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = Elem<T>::cvt(0.f);
+  return r;
+}
+
+// Row `row` of a [T][*] matrix, eight elements from column `col`; zero when
+// row >= nrows.
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::frag load_frag_row(const T* base, int64_t ld, int row,
+                                                                int nrows, int col) {
+  if (row < nrows) return load_frag<T>(base + (int64_t)row * ld + col);
+  return zero_frag<T>();
+}
+
+// Store eight consecutive elements (16-bit types: one 16-byte store).
+template <typename T>
+__device__ __forceinline__ void store8(T* p, const float* v) {
+  if constexpr (sizeof(T) == 2) {
+    typename Elem<T>::frag f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f[j] = Elem<T>::cvt(v[j]);
+    *reinterpret_cast<typename Elem<T>::frag*>(p) = f;
+  } else {
+    f32x4 lo, hi;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { lo[j] = v[j]; hi[j] = v[4 + j]; }
+    *reinterpret_cast<f32x4*>(p) = lo;
+    *reinterpret_cast<f32x4*>(p + 4) = hi;
+  }
+}
+
+// Store four consecutive elements.
+template <typename T>
+__device__ __forceinline__ void store4(T* p, f32x4 v) {
+  if constexpr (sizeof(T) == 2) {
+    typedef T t4 __attribute__((ext_vector_type(4)));
+    t4 f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f[j] = Elem<T>::cvt(v[j]);
+    *reinterpret_cast<t4*>(p) = f;
+  } else {
+    *reinterpret_cast<f32x4*>(p) = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Score-tile container: 64 streamed x 16 stationary values per wave, held as
+// four MFMA accumulators.  at(kb, j) is the value at streamed index
+// 32*kb + 8*g + j for this lane's stationary row.
+// ---------------------------------------------------------------------------
+struct Tile {
+  f32x4 q[4];
+  __device__ __forceinline__ float at(int kb, int j) const { return q[2 * kb + (j >> 2)][j & 3]; }
+  __device__ __forceinline__ void set(int kb, int j, float x) { q[2 * kb + (j >> 2)][j & 3] = x; }
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int a = 0; a < 4; ++a) q[a] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+};
+
+__device__ __forceinline__ int stream_index(int kb, int g, int j) { return 32 * kb + 8 * g + j; }
+
+// Streamed row fed to A-operand row r of subtile a, chosen so that the
+// accumulator row 4g+i of subtile a holds stream_index(a>>1, g, 4*(a&1)+i).
+__device__ __forceinline__ int sigma(int a, int r) {
+  return 32 * (a >> 1) + 8 * (r >> 2) + 4 * (a & 1) + (r & 3);
+}
+
+// B fragment for k-block kb built from a score tile (converted to T).
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::frag tile_frag(const Tile& s, int kb) {
+  typename Elem<T>::frag f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) f[j] = Elem<T>::cvt(s.at(kb, j));
+  return f;
+}
+
+// Same, from a pair of values arrays v[kb][j] (used when the values already
+// sit in a plain array).
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::frag vals_frag(const float* v) {
+  typename Elem<T>::frag f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) f[j] = Elem<T>::cvt(v[j]);
+  return f;
+}
+
+// ---------------------------------------------------------------------------
+// LDS tile geometry.  A row-major tile is 64 rows x NCOL with pitch NCOL+chunk;
+// a transposed tile is NCOL rows x 64 with pitch 64+chunk.  Both pitches keep
+// every 8-element fragment 16-byte aligned.
+// ---------------------------------------------------------------------------
+template <typename T, int NCOL>
+struct Lds {
+  static constexpr int kChunk = Elem<T>::kChunk;
+  static constexpr int kRowPitch = NCOL + kChunk;
+  static constexpr int kTrPitch = kBlk + kChunk;
+  static constexpr int kRowElems = kBlk * kRowPitch;
+  static constexpr int kTrElems = NCOL * kTrPitch;
+};
+
+// Staged registers of one 64 x NCOL tile: each thread owns pairs of
+// consecutive rows (2r, 2r+1) at one 16-byte column chunk.
+template <typename T, int NCOL>
+struct Stage {
+  static constexpr int kChunk = Elem<T>::kChunk;
+  static constexpr int kChunksPerRow = NCOL / kChunk;
+  static constexpr int kPairsPerPass = kThreads / kChunksPerRow;
+  static constexpr int kPasses = (kBlk / 2) / kPairsPerPass;
+  static_assert(kPasses >= 1 && kPairsPerPass * kChunksPerRow == kThreads, "tile shape");
+  u32x4 x0[kPasses], x1[kPasses];
+};
+
+__device__ __forceinline__ u32x4 load16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// Load a 64 x NCOL tile whose element [0][0] is at g (row stride ld).  Rows at
+// or beyond rows_valid and columns at or beyond cols_valid read as zero.
+template <typename T, int NCOL>
+__device__ __forceinline__ void stage_load(Stage<T, NCOL>& st, const T* __restrict__ g, int64_t ld,
+                                           int rows_valid, int cols_valid) {
+  typedef Stage<T, NCOL> S;
+  const int tid = threadIdx.x;
+  const int ch = tid % S::kChunksPerRow;
+  const int col = ch * S::kChunk;
+#pragma unroll
+  for (int ps = 0; ps < S::kPasses; ++ps) {
+    const int r = 2 * (tid / S::kChunksPerRow + ps * S::kPairsPerPass);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int row = r + h;
+      u32x4 x = u32x4{0u, 0u, 0u, 0u};
+      if (row < rows_valid) {
+        const T* src = g + (int64_t)row * ld + col;
+        if (col + S::kChunk <= cols_valid) {
+          x = load16(src);
+        } else {
+          T tmp[S::kChunk];
+#pragma unroll
+          for (int e = 0; e < S::kChunk; ++e) tmp[e] = (col + e < cols_valid) ? src[e] : Elem<T>::cvt(0.f);
+          __builtin_memcpy(&x, tmp, 16);
+        }
+      }
+      if (h == 0) st.x0[ps] = x; else st.x1[ps] = x;
+    }
+  }
+}
+
+// Write staged registers to a row-major LDS tile.
+template <typename T, int NCOL>
+__device__ __forceinline__ void stage_store_rows(const Stage<T, NCOL>& st, T* lds) {
+  typedef Stage<T, NCOL> S;
+  constexpr int P = Lds<T, NCOL>::kRowPitch;
+  const int tid = threadIdx.x;
+  const int col = (tid % S::kChunksPerRow) * S::kChunk;
+#pragma unroll
+  for (int ps = 0; ps < S::kPasses; ++ps) {
+    const int r = 2 * (tid / S::kChunksPerRow + ps * S::kPairsPerPass);
+    *reinterpret_cast<u32x4*>(lds + r * P + col) = st.x0[ps];
+    *reinterpret_cast<u32x4*>(lds + (r + 1) * P + col) = st.x1[ps];
+  }
+}
+
+// Write staged registers to a transposed LDS tile (element [row][col] goes to
+// lds[col][row]).  Rows are paired so each write is 32 bits (16-bit types) or
+// 64 bits (fp32).
+template <typename T, int NCOL>
+__device__ __forceinline__ void stage_store_tr(const Stage<T, NCOL>& st, T* lds) {
+  typedef Stage<T, NCOL> S;
+  constexpr int P = Lds<T, NCOL>::kTrPitch;
+  const int tid = threadIdx.x;
+  const int col = (tid % S::kChunksPerRow) * S::kChunk;
+#pragma unroll
+  for (int ps = 0; ps < S::kPasses; ++ps) {
+    const int r = 2 * (tid / S::kChunksPerRow + ps * S::kPairsPerPass);
+    if constexpr (sizeof(T) == 2) {
+      const uint32_t* a = reinterpret_cast<const uint32_t*>(&st.x0[ps]);
+      const uint32_t* b = reinterpret_cast<const uint32_t*>(&st.x1[ps]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t lo = (a[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+        const uint32_t hi = (b[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+        *reinterpret_cast<uint32_t*>(lds + (col + e) * P + r) = lo | (hi << 16);
+      }
+    } else {
+      const uint32_t* a = reinterpret_cast<const uint32_t*>(&st.x0[ps]);
+      const uint32_t* b = reinterpret_cast<const uint32_t*>(&st.x1[ps]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        *reinterpret_cast<u32x2*>(lds + (col + e) * P + r) = u32x2{a[e], b[e]};
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Tile products.
+//
+// mm_d: out(streamed, stationary) += sum_d Str[streamed][d] * Sta[stationary][d]
+//   rows: row-major LDS tile of the streamed operand (64 x D);
+//   sta:  this lane's stationary fragments, sta[ks] = Sta[row][32ks+8g .. +7].
+//
+// mm_s: acc^T[d][stationary] += sum_streamed Tr[d][streamed] * Y[streamed][stationary]
+//   tr: transposed LDS tile of the streamed operand (D x 64);
+//   y:  per k-block B fragments built from a score tile.
+//   acc[dsub] holds d = 16*dsub + 4*g + i for this lane's stationary row.
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__device__ __forceinline__ void mm_d(Tile& out, const T* rows, const typename Elem<T>::frag* sta) {
+  constexpr int P = Lds<T, D>::kRowPitch;
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const T* rp = rows + sigma(a, c) * P + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) out.q[a] = Elem<T>::mma(out.q[a], load_frag<T>(rp + 32 * ks), sta[ks]);
+  }
+}
+
+template <typename T, int D>
+__device__ __forceinline__ void mm_s(f32x4* acc, const T* tr, const typename Elem<T>::frag* y) {
+  constexpr int P = Lds<T, D>::kTrPitch;
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+    for (int ds = 0; ds < D / 16; ++ds) {
+      acc[ds] = Elem<T>::mma(acc[ds], load_frag<T>(tr + (16 * ds + c) * P + 32 * kb + 8 * g), y[kb]);
+    }
+  }
+}
+
+// Sum over the four lane groups (same c): xor 16 and xor 32.
+__device__ __forceinline__ float group_sum(float x) {
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+__device__ __forceinline__ float group_max(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16));
+  x = fmaxf(x, __shfl_xor(x, 32));
+  return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Store a transposed accumulator acc^T[d][stationary] (this lane: stationary
+// row `row`, d = 16*ds + 4*g + i) to a row-major [T][D] output, scaled.
+template <typename T, int D>
+__device__ __forceinline__ void store_acc_rows(T* base, int64_t ld, int row, int nrows, const f32x4* acc,
+                                               float mul) {
+  if (row >= nrows) return;
+  const int g = (threadIdx.x & 63) >> 4;
+  T* rp = base + (int64_t)row * ld + 4 * g;
+#pragma unroll
+  for (int ds = 0; ds < D / 16; ++ds) store4<T>(rp + 16 * ds, acc[ds] * mul);
+}
+
+// Eight consecutive fp32 values v[0..7] = src[idx0 .. idx0+7], zero past n.
+__device__ __forceinline__ void load_vec8(float* v, const float* src, int idx0, int n) {
+  if (idx0 + 8 <= n && ((reinterpret_cast<uintptr_t>(src + idx0) & 15) == 0)) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(src + idx0);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(src + idx0 + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { v[j] = a[j]; v[4 + j] = b[j]; }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = (idx0 + j < n) ? src[idx0 + j] : 0.f;
+  }
+}
+
+}  // namespace ttt

@@ -1,0 +1,419 @@
+// ttt_gg.hip — double backward of attention (gradients of the first-backward
+// outputs dQ, dK, dV with respect to q, k, v and dO) for gfx950.
+//
+// With cotangents gQ, gK, gV on (dQ, dK, dV), per (b,h) slice:
+//   gdS = s*(gQ*K^T + Q*gK^T)         gP1 = dO*gV^T
+//   dS  = P o (dP - D)                E   = rowsum(gdS o P)
+//   gdP = P o (gdS - E)               gP  = gP1 + gdS o (dP - D) - E o dP
+//   F   = rowsum(gP o P)              gS  = P o (gP - F)
+//   GQ  = s*(dS*gK + gS*K)            GK  = s*(dS^T*gQ + gS^T*Q)
+//   GV  = gdP^T*dO                    GdO = P*gV + gdP*V
+//
+// k_gg_row (stationary query rows, streamed key tiles) needs E and F, which
+// are full-row sums, before gS is known.  It avoids a second sweep by
+// accumulating four products whose combination gives gS*K exactly:
+//   gS = Z1 - E o Z2 - F o P,  Z1 = P o gP1 + gdS o dS,  Z2 = P o dP,
+//   so gS*K = Z1*K - E o (Z2*K) - F o (P*K)   (E, F scale rows),
+// and F = rowsum(Z1) - E * rowsum(Z2).  Likewise
+//   gdP*V = (P o gdS)*V - E o (P*V).
+// It writes GQ, optionally GdO, and E and F for the column pass.
+//
+// k_gg_col (stationary key rows, streamed query tiles) reads D, E, F per
+// streamed row and forms dS, gdP, gS tile by tile for GK and GV.
+//
+// Reference: the reference's double backward is the torch code of
+// ttt_kernels/backward_stubs.py:434-514 (whose grad_ds term at :491-492 has
+// gdk*Q^T where Q*gK^T is required, and which drops every term through P
+// because its cached P carries no graph), and the exact ATen double backward
+// of the recompute path, ttt_kernels/triton_attention.py:416-420.  These
+// kernels compute the exact second derivative of the math path
+// (triton_attention.py:18-25) in closed form.
+#include "ttt_common.h"
+#include "ttt_launch.h"
+
+namespace ttt {
+
+template <typename T>
+__device__ __forceinline__ void load_p_row_gg(Tile& p, const T* pm, int n0, int T_, bool row_ok) {
+  const int g = (threadIdx.x & 63) >> 4;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    const int n = n0 + stream_index(kb, g, 0);
+    if (row_ok && n + 8 <= T_) {
+      const typename Elem<T>::frag f = load_frag<T>(pm + n);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) p.set(kb, j, Elem<T>::f32(f[j]));
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) p.set(kb, j, (row_ok && n + j < T_) ? Elem<T>::f32(pm[n + j]) : 0.f);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool LOADP, bool GDO>
+__global__ __launch_bounds__(kThreads) void k_gg_row(Params a) {
+  typedef Elem<T> E;
+  typedef typename E::frag frag;
+  typedef Lds<T, D> L;
+  constexpr int kA = 4 * L::kRowElems;                 // K, V, gK, gV rows
+  constexpr int kB = (GDO ? 4 : 2) * L::kTrElems;      // K^T, gK^T (, V^T, gV^T)
+  __shared__ __align__(16) T smem[kA > kB ? kA : kB];
+  T* sK = smem;
+  T* sV = smem + L::kRowElems;
+  T* sgK = smem + 2 * L::kRowElems;
+  T* sgV = smem + 3 * L::kRowElems;
+  T* sKt = smem;
+  T* sgKt = smem + L::kTrElems;
+  T* sVt = smem + 2 * L::kTrElems;
+  T* sgVt = smem + 3 * L::kTrElems;
+
+  const int T_ = a.T;
+  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+  const int nblk = (T_ + kBlk - 1) / kBlk;
+  const int mb = a.causal ? (nblk - 1 - (int)blockIdx.x) : (int)blockIdx.x;
+  const int m0 = mb * kBlk;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c = lane & 15, g = lane >> 4;
+  const int m = m0 + 16 * w + c;
+  const bool row_ok = m < T_;
+
+  const T* Q = at<const T>(a.q, b, h);
+  const T* K = at<const T>(a.k, b, h);
+  const T* V = at<const T>(a.v, b, h);
+  const T* dO = at<const T>(a.dout, b, h);
+  const T* gQ = at<const T>(a.gq, b, h);
+  const T* gK = at<const T>(a.gk, b, h);
+  const T* gV = at<const T>(a.gv, b, h);
+
+  frag qf[D / 32], gqf[D / 32], dof[D / 32];
+#pragma unroll
+  for (int ks = 0; ks < D / 32; ++ks) {
+    qf[ks] = load_frag_row<T>(Q, a.q.st, m, T_, 32 * ks + 8 * g);
+    gqf[ks] = load_frag_row<T>(gQ, a.gq.st, m, T_, 32 * ks + 8 * g);
+    dof[ks] = load_frag_row<T>(dO, a.dout.st, m, T_, 32 * ks + 8 * g);
+  }
+  const int64_t ridx = (int64_t)bh * T_ + m;
+  const float Dm = row_ok ? a.rowsum_in[ridx] : 0.f;
+  const float lse2 = (!LOADP && row_ok) ? a.lse[ridx] * kLog2e : 0.f;
+  const T* Pm = LOADP ? at<const T>(a.p, b, h) + (int64_t)(row_ok ? m : 0) * a.p.st : nullptr;
+  const float s = a.scale;
+
+  f32x4 a1[D / 16], a2[D / 16], a3[D / 16], a4[D / 16];
+  f32x4 b1[GDO ? D / 16 : 1], b2[GDO ? D / 16 : 1], b3[GDO ? D / 16 : 1];
+#pragma unroll
+  for (int i = 0; i < D / 16; ++i) {
+    a1[i] = a2[i] = a3[i] = a4[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (GDO) b1[i] = b2[i] = b3[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  float e_acc = 0.f, x_acc = 0.f, d_acc = 0.f;
+
+  const int n_end = a.causal ? mb + 1 : nblk;
+  for (int nb = 0; nb < n_end; ++nb) {
+    const int n0 = nb * kBlk;
+    const int rows_valid = T_ - n0;
+    {
+      Stage<T, D> s0, s1, s2, s3;
+      stage_load<T, D>(s0, K + (int64_t)n0 * a.k.st, a.k.st, rows_valid, D);
+      stage_load<T, D>(s1, V + (int64_t)n0 * a.v.st, a.v.st, rows_valid, D);
+      stage_load<T, D>(s2, gK + (int64_t)n0 * a.gk.st, a.gk.st, rows_valid, D);
+      stage_load<T, D>(s3, gV + (int64_t)n0 * a.gv.st, a.gv.st, rows_valid, D);
+      __syncthreads();
+      stage_store_rows<T, D>(s0, sK);
+      stage_store_rows<T, D>(s1, sV);
+      stage_store_rows<T, D>(s2, sgK);
+      stage_store_rows<T, D>(s3, sgV);
+      __syncthreads();
+    }
+    Tile p, dp, gds, gp1;
+    if constexpr (LOADP) {
+      load_p_row_gg<T>(p, Pm, n0, T_, row_ok);
+    } else {
+      p.zero();
+      mm_d<T, D>(p, sK, qf);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) p.set(kb, j, fast_exp2(p.at(kb, j) * a.scale_log2 - lse2));
+    }
+    const bool need_mask = (a.causal && nb == mb) || (n0 + kBlk > T_);
+    if (need_mask) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int n = n0 + stream_index(kb, g, j);
+          if (n >= T_ || (a.causal && n > m)) p.set(kb, j, 0.f);
+        }
+    }
+    dp.zero();
+    gds.zero();
+    gp1.zero();
+    mm_d<T, D>(dp, sV, dof);
+    mm_d<T, D>(gds, sgK, qf);
+    mm_d<T, D>(gds, sK, gqf);
+    mm_d<T, D>(gp1, sgV, dof);
+
+    frag dsf[2], z1f[2], z2f[2], pf[2], z4f[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      float vds[8], vz1[8], vz2[8], vz4[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float P = p.at(kb, j);
+        const float gd = s * gds.at(kb, j);
+        const float dpv = dp.at(kb, j);
+        const float ds = P * (dpv - Dm);
+        const float z1 = P * gp1.at(kb, j) + gd * ds;
+        const float z2 = P * dpv;
+        e_acc += gd * P;
+        x_acc += z1;
+        d_acc += z2;
+        vds[j] = ds;
+        vz1[j] = z1;
+        vz2[j] = z2;
+        vz4[j] = P * gd;
+      }
+      dsf[kb] = vals_frag<T>(vds);
+      z1f[kb] = vals_frag<T>(vz1);
+      z2f[kb] = vals_frag<T>(vz2);
+      pf[kb] = tile_frag<T>(p, kb);
+      if constexpr (GDO) z4f[kb] = vals_frag<T>(vz4);
+    }
+    {
+      Stage<T, D> s0, s1, s2, s3;
+      stage_load<T, D>(s0, K + (int64_t)n0 * a.k.st, a.k.st, rows_valid, D);
+      stage_load<T, D>(s1, gK + (int64_t)n0 * a.gk.st, a.gk.st, rows_valid, D);
+      if constexpr (GDO) {
+        stage_load<T, D>(s2, V + (int64_t)n0 * a.v.st, a.v.st, rows_valid, D);
+        stage_load<T, D>(s3, gV + (int64_t)n0 * a.gv.st, a.gv.st, rows_valid, D);
+      }
+      __syncthreads();
+      stage_store_tr<T, D>(s0, sKt);
+      stage_store_tr<T, D>(s1, sgKt);
+      if constexpr (GDO) {
+        stage_store_tr<T, D>(s2, sVt);
+        stage_store_tr<T, D>(s3, sgVt);
+      }
+      __syncthreads();
+    }
+    mm_s<T, D>(a1, sgKt, dsf);
+    mm_s<T, D>(a2, sKt, z1f);
+    mm_s<T, D>(a3, sKt, z2f);
+    mm_s<T, D>(a4, sKt, pf);
+    if constexpr (GDO) {
+      mm_s<T, D>(b1, sgVt, pf);
+      mm_s<T, D>(b2, sVt, z4f);
+      mm_s<T, D>(b3, sVt, pf);
+    }
+  }
+  const float Ev = group_sum(e_acc);
+  const float Xv = group_sum(x_acc);
+  const float Dv = group_sum(d_acc);
+  const float Fv = Xv - Ev * Dv;
+  f32x4 gq[D / 16];
+#pragma unroll
+  for (int i = 0; i < D / 16; ++i) gq[i] = a1[i] + a2[i] - Ev * a3[i] - Fv * a4[i];
+  store_acc_rows<T, D>(at<T>(a.gq_out, b, h), a.gq_out.st, m, T_, gq, s);
+  if constexpr (GDO) {
+    f32x4 go[D / 16];
+#pragma unroll
+    for (int i = 0; i < D / 16; ++i) go[i] = b1[i] + b2[i] - Ev * b3[i];
+    store_acc_rows<T, D>(at<T>(a.gdout, b, h), a.gdout.st, m, T_, go, 1.f);
+  }
+  if (row_ok && g == 0) {
+    a.e[ridx] = Ev;
+    a.f[ridx] = Fv;
+  }
+}
+
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool LOADP>
+__global__ __launch_bounds__(kThreads) void k_gg_col(Params a) {
+  typedef Elem<T> E;
+  typedef typename E::frag frag;
+  typedef Lds<T, D> L;
+  typedef Lds<T, kBlk> LP;
+  constexpr int kA = 3 * L::kRowElems + (LOADP ? LP::kTrElems : 0);  // Q, gQ, dO rows (+ P^T)
+  constexpr int kB = 3 * L::kTrElems;                                  // gQ^T, Q^T, dO^T
+  __shared__ __align__(16) T smem[kA > kB ? kA : kB];
+  T* sQ = smem;
+  T* sgQ = smem + L::kRowElems;
+  T* sdO = smem + 2 * L::kRowElems;
+  T* sPt = smem + 3 * L::kRowElems;
+  T* sgQt = smem;
+  T* sQt = smem + L::kTrElems;
+  T* sdOt = smem + 2 * L::kTrElems;
+
+  const int T_ = a.T;
+  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+  const int nblk = (T_ + kBlk - 1) / kBlk;
+  const int nb = (int)blockIdx.x;
+  const int n0 = nb * kBlk;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c = lane & 15, g = lane >> 4;
+  const int n = n0 + 16 * w + c;
+
+  const T* Q = at<const T>(a.q, b, h);
+  const T* K = at<const T>(a.k, b, h);
+  const T* V = at<const T>(a.v, b, h);
+  const T* dO = at<const T>(a.dout, b, h);
+  const T* gQ = at<const T>(a.gq, b, h);
+  const T* gK = at<const T>(a.gk, b, h);
+  const T* gV = at<const T>(a.gv, b, h);
+  const T* Pb = LOADP ? at<const T>(a.p, b, h) : nullptr;
+  const float* rs = a.rowsum_in + (int64_t)bh * T_;
+  const float* ev = a.e + (int64_t)bh * T_;
+  const float* fv = a.f + (int64_t)bh * T_;
+  const float* lse = a.lse + (int64_t)bh * T_;
+  const float s = a.scale;
+
+  frag kf[D / 32], gkf[D / 32], vf[D / 32], gvf[D / 32];
+#pragma unroll
+  for (int ks = 0; ks < D / 32; ++ks) {
+    kf[ks] = load_frag_row<T>(K, a.k.st, n, T_, 32 * ks + 8 * g);
+    gkf[ks] = load_frag_row<T>(gK, a.gk.st, n, T_, 32 * ks + 8 * g);
+    vf[ks] = load_frag_row<T>(V, a.v.st, n, T_, 32 * ks + 8 * g);
+    gvf[ks] = load_frag_row<T>(gV, a.gv.st, n, T_, 32 * ks + 8 * g);
+  }
+
+  f32x4 acc_gk[D / 16], acc_gv[D / 16];
+#pragma unroll
+  for (int i = 0; i < D / 16; ++i) acc_gk[i] = acc_gv[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int m_begin = a.causal ? nb : 0;
+  for (int mb = m_begin; mb < nblk; ++mb) {
+    const int m0 = mb * kBlk;
+    const int rows_valid = T_ - m0;
+    {
+      Stage<T, D> s0, s1, s2;
+      Stage<T, kBlk> sp;
+      stage_load<T, D>(s0, Q + (int64_t)m0 * a.q.st, a.q.st, rows_valid, D);
+      stage_load<T, D>(s1, gQ + (int64_t)m0 * a.gq.st, a.gq.st, rows_valid, D);
+      stage_load<T, D>(s2, dO + (int64_t)m0 * a.dout.st, a.dout.st, rows_valid, D);
+      if constexpr (LOADP) stage_load<T, kBlk>(sp, Pb + (int64_t)m0 * a.p.st + n0, a.p.st, rows_valid, T_ - n0);
+      __syncthreads();
+      stage_store_rows<T, D>(s0, sQ);
+      stage_store_rows<T, D>(s1, sgQ);
+      stage_store_rows<T, D>(s2, sdO);
+      if constexpr (LOADP) stage_store_tr<T, kBlk>(sp, sPt);
+      __syncthreads();
+    }
+    Tile p, dp, gds, gp1;
+    if constexpr (LOADP) {
+      constexpr int PP = LP::kTrPitch;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const frag f = load_frag<T>(sPt + (16 * w + c) * PP + stream_index(kb, g, 0));
+#pragma unroll
+        for (int j = 0; j < 8; ++j) p.set(kb, j, E::f32(f[j]));
+      }
+    } else {
+      p.zero();
+      mm_d<T, D>(p, sQ, kf);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        float l2[8];
+        load_vec8(l2, lse, m0 + stream_index(kb, g, 0), T_);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) p.set(kb, j, fast_exp2(p.at(kb, j) * a.scale_log2 - l2[j] * kLog2e));
+      }
+    }
+    const bool need_mask = (a.causal && mb == nb) || (m0 + kBlk > T_) || (n0 + kBlk > T_);
+    if (need_mask) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int mm = m0 + stream_index(kb, g, j);
+          if (mm >= T_ || n >= T_ || (a.causal && n > mm)) p.set(kb, j, 0.f);
+        }
+    }
+    dp.zero();
+    gds.zero();
+    gp1.zero();
+    mm_d<T, D>(dp, sdO, vf);
+    mm_d<T, D>(gds, sgQ, kf);
+    mm_d<T, D>(gds, sQ, gkf);
+    mm_d<T, D>(gp1, sdO, gvf);
+
+    frag dsf[2], gsf[2], gdpf[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      float d8[8], e8[8], f8[8];
+      const int idx = m0 + stream_index(kb, g, 0);
+      load_vec8(d8, rs, idx, T_);
+      load_vec8(e8, ev, idx, T_);
+      load_vec8(f8, fv, idx, T_);
+      float vds[8], vgs[8], vgdp[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float P = p.at(kb, j);
+        const float dpv = dp.at(kb, j);
+        const float gd = s * gds.at(kb, j);
+        const float dmd = dpv - d8[j];
+        const float gp = gp1.at(kb, j) + gd * dmd - e8[j] * dpv;
+        vds[j] = P * dmd;
+        vgdp[j] = P * (gd - e8[j]);
+        vgs[j] = P * (gp - f8[j]);
+      }
+      dsf[kb] = vals_frag<T>(vds);
+      gsf[kb] = vals_frag<T>(vgs);
+      gdpf[kb] = vals_frag<T>(vgdp);
+    }
+    {
+      Stage<T, D> s0, s1, s2;
+      stage_load<T, D>(s0, gQ + (int64_t)m0 * a.gq.st, a.gq.st, rows_valid, D);
+      stage_load<T, D>(s1, Q + (int64_t)m0 * a.q.st, a.q.st, rows_valid, D);
+      stage_load<T, D>(s2, dO + (int64_t)m0 * a.dout.st, a.dout.st, rows_valid, D);
+      __syncthreads();
+      stage_store_tr<T, D>(s0, sgQt);
+      stage_store_tr<T, D>(s1, sQt);
+      stage_store_tr<T, D>(s2, sdOt);
+      __syncthreads();
+    }
+    mm_s<T, D>(acc_gk, sgQt, dsf);
+    mm_s<T, D>(acc_gk, sQt, gsf);
+    mm_s<T, D>(acc_gv, sdOt, gdpf);
+  }
+  store_acc_rows<T, D>(at<T>(a.gk_out, b, h), a.gk_out.st, n, T_, acc_gk, s);
+  store_acc_rows<T, D>(at<T>(a.gv_out, b, h), a.gv_out.st, n, T_, acc_gv, 1.f);
+}
+
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+static hipError_t launch_gg_row_t(const Params& a, bool load_p, bool gdo, hipStream_t st) {
+  dim3 grid((a.T + kBlk - 1) / kBlk, a.B * a.H);
+  if (load_p) {
+    if (gdo)
+      hipLaunchKernelGGL((k_gg_row<T, D, true, true>), grid, dim3(kThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((k_gg_row<T, D, true, false>), grid, dim3(kThreads), 0, st, a);
+  } else {
+    if (gdo)
+      hipLaunchKernelGGL((k_gg_row<T, D, false, true>), grid, dim3(kThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((k_gg_row<T, D, false, false>), grid, dim3(kThreads), 0, st, a);
+  }
+  return hipGetLastError();
+}
+
+template <typename T, int D>
+static hipError_t launch_gg_col_t(const Params& a, bool load_p, hipStream_t st) {
+  dim3 grid((a.T + kBlk - 1) / kBlk, a.B * a.H);
+  if (load_p)
+    hipLaunchKernelGGL((k_gg_col<T, D, true>), grid, dim3(kThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL((k_gg_col<T, D, false>), grid, dim3(kThreads), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_gg_row(int dtype, int D, const Params& a, bool load_p, bool want_gdout, hipStream_t st) {
+  DISPATCH_DTYPE_D(dtype, D, return launch_gg_row_t<ElemT, kD>(a, load_p, want_gdout, st));
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_gg_col(int dtype, int D, const Params& a, bool load_p, hipStream_t st) {
+  DISPATCH_DTYPE_D(dtype, D, return launch_gg_col_t<ElemT, kD>(a, load_p, st));
+  return hipErrorInvalidValue;
+}
+
+}  // namespace ttt

@@ -1,0 +1,39 @@
+// ttt_launch.h — host-side launchers of the gfx950 attention kernels (one per
+// kernel family), called by the C ABI in ttt_capi.hip after validation.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "ttt_common.h"
+
+namespace ttt {
+
+// dtype codes match ttt_dtype in include/ttt_attn.h.
+enum : int { kF16 = 0, kBF16 = 1, kF32 = 2 };
+
+// Runs `stmt` with ElemT / kD bound to the element type and head dim.
+#define DISPATCH_DTYPE_D(dtype, D, ...)                                   \
+  do {                                                                     \
+    if ((dtype) == ::ttt::kF16) {                                          \
+      typedef _Float16 ElemT;                                              \
+      if ((D) == 64) { constexpr int kD = 64; __VA_ARGS__; }                      \
+      if ((D) == 128) { constexpr int kD = 128; __VA_ARGS__; }                    \
+    } else if ((dtype) == ::ttt::kBF16) {                                  \
+      typedef __bf16 ElemT;                                                \
+      if ((D) == 64) { constexpr int kD = 64; __VA_ARGS__; }                      \
+      if ((D) == 128) { constexpr int kD = 128; __VA_ARGS__; }                    \
+    } else if ((dtype) == ::ttt::kF32) {                                   \
+      typedef float ElemT;                                                 \
+      if ((D) == 64) { constexpr int kD = 64; __VA_ARGS__; }                      \
+      if ((D) == 128) { constexpr int kD = 128; __VA_ARGS__; }                    \
+    }                                                                      \
+  } while (0)
+
+hipError_t launch_fwd(int dtype, int D, const Params& a, bool write_p, hipStream_t st);
+hipError_t launch_bwd_dq(int dtype, int D, const Params& a, bool load_p, hipStream_t st);
+hipError_t launch_bwd_dkdv(int dtype, int D, const Params& a, bool load_p, bool dv_only, hipStream_t st);
+hipError_t launch_bwd_rowsum(int dtype, int D, const Params& a, hipStream_t st);
+hipError_t launch_gg_row(int dtype, int D, const Params& a, bool load_p, bool want_gdout, hipStream_t st);
+hipError_t launch_gg_col(int dtype, int D, const Params& a, bool load_p, hipStream_t st);
+
+}  // namespace ttt

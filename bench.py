@@ -1,0 +1,188 @@
+"""Benchmark of the grad-grad attention step on one MI355X.
+
+Workload: b=1 h=1 T=8192 d=64 fp16, causal with 64x64
+block-sparse tiles, bwd_mode='save_p_triton_full'.  One step is
+
+    O = triton_attention(q, k, v, causal=True, bwd_mode='save_p_triton_full')
+    dQ, dK, dV = grad(O, (q, k, v), dO, create_graph=True)
+    GQ, GK, GV = grad(sum(dQ*rq + dK*rk + dV*rv), (q, k, v))
+
+with q, k, v, dO, rq, rk, rv ~ N(0,1) drawn from a seeded CPU generator and
+resident in HBM before timing starts.  Prints one JSON line (rank 0).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C3]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+import torch  # noqa: E402
+
+from testtimeideas_amd import _lib, workloads  # noqa: E402
+from ttt_kernels import triton_attention  # noqa: E402
+
+METRIC = "fwd+bwd+grad-grad ms at T=8k/16k d=64 fp16 causal; MFMA/HBM % of peak"
+REFERENCE_H100_MS = {"C3": 4.054, "C4_16k": 13.649}  # artifacts/gradgrad_sweep.csv (reduced grad-grad)
+
+
+def make_step(cfg: workloads.Config, x):
+    q, k, v = (x[n].requires_grad_(True) for n in ("q", "k", "v"))
+    do, rq, rk, rv = x["do"], x["rq"], x["rk"], x["rv"]
+
+    def step():
+        o = triton_attention(q, k, v, causal=cfg.causal, bwd_mode=cfg.bwd_mode)
+        dq, dk, dv = torch.autograd.grad(o, (q, k, v), do, create_graph=cfg.gradgrad)
+        if not cfg.gradgrad:
+            return dq
+        s = (dq * rq).sum() + (dk * rk).sum() + (dv * rv).sum()
+        return torch.autograd.grad(s, (q, k, v))
+
+    return step
+
+
+def time_steps(step, steps: int, warmup: int) -> float:
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def kernel_times(step, reps: int = 10):
+    """Mean duration (ms) of each kernel, from HIP events recorded on the launch stream."""
+    with _lib.kernel_timing() as rec:
+        for _ in range(reps):
+            step()
+        torch.cuda.synchronize()
+        return _lib.mean_ms(rec)
+
+
+def roofline_entry(cfg, ktimes, with_p=True):
+    name = max(ktimes, key=ktimes.get)
+    model = workloads.kernel_model(name, cfg, with_p)
+    dur_s = ktimes[name] * 1e-3
+    tag = workloads.DTYPE_TAG[cfg.torch_dtype]
+    if model["bound"] == "mfma":
+        achieved = model["flops"] / dur_s / 1e12
+        peak, unit = workloads.PEAK_TFLOPS[tag], "TFLOP/s"
+    else:
+        achieved = model["bytes"] / dur_s / 1e9
+        peak, unit = workloads.PEAK_HBM_GBS, "GB/s"
+    return {"kernel": name, "bound": model["bound"], "achieved": round(achieved, 2), "peak": peak,
+            "unit": unit, "frac": round(achieved / peak, 4), "traffic": None,
+            "avg_us": round(ktimes[name] * 1e3, 2), "algorithmic_flops": model["flops"],
+            "algorithmic_bytes": model["bytes"]}
+
+
+def cpu_baseline(cfg: workloads.Config, budget_s: float = 20.0):
+    """The math path (oracle.math_path, the reference's _attention_math + autograd
+    restated) on the host CPU, on the same seeded inputs in the config dtype."""
+    from oracle import math_path
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    x = workloads.make_inputs(cfg, seed=0)
+    args = [x[n] for n in ("q", "k", "v", "do", "rq", "rk", "rv")]
+    times = []
+    t_start = time.perf_counter()
+    math_path.gradgrad_step(*args, cfg.causal, cfg.scale)  # warmup
+    while len(times) < 20 and (time.perf_counter() - t_start) < budget_s or len(times) < 3:
+        t0 = time.perf_counter()
+        math_path.gradgrad_step(*args, cfg.causal, cfg.scale)
+        times.append((time.perf_counter() - t0) * 1e3)
+    return {"value": round(statistics.median(times), 3), "unit": "ms", "cores": threads, "kind": "port",
+            "sample": f"{len(times)} full {cfg.name} steps (b{cfg.b} h{cfg.h} T{cfg.t} d{cfg.d} {cfg.dtype} "
+                      f"causal={cfg.causal}) after 1 warmup, median; torch CPU math path with autograd"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="C3", choices=sorted(workloads.CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the T=16k point and forward-only metrics")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(the (b,h) slices would shard across GPUs with no communication); run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(2)
+
+    dev = torch.device("cuda", 0)
+    cfg = workloads.CONFIGS[args.config]
+    x = workloads.make_inputs(cfg, seed=0, device=dev)
+    step = make_step(cfg, x)
+    ms = time_steps(step, args.steps, args.warmup)
+    ktimes = kernel_times(step)
+    roof = workloads.roofline_us(cfg)
+
+    out = {
+        "metric": METRIC,
+        "value": round(ms, 4),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {"fp16": "f16", "bf16": "bf16", "fp32": "f32"}[cfg.dtype],
+        "data": "synthetic N(0,1) q,k,v,dO,rq,rk,rv from a seeded CPU generator",
+        "config": {"workload": f"{cfg.name}: b{cfg.b} h{cfg.h} T{cfg.t} d{cfg.d} {cfg.dtype} "
+                               f"{'causal 64x64 block-sparse' if cfg.causal else 'non-causal'} "
+                               f"{cfg.bwd_mode} fwd+bwd{'+grad-grad' if cfg.gradgrad else ''}",
+                   "batch": cfg.b, "heads": cfg.h, "seq_len": cfg.t, "head_dim": cfg.d,
+                   "bwd_mode": cfg.bwd_mode},
+        "tflops": round(roof["flops"] / (ms * 1e-3) / 1e12, 3),
+        "step_roofline_us": round(roof["roofline_us"], 2),
+        "step_roofline_frac": round(roof["roofline_us"] * 1e-3 / ms, 5),
+        "kernel_us": {k: round(v * 1e3, 2) for k, v in sorted(ktimes.items())},
+        "kernel_sum_us": round(sum(ktimes.values()) * 1e3, 2),
+        "roofline": roofline_entry(cfg, ktimes),
+        "reference_h100_ms": REFERENCE_H100_MS.get(cfg.name),
+    }
+
+    if not args.no_extra and cfg.name == "C3":
+        cfg16 = workloads.CONFIGS["C4_16k"]
+        x16 = workloads.make_inputs(cfg16, seed=0, device=dev)
+        out["t16k_causal_ms"] = round(time_steps(make_step(cfg16, x16), max(5, args.steps // 2), 3), 4)
+        del x16
+        # forward-only, O + LSE (recompute mode): MFMA utilisation of the contraction kernel
+        q, k, v = (x[n].detach() for n in ("q", "k", "v"))
+        with torch.no_grad():
+            with _lib.kernel_timing() as rec:
+                for _ in range(20):
+                    _lib.fwd(q, k, v, True, cfg.scale, False)
+                torch.cuda.synchronize()
+                fwd_ms = _lib.mean_ms(rec)["ttt_attn_fwd"]
+        fwd_flops = 4.0 * cfg.b * cfg.h * cfg.d * workloads.active_area(cfg.t, cfg.causal)
+        out["fwd_lse_us"] = round(fwd_ms * 1e3, 2)
+        out["fwd_lse_mfma_frac"] = round(fwd_flops / (fwd_ms * 1e-3) / (workloads.PEAK_TFLOPS["f16"] * 1e12), 4)
+
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(cfg)
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -118,7 +118,11 @@ class TritonAttentionFn(torch.autograd.Function):
             dv = backward_stubs.triton_attn_bwd_dv(q, k, v, grad_out, causal=causal, scale=scale)
             return dq, dk, dv, None, None, None
         if torch.is_grad_enabled():
-            dq, dk, dv = _AttnBwdFn.apply(q, k, v, grad_out, qp, kp, vp, op, lse, p, causal, scale)
+            # The kernel operands go in detached: the closed-form double backward
+            # already covers every dependence on q, k, v, so no gradient may flow
+            # into O (an output of this node) or into the saved inputs a second time.
+            dq, dk, dv = _AttnBwdFn.apply(q, k, v, grad_out, qp.detach(), kp.detach(), vp.detach(),
+                                          op.detach(), lse, p, causal, scale)
         else:
             d = q.size(-1)
             dop = _lib.prep(grad_out, qp.size(-1))

@@ -4,10 +4,18 @@
  * libttt_attn.so exports these entry points.  They take raw device pointers,
  * int64 sizes and element strides, and a HIP stream passed as `void*`.  No
  * entry point allocates device memory: the caller owns every input, output and
- * statistics buffer.  Kernels are enqueued asynchronously on `stream`; the
- * return value is 0 on success or a nonzero ttt_status, with a message
- * available from ttt_last_error() (thread-local).  No C++ exception crosses
- * this boundary.
+ * statistics buffer, and a workspace whose size ttt_attn_workspace_size()
+ * reports (0 bytes when no loop is split; then workspace may be NULL).
+ * Kernels are enqueued asynchronously on `stream`; the return value is 0 on
+ * success or a nonzero ttt_status, with a message available from
+ * ttt_last_error() (thread-local).  No C++ exception crosses this boundary.
+ * Calls that run concurrently (different streams) need separate workspaces.
+ *
+ * Work split: a workgroup owns 64 rows of one (b,h) slice and walks 64-row
+ * tiles of the other index.  When a slice has few blocks, the walk is split
+ * into chunks of `split_chunk` tiles (0: chosen from the problem size) whose
+ * fp32 partial sums go to the workspace and are combined in chunk order, so
+ * results do not depend on scheduling.
  *
  * Layout contract (all entry points):
  *   - [B,H,T,D] operands (q, k, v, o, dO, cotangents, gradients) are described
@@ -55,8 +63,21 @@ typedef enum ttt_status {
   TTT_OK = 0,
   TTT_ERR_INVALID_ARGUMENT = 1, /* null pointer, bad size, misaligned stride */
   TTT_ERR_UNSUPPORTED = 2,      /* head_dim or dtype outside what is built  */
-  TTT_ERR_LAUNCH = 3            /* HIP reported an error on kernel launch   */
+  TTT_ERR_LAUNCH = 3,           /* HIP reported an error on kernel launch   */
+  TTT_ERR_WORKSPACE = 4         /* workspace missing or too small           */
 } ttt_status;
+
+/* Entry points, for ttt_attn_workspace_size(). */
+typedef enum ttt_entry {
+  TTT_ENTRY_FWD = 0,       /* ttt_attn_fwd without P   */
+  TTT_ENTRY_FWD_P = 1,     /* ttt_attn_fwd with P      */
+  TTT_ENTRY_BWD_DQ = 2,
+  TTT_ENTRY_BWD_DKDV = 3,
+  TTT_ENTRY_BWD = 4,
+  TTT_ENTRY_GG_ROW = 5,
+  TTT_ENTRY_GG_COL = 6,
+  TTT_ENTRY_GG = 7
+} ttt_entry;
 
 /* Problem description shared by every entry point. */
 typedef struct ttt_problem {
@@ -67,6 +88,7 @@ typedef struct ttt_problem {
   int64_t seqlen;   /* T                                          */
   int64_t head_dim; /* D: 64 or 128                               */
   float scale;      /* softmax scale s                            */
+  int32_t split_chunk; /* tiles per workgroup; 0 = automatic      */
 } ttt_problem;
 
 /* A strided [B,H,T,X] operand (X = D, or T for P). Strides are in elements. */
@@ -84,6 +106,13 @@ int ttt_version(void);
 const char* ttt_last_error(void);
 
 /*
+ * Workspace bytes `entry` needs for this problem (want_gdout: whether the
+ * double backward also forms GdO).  Returns -1 for an invalid problem.  No
+ * reference counterpart: the reference's kernels are not split.
+ */
+int64_t ttt_attn_workspace_size(const ttt_problem* pr, int32_t entry, int32_t want_gdout);
+
+/*
  * Forward.  Writes O and lse; if p != NULL (and p->data != NULL) also writes
  * P = softmax(S) rounded to the input dtype, and computes O from that rounded
  * P (two passes over K: row statistics, then P and P*V).  With p == NULL it
@@ -95,7 +124,8 @@ const char* ttt_last_error(void);
  */
 int ttt_attn_fwd(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
                  const ttt_view* v, const ttt_view* o, float* lse,
-                 const ttt_view* p, void* stream);
+                 const ttt_view* p, void* workspace,
+                 int64_t workspace_bytes, void* stream);
 
 /*
  * dQ (row-block kernel).  P is read from p when p != NULL, otherwise it is
@@ -110,7 +140,8 @@ int ttt_attn_bwd_dq(const ttt_problem* pr, const ttt_view* q,
                     const ttt_view* k, const ttt_view* v, const ttt_view* o,
                     const ttt_view* dout, const float* lse, const ttt_view* p,
                     const float* rowsum_in, float* rowsum_out,
-                    const ttt_view* dq, void* stream);
+                    const ttt_view* dq, void* workspace, int64_t workspace_bytes,
+                    void* stream);
 
 /*
  * dK and dV (column-block kernel), from P (p != NULL) or recomputed from lse.
@@ -125,7 +156,8 @@ int ttt_attn_bwd_dkdv(const ttt_problem* pr, const ttt_view* q,
                       const ttt_view* k, const ttt_view* v,
                       const ttt_view* dout, const float* lse,
                       const ttt_view* p, const float* rowsum,
-                      const ttt_view* dk, const ttt_view* dv, void* stream);
+                      const ttt_view* dk, const ttt_view* dv, void* workspace,
+                      int64_t workspace_bytes, void* stream);
 
 /*
  * Full first backward in one call: ttt_attn_bwd_dq (computing D from O into
@@ -137,7 +169,7 @@ int ttt_attn_bwd(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
                  const ttt_view* v, const ttt_view* o, const ttt_view* dout,
                  const float* lse, const ttt_view* p, float* rowsum_out,
                  const ttt_view* dq, const ttt_view* dk, const ttt_view* dv,
-                 void* stream);
+                 void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Row statistic from P, with the reference's definition
@@ -162,7 +194,8 @@ int ttt_attn_gg_row(const ttt_problem* pr, const ttt_view* q,
                     const float* rowsum, const ttt_view* gq,
                     const ttt_view* gk, const ttt_view* gv,
                     const ttt_view* gq_out, const ttt_view* gdout,
-                    float* e_out, float* f_out, void* stream);
+                    float* e_out, float* f_out, void* workspace,
+                    int64_t workspace_bytes, void* stream);
 
 /*
  * Double backward, column-block pass: GK and GV, reading E and F from
@@ -176,7 +209,8 @@ int ttt_attn_gg_col(const ttt_problem* pr, const ttt_view* q,
                     const float* rowsum, const float* e_in, const float* f_in,
                     const ttt_view* gq, const ttt_view* gk,
                     const ttt_view* gv, const ttt_view* gk_out,
-                    const ttt_view* gv_out, void* stream);
+                    const ttt_view* gv_out, void* workspace,
+                    int64_t workspace_bytes, void* stream);
 
 /*
  * Full double backward in one call: ttt_attn_gg_row then ttt_attn_gg_col on
@@ -191,7 +225,7 @@ int ttt_attn_gg(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
                 const ttt_view* gk, const ttt_view* gv, const ttt_view* gq_out,
                 const ttt_view* gk_out, const ttt_view* gv_out,
                 const ttt_view* gdout, float* e_buf, float* f_buf,
-                void* stream);
+                void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -39,6 +39,7 @@ class _Problem(ctypes.Structure):
         ("seqlen", ctypes.c_int64),
         ("head_dim", ctypes.c_int64),
         ("scale", ctypes.c_float),
+        ("split_chunk", ctypes.c_int32),
     ]
 
 
@@ -53,20 +54,25 @@ class _View(ctypes.Structure):
 
 _P = ctypes.POINTER
 _VP = _P(_View)
-_FP = ctypes.c_void_p  # float* passed as an address
+_FP = ctypes.c_void_p  # float* / workspace passed as an address
+_WS = [_FP, ctypes.c_int64]  # workspace, workspace_bytes
+_ST = [ctypes.c_void_p]  # stream
 _SIGS = {
-    "ttt_attn_fwd": [_P(_Problem), _VP, _VP, _VP, _VP, _FP, _VP, ctypes.c_void_p],
-    "ttt_attn_bwd_dq": [_P(_Problem), _VP, _VP, _VP, _VP, _VP, _FP, _VP, _FP, _FP, _VP, ctypes.c_void_p],
-    "ttt_attn_bwd_dkdv": [_P(_Problem), _VP, _VP, _VP, _VP, _FP, _VP, _FP, _VP, _VP, ctypes.c_void_p],
-    "ttt_attn_bwd": [_P(_Problem), _VP, _VP, _VP, _VP, _VP, _FP, _VP, _FP, _VP, _VP, _VP, ctypes.c_void_p],
-    "ttt_attn_bwd_rowsum": [_P(_Problem), _VP, _VP, _VP, _FP, ctypes.c_void_p],
-    "ttt_attn_gg_row": [_P(_Problem), _VP, _VP, _VP, _VP, _FP, _VP, _FP, _VP, _VP, _VP, _VP, _VP, _FP, _FP,
-                        ctypes.c_void_p],
-    "ttt_attn_gg_col": [_P(_Problem), _VP, _VP, _VP, _VP, _FP, _VP, _FP, _FP, _FP, _VP, _VP, _VP, _VP, _VP,
-                        ctypes.c_void_p],
+    "ttt_attn_fwd": [_P(_Problem), _VP, _VP, _VP, _VP, _FP, _VP] + _WS + _ST,
+    "ttt_attn_bwd_dq": [_P(_Problem), _VP, _VP, _VP, _VP, _VP, _FP, _VP, _FP, _FP, _VP] + _WS + _ST,
+    "ttt_attn_bwd_dkdv": [_P(_Problem), _VP, _VP, _VP, _VP, _FP, _VP, _FP, _VP, _VP] + _WS + _ST,
+    "ttt_attn_bwd": [_P(_Problem), _VP, _VP, _VP, _VP, _VP, _FP, _VP, _FP, _VP, _VP, _VP] + _WS + _ST,
+    "ttt_attn_bwd_rowsum": [_P(_Problem), _VP, _VP, _VP, _FP] + _ST,
+    "ttt_attn_gg_row": [_P(_Problem), _VP, _VP, _VP, _VP, _FP, _VP, _FP, _VP, _VP, _VP, _VP, _VP, _FP, _FP]
+                       + _WS + _ST,
+    "ttt_attn_gg_col": [_P(_Problem), _VP, _VP, _VP, _VP, _FP, _VP, _FP, _FP, _FP, _VP, _VP, _VP, _VP, _VP]
+                       + _WS + _ST,
     "ttt_attn_gg": [_P(_Problem), _VP, _VP, _VP, _VP, _FP, _VP, _FP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _FP,
-                    _FP, ctypes.c_void_p],
+                    _FP] + _WS + _ST,
 }
+
+# ttt_entry codes (include/ttt_attn.h)
+ENTRY_FWD, ENTRY_FWD_P, ENTRY_BWD_DQ, ENTRY_BWD_DKDV, ENTRY_BWD, ENTRY_GG_ROW, ENTRY_GG_COL, ENTRY_GG = range(8)
 
 _lib: Optional[ctypes.CDLL] = None
 
@@ -89,6 +95,8 @@ def load() -> ctypes.CDLL:
     lib.ttt_last_error.restype = ctypes.c_char_p
     lib.ttt_version.argtypes = []
     lib.ttt_version.restype = ctypes.c_int
+    lib.ttt_attn_workspace_size.argtypes = [_P(_Problem), ctypes.c_int32, ctypes.c_int32]
+    lib.ttt_attn_workspace_size.restype = ctypes.c_int64
     _lib = lib
     return lib
 
@@ -205,9 +213,49 @@ def check_inputs(*ts: torch.Tensor) -> None:
             raise ValueError("all operands must share dtype and device")
 
 
+# Tiles per workgroup of the split streamed loop; 0 lets the library choose.
+_split_chunk = 0
+
+
+@contextlib.contextmanager
+def split_chunk(n: int):
+    """Force the chunk length (tiles per workgroup) of every launch inside the
+    block; used by tests to exercise the split/combine path at small sizes."""
+    global _split_chunk
+    prev = _split_chunk
+    _split_chunk = int(n)
+    try:
+        yield
+    finally:
+        _split_chunk = prev
+
+
 def _problem(x: torch.Tensor, causal: bool, scale: float) -> _Problem:
     b, h, t, d = x.shape
-    return _Problem(_DTYPE_CODE[x.dtype], 1 if causal else 0, b, h, t, d, float(scale))
+    return _Problem(_DTYPE_CODE[x.dtype], 1 if causal else 0, b, h, t, d, float(scale), _split_chunk)
+
+
+_ws_sizes: Dict[tuple, int] = {}
+
+
+def workspace_bytes(pr: _Problem, entry: int, gdo: bool = False) -> int:
+    key = (pr.dtype, pr.causal, pr.batch, pr.heads, pr.seqlen, pr.head_dim, pr.split_chunk, entry, gdo)
+    n = _ws_sizes.get(key)
+    if n is None:
+        n = int(load().ttt_attn_workspace_size(ctypes.byref(pr), entry, 1 if gdo else 0))
+        if n < 0:
+            raise RuntimeError(f"ttt_attn_workspace_size: {load().ttt_last_error().decode(errors='replace')}")
+        _ws_sizes[key] = n
+    return n
+
+
+def _workspace(pr: _Problem, entry: int, device, gdo: bool = False):
+    """(pointer, bytes, tensor) of a fresh workspace from torch's caching allocator."""
+    n = workspace_bytes(pr, entry, gdo)
+    if n == 0:
+        return None, 0, None
+    buf = torch.empty(n, dtype=torch.uint8, device=device)
+    return buf.data_ptr(), n, buf
 
 
 def alloc_p(like: torch.Tensor) -> torch.Tensor:
@@ -249,8 +297,9 @@ def fwd(q, k, v, causal: bool, scale: float, want_p: bool):
     if q.numel() == 0:
         return o, lse, p
     pr = _problem(q, causal, scale)
+    wp, wn, _wbuf = _workspace(pr, ENTRY_FWD_P if want_p else ENTRY_FWD, q.device)
     _timed("ttt_attn_fwd", ctypes.byref(pr), _view(q), _view(k), _view(v), _view(o), lse.data_ptr(),
-           _view(p), _stream())
+           _view(p), wp, wn, _stream())
     return o, lse, p
 
 
@@ -264,17 +313,19 @@ def bwd(q, k, v, o, do, lse, p, causal: bool, scale: float):
     rowsum = _stats(q)
     if q.numel() == 0:
         return dq, dk, dv, rowsum
-    pr = ctypes.byref(_problem(q, causal, scale))
+    prob = _problem(q, causal, scale)
+    pr = ctypes.byref(prob)
     st = _stream()
     lse_p = _fptr(lse)
+    wp, wn, _wbuf = _workspace(prob, ENTRY_BWD, q.device)
     if _timing is None:
         _call("ttt_attn_bwd", pr, _view(q), _view(k), _view(v), _view(o), _view(do), lse_p, _view(p),
-              rowsum.data_ptr(), _view(dq), _view(dk), _view(dv), st)
+              rowsum.data_ptr(), _view(dq), _view(dk), _view(dv), wp, wn, st)
     else:
         _timed("ttt_attn_bwd_dq", pr, _view(q), _view(k), _view(v), _view(o), _view(do), lse_p, _view(p),
-               None, rowsum.data_ptr(), _view(dq), st)
+               None, rowsum.data_ptr(), _view(dq), wp, wn, st)
         _timed("ttt_attn_bwd_dkdv", pr, _view(q), _view(k), _view(v), _view(do), lse_p, _view(p),
-               rowsum.data_ptr(), _view(dk), _view(dv), st)
+               rowsum.data_ptr(), _view(dk), _view(dv), wp, wn, st)
     return dq, dk, dv, rowsum
 
 
@@ -284,9 +335,10 @@ def bwd_dq(q, k, v, do, p, lse, rowsum, causal: bool, scale: float, o=None):
     dq = _empty_like_out(q)
     if q.numel() == 0:
         return dq
-    pr = ctypes.byref(_problem(q, causal, scale))
-    _timed("ttt_attn_bwd_dq", pr, _view(q), _view(k), _view(v), _view(o), _view(do), _fptr(lse), _view(p),
-           _fptr(rowsum), None, _view(dq), _stream())
+    prob = _problem(q, causal, scale)
+    wp, wn, _wbuf = _workspace(prob, ENTRY_BWD_DQ, q.device)
+    _timed("ttt_attn_bwd_dq", ctypes.byref(prob), _view(q), _view(k), _view(v), _view(o), _view(do),
+           _fptr(lse), _view(p), _fptr(rowsum), None, _view(dq), wp, wn, _stream())
     return dq
 
 
@@ -296,9 +348,10 @@ def bwd_dkdv(q, k, v, do, p, lse, rowsum, causal: bool, scale: float, want_dk: b
     dv = _empty_like_out(do)
     if do.numel() == 0:
         return dk, dv
-    pr = ctypes.byref(_problem(do, causal, scale))
-    _timed("ttt_attn_bwd_dkdv", pr, _view(q), _view(k), _view(v), _view(do), _fptr(lse), _view(p),
-           _fptr(rowsum), _view(dk), _view(dv), _stream())
+    prob = _problem(do, causal, scale)
+    wp, wn, _wbuf = _workspace(prob, ENTRY_BWD_DKDV, do.device)
+    _timed("ttt_attn_bwd_dkdv", ctypes.byref(prob), _view(q), _view(k), _view(v), _view(do), _fptr(lse),
+           _view(p), _fptr(rowsum), _view(dk), _view(dv), wp, wn, _stream())
     return dk, dv
 
 
@@ -323,23 +376,25 @@ def gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, causal: bool, scale: float, want
     f = _stats(q)
     if q.numel() == 0:
         return gq_out, gk_out, gv_out, gdo
-    pr = ctypes.byref(_problem(q, causal, scale))
+    prob = _problem(q, causal, scale)
+    pr = ctypes.byref(prob)
     st = _stream()
     lse_p = _fptr(lse)
+    wp, wn, _wbuf = _workspace(prob, ENTRY_GG, q.device, want_gdo)
     if _timing is None:
         _call("ttt_attn_gg", pr, _view(q), _view(k), _view(v), _view(do), lse_p, _view(p), rowsum.data_ptr(),
               _view(gq), _view(gk), _view(gv), _view(gq_out), _view(gk_out), _view(gv_out), _view(gdo),
-              e.data_ptr(), f.data_ptr(), st)
+              e.data_ptr(), f.data_ptr(), wp, wn, st)
     else:
         _timed("ttt_attn_gg_row", pr, _view(q), _view(k), _view(v), _view(do), lse_p, _view(p),
                rowsum.data_ptr(), _view(gq), _view(gk), _view(gv), _view(gq_out), _view(gdo), e.data_ptr(),
-               f.data_ptr(), st)
+               f.data_ptr(), wp, wn, st)
         _timed("ttt_attn_gg_col", pr, _view(q), _view(k), _view(v), _view(do), lse_p, _view(p),
                rowsum.data_ptr(), e.data_ptr(), f.data_ptr(), _view(gq), _view(gk), _view(gv), _view(gk_out),
-               _view(gv_out), st)
+               _view(gv_out), wp, wn, st)
     return gq_out, gk_out, gv_out, gdo
 
 
 def exported_symbols() -> List[str]:
     """Names of the C entry points this binding uses (for ABI checks)."""
-    return list(_SIGS) + ["ttt_last_error", "ttt_version"]
+    return list(_SIGS) + ["ttt_last_error", "ttt_version", "ttt_attn_workspace_size"]

@@ -1,9 +1,11 @@
 // ttt_capi.hip — the extern "C" entry points declared in include/ttt_attn.h.
 // Validates every argument on the host before anything is enqueued (shapes,
-// null pointers, 16-byte alignment of bases and row strides, grid limits),
-// packs the kernel argument block and calls the per-family launchers.
+// null pointers, 16-byte alignment of bases and row strides, grid limits,
+// workspace size), chooses the split of the streamed loop, packs the kernel
+// argument block and calls the per-family launchers.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -22,6 +24,11 @@ int fail(int code, const char* fmt, ...) {
   va_end(ap);
   return code;
 }
+
+// Workgroups the split aims for: two per CU of an MI355X (256 CUs).
+constexpr int64_t kTargetWorkgroups = 512;
+// Chunks shorter than this are not worth a combine pass.
+constexpr int kMinChunk = 4;
 
 size_t elem_bytes(int dtype) { return dtype == TTT_F32 ? 4 : 2; }
 
@@ -58,7 +65,60 @@ int check_problem(const ttt_problem* pr) {
   if (pr->seqlen > (int64_t)1 << 24)
     return fail(TTT_ERR_INVALID_ARGUMENT, "seqlen %lld exceeds 2^24", (long long)pr->seqlen);
   if (pr->causal != 0 && pr->causal != 1) return fail(TTT_ERR_INVALID_ARGUMENT, "causal must be 0 or 1");
+  if (pr->split_chunk < 0) return fail(TTT_ERR_INVALID_ARGUMENT, "split_chunk must be >= 0");
   return TTT_OK;
+}
+
+struct Split {
+  int nblk, chunk, nchunk_max;
+};
+
+// Tiles per workgroup: enough workgroups to fill the chip, no chunk shorter
+// than kMinChunk, no split at all when the blocks alone fill it.
+Split choose_split(const ttt_problem* pr) {
+  Split s;
+  s.nblk = (int)((pr->seqlen + ttt::kBlk - 1) / ttt::kBlk);
+  const int64_t bh = pr->batch * pr->heads;
+  int c;
+  if (pr->split_chunk > 0) {
+    c = pr->split_chunk;
+  } else {
+    const int64_t tiles = pr->causal ? (int64_t)s.nblk * (s.nblk + 1) / 2 : (int64_t)s.nblk * s.nblk;
+    const int64_t total = bh * tiles;
+    c = (int)std::max<int64_t>(kMinChunk, (total + kTargetWorkgroups - 1) / kTargetWorkgroups);
+  }
+  s.chunk = std::min(c, s.nblk);
+  s.nchunk_max = (s.nblk + s.chunk - 1) / s.chunk;
+  return s;
+}
+
+int family_of(int entry, bool gdo) {
+  switch (entry) {
+    case TTT_ENTRY_FWD: return ttt::kFamFwdOnline;
+    case TTT_ENTRY_FWD_P: return ttt::kFamFwdP;
+    case TTT_ENTRY_BWD_DQ: return ttt::kFamDq;
+    case TTT_ENTRY_BWD_DKDV: return ttt::kFamDkdv;
+    case TTT_ENTRY_GG_ROW: return gdo ? ttt::kFamGgRowGdo : ttt::kFamGgRow;
+    case TTT_ENTRY_GG_COL: return ttt::kFamGgCol;
+    default: return -1;
+  }
+}
+
+// Bytes of partial accumulators + partial row scalars for one kernel family.
+int64_t family_bytes(const ttt_problem* pr, const Split& s, int fam) {
+  if (s.nchunk_max <= 1) return 0;
+  const int64_t parts = pr->batch * pr->heads * s.nblk * s.nchunk_max;
+  return parts * ttt::kBlk * (ttt::kFamNacc[fam] * pr->head_dim + ttt::kFamNsc[fam]) * (int64_t)sizeof(float);
+}
+
+int64_t entry_bytes(const ttt_problem* pr, int entry, bool gdo) {
+  const Split s = choose_split(pr);
+  if (entry == TTT_ENTRY_BWD)
+    return std::max(family_bytes(pr, s, ttt::kFamDq), family_bytes(pr, s, ttt::kFamDkdv));
+  if (entry == TTT_ENTRY_GG)
+    return std::max(family_bytes(pr, s, family_of(TTT_ENTRY_GG_ROW, gdo)), family_bytes(pr, s, ttt::kFamGgCol));
+  const int fam = family_of(entry, gdo);
+  return fam < 0 ? -1 : family_bytes(pr, s, fam);
 }
 
 ttt::Params base_params(const ttt_problem* pr) {
@@ -73,6 +133,24 @@ ttt::Params base_params(const ttt_problem* pr) {
   return a;
 }
 
+// Attach the split and the workspace for kernel family `fam`.
+int attach_split(const ttt_problem* pr, int fam, void* ws, int64_t ws_bytes, ttt::Params* a) {
+  const Split s = choose_split(pr);
+  a->chunk = s.chunk;
+  a->nchunk_max = s.nchunk_max;
+  const int64_t need = family_bytes(pr, s, fam);
+  if (need > 0) {
+    if (!ws || ws_bytes < need)
+      return fail(TTT_ERR_WORKSPACE, "workspace of %lld bytes needed, %lld given", (long long)need,
+                  (long long)(ws ? ws_bytes : 0));
+    if (!aligned16(ws)) return fail(TTT_ERR_INVALID_ARGUMENT, "workspace not 16-byte aligned");
+    const int64_t parts = pr->batch * pr->heads * s.nblk * s.nchunk_max;
+    a->ws_acc = reinterpret_cast<float*>(ws);
+    a->ws_sc = a->ws_acc + parts * ttt::kBlk * ttt::kFamNacc[fam] * pr->head_dim;
+  }
+  return TTT_OK;
+}
+
 bool has_p(const ttt_view* p) { return p && p->data; }
 
 int launched(hipError_t e, const char* what) {
@@ -80,9 +158,9 @@ int launched(hipError_t e, const char* what) {
   return TTT_OK;
 }
 
-#define TRY(x)                   \
-  do {                           \
-    const int rc_ = (x);         \
+#define TRY(x)                     \
+  do {                             \
+    const int rc_ = (x);           \
     if (rc_ != TTT_OK) return rc_; \
   } while (0)
 
@@ -90,12 +168,22 @@ int launched(hipError_t e, const char* what) {
 
 extern "C" {
 
-int ttt_version(void) { return 100; }
+int ttt_version(void) { return 200; }
 
 const char* ttt_last_error(void) { return g_err; }
 
+int64_t ttt_attn_workspace_size(const ttt_problem* pr, int32_t entry, int32_t want_gdout) {
+  if (check_problem(pr) != TTT_OK) return -1;
+  if (entry < TTT_ENTRY_FWD || entry > TTT_ENTRY_GG) {
+    fail(TTT_ERR_INVALID_ARGUMENT, "unknown entry %d", entry);
+    return -1;
+  }
+  return entry_bytes(pr, entry, want_gdout != 0);
+}
+
 int ttt_attn_fwd(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
-                 const ttt_view* o, float* lse, const ttt_view* p, void* stream) {
+                 const ttt_view* o, float* lse, const ttt_view* p, void* workspace, int64_t workspace_bytes,
+                 void* stream) {
   TRY(check_problem(pr));
   ttt::Params a = base_params(pr);
   TRY(take_view(pr, q, "q", &a.q));
@@ -106,12 +194,14 @@ int ttt_attn_fwd(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, co
   a.lse = lse;
   const bool wp = has_p(p);
   if (wp) TRY(take_view(pr, p, "p", &a.p));
+  TRY(attach_split(pr, wp ? ttt::kFamFwdP : ttt::kFamFwdOnline, workspace, workspace_bytes, &a));
   return launched(ttt::launch_fwd(pr->dtype, (int)pr->head_dim, a, wp, (hipStream_t)stream), "ttt_attn_fwd");
 }
 
 int ttt_attn_bwd_dq(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
                     const ttt_view* o, const ttt_view* dout, const float* lse, const ttt_view* p,
-                    const float* rowsum_in, float* rowsum_out, const ttt_view* dq, void* stream) {
+                    const float* rowsum_in, float* rowsum_out, const ttt_view* dq, void* workspace,
+                    int64_t workspace_bytes, void* stream) {
   TRY(check_problem(pr));
   ttt::Params a = base_params(pr);
   TRY(take_view(pr, k, "k", &a.k));
@@ -129,13 +219,15 @@ int ttt_attn_bwd_dq(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
   a.rowsum_in = rowsum_in;
   a.rowsum_out = rowsum_out;
   if (!rowsum_in) TRY(take_view(pr, o, "o (needed to form D without rowsum_in)", &a.o));
+  TRY(attach_split(pr, ttt::kFamDq, workspace, workspace_bytes, &a));
   return launched(ttt::launch_bwd_dq(pr->dtype, (int)pr->head_dim, a, lp, (hipStream_t)stream),
                   "ttt_attn_bwd_dq");
 }
 
 int ttt_attn_bwd_dkdv(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
                       const ttt_view* dout, const float* lse, const ttt_view* p, const float* rowsum,
-                      const ttt_view* dk, const ttt_view* dv, void* stream) {
+                      const ttt_view* dk, const ttt_view* dv, void* workspace, int64_t workspace_bytes,
+                      void* stream) {
   TRY(check_problem(pr));
   ttt::Params a = base_params(pr);
   const bool lp = has_p(p);
@@ -155,6 +247,7 @@ int ttt_attn_bwd_dkdv(const ttt_problem* pr, const ttt_view* q, const ttt_view* 
   }
   a.lse = const_cast<float*>(lse);
   a.rowsum_in = rowsum;
+  TRY(attach_split(pr, ttt::kFamDkdv, workspace, workspace_bytes, &a));
   return launched(ttt::launch_bwd_dkdv(pr->dtype, (int)pr->head_dim, a, lp, dv_only, (hipStream_t)stream),
                   "ttt_attn_bwd_dkdv");
 }
@@ -162,11 +255,12 @@ int ttt_attn_bwd_dkdv(const ttt_problem* pr, const ttt_view* q, const ttt_view* 
 int ttt_attn_bwd(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
                  const ttt_view* o, const ttt_view* dout, const float* lse, const ttt_view* p,
                  float* rowsum_out, const ttt_view* dq, const ttt_view* dk, const ttt_view* dv,
-                 void* stream) {
+                 void* workspace, int64_t workspace_bytes, void* stream) {
   if (!rowsum_out) return fail(TTT_ERR_INVALID_ARGUMENT, "rowsum_out: null pointer");
   if (!dk || !dk->data) return fail(TTT_ERR_INVALID_ARGUMENT, "dk: null pointer");
-  TRY(ttt_attn_bwd_dq(pr, q, k, v, o, dout, lse, p, nullptr, rowsum_out, dq, stream));
-  return ttt_attn_bwd_dkdv(pr, q, k, v, dout, lse, p, rowsum_out, dk, dv, stream);
+  TRY(ttt_attn_bwd_dq(pr, q, k, v, o, dout, lse, p, nullptr, rowsum_out, dq, workspace, workspace_bytes,
+                      stream));
+  return ttt_attn_bwd_dkdv(pr, q, k, v, dout, lse, p, rowsum_out, dk, dv, workspace, workspace_bytes, stream);
 }
 
 int ttt_attn_bwd_rowsum(const ttt_problem* pr, const ttt_view* p, const ttt_view* dout, const ttt_view* v,
@@ -185,7 +279,8 @@ int ttt_attn_bwd_rowsum(const ttt_problem* pr, const ttt_view* p, const ttt_view
 int ttt_attn_gg_row(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
                     const ttt_view* dout, const float* lse, const ttt_view* p, const float* rowsum,
                     const ttt_view* gq, const ttt_view* gk, const ttt_view* gv, const ttt_view* gq_out,
-                    const ttt_view* gdout, float* e_out, float* f_out, void* stream) {
+                    const ttt_view* gdout, float* e_out, float* f_out, void* workspace, int64_t workspace_bytes,
+                    void* stream) {
   TRY(check_problem(pr));
   ttt::Params a = base_params(pr);
   TRY(take_view(pr, q, "q", &a.q));
@@ -206,6 +301,7 @@ int ttt_attn_gg_row(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
   a.rowsum_in = rowsum;
   a.e = e_out;
   a.f = f_out;
+  TRY(attach_split(pr, gdo ? ttt::kFamGgRowGdo : ttt::kFamGgRow, workspace, workspace_bytes, &a));
   return launched(ttt::launch_gg_row(pr->dtype, (int)pr->head_dim, a, lp, gdo, (hipStream_t)stream),
                   "ttt_attn_gg_row");
 }
@@ -213,7 +309,8 @@ int ttt_attn_gg_row(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
 int ttt_attn_gg_col(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
                     const ttt_view* dout, const float* lse, const ttt_view* p, const float* rowsum,
                     const float* e_in, const float* f_in, const ttt_view* gq, const ttt_view* gk,
-                    const ttt_view* gv, const ttt_view* gk_out, const ttt_view* gv_out, void* stream) {
+                    const ttt_view* gv, const ttt_view* gk_out, const ttt_view* gv_out, void* workspace,
+                    int64_t workspace_bytes, void* stream) {
   TRY(check_problem(pr));
   ttt::Params a = base_params(pr);
   TRY(take_view(pr, q, "q", &a.q));
@@ -233,6 +330,7 @@ int ttt_attn_gg_col(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
   a.rowsum_in = rowsum;
   a.e = const_cast<float*>(e_in);
   a.f = const_cast<float*>(f_in);
+  TRY(attach_split(pr, ttt::kFamGgCol, workspace, workspace_bytes, &a));
   return launched(ttt::launch_gg_col(pr->dtype, (int)pr->head_dim, a, lp, (hipStream_t)stream),
                   "ttt_attn_gg_col");
 }
@@ -241,9 +339,11 @@ int ttt_attn_gg(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, con
                 const ttt_view* dout, const float* lse, const ttt_view* p, const float* rowsum,
                 const ttt_view* gq, const ttt_view* gk, const ttt_view* gv, const ttt_view* gq_out,
                 const ttt_view* gk_out, const ttt_view* gv_out, const ttt_view* gdout, float* e_buf,
-                float* f_buf, void* stream) {
-  TRY(ttt_attn_gg_row(pr, q, k, v, dout, lse, p, rowsum, gq, gk, gv, gq_out, gdout, e_buf, f_buf, stream));
-  return ttt_attn_gg_col(pr, q, k, v, dout, lse, p, rowsum, e_buf, f_buf, gq, gk, gv, gk_out, gv_out, stream);
+                float* f_buf, void* workspace, int64_t workspace_bytes, void* stream) {
+  TRY(ttt_attn_gg_row(pr, q, k, v, dout, lse, p, rowsum, gq, gk, gv, gq_out, gdout, e_buf, f_buf, workspace,
+                      workspace_bytes, stream));
+  return ttt_attn_gg_col(pr, q, k, v, dout, lse, p, rowsum, e_buf, f_buf, gq, gk, gv, gk_out, gv_out, workspace,
+                         workspace_bytes, stream);
 }
 
 }  // extern "C"

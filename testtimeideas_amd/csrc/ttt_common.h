@@ -19,6 +19,16 @@
 // tiles chain into the next product straight from registers, and per-row
 // statistics of the stationary row stay inside one lane plus two cross-lane
 // steps (xor 16, xor 32).
+//
+// Every streamed tile is staged once, row-major, in LDS.  Products that
+// contract over the head dim read 8-element row fragments (ds_read_b128);
+// products that contract over the streamed index read column fragments of the
+// same tile: ds_read_b64_tr_b16 for 16-bit types, eight 32-bit reads for fp32.
+//
+// Long streamed loops are split into chunks of `chunk` tiles, one workgroup
+// per (block, chunk).  A block with a single chunk writes its outputs
+// directly; otherwise each chunk writes fp32 partial accumulators (and row
+// scalars) to the caller's workspace and a combine kernel finishes the block.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -61,7 +71,33 @@ struct Params {
   float* rowsum_out;         // D (written), or nullptr
   float* e;                  // E row statistic
   float* f;                  // F row statistic
+  // split of the streamed loop
+  int chunk;                 // tiles per workgroup
+  int nchunk_max;            // chunks of the longest block
+  float* ws_acc;             // [BH][nblk][nchunk_max][nacc][64][D] partial accumulators
+  float* ws_sc;              // [BH][nblk][nchunk_max][nsc][64] partial row scalars
 };
+
+// Streamed tiles [t0, t1) of chunk `ch` of a block whose tiles are [lo, hi).
+struct Chunk {
+  int t0, t1, nch;
+};
+
+__device__ __forceinline__ Chunk chunk_of(int lo, int hi, int ch, int chunk) {
+  Chunk r;
+  r.nch = (hi - lo + chunk - 1) / chunk;
+  r.t0 = lo + ch * chunk;
+  r.t1 = min(r.t0 + chunk, hi);
+  return r;
+}
+
+// Tile range of a row block (query rows) and of a column block (key rows).
+__device__ __forceinline__ int row_block_hi(int mb, int nblk, int causal) { return causal ? mb + 1 : nblk; }
+__device__ __forceinline__ int col_block_lo(int nb, int causal) { return causal ? nb : 0; }
+
+__device__ __forceinline__ int64_t part_index(const Params& a, int bh, int nblk, int blk, int ch) {
+  return ((int64_t)bh * nblk + blk) * a.nchunk_max + ch;
+}
 
 template <typename T>
 __device__ __forceinline__ T* at(const View& v, int b, int h) {
@@ -221,17 +257,14 @@ __device__ __forceinline__ typename Elem<T>::frag vals_frag(const float* v) {
 }
 
 // ---------------------------------------------------------------------------
-// LDS tile geometry.  A row-major tile is 64 rows x NCOL with pitch NCOL+chunk;
-// a transposed tile is NCOL rows x 64 with pitch 64+chunk.  Both pitches keep
-// every 8-element fragment 16-byte aligned.
+// LDS tile geometry: 64 rows x NCOL, row pitch NCOL + one 16-byte chunk, which
+// keeps every 8-element row fragment 16-byte aligned.
 // ---------------------------------------------------------------------------
 template <typename T, int NCOL>
 struct Lds {
   static constexpr int kChunk = Elem<T>::kChunk;
   static constexpr int kRowPitch = NCOL + kChunk;
-  static constexpr int kTrPitch = kBlk + kChunk;
   static constexpr int kRowElems = kBlk * kRowPitch;
-  static constexpr int kTrElems = NCOL * kTrPitch;
 };
 
 // Staged registers of one 64 x NCOL tile: each thread owns pairs of
@@ -295,48 +328,43 @@ __device__ __forceinline__ void stage_store_rows(const Stage<T, NCOL>& st, T* ld
   }
 }
 
-// Write staged registers to a transposed LDS tile (element [row][col] goes to
-// lds[col][row]).  Rows are paired so each write is 32 bits (16-bit types) or
-// 64 bits (fp32).
-template <typename T, int NCOL>
-__device__ __forceinline__ void stage_store_tr(const Stage<T, NCOL>& st, T* lds) {
-  typedef Stage<T, NCOL> S;
-  constexpr int P = Lds<T, NCOL>::kTrPitch;
-  const int tid = threadIdx.x;
-  const int col = (tid % S::kChunksPerRow) * S::kChunk;
+// ---------------------------------------------------------------------------
+// Column fragment of a row-major LDS tile X (pitch P elements):
+//   f[j] = X[r0 + 8g + j][c0 + c],  j = 0..7,  lane (c, g).
+// 16-bit types use ds_read_b64_tr_b16: within each 16-lane group, lane i gets
+// element i%4 of the 8-byte chunk read by lane 4j + i/4, so pointing lane i at
+// X[rb + i/4][c0 + 4(i%4)] delivers X[rb + j][c0 + i] for j = 0..3; two reads
+// (rb = r0+8g and r0+8g+4) give the eight rows.  fp32 gathers eight words.
+// ---------------------------------------------------------------------------
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+template <typename T, int P>
+__device__ __forceinline__ typename Elem<T>::frag load_frag_tr(const T* X, int r0, int c0) {
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  typename Elem<T>::frag f;
+  if constexpr (sizeof(T) == 2) {
+    const T* a0 = X + (r0 + 8 * g + (c >> 2)) * P + c0 + 4 * (c & 3);
+    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(a0));
+    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(a0 + 4 * P));
+    i16x4 both[2] = {lo, hi};
+    __builtin_memcpy(&f, both, 16);
+  } else {
+    const T* a0 = X + (r0 + 8 * g) * P + c0 + c;
 #pragma unroll
-  for (int ps = 0; ps < S::kPasses; ++ps) {
-    const int r = 2 * (tid / S::kChunksPerRow + ps * S::kPairsPerPass);
-    if constexpr (sizeof(T) == 2) {
-      const uint32_t* a = reinterpret_cast<const uint32_t*>(&st.x0[ps]);
-      const uint32_t* b = reinterpret_cast<const uint32_t*>(&st.x1[ps]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t lo = (a[e >> 1] >> (16 * (e & 1))) & 0xffffu;
-        const uint32_t hi = (b[e >> 1] >> (16 * (e & 1))) & 0xffffu;
-        *reinterpret_cast<uint32_t*>(lds + (col + e) * P + r) = lo | (hi << 16);
-      }
-    } else {
-      const uint32_t* a = reinterpret_cast<const uint32_t*>(&st.x0[ps]);
-      const uint32_t* b = reinterpret_cast<const uint32_t*>(&st.x1[ps]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        *reinterpret_cast<u32x2*>(lds + (col + e) * P + r) = u32x2{a[e], b[e]};
-      }
-    }
+    for (int j = 0; j < 8; ++j) f[j] = a0[j * P];
   }
+  return f;
 }
 
 // ---------------------------------------------------------------------------
-// Tile products.
+// Tile products over a row-major LDS tile X of the streamed operand (64 x D).
 //
-// mm_d: out(streamed, stationary) += sum_d Str[streamed][d] * Sta[stationary][d]
-//   rows: row-major LDS tile of the streamed operand (64 x D);
-//   sta:  this lane's stationary fragments, sta[ks] = Sta[row][32ks+8g .. +7].
+// mm_d: out(streamed, stationary) += sum_d X[streamed][d] * Sta[stationary][d]
+//   sta: this lane's stationary fragments, sta[ks] = Sta[row][32ks+8g .. +7].
 //
-// mm_s: acc^T[d][stationary] += sum_streamed Tr[d][streamed] * Y[streamed][stationary]
-//   tr: transposed LDS tile of the streamed operand (D x 64);
-//   y:  per k-block B fragments built from a score tile.
+// mm_s: acc^T[d][stationary] += sum_streamed X[streamed][d] * Y[streamed][stationary]
+//   y: per k-block B fragments built from a score tile;
 //   acc[dsub] holds d = 16*dsub + 4*g + i for this lane's stationary row.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
@@ -352,15 +380,12 @@ __device__ __forceinline__ void mm_d(Tile& out, const T* rows, const typename El
 }
 
 template <typename T, int D>
-__device__ __forceinline__ void mm_s(f32x4* acc, const T* tr, const typename Elem<T>::frag* y) {
-  constexpr int P = Lds<T, D>::kTrPitch;
-  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+__device__ __forceinline__ void mm_s(f32x4* acc, const T* X, const typename Elem<T>::frag* y) {
+  constexpr int P = Lds<T, D>::kRowPitch;
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-    for (int ds = 0; ds < D / 16; ++ds) {
-      acc[ds] = Elem<T>::mma(acc[ds], load_frag<T>(tr + (16 * ds + c) * P + 32 * kb + 8 * g), y[kb]);
-    }
+    for (int ds = 0; ds < D / 16; ++ds) acc[ds] = Elem<T>::mma(acc[ds], load_frag_tr<T, P>(X, 32 * kb, 16 * ds), y[kb]);
   }
 }
 
@@ -388,6 +413,15 @@ __device__ __forceinline__ void store_acc_rows(T* base, int64_t ld, int row, int
   T* rp = base + (int64_t)row * ld + 4 * g;
 #pragma unroll
   for (int ds = 0; ds < D / 16; ++ds) store4<T>(rp + 16 * ds, acc[ds] * mul);
+}
+
+// Store a transposed accumulator as fp32 partial rows: dst[row_local][d].
+template <int D>
+__device__ __forceinline__ void store_acc_partial(float* dst, int row_local, const f32x4* acc) {
+  const int g = (threadIdx.x & 63) >> 4;
+  float* rp = dst + row_local * D + 4 * g;
+#pragma unroll
+  for (int ds = 0; ds < D / 16; ++ds) *reinterpret_cast<f32x4*>(rp + 16 * ds) = acc[ds];
 }
 
 // Eight consecutive fp32 values v[0..7] = src[idx0 .. idx0+7], zero past n.

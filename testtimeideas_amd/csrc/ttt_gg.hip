@@ -16,7 +16,9 @@
 //   so gS*K = Z1*K - E o (Z2*K) - F o (P*K)   (E, F scale rows),
 // and F = rowsum(Z1) - E * rowsum(Z2).  Likewise
 //   gdP*V = (P o gdS)*V - E o (P*V).
-// It writes GQ, optionally GdO, and E and F for the column pass.
+// It writes GQ, optionally GdO, and E and F for the column pass.  When the
+// key loop is split, chunks write the four (seven) accumulators and the three
+// row sums, and k_combine_gg_row applies the same formulas to the totals.
 //
 // k_gg_col (stationary key rows, streamed query tiles) reads D, E, F per
 // streamed row and forms dS, gdP, gS tile by tile for GK and GV.
@@ -34,18 +36,16 @@
 namespace ttt {
 
 template <typename T>
-__device__ __forceinline__ void load_p_row_gg(Tile& p, const T* pm, int n0, int T_, bool row_ok) {
+__device__ __forceinline__ void gg_load_p_frags(typename Elem<T>::frag* f, const T* pm, int n0, int T_, bool row_ok) {
   const int g = (threadIdx.x & 63) >> 4;
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
     const int n = n0 + stream_index(kb, g, 0);
     if (row_ok && n + 8 <= T_) {
-      const typename Elem<T>::frag f = load_frag<T>(pm + n);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) p.set(kb, j, Elem<T>::f32(f[j]));
+      f[kb] = load_frag<T>(pm + n);
     } else {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) p.set(kb, j, (row_ok && n + j < T_) ? Elem<T>::f32(pm[n + j]) : 0.f);
+      for (int j = 0; j < 8; ++j) f[kb][j] = (row_ok && n + j < T_) ? pm[n + j] : Elem<T>::cvt(0.f);
     }
   }
 }
@@ -56,25 +56,22 @@ __global__ __launch_bounds__(kThreads) void k_gg_row(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
-  constexpr int kA = 4 * L::kRowElems;                 // K, V, gK, gV rows
-  constexpr int kB = (GDO ? 4 : 2) * L::kTrElems;      // K^T, gK^T (, V^T, gV^T)
-  __shared__ __align__(16) T smem[kA > kB ? kA : kB];
-  T* sK = smem;
-  T* sV = smem + L::kRowElems;
-  T* sgK = smem + 2 * L::kRowElems;
-  T* sgV = smem + 3 * L::kRowElems;
-  T* sKt = smem;
-  T* sgKt = smem + L::kTrElems;
-  T* sVt = smem + 2 * L::kTrElems;
-  T* sgVt = smem + 3 * L::kTrElems;
+  constexpr int NACC = GDO ? 7 : 4;
+  __shared__ __align__(16) T sK[L::kRowElems];
+  __shared__ __align__(16) T sV[L::kRowElems];
+  __shared__ __align__(16) T sgK[L::kRowElems];
+  __shared__ __align__(16) T sgV[L::kRowElems];
 
   const int T_ = a.T;
-  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
   const int nblk = (T_ + kBlk - 1) / kBlk;
-  const int mb = a.causal ? (nblk - 1 - (int)blockIdx.x) : (int)blockIdx.x;
-  const int m0 = mb * kBlk;
+  const int bi = blockIdx.x % nblk, ch = blockIdx.x / nblk;
+  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+  const int mb = a.causal ? (nblk - 1 - bi) : bi;
+  const Chunk cr = chunk_of(0, row_block_hi(mb, nblk, a.causal), ch, a.chunk);
+  if (ch >= cr.nch) return;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c = lane & 15, g = lane >> 4;
-  const int m = m0 + 16 * w + c;
+  const int rl = 16 * w + c;
+  const int m = mb * kBlk + rl;
   const bool row_ok = m < T_;
 
   const T* Q = at<const T>(a.q, b, h);
@@ -107,27 +104,34 @@ __global__ __launch_bounds__(kThreads) void k_gg_row(Params a) {
   }
   float e_acc = 0.f, x_acc = 0.f, d_acc = 0.f;
 
-  const int n_end = a.causal ? mb + 1 : nblk;
-  for (int nb = 0; nb < n_end; ++nb) {
+  Stage<T, D> s0, s1, s2, s3;
+  frag pn[2];
+  auto load_tile = [&](int nb) {
     const int n0 = nb * kBlk;
-    const int rows_valid = T_ - n0;
-    {
-      Stage<T, D> s0, s1, s2, s3;
-      stage_load<T, D>(s0, K + (int64_t)n0 * a.k.st, a.k.st, rows_valid, D);
-      stage_load<T, D>(s1, V + (int64_t)n0 * a.v.st, a.v.st, rows_valid, D);
-      stage_load<T, D>(s2, gK + (int64_t)n0 * a.gk.st, a.gk.st, rows_valid, D);
-      stage_load<T, D>(s3, gV + (int64_t)n0 * a.gv.st, a.gv.st, rows_valid, D);
-      __syncthreads();
-      stage_store_rows<T, D>(s0, sK);
-      stage_store_rows<T, D>(s1, sV);
-      stage_store_rows<T, D>(s2, sgK);
-      stage_store_rows<T, D>(s3, sgV);
-      __syncthreads();
-    }
+    stage_load<T, D>(s0, K + (int64_t)n0 * a.k.st, a.k.st, T_ - n0, D);
+    stage_load<T, D>(s1, V + (int64_t)n0 * a.v.st, a.v.st, T_ - n0, D);
+    stage_load<T, D>(s2, gK + (int64_t)n0 * a.gk.st, a.gk.st, T_ - n0, D);
+    stage_load<T, D>(s3, gV + (int64_t)n0 * a.gv.st, a.gv.st, T_ - n0, D);
+    if constexpr (LOADP) gg_load_p_frags<T>(pn, Pm, n0, T_, row_ok);
+  };
+  load_tile(cr.t0);
+  for (int nb = cr.t0; nb < cr.t1; ++nb) {
+    const int n0 = nb * kBlk;
+    __syncthreads();
+    stage_store_rows<T, D>(s0, sK);
+    stage_store_rows<T, D>(s1, sV);
+    stage_store_rows<T, D>(s2, sgK);
+    stage_store_rows<T, D>(s3, sgV);
+    __syncthreads();
     Tile p, dp, gds, gp1;
     if constexpr (LOADP) {
-      load_p_row_gg<T>(p, Pm, n0, T_, row_ok);
-    } else {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) p.set(kb, j, E::f32(pn[kb][j]));
+    }
+    if (nb + 1 < cr.t1) load_tile(nb + 1);
+    if constexpr (!LOADP) {
       p.zero();
       mm_d<T, D>(p, sK, qf);
 #pragma unroll
@@ -135,8 +139,7 @@ __global__ __launch_bounds__(kThreads) void k_gg_row(Params a) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) p.set(kb, j, fast_exp2(p.at(kb, j) * a.scale_log2 - lse2));
     }
-    const bool need_mask = (a.causal && nb == mb) || (n0 + kBlk > T_);
-    if (need_mask) {
+    if ((a.causal && nb == mb) || (n0 + kBlk > T_)) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -179,50 +182,53 @@ __global__ __launch_bounds__(kThreads) void k_gg_row(Params a) {
       pf[kb] = tile_frag<T>(p, kb);
       if constexpr (GDO) z4f[kb] = vals_frag<T>(vz4);
     }
-    {
-      Stage<T, D> s0, s1, s2, s3;
-      stage_load<T, D>(s0, K + (int64_t)n0 * a.k.st, a.k.st, rows_valid, D);
-      stage_load<T, D>(s1, gK + (int64_t)n0 * a.gk.st, a.gk.st, rows_valid, D);
-      if constexpr (GDO) {
-        stage_load<T, D>(s2, V + (int64_t)n0 * a.v.st, a.v.st, rows_valid, D);
-        stage_load<T, D>(s3, gV + (int64_t)n0 * a.gv.st, a.gv.st, rows_valid, D);
-      }
-      __syncthreads();
-      stage_store_tr<T, D>(s0, sKt);
-      stage_store_tr<T, D>(s1, sgKt);
-      if constexpr (GDO) {
-        stage_store_tr<T, D>(s2, sVt);
-        stage_store_tr<T, D>(s3, sgVt);
-      }
-      __syncthreads();
-    }
-    mm_s<T, D>(a1, sgKt, dsf);
-    mm_s<T, D>(a2, sKt, z1f);
-    mm_s<T, D>(a3, sKt, z2f);
-    mm_s<T, D>(a4, sKt, pf);
+    mm_s<T, D>(a1, sgK, dsf);
+    mm_s<T, D>(a2, sK, z1f);
+    mm_s<T, D>(a3, sK, z2f);
+    mm_s<T, D>(a4, sK, pf);
     if constexpr (GDO) {
-      mm_s<T, D>(b1, sgVt, pf);
-      mm_s<T, D>(b2, sVt, z4f);
-      mm_s<T, D>(b3, sVt, pf);
+      mm_s<T, D>(b1, sgV, pf);
+      mm_s<T, D>(b2, sV, z4f);
+      mm_s<T, D>(b3, sV, pf);
     }
   }
   const float Ev = group_sum(e_acc);
   const float Xv = group_sum(x_acc);
   const float Dv = group_sum(d_acc);
-  const float Fv = Xv - Ev * Dv;
-  f32x4 gq[D / 16];
+  if (cr.nch == 1) {
+    const float Fv = Xv - Ev * Dv;
+    f32x4 gq[D / 16];
 #pragma unroll
-  for (int i = 0; i < D / 16; ++i) gq[i] = a1[i] + a2[i] - Ev * a3[i] - Fv * a4[i];
-  store_acc_rows<T, D>(at<T>(a.gq_out, b, h), a.gq_out.st, m, T_, gq, s);
-  if constexpr (GDO) {
-    f32x4 go[D / 16];
+    for (int i = 0; i < D / 16; ++i) gq[i] = a1[i] + a2[i] - Ev * a3[i] - Fv * a4[i];
+    store_acc_rows<T, D>(at<T>(a.gq_out, b, h), a.gq_out.st, m, T_, gq, s);
+    if constexpr (GDO) {
+      f32x4 go[D / 16];
 #pragma unroll
-    for (int i = 0; i < D / 16; ++i) go[i] = b1[i] + b2[i] - Ev * b3[i];
-    store_acc_rows<T, D>(at<T>(a.gdout, b, h), a.gdout.st, m, T_, go, 1.f);
-  }
-  if (row_ok && g == 0) {
-    a.e[ridx] = Ev;
-    a.f[ridx] = Fv;
+      for (int i = 0; i < D / 16; ++i) go[i] = b1[i] + b2[i] - Ev * b3[i];
+      store_acc_rows<T, D>(at<T>(a.gdout, b, h), a.gdout.st, m, T_, go, 1.f);
+    }
+    if (row_ok && g == 0) {
+      a.e[ridx] = Ev;
+      a.f[ridx] = Fv;
+    }
+  } else {
+    const int64_t part = part_index(a, bh, nblk, mb, ch);
+    float* base = a.ws_acc + part * NACC * kBlk * D;
+    store_acc_partial<D>(base, rl, a1);
+    store_acc_partial<D>(base + kBlk * D, rl, a2);
+    store_acc_partial<D>(base + 2 * kBlk * D, rl, a3);
+    store_acc_partial<D>(base + 3 * kBlk * D, rl, a4);
+    if constexpr (GDO) {
+      store_acc_partial<D>(base + 4 * kBlk * D, rl, b1);
+      store_acc_partial<D>(base + 5 * kBlk * D, rl, b2);
+      store_acc_partial<D>(base + 6 * kBlk * D, rl, b3);
+    }
+    if (g == 0) {
+      float* sc = a.ws_sc + part * 3 * kBlk;
+      sc[rl] = Ev;
+      sc[kBlk + rl] = Xv;
+      sc[2 * kBlk + rl] = Dv;
+    }
   }
 }
 
@@ -233,24 +239,21 @@ __global__ __launch_bounds__(kThreads) void k_gg_col(Params a) {
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
   typedef Lds<T, kBlk> LP;
-  constexpr int kA = 3 * L::kRowElems + (LOADP ? LP::kTrElems : 0);  // Q, gQ, dO rows (+ P^T)
-  constexpr int kB = 3 * L::kTrElems;                                  // gQ^T, Q^T, dO^T
-  __shared__ __align__(16) T smem[kA > kB ? kA : kB];
-  T* sQ = smem;
-  T* sgQ = smem + L::kRowElems;
-  T* sdO = smem + 2 * L::kRowElems;
-  T* sPt = smem + 3 * L::kRowElems;
-  T* sgQt = smem;
-  T* sQt = smem + L::kTrElems;
-  T* sdOt = smem + 2 * L::kTrElems;
+  __shared__ __align__(16) T sQ[L::kRowElems];
+  __shared__ __align__(16) T sgQ[L::kRowElems];
+  __shared__ __align__(16) T sdO[L::kRowElems];
+  __shared__ __align__(16) T sP[LOADP ? LP::kRowElems : 8];
 
   const int T_ = a.T;
-  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
   const int nblk = (T_ + kBlk - 1) / kBlk;
-  const int nb = (int)blockIdx.x;
+  const int nb = blockIdx.x % nblk, ch = blockIdx.x / nblk;
+  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+  const Chunk cr = chunk_of(col_block_lo(nb, a.causal), nblk, ch, a.chunk);
+  if (ch >= cr.nch) return;
   const int n0 = nb * kBlk;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c = lane & 15, g = lane >> 4;
-  const int n = n0 + 16 * w + c;
+  const int cl = 16 * w + c;
+  const int n = n0 + cl;
 
   const T* Q = at<const T>(a.q, b, h);
   const T* K = at<const T>(a.k, b, h);
@@ -263,7 +266,7 @@ __global__ __launch_bounds__(kThreads) void k_gg_col(Params a) {
   const float* rs = a.rowsum_in + (int64_t)bh * T_;
   const float* ev = a.e + (int64_t)bh * T_;
   const float* fv = a.f + (int64_t)bh * T_;
-  const float* lse = a.lse + (int64_t)bh * T_;
+  const float* lse = LOADP ? nullptr : a.lse + (int64_t)bh * T_;
   const float s = a.scale;
 
   frag kf[D / 32], gkf[D / 32], vf[D / 32], gvf[D / 32];
@@ -279,30 +282,31 @@ __global__ __launch_bounds__(kThreads) void k_gg_col(Params a) {
 #pragma unroll
   for (int i = 0; i < D / 16; ++i) acc_gk[i] = acc_gv[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int m_begin = a.causal ? nb : 0;
-  for (int mb = m_begin; mb < nblk; ++mb) {
+  Stage<T, D> s0, s1, s2;
+  Stage<T, kBlk> sp;
+  auto load_tile = [&](int mb) {
     const int m0 = mb * kBlk;
-    const int rows_valid = T_ - m0;
-    {
-      Stage<T, D> s0, s1, s2;
-      Stage<T, kBlk> sp;
-      stage_load<T, D>(s0, Q + (int64_t)m0 * a.q.st, a.q.st, rows_valid, D);
-      stage_load<T, D>(s1, gQ + (int64_t)m0 * a.gq.st, a.gq.st, rows_valid, D);
-      stage_load<T, D>(s2, dO + (int64_t)m0 * a.dout.st, a.dout.st, rows_valid, D);
-      if constexpr (LOADP) stage_load<T, kBlk>(sp, Pb + (int64_t)m0 * a.p.st + n0, a.p.st, rows_valid, T_ - n0);
-      __syncthreads();
-      stage_store_rows<T, D>(s0, sQ);
-      stage_store_rows<T, D>(s1, sgQ);
-      stage_store_rows<T, D>(s2, sdO);
-      if constexpr (LOADP) stage_store_tr<T, kBlk>(sp, sPt);
-      __syncthreads();
-    }
+    stage_load<T, D>(s0, Q + (int64_t)m0 * a.q.st, a.q.st, T_ - m0, D);
+    stage_load<T, D>(s1, gQ + (int64_t)m0 * a.gq.st, a.gq.st, T_ - m0, D);
+    stage_load<T, D>(s2, dO + (int64_t)m0 * a.dout.st, a.dout.st, T_ - m0, D);
+    if constexpr (LOADP) stage_load<T, kBlk>(sp, Pb + (int64_t)m0 * a.p.st + n0, a.p.st, T_ - m0, T_ - n0);
+  };
+  load_tile(cr.t0);
+  for (int mb = cr.t0; mb < cr.t1; ++mb) {
+    const int m0 = mb * kBlk;
+    __syncthreads();
+    stage_store_rows<T, D>(s0, sQ);
+    stage_store_rows<T, D>(s1, sgQ);
+    stage_store_rows<T, D>(s2, sdO);
+    if constexpr (LOADP) stage_store_rows<T, kBlk>(sp, sP);
+    __syncthreads();
+    if (mb + 1 < cr.t1) load_tile(mb + 1);
+
     Tile p, dp, gds, gp1;
     if constexpr (LOADP) {
-      constexpr int PP = LP::kTrPitch;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const frag f = load_frag<T>(sPt + (16 * w + c) * PP + stream_index(kb, g, 0));
+        const frag f = load_frag_tr<T, LP::kRowPitch>(sP, 32 * kb, 16 * w);
 #pragma unroll
         for (int j = 0; j < 8; ++j) p.set(kb, j, E::f32(f[j]));
       }
@@ -317,8 +321,7 @@ __global__ __launch_bounds__(kThreads) void k_gg_col(Params a) {
         for (int j = 0; j < 8; ++j) p.set(kb, j, fast_exp2(p.at(kb, j) * a.scale_log2 - l2[j] * kLog2e));
       }
     }
-    const bool need_mask = (a.causal && mb == nb) || (m0 + kBlk > T_) || (n0 + kBlk > T_);
-    if (need_mask) {
+    if ((a.causal && mb == nb) || (m0 + kBlk > T_) || (n0 + kBlk > T_)) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -359,29 +362,25 @@ __global__ __launch_bounds__(kThreads) void k_gg_col(Params a) {
       gsf[kb] = vals_frag<T>(vgs);
       gdpf[kb] = vals_frag<T>(vgdp);
     }
-    {
-      Stage<T, D> s0, s1, s2;
-      stage_load<T, D>(s0, gQ + (int64_t)m0 * a.gq.st, a.gq.st, rows_valid, D);
-      stage_load<T, D>(s1, Q + (int64_t)m0 * a.q.st, a.q.st, rows_valid, D);
-      stage_load<T, D>(s2, dO + (int64_t)m0 * a.dout.st, a.dout.st, rows_valid, D);
-      __syncthreads();
-      stage_store_tr<T, D>(s0, sgQt);
-      stage_store_tr<T, D>(s1, sQt);
-      stage_store_tr<T, D>(s2, sdOt);
-      __syncthreads();
-    }
-    mm_s<T, D>(acc_gk, sgQt, dsf);
-    mm_s<T, D>(acc_gk, sQt, gsf);
-    mm_s<T, D>(acc_gv, sdOt, gdpf);
+    mm_s<T, D>(acc_gk, sgQ, dsf);
+    mm_s<T, D>(acc_gk, sQ, gsf);
+    mm_s<T, D>(acc_gv, sdO, gdpf);
   }
-  store_acc_rows<T, D>(at<T>(a.gk_out, b, h), a.gk_out.st, n, T_, acc_gk, s);
-  store_acc_rows<T, D>(at<T>(a.gv_out, b, h), a.gv_out.st, n, T_, acc_gv, 1.f);
+  if (cr.nch == 1) {
+    store_acc_rows<T, D>(at<T>(a.gk_out, b, h), a.gk_out.st, n, T_, acc_gk, s);
+    store_acc_rows<T, D>(at<T>(a.gv_out, b, h), a.gv_out.st, n, T_, acc_gv, 1.f);
+  } else {
+    float* base = a.ws_acc + part_index(a, bh, nblk, nb, ch) * 2 * kBlk * D;
+    store_acc_partial<D>(base, cl, acc_gk);
+    store_acc_partial<D>(base + kBlk * D, cl, acc_gv);
+  }
 }
 
 // ---------------------------------------------------------------------------
 template <typename T, int D>
-static hipError_t launch_gg_row_t(const Params& a, bool load_p, bool gdo, hipStream_t st) {
-  dim3 grid((a.T + kBlk - 1) / kBlk, a.B * a.H);
+static hipError_t launch_gg_row_t(int dtype, const Params& a, bool load_p, bool gdo, hipStream_t st) {
+  const int nblk = (a.T + kBlk - 1) / kBlk;
+  dim3 grid(nblk * a.nchunk_max, a.B * a.H);
   if (load_p) {
     if (gdo)
       hipLaunchKernelGGL((k_gg_row<T, D, true, true>), grid, dim3(kThreads), 0, st, a);
@@ -393,26 +392,29 @@ static hipError_t launch_gg_row_t(const Params& a, bool load_p, bool gdo, hipStr
     else
       hipLaunchKernelGGL((k_gg_row<T, D, false, false>), grid, dim3(kThreads), 0, st, a);
   }
+  if (a.nchunk_max > 1) return launch_combine_gg_row(dtype, D, a, gdo, st);
   return hipGetLastError();
 }
 
 template <typename T, int D>
-static hipError_t launch_gg_col_t(const Params& a, bool load_p, hipStream_t st) {
-  dim3 grid((a.T + kBlk - 1) / kBlk, a.B * a.H);
+static hipError_t launch_gg_col_t(int dtype, const Params& a, bool load_p, hipStream_t st) {
+  const int nblk = (a.T + kBlk - 1) / kBlk;
+  dim3 grid(nblk * a.nchunk_max, a.B * a.H);
   if (load_p)
     hipLaunchKernelGGL((k_gg_col<T, D, true>), grid, dim3(kThreads), 0, st, a);
   else
     hipLaunchKernelGGL((k_gg_col<T, D, false>), grid, dim3(kThreads), 0, st, a);
+  if (a.nchunk_max > 1) return launch_combine_sum(dtype, D, a, kOutGKGV, st);
   return hipGetLastError();
 }
 
 hipError_t launch_gg_row(int dtype, int D, const Params& a, bool load_p, bool want_gdout, hipStream_t st) {
-  DISPATCH_DTYPE_D(dtype, D, return launch_gg_row_t<ElemT, kD>(a, load_p, want_gdout, st));
+  DISPATCH_DTYPE_D(dtype, D, return launch_gg_row_t<ElemT, kD>(dtype, a, load_p, want_gdout, st));
   return hipErrorInvalidValue;
 }
 
 hipError_t launch_gg_col(int dtype, int D, const Params& a, bool load_p, hipStream_t st) {
-  DISPATCH_DTYPE_D(dtype, D, return launch_gg_col_t<ElemT, kD>(a, load_p, st));
+  DISPATCH_DTYPE_D(dtype, D, return launch_gg_col_t<ElemT, kD>(dtype, a, load_p, st));
   return hipErrorInvalidValue;
 }
 

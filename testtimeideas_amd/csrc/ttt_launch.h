@@ -29,7 +29,19 @@ enum : int { kF16 = 0, kBF16 = 1, kF32 = 2 };
     }                                                                      \
   } while (0)
 
+// Which outputs a sum-combine finishes (see ttt_combine.hip).
+enum : int { kOutO = 0, kOutDQ = 1, kOutDKDV = 2, kOutDV = 3, kOutGKGV = 4 };
+
+// Partial accumulators and row scalars per chunk, by kernel family.
+enum : int { kFamFwdOnline = 0, kFamFwdP = 1, kFamDq = 2, kFamDkdv = 3, kFamGgRow = 4, kFamGgRowGdo = 5,
+             kFamGgCol = 6 };
+constexpr int kFamNacc[] = {1, 1, 1, 2, 4, 7, 2};
+constexpr int kFamNsc[] = {2, 2, 0, 0, 3, 3, 0};
+
 hipError_t launch_fwd(int dtype, int D, const Params& a, bool write_p, hipStream_t st);
+hipError_t launch_combine_sum(int dtype, int D, const Params& a, int which, hipStream_t st);
+hipError_t launch_combine_fwd(int dtype, int D, const Params& a, hipStream_t st);
+hipError_t launch_combine_gg_row(int dtype, int D, const Params& a, bool gdo, hipStream_t st);
 hipError_t launch_bwd_dq(int dtype, int D, const Params& a, bool load_p, hipStream_t st);
 hipError_t launch_bwd_dkdv(int dtype, int D, const Params& a, bool load_p, bool dv_only, hipStream_t st);
 hipError_t launch_bwd_rowsum(int dtype, int D, const Params& a, hipStream_t st);

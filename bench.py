@@ -81,29 +81,80 @@ def roofline_entry(cfg, ktimes, with_p=True):
         achieved = model["bytes"] / dur_s / 1e9
         peak, unit = workloads.PEAK_HBM_GBS, "GB/s"
     return {"kernel": name, "bound": model["bound"], "achieved": round(achieved, 2), "peak": peak,
-            "unit": unit, "frac": round(achieved / peak, 4), "traffic": None,
+            "unit": unit, "frac": round(achieved / peak, 4), "traffic": measured_traffic(name, cfg),
             "avg_us": round(ktimes[name] * 1e3, 2), "algorithmic_flops": model["flops"],
             "algorithmic_bytes": model["bytes"]}
 
 
+# Kernels behind each entry point, as named in the rocprof summaries.
+_ENTRY_KERNELS = {
+    "ttt_attn_fwd": ("k_fwd_stats", "k_fwd_p"),
+    "ttt_attn_bwd_dq": ("k_bwd_dq",),
+    "ttt_attn_bwd_dkdv": ("k_bwd_dkdv",),
+    "ttt_attn_gg_row": ("k_gg_row", "k_combine_gg_row"),
+    "ttt_attn_gg_col": ("k_gg_col",),
+}
+
+
+def measured_traffic(entry: str, cfg: workloads.Config):
+    """HBM bytes per launch of `entry` from the committed rocprof PMC summary
+    (FETCH_SIZE + WRITE_SIZE scaled by a plain-copy calibration), or None."""
+    path = os.path.join(ROOT, "profiles", f"pmc_traffic_{cfg.name}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        data = json.load(f)["kernels"]
+    tag = {"fp16": "DF16_", "bf16": "DF16b", "fp32": "f"}[cfg.dtype]
+    total, found = 0.0, False
+    for kname, rec in data.items():
+        base, _, args = kname.partition("<")
+        if base in _ENTRY_KERNELS.get(entry, ()) and args.startswith(f"{tag},{cfg.d}".replace("_,", ",")):
+            total += rec["fetch_bytes"] + rec["write_bytes"]
+            found = True
+    return round(total) if found else None
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(cfg: workloads.Config, budget_s: float = 20.0):
     """The math path (oracle.math_path, the reference's _attention_math + autograd
-    restated) on the host CPU, on the same seeded inputs in the config dtype."""
+    restated) on the host CPU, on the same seeded inputs in the config dtype.
+    Bounded sample: one warmup step, then whole steps until ~budget_s of timed
+    CPU work (at least one)."""
     from oracle import math_path
     threads = min(os.cpu_count() or 1, 16)
     torch.set_num_threads(threads)
     x = workloads.make_inputs(cfg, seed=0)
     args = [x[n] for n in ("q", "k", "v", "do", "rq", "rk", "rv")]
-    times = []
-    t_start = time.perf_counter()
     math_path.gradgrad_step(*args, cfg.causal, cfg.scale)  # warmup
-    while len(times) < 20 and (time.perf_counter() - t_start) < budget_s or len(times) < 3:
+    times = []
+    while not times or (sum(times) < budget_s * 1e3 and len(times) < 20):
         t0 = time.perf_counter()
         math_path.gradgrad_step(*args, cfg.causal, cfg.scale)
         times.append((time.perf_counter() - t0) * 1e3)
     return {"value": round(statistics.median(times), 3), "unit": "ms", "cores": threads, "kind": "port",
             "sample": f"{len(times)} full {cfg.name} steps (b{cfg.b} h{cfg.h} T{cfg.t} d{cfg.d} {cfg.dtype} "
-                      f"causal={cfg.causal}) after 1 warmup, median; torch CPU math path with autograd"}
+                      f"causal={cfg.causal}) after 1 warmup, median; torch CPU math path with autograd; "
+                      f"{threads} threads on {_cpu_model()}"}
+
+
+def copy_calibration(mb: int, reps: int = 5) -> None:
+    """A plain device copy of `mb` MiB (read mb, write mb), for scaling rocprof's
+    FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    src = torch.empty(mb << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
 
 
 def main():
@@ -114,6 +165,8 @@ def main():
     ap.add_argument("--config", default="C3", choices=sorted(workloads.CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the T=16k point and forward-only metrics")
+    ap.add_argument("--copy-mb", type=int, default=0,
+                    help="also run a plain device copy of this many MiB (counter calibration for rocprof)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -126,6 +179,8 @@ def main():
         sys.exit(2)
 
     dev = torch.device("cuda", 0)
+    if args.copy_mb:
+        copy_calibration(args.copy_mb)
     cfg = workloads.CONFIGS[args.config]
     x = workloads.make_inputs(cfg, seed=0, device=dev)
     step = make_step(cfg, x)

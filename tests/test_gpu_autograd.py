@@ -146,3 +146,16 @@ def test_alias_package_identity():
     # as in the reference package, the attribute ttt_kernels.triton_attention is the function
     assert ttt_kernels.triton_attention is impl.triton_attention
     assert alias.TritonAttentionFn is impl.TritonAttentionFn is TritonAttentionFn
+
+
+def test_c1_golden_fixture_fp32():
+    """C1 (b1 h1 T64 d64 fp32, non-causal) through the public API, with dO
+    requiring grad, against the committed fixture: max-abs <= 1e-5."""
+    import os
+    import numpy as np
+    f = np.load(os.path.join(os.path.dirname(__file__), "golden", "c1_b1h1_t64_d64_fp32.npz"))
+    xs = [torch.from_numpy(f[f"in_{n}"]) for n in ("q", "k", "v", "do", "rq", "rk", "rv")]
+    print("[case] c1 fixture", flush=True)
+    got = _gpu_step(xs, False, None, "save_p_triton_full", do_requires_grad=True)
+    for n in ("o", "dq", "dk", "dv", "gq", "gk", "gv", "gdo"):
+        check(n, got[n], f[f"out_{n}"], torch.float32)

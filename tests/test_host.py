@@ -1,0 +1,180 @@
+"""Host-side logic on the CPU: the C ABI library loads and exports every
+declared symbol, argument validation fails before anything is enqueued,
+workspace sizing, the roofline model, the bwd_mode registry, the number of
+launches per grad-grad step, and the C1 golden fixture."""
+import ctypes
+import importlib
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from testtimeideas_amd import _lib, workloads
+
+ROOT = os.path.abspath(os.path.join(os.path.dirname(__file__), ".."))
+HEADER = os.path.join(ROOT, "include", "ttt_attn.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^[A-Za-z_][\w\s\*]*?\b(ttt_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = _declared()
+    assert "ttt_attn_fwd" in names and "ttt_attn_gg" in names
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(_lib.exported_symbols()) == set(names)
+    assert lib.ttt_version() >= 200
+
+
+def _prob(**kw):
+    d = dict(dtype=0, causal=1, batch=1, heads=1, seqlen=128, head_dim=64, scale=0.125, split_chunk=0)
+    d.update(kw)
+    return _lib._Problem(d["dtype"], d["causal"], d["batch"], d["heads"], d["seqlen"], d["head_dim"],
+                         d["scale"], d["split_chunk"])
+
+
+def _v(addr=0x10000, st=64):
+    return ctypes.byref(_lib._View(addr, 128 * st, 128 * st, st))
+
+
+def _fwd_rc(pr, q=None, ws=None, wsn=0, p=None):
+    lib = _lib.load()
+    q = q if q is not None else _v()
+    return lib.ttt_attn_fwd(ctypes.byref(pr), q, _v(), _v(), _v(), 0x20000, p, ws, wsn, None)
+
+
+def test_validation_errors_without_gpu():
+    lib = _lib.load()
+    # unsupported head dim / dtype
+    assert _fwd_rc(_prob(head_dim=96)) == 2
+    assert b"head_dim" in lib.ttt_last_error()
+    assert _fwd_rc(_prob(dtype=7)) == 2
+    # bad sizes
+    assert _fwd_rc(_prob(seqlen=0)) == 1
+    assert _fwd_rc(_prob(batch=70000)) == 1
+    # null and misaligned operands
+    assert lib.ttt_attn_fwd(ctypes.byref(_prob()), None, _v(), _v(), _v(), 0x20000, None, None, 0, None) == 1
+    assert _fwd_rc(_prob(), q=_v(addr=0x10002)) == 1
+    assert b"aligned" in lib.ttt_last_error()
+    assert _fwd_rc(_prob(), q=_v(st=60)) == 1
+    # a split problem without a workspace
+    big = _prob(seqlen=8192)
+    assert _lib.workspace_bytes(big, _lib.ENTRY_FWD) > 0
+    assert _fwd_rc(big) == 4
+    assert b"workspace" in lib.ttt_last_error()
+    # rowsum missing for dK
+    assert lib.ttt_attn_bwd_dkdv(ctypes.byref(_prob()), _v(), _v(), _v(), _v(), 0x20000, None, None, _v(), _v(),
+                                 None, 0, None) == 1
+
+
+def test_workspace_sizes():
+    # C3: 128 blocks, chunk 17 -> 8 chunks; forward partials = 1 acc x 64 + 2 scalars per row
+    c3 = _prob(seqlen=8192)
+    assert _lib.workspace_bytes(c3, _lib.ENTRY_FWD) == 128 * 8 * 64 * (64 + 2) * 4
+    assert _lib.workspace_bytes(c3, _lib.ENTRY_GG_ROW) == 128 * 8 * 64 * (4 * 64 + 3) * 4
+    assert _lib.workspace_bytes(c3, _lib.ENTRY_GG, True) == 128 * 8 * 64 * (7 * 64 + 3) * 4
+    assert _lib.workspace_bytes(c3, _lib.ENTRY_BWD) == 128 * 8 * 64 * (2 * 64) * 4
+    # C5 fills the chip with blocks alone: no split, no workspace
+    c5 = _prob(batch=4, heads=16, seqlen=8192, head_dim=128, dtype=1)
+    assert all(_lib.workspace_bytes(c5, e) == 0 for e in range(8))
+    # no chunk is shorter than 4 tiles: 4 blocks never split, 5 blocks split once
+    assert _lib.workspace_bytes(_prob(seqlen=256), _lib.ENTRY_GG_COL) == 0
+    assert _lib.workspace_bytes(_prob(seqlen=300), _lib.ENTRY_GG_COL) == 5 * 2 * 64 * 128 * 4
+    assert _lib.workspace_bytes(_prob(seqlen=300, split_chunk=2), _lib.ENTRY_GG_COL) == 5 * 3 * 64 * 128 * 4
+    assert _lib.load().ttt_attn_workspace_size(ctypes.byref(_prob()), 99, 0) == -1
+
+
+def test_roofline_model_matches_baseline_table():
+    r = workloads.roofline_us(workloads.CONFIGS["C3"])
+    assert round(r["flops"] / 1e9, 2) == 60.60 and round(r["bytes"] / 1e6, 1) == 225.0
+    assert round(r["roofline_us"], 1) == 28.1 and r["bound"] == "hbm"
+    r = workloads.roofline_us(workloads.CONFIGS["C5"])
+    assert round(r["flops"] / 1e9, 1) == 7756.7 and r["bound"] == "mfma"
+    r = workloads.roofline_us(workloads.CONFIGS["C2"])
+    assert round(r["flops"] / 1e9, 2) == 51.54 and round(r["bytes"] / 1e6, 1) == 180.5
+    r = workloads.roofline_us(workloads.CONFIGS["C4_16k"])
+    assert round(r["roofline_us"], 1) == 106.6
+    assert workloads.active_area(8192, True) == 64 * 64 * 128 * 129 // 2
+
+
+def test_inputs_are_seeded_and_ordered():
+    cfg = workloads.CONFIGS["C1"]
+    a = workloads.make_inputs(cfg, seed=0)
+    b = workloads.make_inputs(cfg, seed=0)
+    g = torch.Generator().manual_seed(0)
+    first = torch.randn((1, 1, 64, 64), generator=g)
+    assert torch.equal(a["q"], first) and all(torch.equal(a[n], b[n]) for n in a)
+    c5 = workloads.Config("x", 1, 1, 64, 64, "fp32", True, qkv_scale=0.5)
+    assert torch.allclose(workloads.make_inputs(c5)["q"], first * 0.5)
+
+
+def test_mode_registry():
+    ta = importlib.import_module("testtimeideas_amd.ttt_kernels.triton_attention")
+    for m in ("save_p", "save_p_triton", "save_p_triton_bwd", "save_p_triton_full"):
+        assert ta.mode_kind(m) == "save_p"
+    for m in ("recompute", "recompute_manual", "recompute_sdp", "recompute_sdp_mem", "recompute_sdp_auto",
+              "recompute_compiled", "dv_only", "anything else"):
+        assert ta.mode_kind(m) == "recompute"
+    assert ta.mode_kind("custom") == "custom"
+    # the reference CLI's twelve choices (tests/bench_gradgrad.py:53-54) are all accepted
+    assert len(ta.BWD_MODES) == 12
+
+
+def test_cpu_tensors_raise():
+    from ttt_kernels import triton_attention
+    q = torch.randn(1, 1, 8, 64)
+    with pytest.raises(RuntimeError, match="ROCm"):
+        triton_attention(q, q, q)
+    with pytest.raises(NotImplementedError):
+        _lib.padded_head_dim(160)
+    assert _lib.padded_head_dim(32) == 64 and _lib.padded_head_dim(80) == 128
+
+
+def test_one_launch_of_each_pass_per_gradgrad_step(monkeypatch):
+    """Regression: the first backward ran a second time during the grad-grad
+    when the forward output reached the backward Function with its graph."""
+    ta = importlib.import_module("testtimeideas_amd.ttt_kernels.triton_attention")
+    calls = {"fwd": 0, "bwd": 0, "gg": 0}
+    monkeypatch.setattr(_lib, "check_inputs", lambda *a: None)
+
+    def fwd(q, k, v, causal, scale, want_p):
+        calls["fwd"] += 1
+        t = q.shape[2]
+        return torch.zeros_like(q), torch.zeros(q.shape[:3]), torch.zeros(q.shape[:3] + (t,)) if want_p else None
+
+    def bwd(q, k, v, o, do, lse, p, causal, scale):
+        calls["bwd"] += 1
+        return torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v), torch.zeros(q.shape[:3])
+
+    def gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, causal, scale, want_gdo):
+        calls["gg"] += 1
+        return torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v), None
+
+    monkeypatch.setattr(_lib, "fwd", fwd)
+    monkeypatch.setattr(_lib, "bwd", bwd)
+    monkeypatch.setattr(_lib, "gg", gg)
+    q, k, v, do, rq, rk, rv = (torch.randn(1, 1, 64, 64) for _ in range(7))
+    for mode in ("save_p_triton_full", "recompute"):
+        for key in calls:
+            calls[key] = 0
+        qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+        o = ta.triton_attention(qq, kk, vv, causal=True, bwd_mode=mode)
+        dq, dk, dv = torch.autograd.grad(o, (qq, kk, vv), do, create_graph=True)
+        s = (dq * rq).sum() + (dk * rk).sum() + (dv * rv).sum()
+        torch.autograd.grad(s, (qq, kk, vv))
+        assert calls == {"fwd": 1, "bwd": 1, "gg": 1}, (mode, calls)
+
+
+def test_golden_fixture_reproduces():
+    """The committed C1 fixture equals what the oracle produces now."""
+    golden = importlib.import_module("tests.golden.make_c1")
+    ref = np.load(os.path.join(ROOT, "tests", "golden", "c1_b1h1_t64_d64_fp32.npz"))
+    now = golden.build()
+    for key in ref.files:
+        assert np.array_equal(ref[key], now[key]), key

@@ -42,8 +42,14 @@ __device__ __forceinline__ float row_dot_do_o(const typename Elem<T>::frag* dof,
 // Raw P fragments of one key tile for this lane's query row: row pm, columns
 // n0 + 32kb + 8g .. +7; zero past T.
 template <typename T>
-__device__ __forceinline__ void load_p_frags(typename Elem<T>::frag* f, const T* pm, int n0, int T_, bool row_ok) {
+__device__ __forceinline__ void load_p_frags(typename Elem<T>::frag* f, const T* pm, int n0, int T_, bool row_ok,
+                                             bool full = false) {
   const int g = (threadIdx.x & 63) >> 4;
+  if (full) {  // every row and column of the tile is inside T (uniform)
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) f[kb] = load_frag<T>(pm + n0 + stream_index(kb, g, 0));
+    return;
+  }
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
     const int n = n0 + stream_index(kb, g, 0);
@@ -115,7 +121,8 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dq(Params a) {
   frag pn[2];
   stage_load<T, D>(stK, K + (int64_t)cr.t0 * kBlk * a.k.st, a.k.st, T_ - cr.t0 * kBlk, D);
   stage_load<T, D>(stV, V + (int64_t)cr.t0 * kBlk * a.v.st, a.v.st, T_ - cr.t0 * kBlk, D);
-  if constexpr (LOADP) load_p_frags<T>(pn, Pm, cr.t0 * kBlk, T_, row_ok);
+  const bool rows_full = mb * kBlk + kBlk <= T_;
+  if constexpr (LOADP) load_p_frags<T>(pn, Pm, cr.t0 * kBlk, T_, row_ok, rows_full && cr.t0 * kBlk + kBlk <= T_);
   for (int nb = cr.t0; nb < cr.t1; ++nb) {
     const int n0 = nb * kBlk;
     __syncthreads();
@@ -128,7 +135,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dq(Params a) {
       const int n1 = n0 + kBlk;
       stage_load<T, D>(stK, K + (int64_t)n1 * a.k.st, a.k.st, T_ - n1, D);
       stage_load<T, D>(stV, V + (int64_t)n1 * a.v.st, a.v.st, T_ - n1, D);
-      if constexpr (LOADP) load_p_frags<T>(pn, Pm, n1, T_, row_ok);
+      if constexpr (LOADP) load_p_frags<T>(pn, Pm, n1, T_, row_ok, rows_full && n1 + kBlk <= T_);
     }
     if constexpr (!LOADP) {
       p.zero();
@@ -196,6 +203,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dkdv(Params a) {
   const T* Pb = LOADP ? at<const T>(a.p, b, h) : nullptr;
   const float* rs = DV_ONLY ? nullptr : a.rowsum_in + (int64_t)bh * T_;
   const float* lse = LOADP ? nullptr : a.lse + (int64_t)bh * T_;
+  const bool stats_vec = (((int64_t)bh * T_) & 3) == 0;  // row-statistic bases are 16-byte aligned
 
   frag vf[D / 32], kf[D / 32];
 #pragma unroll
@@ -241,7 +249,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dkdv(Params a) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         float l2[8];
-        load_vec8(l2, lse, m0 + stream_index(kb, g, 0), T_);
+        load_vec8(l2, lse, m0 + stream_index(kb, g, 0), T_, stats_vec && m0 + kBlk <= T_);
 #pragma unroll
         for (int j = 0; j < 8; ++j) p.set(kb, j, fast_exp2(p.at(kb, j) * a.scale_log2 - l2[j] * kLog2e));
       }
@@ -267,7 +275,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dkdv(Params a) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         float d8[8], v[8];
-        load_vec8(d8, rs, m0 + stream_index(kb, g, 0), T_);
+        load_vec8(d8, rs, m0 + stream_index(kb, g, 0), T_, stats_vec && m0 + kBlk <= T_);
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = p.at(kb, j) * (dp.at(kb, j) - d8[j]);
         dsf[kb] = vals_frag<T>(v);
@@ -321,7 +329,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_rowsum(Params a) {
     __syncthreads();
     if (nb + 1 < n_end) stage_load<T, D>(stV, V + (int64_t)(n0 + kBlk) * a.v.st, a.v.st, T_ - n0 - kBlk, D);
     frag pr[2];
-    load_p_frags<T>(pr, Pm, n0, T_, row_ok);
+    load_p_frags<T>(pr, Pm, n0, T_, row_ok, mb * kBlk + kBlk <= T_ && n0 + kBlk <= T_);
     Tile p, dp;
     frags_to_tile<T>(p, pr);
     dp.zero();

@@ -9,6 +9,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <initializer_list>
 
 #include "../../include/ttt_attn.h"
 #include "ttt_launch.h"
@@ -25,8 +26,20 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
-// Workgroups the split aims for: two per CU of an MI355X (256 CUs).
-constexpr int64_t kTargetWorkgroups = 512;
+// Workgroups the split aims for, per kernel family, on an MI355X (256 CUs):
+// the light forward/backward kernels keep several workgroups resident per CU,
+// the register-heavy grad-grad kernels two.
+#ifndef TTT_TARGET_FWD
+#define TTT_TARGET_FWD 1024
+#endif
+#ifndef TTT_TARGET_BWD
+#define TTT_TARGET_BWD 512
+#endif
+#ifndef TTT_TARGET_GG
+#define TTT_TARGET_GG 1024
+#endif
+constexpr int64_t kFamTarget[] = {TTT_TARGET_FWD, TTT_TARGET_FWD, TTT_TARGET_BWD, TTT_TARGET_BWD,
+                                  TTT_TARGET_GG, TTT_TARGET_GG, TTT_TARGET_GG};
 // Chunks shorter than this are not worth a combine pass.
 constexpr int kMinChunk = 4;
 
@@ -75,7 +88,7 @@ struct Split {
 
 // Tiles per workgroup: enough workgroups to fill the chip, no chunk shorter
 // than kMinChunk, no split at all when the blocks alone fill it.
-Split choose_split(const ttt_problem* pr) {
+Split choose_split(const ttt_problem* pr, int fam) {
   Split s;
   s.nblk = (int)((pr->seqlen + ttt::kBlk - 1) / ttt::kBlk);
   const int64_t bh = pr->batch * pr->heads;
@@ -85,7 +98,8 @@ Split choose_split(const ttt_problem* pr) {
   } else {
     const int64_t tiles = pr->causal ? (int64_t)s.nblk * (s.nblk + 1) / 2 : (int64_t)s.nblk * s.nblk;
     const int64_t total = bh * tiles;
-    c = (int)std::max<int64_t>(kMinChunk, (total + kTargetWorkgroups - 1) / kTargetWorkgroups);
+    const int64_t target = kFamTarget[fam];
+    c = (int)std::max<int64_t>(kMinChunk, (total + target - 1) / target);
   }
   s.chunk = std::min(c, s.nblk);
   s.nchunk_max = (s.nblk + s.chunk - 1) / s.chunk;
@@ -111,14 +125,14 @@ int64_t family_bytes(const ttt_problem* pr, const Split& s, int fam) {
   return parts * ttt::kBlk * (ttt::kFamNacc[fam] * pr->head_dim + ttt::kFamNsc[fam]) * (int64_t)sizeof(float);
 }
 
+int64_t fam_bytes(const ttt_problem* pr, int fam) { return family_bytes(pr, choose_split(pr, fam), fam); }
+
 int64_t entry_bytes(const ttt_problem* pr, int entry, bool gdo) {
-  const Split s = choose_split(pr);
-  if (entry == TTT_ENTRY_BWD)
-    return std::max(family_bytes(pr, s, ttt::kFamDq), family_bytes(pr, s, ttt::kFamDkdv));
+  if (entry == TTT_ENTRY_BWD) return std::max(fam_bytes(pr, ttt::kFamDq), fam_bytes(pr, ttt::kFamDkdv));
   if (entry == TTT_ENTRY_GG)
-    return std::max(family_bytes(pr, s, family_of(TTT_ENTRY_GG_ROW, gdo)), family_bytes(pr, s, ttt::kFamGgCol));
+    return std::max(fam_bytes(pr, family_of(TTT_ENTRY_GG_ROW, gdo)), fam_bytes(pr, ttt::kFamGgCol));
   const int fam = family_of(entry, gdo);
-  return fam < 0 ? -1 : family_bytes(pr, s, fam);
+  return fam < 0 ? -1 : fam_bytes(pr, fam);
 }
 
 ttt::Params base_params(const ttt_problem* pr) {
@@ -135,7 +149,7 @@ ttt::Params base_params(const ttt_problem* pr) {
 
 // Attach the split and the workspace for kernel family `fam`.
 int attach_split(const ttt_problem* pr, int fam, void* ws, int64_t ws_bytes, ttt::Params* a) {
-  const Split s = choose_split(pr);
+  const Split s = choose_split(pr, fam);
   a->chunk = s.chunk;
   a->nchunk_max = s.nchunk_max;
   const int64_t need = family_bytes(pr, s, fam);
@@ -152,6 +166,13 @@ int attach_split(const ttt_problem* pr, int fam, void* ws, int64_t ws_bytes, ttt
 }
 
 bool has_p(const ttt_view* p) { return p && p->data; }
+
+// Row-statistic arrays (lse, rowsum, E, F) must be 16-byte aligned.
+int check_stats(std::initializer_list<const void*> ptrs) {
+  for (const void* q : ptrs)
+    if (q && !aligned16(q)) return fail(TTT_ERR_INVALID_ARGUMENT, "row-statistic array not 16-byte aligned");
+  return TTT_OK;
+}
 
 int launched(hipError_t e, const char* what) {
   if (e != hipSuccess) return fail(TTT_ERR_LAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
@@ -191,6 +212,7 @@ int ttt_attn_fwd(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, co
   TRY(take_view(pr, v, "v", &a.v));
   TRY(take_view(pr, o, "o", &a.o));
   if (!lse) return fail(TTT_ERR_INVALID_ARGUMENT, "lse: null pointer");
+  TRY(check_stats({lse}));
   a.lse = lse;
   const bool wp = has_p(p);
   if (wp) TRY(take_view(pr, p, "p", &a.p));
@@ -215,6 +237,7 @@ int ttt_attn_bwd_dq(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
     TRY(take_view(pr, q, "q", &a.q));
     if (!lse) return fail(TTT_ERR_INVALID_ARGUMENT, "lse: null pointer (required without p)");
   }
+  TRY(check_stats({lse, rowsum_in, rowsum_out}));
   a.lse = const_cast<float*>(lse);
   a.rowsum_in = rowsum_in;
   a.rowsum_out = rowsum_out;
@@ -245,6 +268,7 @@ int ttt_attn_bwd_dkdv(const ttt_problem* pr, const ttt_view* q, const ttt_view* 
     TRY(take_view(pr, dk, "dk", &a.dk));
     if (!rowsum) return fail(TTT_ERR_INVALID_ARGUMENT, "rowsum: null pointer (required for dk)");
   }
+  TRY(check_stats({lse, rowsum}));
   a.lse = const_cast<float*>(lse);
   a.rowsum_in = rowsum;
   TRY(attach_split(pr, ttt::kFamDkdv, workspace, workspace_bytes, &a));
@@ -271,6 +295,7 @@ int ttt_attn_bwd_rowsum(const ttt_problem* pr, const ttt_view* p, const ttt_view
   TRY(take_view(pr, dout, "dout", &a.dout));
   TRY(take_view(pr, v, "v", &a.v));
   if (!rowsum) return fail(TTT_ERR_INVALID_ARGUMENT, "rowsum: null pointer");
+  TRY(check_stats({rowsum}));
   a.rowsum_out = rowsum;
   return launched(ttt::launch_bwd_rowsum(pr->dtype, (int)pr->head_dim, a, (hipStream_t)stream),
                   "ttt_attn_bwd_rowsum");
@@ -297,6 +322,7 @@ int ttt_attn_gg_row(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
   const bool gdo = gdout && gdout->data;
   if (gdo) TRY(take_view(pr, gdout, "gdout", &a.gdout));
   if (!rowsum || !e_out || !f_out) return fail(TTT_ERR_INVALID_ARGUMENT, "rowsum/e_out/f_out: null pointer");
+  TRY(check_stats({lse, rowsum, e_out, f_out}));
   a.lse = const_cast<float*>(lse);
   a.rowsum_in = rowsum;
   a.e = e_out;
@@ -326,6 +352,7 @@ int ttt_attn_gg_col(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
   if (lp) TRY(take_view(pr, p, "p", &a.p));
   if (!lp && !lse) return fail(TTT_ERR_INVALID_ARGUMENT, "lse: null pointer (required without p)");
   if (!rowsum || !e_in || !f_in) return fail(TTT_ERR_INVALID_ARGUMENT, "rowsum/e_in/f_in: null pointer");
+  TRY(check_stats({lse, rowsum, e_in, f_in}));
   a.lse = const_cast<float*>(lse);
   a.rowsum_in = rowsum;
   a.e = const_cast<float*>(e_in);

@@ -34,6 +34,11 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// Unguarded staging loads for interior tiles (1) or guards on every tile (0).
+#ifndef TTT_STAGE_FAST
+#define TTT_STAGE_FAST 1
+#endif
+
 namespace ttt {
 
 constexpr int kThreads = 256;  // four wave64s per workgroup
@@ -290,6 +295,15 @@ __device__ __forceinline__ void stage_load(Stage<T, NCOL>& st, const T* __restri
   const int tid = threadIdx.x;
   const int ch = tid % S::kChunksPerRow;
   const int col = ch * S::kChunk;
+  if (TTT_STAGE_FAST && rows_valid >= kBlk && cols_valid >= NCOL) {  // interior tile (uniform): no guards
+#pragma unroll
+    for (int ps = 0; ps < S::kPasses; ++ps) {
+      const int r = 2 * (tid / S::kChunksPerRow + ps * S::kPairsPerPass);
+      st.x0[ps] = load16(g + (int64_t)r * ld + col);
+      st.x1[ps] = load16(g + (int64_t)(r + 1) * ld + col);
+    }
+    return;
+  }
 #pragma unroll
   for (int ps = 0; ps < S::kPasses; ++ps) {
     const int r = 2 * (tid / S::kChunksPerRow + ps * S::kPairsPerPass);
@@ -389,16 +403,21 @@ __device__ __forceinline__ void mm_s(f32x4* acc, const T* X, const typename Elem
   }
 }
 
-// Sum over the four lane groups (same c): xor 16 and xor 32.
+// Reductions over the four lane groups (same c), with the gfx950 VALU lane
+// swaps: permlane16_swap(x, x) returns, in each lane, the pair {x[l], x[l^16]}
+// (order depending on the lane's 16-lane row); permlane32_swap does the same
+// for l^32.  Sum or max of the pair is the xor-16 / xor-32 reduction step.
 __device__ __forceinline__ float group_sum(float x) {
-  x += __shfl_xor(x, 16);
-  x += __shfl_xor(x, 32);
-  return x;
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 __device__ __forceinline__ float group_max(float x) {
-  x = fmaxf(x, __shfl_xor(x, 16));
-  x = fmaxf(x, __shfl_xor(x, 32));
-  return x;
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -425,7 +444,15 @@ __device__ __forceinline__ void store_acc_partial(float* dst, int row_local, con
 }
 
 // Eight consecutive fp32 values v[0..7] = src[idx0 .. idx0+7], zero past n.
-__device__ __forceinline__ void load_vec8(float* v, const float* src, int idx0, int n) {
+// `fast` (uniform) asserts idx0 + 8 <= n and a 16-byte aligned src + idx0.
+__device__ __forceinline__ void load_vec8(float* v, const float* src, int idx0, int n, bool fast = false) {
+  if (fast) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(src + idx0);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(src + idx0 + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { v[j] = a[j]; v[4 + j] = b[j]; }
+    return;
+  }
   if (idx0 + 8 <= n && ((reinterpret_cast<uintptr_t>(src + idx0) & 15) == 0)) {
     const f32x4 a = *reinterpret_cast<const f32x4*>(src + idx0);
     const f32x4 b = *reinterpret_cast<const f32x4*>(src + idx0 + 4);

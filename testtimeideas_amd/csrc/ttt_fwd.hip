@@ -119,13 +119,14 @@ __global__ __launch_bounds__(kThreads) void k_fwd_online(Params a) {
       }
       pf[kb] = vals_frag<T>(pv);
     }
-    l = l * alpha + group_sum(ts);
+    l = l * alpha + ts;  // this lane's share of the row sum (all lanes share mnew)
     mx = mnew;
 #pragma unroll
     for (int i = 0; i < D / 16; ++i) acc[i] *= alpha;
     mm_s<T, D>(acc, sV, pf);
   }
 
+  l = group_sum(l);
   const int64_t ridx = (int64_t)bh * T_ + m;
   if (cr.nch == 1) {
     if (m < T_ && g == 0) a.lse[ridx] = (mx + __log2f(l)) * kLn2;
@@ -178,14 +179,28 @@ __global__ __launch_bounds__(kThreads) void k_fwd_stats(Params a) {
     }
     Tile s;
     fwd_scores<T, D>(s, sK, qf, a, nb, mb, m);
-    const float mnew = fmaxf(mx, tile_max(s));
+    // Per-lane running max and sum over this lane's columns; combined across
+    // the four lane groups after the loop.  A lane whose columns are all
+    // masked so far keeps max -inf and sum 0 (shift by 0 avoids -inf - -inf).
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) tmax = fmaxf(tmax, s.at(kb, j));
+    const float mnew = fmaxf(mx, tmax);
+    const float shift = mnew == -INFINITY ? 0.f : mnew;
     float ts = 0.f;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) ts += fast_exp2(s.at(kb, j) - mnew);
-    l = l * fast_exp2(mx - mnew) + group_sum(ts);
+      for (int j = 0; j < 8; ++j) ts += fast_exp2(s.at(kb, j) - shift);
+    l = l * fast_exp2(mx - shift) + ts;
     mx = mnew;
+  }
+  {
+    const float mrow = group_max(mx);  // finite: every row has a valid column in tile 0
+    l = group_sum(l * fast_exp2(mx - mrow));
+    mx = mrow;
   }
   if (g != 0) return;
   if (cr.nch == 1) {

@@ -33,11 +33,23 @@
 #include "ttt_common.h"
 #include "ttt_launch.h"
 
+// Waves per SIMD the grad-grad kernels are compiled for (registers are
+// limited to 512 / this per lane).
+#ifndef TTT_GG_WAVES_PER_EU
+#define TTT_GG_WAVES_PER_EU 2
+#endif
+
 namespace ttt {
 
 template <typename T>
-__device__ __forceinline__ void gg_load_p_frags(typename Elem<T>::frag* f, const T* pm, int n0, int T_, bool row_ok) {
+__device__ __forceinline__ void gg_load_p_frags(typename Elem<T>::frag* f, const T* pm, int n0, int T_, bool row_ok,
+                                                bool full) {
   const int g = (threadIdx.x & 63) >> 4;
+  if (full) {  // every row and column of the tile is inside T (uniform)
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) f[kb] = load_frag<T>(pm + n0 + stream_index(kb, g, 0));
+    return;
+  }
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
     const int n = n0 + stream_index(kb, g, 0);
@@ -52,7 +64,8 @@ __device__ __forceinline__ void gg_load_p_frags(typename Elem<T>::frag* f, const
 
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool LOADP, bool GDO>
-__global__ __launch_bounds__(kThreads) void k_gg_row(Params a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TTT_GG_WAVES_PER_EU)))
+void k_gg_row(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
@@ -112,7 +125,7 @@ __global__ __launch_bounds__(kThreads) void k_gg_row(Params a) {
     stage_load<T, D>(s1, V + (int64_t)n0 * a.v.st, a.v.st, T_ - n0, D);
     stage_load<T, D>(s2, gK + (int64_t)n0 * a.gk.st, a.gk.st, T_ - n0, D);
     stage_load<T, D>(s3, gV + (int64_t)n0 * a.gv.st, a.gv.st, T_ - n0, D);
-    if constexpr (LOADP) gg_load_p_frags<T>(pn, Pm, n0, T_, row_ok);
+    if constexpr (LOADP) gg_load_p_frags<T>(pn, Pm, n0, T_, row_ok, mb * kBlk + kBlk <= T_ && n0 + kBlk <= T_);
   };
   load_tile(cr.t0);
   for (int nb = cr.t0; nb < cr.t1; ++nb) {
@@ -234,7 +247,8 @@ __global__ __launch_bounds__(kThreads) void k_gg_row(Params a) {
 
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool LOADP>
-__global__ __launch_bounds__(kThreads) void k_gg_col(Params a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TTT_GG_WAVES_PER_EU)))
+void k_gg_col(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
@@ -268,6 +282,7 @@ __global__ __launch_bounds__(kThreads) void k_gg_col(Params a) {
   const float* fv = a.f + (int64_t)bh * T_;
   const float* lse = LOADP ? nullptr : a.lse + (int64_t)bh * T_;
   const float s = a.scale;
+  const bool stats_vec = (((int64_t)bh * T_) & 3) == 0;  // row-statistic bases are 16-byte aligned
 
   frag kf[D / 32], gkf[D / 32], vf[D / 32], gvf[D / 32];
 #pragma unroll
@@ -316,7 +331,7 @@ __global__ __launch_bounds__(kThreads) void k_gg_col(Params a) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         float l2[8];
-        load_vec8(l2, lse, m0 + stream_index(kb, g, 0), T_);
+        load_vec8(l2, lse, m0 + stream_index(kb, g, 0), T_, stats_vec && m0 + kBlk <= T_);
 #pragma unroll
         for (int j = 0; j < 8; ++j) p.set(kb, j, fast_exp2(p.at(kb, j) * a.scale_log2 - l2[j] * kLog2e));
       }
@@ -343,9 +358,10 @@ __global__ __launch_bounds__(kThreads) void k_gg_col(Params a) {
     for (int kb = 0; kb < 2; ++kb) {
       float d8[8], e8[8], f8[8];
       const int idx = m0 + stream_index(kb, g, 0);
-      load_vec8(d8, rs, idx, T_);
-      load_vec8(e8, ev, idx, T_);
-      load_vec8(f8, fv, idx, T_);
+      const bool vf8 = stats_vec && m0 + kBlk <= T_;
+      load_vec8(d8, rs, idx, T_, vf8);
+      load_vec8(e8, ev, idx, T_, vf8);
+      load_vec8(f8, fv, idx, T_, vf8);
       float vds[8], vgs[8], vgdp[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {

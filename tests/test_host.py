@@ -74,11 +74,14 @@ def test_validation_errors_without_gpu():
 
 
 def test_workspace_sizes():
-    # C3: 128 blocks, chunk 17 -> 8 chunks; forward partials = 1 acc x 64 + 2 scalars per row
+    # C3: 128 blocks, 8256 active tiles.  Forward and grad-grad aim at 1024
+    # workgroups: chunk ceil(8256/1024) = 9 tiles -> 15 chunks; the first
+    # backward aims at 512: chunk 17 -> 8 chunks.  Forward partials = 1 acc x 64
+    # + 2 scalars per row.
     c3 = _prob(seqlen=8192)
-    assert _lib.workspace_bytes(c3, _lib.ENTRY_FWD) == 128 * 8 * 64 * (64 + 2) * 4
-    assert _lib.workspace_bytes(c3, _lib.ENTRY_GG_ROW) == 128 * 8 * 64 * (4 * 64 + 3) * 4
-    assert _lib.workspace_bytes(c3, _lib.ENTRY_GG, True) == 128 * 8 * 64 * (7 * 64 + 3) * 4
+    assert _lib.workspace_bytes(c3, _lib.ENTRY_FWD) == 128 * 15 * 64 * (64 + 2) * 4
+    assert _lib.workspace_bytes(c3, _lib.ENTRY_GG_ROW) == 128 * 15 * 64 * (4 * 64 + 3) * 4
+    assert _lib.workspace_bytes(c3, _lib.ENTRY_GG, True) == 128 * 15 * 64 * (7 * 64 + 3) * 4
     assert _lib.workspace_bytes(c3, _lib.ENTRY_BWD) == 128 * 8 * 64 * (2 * 64) * 4
     # C5 fills the chip with blocks alone: no split, no workspace
     c5 = _prob(batch=4, heads=16, seqlen=8192, head_dim=128, dtype=1)

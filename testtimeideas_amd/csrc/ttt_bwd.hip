@@ -184,6 +184,11 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dkdv(Params a) {
   __shared__ __align__(16) T sdO[L::kRowElems];
   __shared__ __align__(16) T sQ[kNeedQ ? L::kRowElems : 8];
   __shared__ __align__(16) T sP[LOADP ? LP::kRowElems : 8];
+  // Staged row statistics of the streamed tile: D (unless DV_ONLY), then lse
+  // (recompute only).
+  constexpr int kNS = (DV_ONLY ? 0 : 1) + (LOADP ? 0 : 1);
+  constexpr int kSD = 0, kSL = DV_ONLY ? 0 : 1;
+  __shared__ __align__(16) float sS[kNS > 0 ? kNS * kBlk : 4];
 
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
@@ -203,7 +208,6 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dkdv(Params a) {
   const T* Pb = LOADP ? at<const T>(a.p, b, h) : nullptr;
   const float* rs = DV_ONLY ? nullptr : a.rowsum_in + (int64_t)bh * T_;
   const float* lse = LOADP ? nullptr : a.lse + (int64_t)bh * T_;
-  const bool stats_vec = (((int64_t)bh * T_) & 3) == 0;  // row-statistic bases are 16-byte aligned
 
   frag vf[D / 32], kf[D / 32];
 #pragma unroll
@@ -218,11 +222,13 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dkdv(Params a) {
 
   Stage<T, D> stdO, stQ;
   Stage<T, kBlk> stP;
+  float stv = 0.f;
   auto load_tile = [&](int mb) {
     const int m0 = mb * kBlk;
     stage_load<T, D>(stdO, dO + (int64_t)m0 * a.dout.st, a.dout.st, T_ - m0, D);
     if constexpr (kNeedQ) stage_load<T, D>(stQ, Q + (int64_t)m0 * a.q.st, a.q.st, T_ - m0, D);
     if constexpr (LOADP) stage_load<T, kBlk>(stP, Pb + (int64_t)m0 * a.p.st + n0, a.p.st, T_ - m0, T_ - n0);
+    if constexpr (kNS > 0) stv = stat_load<kNS>(DV_ONLY ? lse : rs, lse, nullptr, nullptr, m0, T_ - m0);
   };
   load_tile(cr.t0);
   for (int mb = cr.t0; mb < cr.t1; ++mb) {
@@ -231,6 +237,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dkdv(Params a) {
     stage_store_rows<T, D>(stdO, sdO);
     if constexpr (kNeedQ) stage_store_rows<T, D>(stQ, sQ);
     if constexpr (LOADP) stage_store_rows<T, kBlk>(stP, sP);
+    if constexpr (kNS > 0) stat_store<kNS>(stv, sS);
     __syncthreads();
     if (mb + 1 < cr.t1) load_tile(mb + 1);
 
@@ -249,7 +256,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dkdv(Params a) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         float l2[8];
-        load_vec8(l2, lse, m0 + stream_index(kb, g, 0), T_, stats_vec && m0 + kBlk <= T_);
+        stat_read8(l2, sS, kSL, kb);
 #pragma unroll
         for (int j = 0; j < 8; ++j) p.set(kb, j, fast_exp2(p.at(kb, j) * a.scale_log2 - l2[j] * kLog2e));
       }
@@ -275,7 +282,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dkdv(Params a) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         float d8[8], v[8];
-        load_vec8(d8, rs, m0 + stream_index(kb, g, 0), T_, stats_vec && m0 + kBlk <= T_);
+        stat_read8(d8, sS, kSD, kb);
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = p.at(kb, j) * (dp.at(kb, j) - d8[j]);
         dsf[kb] = vals_frag<T>(v);

@@ -2,16 +2,32 @@
 //
 // Each main-kernel workgroup of a split block wrote fp32 partials to the
 // workspace: accumulators [part][nacc][64][D] and row scalars [part][nsc][64],
-// part = (bh*nblk + block)*nchunk_max + chunk.  One combine workgroup per
-// (block, bh) reads every chunk of its block in chunk order (so results do not
-// depend on scheduling) and writes the outputs.  Blocks with a single chunk
-// were finished by the main kernel and are skipped here.
+// part = (bh*nblk + block)*nchunk_max + chunk.  The combine kernels read every
+// chunk of a block in chunk order (so results do not depend on scheduling) and
+// write the outputs.  Blocks with a single chunk were finished by the main
+// kernel and are skipped here.
 //
-// Thread t of 256 owns block row t/4 and a quarter of the head dim.
+// A block's 64 x D outputs are covered by D/16 workgroups; thread t of
+// workgroup `sub` owns one 4-wide slot: slot = 256*sub + t, row slot/(D/4),
+// columns 4*(slot % (D/4)) .. +3.  Loads of all accumulators of a chunk are
+// issued together and the chunk loop is unrolled; the sums still run in chunk
+// order.
 #include "ttt_common.h"
 #include "ttt_launch.h"
 
 namespace ttt {
+
+template <int D>
+struct CombineSlot {
+  static constexpr int kSub = kBlk * (D / 4) / kThreads;  // workgroups per block
+  int blk, r, d0;
+  __device__ __forceinline__ CombineSlot() {
+    blk = blockIdx.x / kSub;
+    const int slot = (blockIdx.x % kSub) * kThreads + threadIdx.x;
+    r = slot / (D / 4);
+    d0 = 4 * (slot % (D / 4));
+  }
+};
 
 __device__ __forceinline__ int block_nch(const Params& a, int blk, int nblk, bool col) {
   const int lo = col ? col_block_lo(blk, a.causal) : 0;
@@ -19,29 +35,27 @@ __device__ __forceinline__ int block_nch(const Params& a, int blk, int nblk, boo
   return (hi - lo + a.chunk - 1) / a.chunk;
 }
 
-template <typename T, int D>
-__device__ __forceinline__ void store_row_quarter(T* dst, const float* v) {
-#pragma unroll
-  for (int e = 0; e < D / 4; e += 4) store4<T>(dst + e, f32x4{v[e], v[e + 1], v[e + 2], v[e + 3]});
-}
-
-// Sum of `nch` chunk partials of accumulator `ai`: out[e] = sum over chunks.
-template <int D>
-__device__ __forceinline__ void sum_parts(float* out, const float* ws, int64_t p0, int nch, int nacc, int ai,
+// out[i] = sum over chunks k (in order) of accumulator a0 + i at (r, d0..d0+3).
+template <int D, int NA>
+__device__ __forceinline__ void sum_parts(f32x4* out, const float* ws, int64_t p0, int nch, int nacc, int a0,
                                           int r, int d0) {
 #pragma unroll
-  for (int e = 0; e < D / 4; ++e) out[e] = 0.f;
+  for (int i = 0; i < NA; ++i) out[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const float* base = ws + (p0 * nacc + a0) * kBlk * D + r * D + d0;
+  const int64_t step = (int64_t)nacc * kBlk * D;
+#pragma unroll 4
   for (int k = 0; k < nch; ++k) {
-    const float* src = ws + ((p0 + k) * nacc + ai) * kBlk * D + r * D + d0;
+    f32x4 x[NA];
 #pragma unroll
-    for (int e = 0; e < D / 4; e += 4) {
-      const f32x4 x = *reinterpret_cast<const f32x4*>(src + e);
-      out[e] += x[0];
-      out[e + 1] += x[1];
-      out[e + 2] += x[2];
-      out[e + 3] += x[3];
-    }
+    for (int i = 0; i < NA; ++i) x[i] = *reinterpret_cast<const f32x4*>(base + k * step + i * kBlk * D);
+#pragma unroll
+    for (int i = 0; i < NA; ++i) out[i] += x[i];
   }
+}
+
+template <typename T>
+__device__ __forceinline__ void store_slot(const View& o, int b, int h, int row, int d0, f32x4 v) {
+  store4<T>(at<T>(o, b, h) + (int64_t)row * o.st + d0, v);
 }
 
 // ---------------------------------------------------------------------------
@@ -50,38 +64,35 @@ template <typename T, int D>
 __global__ __launch_bounds__(kThreads) void k_combine_sum(Params a, int which) {
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
-  const int blk = blockIdx.x, bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+  const CombineSlot<D> cs;
+  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
   const bool col = which == kOutDKDV || which == kOutDV || which == kOutGKGV;
-  const int nch = block_nch(a, blk, nblk, col);
+  const int nch = block_nch(a, cs.blk, nblk, col);
   if (nch <= 1) return;
-  const int r = threadIdx.x >> 2, d0 = (threadIdx.x & 3) * (D / 4);
-  const int row = blk * kBlk + r;
+  const int row = cs.blk * kBlk + cs.r;
   if (row >= T_) return;
-  const int64_t p0 = part_index(a, bh, nblk, blk, 0);
-  float v[D / 4];
+  const int64_t p0 = part_index(a, bh, nblk, cs.blk, 0);
   if (which == kOutO || which == kOutDQ) {
-    sum_parts<D>(v, a.ws_acc, p0, nch, 1, 0, r, d0);
-    const View& o = which == kOutO ? a.o : a.dq;
-    const float s = which == kOutO ? 1.f : a.scale;
-#pragma unroll
-    for (int e = 0; e < D / 4; ++e) v[e] *= s;
-    store_row_quarter<T, D>(at<T>(o, b, h) + (int64_t)row * o.st + d0, v);
+    f32x4 v;
+    sum_parts<D, 1>(&v, a.ws_acc, p0, nch, 1, 0, cs.r, cs.d0);
+    if (which == kOutO)
+      store_slot<T>(a.o, b, h, row, cs.d0, v);
+    else
+      store_slot<T>(a.dq, b, h, row, cs.d0, v * a.scale);
     return;
   }
   // two-accumulator column kernels: index 0 = dV / GK, index 1 = dK / GV
-  const View& o0 = which == kOutGKGV ? a.gk_out : a.dv;
-  const float s0 = which == kOutGKGV ? a.scale : 1.f;
-  sum_parts<D>(v, a.ws_acc, p0, nch, 2, 0, r, d0);
-#pragma unroll
-  for (int e = 0; e < D / 4; ++e) v[e] *= s0;
-  store_row_quarter<T, D>(at<T>(o0, b, h) + (int64_t)row * o0.st + d0, v);
-  if (which == kOutDV) return;
-  const View& o1 = which == kOutGKGV ? a.gv_out : a.dk;
-  const float s1 = which == kOutGKGV ? 1.f : a.scale;
-  sum_parts<D>(v, a.ws_acc, p0, nch, 2, 1, r, d0);
-#pragma unroll
-  for (int e = 0; e < D / 4; ++e) v[e] *= s1;
-  store_row_quarter<T, D>(at<T>(o1, b, h) + (int64_t)row * o1.st + d0, v);
+  const bool gg = which == kOutGKGV;
+  if (which == kOutDV) {
+    f32x4 v;
+    sum_parts<D, 1>(&v, a.ws_acc, p0, nch, 2, 0, cs.r, cs.d0);
+    store_slot<T>(a.dv, b, h, row, cs.d0, v);
+    return;
+  }
+  f32x4 v[2];
+  sum_parts<D, 2>(v, a.ws_acc, p0, nch, 2, 0, cs.r, cs.d0);
+  store_slot<T>(gg ? a.gk_out : a.dv, b, h, row, cs.d0, v[0] * (gg ? a.scale : 1.f));
+  store_slot<T>(gg ? a.gv_out : a.dk, b, h, row, cs.d0, v[1] * (gg ? 1.f : a.scale));
 }
 
 // ---------------------------------------------------------------------------
@@ -90,31 +101,26 @@ template <typename T, int D>
 __global__ __launch_bounds__(kThreads) void k_combine_fwd(Params a) {
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
-  const int blk = blockIdx.x, bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
-  const int nch = block_nch(a, blk, nblk, false);
+  const CombineSlot<D> cs;
+  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+  const int nch = block_nch(a, cs.blk, nblk, false);
   if (nch <= 1) return;
-  const int r = threadIdx.x >> 2, d0 = (threadIdx.x & 3) * (D / 4);
-  const int row = blk * kBlk + r;
+  const int r = cs.r;
+  const int row = cs.blk * kBlk + r;
   if (row >= T_) return;
-  const int64_t p0 = part_index(a, bh, nblk, blk, 0);
+  const int64_t p0 = part_index(a, bh, nblk, cs.blk, 0);
   float mm = -INFINITY;
   for (int k = 0; k < nch; ++k) mm = fmaxf(mm, a.ws_sc[(p0 + k) * 2 * kBlk + r]);
   float ll = 0.f;
-  float v[D / 4];
-#pragma unroll
-  for (int e = 0; e < D / 4; ++e) v[e] = 0.f;
+  f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
   for (int k = 0; k < nch; ++k) {
     const float wk = fast_exp2(a.ws_sc[(p0 + k) * 2 * kBlk + r] - mm);
     ll += a.ws_sc[(p0 + k) * 2 * kBlk + kBlk + r] * wk;
-    const float* src = a.ws_acc + (p0 + k) * kBlk * D + r * D + d0;
-#pragma unroll
-    for (int e = 0; e < D / 4; ++e) v[e] += wk * src[e];
+    v += wk * *reinterpret_cast<const f32x4*>(a.ws_acc + (p0 + k) * kBlk * D + r * D + cs.d0);
   }
-  const float inv = 1.f / ll;
-#pragma unroll
-  for (int e = 0; e < D / 4; ++e) v[e] *= inv;
-  store_row_quarter<T, D>(at<T>(a.o, b, h) + (int64_t)row * a.o.st + d0, v);
-  if ((threadIdx.x & 3) == 0) a.lse[(int64_t)bh * T_ + row] = (mm + __log2f(ll)) * kLn2;
+  store_slot<T>(a.o, b, h, row, cs.d0, v * (1.f / ll));
+  if (cs.d0 == 0) a.lse[(int64_t)bh * T_ + row] = (mm + __log2f(ll)) * kLn2;
 }
 
 // ---------------------------------------------------------------------------
@@ -126,13 +132,14 @@ __global__ __launch_bounds__(kThreads) void k_combine_gg_row(Params a) {
   constexpr int NACC = GDO ? 7 : 4;
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
-  const int blk = blockIdx.x, bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
-  const int nch = block_nch(a, blk, nblk, false);
+  const CombineSlot<D> cs;
+  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+  const int nch = block_nch(a, cs.blk, nblk, false);
   if (nch <= 1) return;
-  const int r = threadIdx.x >> 2, d0 = (threadIdx.x & 3) * (D / 4);
-  const int row = blk * kBlk + r;
+  const int r = cs.r;
+  const int row = cs.blk * kBlk + r;
   if (row >= T_) return;
-  const int64_t p0 = part_index(a, bh, nblk, blk, 0);
+  const int64_t p0 = part_index(a, bh, nblk, cs.blk, 0);
   float ev = 0.f, xv = 0.f, dv = 0.f;
   for (int k = 0; k < nch; ++k) {
     const float* sc = a.ws_sc + (p0 + k) * 3 * kBlk + r;
@@ -141,29 +148,20 @@ __global__ __launch_bounds__(kThreads) void k_combine_gg_row(Params a) {
     dv += sc[2 * kBlk];
   }
   const float fv = xv - ev * dv;
-  float acc[D / 4], t[D / 4];
-  sum_parts<D>(acc, a.ws_acc, p0, nch, NACC, 0, r, d0);
-  sum_parts<D>(t, a.ws_acc, p0, nch, NACC, 1, r, d0);
-#pragma unroll
-  for (int e = 0; e < D / 4; ++e) acc[e] += t[e];
-  sum_parts<D>(t, a.ws_acc, p0, nch, NACC, 2, r, d0);
-#pragma unroll
-  for (int e = 0; e < D / 4; ++e) acc[e] -= ev * t[e];
-  sum_parts<D>(t, a.ws_acc, p0, nch, NACC, 3, r, d0);
-#pragma unroll
-  for (int e = 0; e < D / 4; ++e) acc[e] = a.scale * (acc[e] - fv * t[e]);
-  store_row_quarter<T, D>(at<T>(a.gq_out, b, h) + (int64_t)row * a.gq_out.st + d0, acc);
+  f32x4 t[4];
+  sum_parts<D, 4>(t, a.ws_acc, p0, nch, NACC, 0, r, cs.d0);
+  f32x4 acc = t[0] + t[1];
+  acc -= ev * t[2];
+  acc = a.scale * (acc - fv * t[3]);
+  store_slot<T>(a.gq_out, b, h, row, cs.d0, acc);
   if constexpr (GDO) {
-    sum_parts<D>(acc, a.ws_acc, p0, nch, NACC, 4, r, d0);
-    sum_parts<D>(t, a.ws_acc, p0, nch, NACC, 5, r, d0);
-#pragma unroll
-    for (int e = 0; e < D / 4; ++e) acc[e] += t[e];
-    sum_parts<D>(t, a.ws_acc, p0, nch, NACC, 6, r, d0);
-#pragma unroll
-    for (int e = 0; e < D / 4; ++e) acc[e] -= ev * t[e];
-    store_row_quarter<T, D>(at<T>(a.gdout, b, h) + (int64_t)row * a.gdout.st + d0, acc);
+    f32x4 u[3];
+    sum_parts<D, 3>(u, a.ws_acc, p0, nch, NACC, 4, r, cs.d0);
+    f32x4 go = u[0] + u[1];
+    go -= ev * u[2];
+    store_slot<T>(a.gdout, b, h, row, cs.d0, go);
   }
-  if ((threadIdx.x & 3) == 0) {
+  if (cs.d0 == 0) {
     a.e[(int64_t)bh * T_ + row] = ev;
     a.f[(int64_t)bh * T_ + row] = fv;
   }
@@ -172,21 +170,21 @@ __global__ __launch_bounds__(kThreads) void k_combine_gg_row(Params a) {
 // ---------------------------------------------------------------------------
 template <typename T, int D>
 static hipError_t combine_sum_t(const Params& a, int which, hipStream_t st) {
-  dim3 grid((a.T + kBlk - 1) / kBlk, a.B * a.H);
+  dim3 grid((a.T + kBlk - 1) / kBlk * CombineSlot<D>::kSub, a.B * a.H);
   hipLaunchKernelGGL((k_combine_sum<T, D>), grid, dim3(kThreads), 0, st, a, which);
   return hipGetLastError();
 }
 
 template <typename T, int D>
 static hipError_t combine_fwd_t(const Params& a, hipStream_t st) {
-  dim3 grid((a.T + kBlk - 1) / kBlk, a.B * a.H);
+  dim3 grid((a.T + kBlk - 1) / kBlk * CombineSlot<D>::kSub, a.B * a.H);
   hipLaunchKernelGGL((k_combine_fwd<T, D>), grid, dim3(kThreads), 0, st, a);
   return hipGetLastError();
 }
 
 template <typename T, int D>
 static hipError_t combine_gg_row_t(const Params& a, bool gdo, hipStream_t st) {
-  dim3 grid((a.T + kBlk - 1) / kBlk, a.B * a.H);
+  dim3 grid((a.T + kBlk - 1) / kBlk * CombineSlot<D>::kSub, a.B * a.H);
   if (gdo)
     hipLaunchKernelGGL((k_combine_gg_row<T, D, true>), grid, dim3(kThreads), 0, st, a);
   else

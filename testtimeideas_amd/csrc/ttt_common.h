@@ -443,6 +443,38 @@ __device__ __forceinline__ void store_acc_partial(float* dst, int row_local, con
   for (int ds = 0; ds < D / 16; ++ds) *reinterpret_cast<f32x4*>(rp + 16 * ds) = acc[ds];
 }
 
+// ---------------------------------------------------------------------------
+// Per-row fp32 statistics (lse, D, E, F) of a streamed 64-row tile, staged
+// through LDS with the tile so that their loads are issued with the next
+// tile's prefetch (vector-memory counters retire in order: a statistic loaded
+// after the prefetch would make the current tile wait for the whole prefetch).
+// Wave w < NS loads statistic w of the tile's rows (one coalesced 256-byte
+// read per wave); rows at or beyond rows_valid read as zero.  LDS: s[stat][row].
+// ---------------------------------------------------------------------------
+template <int NS>
+__device__ __forceinline__ float stat_load(const float* s0, const float* s1, const float* s2, const float* s3,
+                                           int m0, int rows_valid) {
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (w >= NS) return 0.f;
+  const float* src = w == 0 ? s0 : w == 1 ? s1 : w == 2 ? s2 : s3;
+  return lane < rows_valid ? src[m0 + lane] : 0.f;
+}
+
+template <int NS>
+__device__ __forceinline__ void stat_store(float v, float* lds) {
+  if ((int)(threadIdx.x >> 6) < NS) lds[threadIdx.x] = v;
+}
+
+// v[j] = statistic `st` of streamed row 32kb + 8g + j of the staged tile.
+__device__ __forceinline__ void stat_read8(float* v, const float* lds, int st, int kb) {
+  const int g = (threadIdx.x & 63) >> 4;
+  const float* p = lds + st * kBlk + stream_index(kb, g, 0);
+  const f32x4 a = *reinterpret_cast<const f32x4*>(p);
+  const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) { v[j] = a[j]; v[4 + j] = b[j]; }
+}
+
 // Eight consecutive fp32 values v[0..7] = src[idx0 .. idx0+7], zero past n.
 // `fast` (uniform) asserts idx0 + 8 <= n and a 16-byte aligned src + idx0.
 __device__ __forceinline__ void load_vec8(float* v, const float* src, int idx0, int n, bool fast = false) {

@@ -257,6 +257,9 @@ void k_gg_col(Params a) {
   __shared__ __align__(16) T sgQ[L::kRowElems];
   __shared__ __align__(16) T sdO[L::kRowElems];
   __shared__ __align__(16) T sP[LOADP ? LP::kRowElems : 8];
+  // Staged row statistics of the streamed tile: D, E, F, then lse (recompute).
+  constexpr int kNS = LOADP ? 3 : 4;
+  __shared__ __align__(16) float sS[kNS * kBlk];
 
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
@@ -282,7 +285,6 @@ void k_gg_col(Params a) {
   const float* fv = a.f + (int64_t)bh * T_;
   const float* lse = LOADP ? nullptr : a.lse + (int64_t)bh * T_;
   const float s = a.scale;
-  const bool stats_vec = (((int64_t)bh * T_) & 3) == 0;  // row-statistic bases are 16-byte aligned
 
   frag kf[D / 32], gkf[D / 32], vf[D / 32], gvf[D / 32];
 #pragma unroll
@@ -299,12 +301,14 @@ void k_gg_col(Params a) {
 
   Stage<T, D> s0, s1, s2;
   Stage<T, kBlk> sp;
+  float stv;
   auto load_tile = [&](int mb) {
     const int m0 = mb * kBlk;
     stage_load<T, D>(s0, Q + (int64_t)m0 * a.q.st, a.q.st, T_ - m0, D);
     stage_load<T, D>(s1, gQ + (int64_t)m0 * a.gq.st, a.gq.st, T_ - m0, D);
     stage_load<T, D>(s2, dO + (int64_t)m0 * a.dout.st, a.dout.st, T_ - m0, D);
     if constexpr (LOADP) stage_load<T, kBlk>(sp, Pb + (int64_t)m0 * a.p.st + n0, a.p.st, T_ - m0, T_ - n0);
+    stv = stat_load<kNS>(rs, ev, fv, lse, m0, T_ - m0);
   };
   load_tile(cr.t0);
   for (int mb = cr.t0; mb < cr.t1; ++mb) {
@@ -314,6 +318,7 @@ void k_gg_col(Params a) {
     stage_store_rows<T, D>(s1, sgQ);
     stage_store_rows<T, D>(s2, sdO);
     if constexpr (LOADP) stage_store_rows<T, kBlk>(sp, sP);
+    stat_store<kNS>(stv, sS);
     __syncthreads();
     if (mb + 1 < cr.t1) load_tile(mb + 1);
 
@@ -331,7 +336,7 @@ void k_gg_col(Params a) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         float l2[8];
-        load_vec8(l2, lse, m0 + stream_index(kb, g, 0), T_, stats_vec && m0 + kBlk <= T_);
+        stat_read8(l2, sS, 3, kb);
 #pragma unroll
         for (int j = 0; j < 8; ++j) p.set(kb, j, fast_exp2(p.at(kb, j) * a.scale_log2 - l2[j] * kLog2e));
       }
@@ -357,11 +362,9 @@ void k_gg_col(Params a) {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       float d8[8], e8[8], f8[8];
-      const int idx = m0 + stream_index(kb, g, 0);
-      const bool vf8 = stats_vec && m0 + kBlk <= T_;
-      load_vec8(d8, rs, idx, T_, vf8);
-      load_vec8(e8, ev, idx, T_, vf8);
-      load_vec8(f8, fv, idx, T_, vf8);
+      stat_read8(d8, sS, 0, kb);
+      stat_read8(e8, sS, 1, kb);
+      stat_read8(f8, sS, 2, kb);
       float vds[8], vgs[8], vgdp[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {

@@ -39,29 +39,6 @@ __device__ __forceinline__ float row_dot_do_o(const typename Elem<T>::frag* dof,
   return group_sum(acc);
 }
 
-// Raw P fragments of one key tile for this lane's query row: row pm, columns
-// n0 + 32kb + 8g .. +7; zero past T.
-template <typename T>
-__device__ __forceinline__ void load_p_frags(typename Elem<T>::frag* f, const T* pm, int n0, int T_, bool row_ok,
-                                             bool full = false) {
-  const int g = (threadIdx.x & 63) >> 4;
-  if (full) {  // every row and column of the tile is inside T (uniform)
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) f[kb] = load_frag<T>(pm + n0 + stream_index(kb, g, 0));
-    return;
-  }
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
-    const int n = n0 + stream_index(kb, g, 0);
-    if (row_ok && n + 8 <= T_) {
-      f[kb] = load_frag<T>(pm + n);
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) f[kb][j] = (row_ok && n + j < T_) ? pm[n + j] : Elem<T>::cvt(0.f);
-    }
-  }
-}
-
 template <typename T>
 __device__ __forceinline__ void frags_to_tile(Tile& p, const typename Elem<T>::frag* f) {
 #pragma unroll
@@ -121,8 +98,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dq(Params a) {
   frag pn[2];
   stage_load<T, D>(stK, K + (int64_t)cr.t0 * kBlk * a.k.st, a.k.st, T_ - cr.t0 * kBlk, D);
   stage_load<T, D>(stV, V + (int64_t)cr.t0 * kBlk * a.v.st, a.v.st, T_ - cr.t0 * kBlk, D);
-  const bool rows_full = mb * kBlk + kBlk <= T_;
-  if constexpr (LOADP) load_p_frags<T>(pn, Pm, cr.t0 * kBlk, T_, row_ok, rows_full && cr.t0 * kBlk + kBlk <= T_);
+  if constexpr (LOADP) load_p_frags<T>(pn, Pm, cr.t0 * kBlk, T_);
   for (int nb = cr.t0; nb < cr.t1; ++nb) {
     const int n0 = nb * kBlk;
     __syncthreads();
@@ -135,7 +111,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dq(Params a) {
       const int n1 = n0 + kBlk;
       stage_load<T, D>(stK, K + (int64_t)n1 * a.k.st, a.k.st, T_ - n1, D);
       stage_load<T, D>(stV, V + (int64_t)n1 * a.v.st, a.v.st, T_ - n1, D);
-      if constexpr (LOADP) load_p_frags<T>(pn, Pm, n1, T_, row_ok, rows_full && n1 + kBlk <= T_);
+      if constexpr (LOADP) load_p_frags<T>(pn, Pm, n1, T_);
     }
     if constexpr (!LOADP) {
       p.zero();
@@ -246,7 +222,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dkdv(Params a) {
     if constexpr (LOADP) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const frag f = load_frag_tr<T, LP::kRowPitch>(sP, 32 * kb, 16 * w);
+        const frag f = load_frag_tr<T, kBlk>(sP, 32 * kb, 16 * w);
 #pragma unroll
         for (int j = 0; j < 8; ++j) p.set(kb, j, E::f32(f[j]));
       }
@@ -336,9 +312,16 @@ __global__ __launch_bounds__(kThreads) void k_bwd_rowsum(Params a) {
     __syncthreads();
     if (nb + 1 < n_end) stage_load<T, D>(stV, V + (int64_t)(n0 + kBlk) * a.v.st, a.v.st, T_ - n0 - kBlk, D);
     frag pr[2];
-    load_p_frags<T>(pr, Pm, n0, T_, row_ok, mb * kBlk + kBlk <= T_ && n0 + kBlk <= T_);
+    load_p_frags<T>(pr, Pm, n0, T_);
     Tile p, dp;
     frags_to_tile<T>(p, pr);
+    if (n0 + kBlk > T_) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (n0 + stream_index(kb, g, j) >= T_) p.set(kb, j, 0.f);
+    }
     dp.zero();
     mm_d<T, D>(dp, sV, dof);
 #pragma unroll

@@ -20,7 +20,8 @@
 // statistics of the stationary row stay inside one lane plus two cross-lane
 // steps (xor 16, xor 32).
 //
-// Every streamed tile is staged once, row-major, in LDS.  Products that
+// Every streamed tile is staged once, row-major (16-byte chunks permuted per
+// row against bank conflicts, see Lds), in LDS.  Products that
 // contract over the head dim read 8-element row fragments (ds_read_b128);
 // products that contract over the streamed index read column fragments of the
 // same tile: ds_read_b64_tr_b16 for 16-bit types, eight 32-bit reads for fp32.
@@ -34,9 +35,16 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-// Unguarded staging loads for interior tiles (1) or guards on every tile (0).
-#ifndef TTT_STAGE_FAST
-#define TTT_STAGE_FAST 1
+// Tile products read all their LDS fragments before the first MFMA (1), or
+// leave the order to the compiler (0), which tends to pair each read with its
+// MFMA and expose every LDS latency.
+#ifndef TTT_MM_BATCH
+#define TTT_MM_BATCH 1
+#endif
+
+// Chunk-permuted (1) or padded (0) LDS rows for 16-bit types.
+#ifndef TTT_LDS_SWIZZLE
+#define TTT_LDS_SWIZZLE 1
 #endif
 
 namespace ttt {
@@ -262,14 +270,44 @@ __device__ __forceinline__ typename Elem<T>::frag vals_frag(const float* v) {
 }
 
 // ---------------------------------------------------------------------------
-// LDS tile geometry: 64 rows x NCOL, row pitch NCOL + one 16-byte chunk, which
-// keeps every 8-element row fragment 16-byte aligned.
+// LDS tile geometry: 64 rows x NCOL.
+//
+// 16-bit types: unpadded rows (pitch NCOL) whose 16-byte chunks are permuted
+// per row, chunk k of row r stored at chunk k ^ swz(r).  Measured on gfx950
+// (64 banks x 4 B): ds_read_b128 serves lanes {0-7,24-31}, {8-15,16-23},
+// {32-39,56-63}, {40-47,48-55} one set per cycle, and ds_read_b64(_tr_b16)
+// lanes {0-31}, {32-63}.  The MFMA row-fragment reads of mm_d (rows
+// sigma(a, c), chunk g + 4ks) and the transposed reads of load_frag_tr (rows
+// r0 + 8g + (c>>2), two chunks) are both conflict-free with
+//   128-byte rows: swz(r) = 2 * (r1 | r3 << 1)
+//   256-byte rows: swz(r) = 2 * (r0 | r1 << 1 | r3 << 2)      (ri = bit i of r)
+// (an unpadded, unswizzled tile costs 4x / 4x the conflict-free time, a
+// 16-byte row pad 2x / 2x).  swz(r) never depends on bit 2, so rows r and r+4
+// of a transposed read share it.
+// fp32 (and 16-bit types when TTT_LDS_SWIZZLE is 0): rows padded by one
+// 16-byte chunk, no permutation.
 // ---------------------------------------------------------------------------
 template <typename T, int NCOL>
 struct Lds {
   static constexpr int kChunk = Elem<T>::kChunk;
-  static constexpr int kRowPitch = NCOL + kChunk;
+  static constexpr bool kSwizzle = TTT_LDS_SWIZZLE && sizeof(T) == 2;
+  static constexpr int kChunksPerRow = NCOL / kChunk;
+  static_assert(!kSwizzle || kChunksPerRow == 8 || kChunksPerRow == 16, "swizzled rows are 128 or 256 bytes");
+  static constexpr int kRowPitch = kSwizzle ? NCOL : NCOL + kChunk;
   static constexpr int kRowElems = kBlk * kRowPitch;
+  static __device__ __forceinline__ int swz(int r) {
+    if constexpr (!kSwizzle) {
+      return 0;
+    } else if constexpr (kChunksPerRow == 8) {
+      return (((r >> 1) & 1) << 1) | (((r >> 3) & 1) << 2);
+    } else {
+      return ((r & 1) << 1) | (((r >> 1) & 1) << 2) | (((r >> 3) & 1) << 3);
+    }
+  }
+  // Element offset of (row r, column col); col % kChunk stays in its chunk.
+  static __device__ __forceinline__ int off(int r, int col) {
+    return r * kRowPitch + (((col / kChunk) ^ swz(r)) * kChunk) + col % kChunk;
+  }
 };
 
 // Staged registers of one 64 x NCOL tile: each thread owns pairs of
@@ -286,87 +324,86 @@ struct Stage {
 
 __device__ __forceinline__ u32x4 load16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 
-// Load a 64 x NCOL tile whose element [0][0] is at g (row stride ld).  Rows at
-// or beyond rows_valid and columns at or beyond cols_valid read as zero.
+// Load a 64 x NCOL tile whose element [0][0] is at g (row stride ld).
+// Every thread issues the same unconditional loads on every tile: rows at or
+// beyond rows_valid repeat row rows_valid-1 and 16-byte chunks starting at or
+// beyond cols_valid repeat chunk 0, and a chunk that straddles cols_valid is
+// read whole (row storage is padded to 16 bytes).  Those positions hold
+// finite copies or padding; every consumer replaces them by masking
+// (streamed index >= T) before they reach a product.  Two code paths here
+// would make the compiler wait for the previous tile's loads at their join.
 template <typename T, int NCOL>
 __device__ __forceinline__ void stage_load(Stage<T, NCOL>& st, const T* __restrict__ g, int64_t ld,
                                            int rows_valid, int cols_valid) {
   typedef Stage<T, NCOL> S;
   const int tid = threadIdx.x;
-  const int ch = tid % S::kChunksPerRow;
-  const int col = ch * S::kChunk;
-  if (TTT_STAGE_FAST && rows_valid >= kBlk && cols_valid >= NCOL) {  // interior tile (uniform): no guards
-#pragma unroll
-    for (int ps = 0; ps < S::kPasses; ++ps) {
-      const int r = 2 * (tid / S::kChunksPerRow + ps * S::kPairsPerPass);
-      st.x0[ps] = load16(g + (int64_t)r * ld + col);
-      st.x1[ps] = load16(g + (int64_t)(r + 1) * ld + col);
-    }
-    return;
-  }
+  const int c0 = (tid % S::kChunksPerRow) * S::kChunk;
+  const int col = c0 < cols_valid ? c0 : 0;
+  const int rmax = rows_valid - 1;
 #pragma unroll
   for (int ps = 0; ps < S::kPasses; ++ps) {
     const int r = 2 * (tid / S::kChunksPerRow + ps * S::kPairsPerPass);
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int row = r + h;
-      u32x4 x = u32x4{0u, 0u, 0u, 0u};
-      if (row < rows_valid) {
-        const T* src = g + (int64_t)row * ld + col;
-        if (col + S::kChunk <= cols_valid) {
-          x = load16(src);
-        } else {
-          T tmp[S::kChunk];
-#pragma unroll
-          for (int e = 0; e < S::kChunk; ++e) tmp[e] = (col + e < cols_valid) ? src[e] : Elem<T>::cvt(0.f);
-          __builtin_memcpy(&x, tmp, 16);
-        }
-      }
-      if (h == 0) st.x0[ps] = x; else st.x1[ps] = x;
-    }
+    st.x0[ps] = load16(g + (int64_t)min(r, rmax) * ld + col);
+    st.x1[ps] = load16(g + (int64_t)min(r + 1, rmax) * ld + col);
   }
 }
 
-// Write staged registers to a row-major LDS tile.
+// Raw P fragments of one streamed tile for this lane's stationary row: row pm,
+// columns n0 + 32kb + 8g .. +7.  Unconditional like stage_load: a fragment
+// starting at or beyond T reads column 0 instead, and callers mask columns
+// >= T (pm is a valid row even for rows beyond T).
+template <typename T>
+__device__ __forceinline__ void load_p_frags(typename Elem<T>::frag* f, const T* pm, int n0, int T_) {
+  const int g = (threadIdx.x & 63) >> 4;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    const int n = n0 + stream_index(kb, g, 0);
+    f[kb] = load_frag<T>(pm + (n < T_ ? n : 0));
+  }
+}
+
+// Write staged registers to an LDS tile (layout of Lds<T, NCOL>).
 template <typename T, int NCOL>
 __device__ __forceinline__ void stage_store_rows(const Stage<T, NCOL>& st, T* lds) {
   typedef Stage<T, NCOL> S;
-  constexpr int P = Lds<T, NCOL>::kRowPitch;
+  typedef Lds<T, NCOL> L;
   const int tid = threadIdx.x;
   const int col = (tid % S::kChunksPerRow) * S::kChunk;
 #pragma unroll
   for (int ps = 0; ps < S::kPasses; ++ps) {
     const int r = 2 * (tid / S::kChunksPerRow + ps * S::kPairsPerPass);
-    *reinterpret_cast<u32x4*>(lds + r * P + col) = st.x0[ps];
-    *reinterpret_cast<u32x4*>(lds + (r + 1) * P + col) = st.x1[ps];
+    *reinterpret_cast<u32x4*>(lds + L::off(r, col)) = st.x0[ps];
+    *reinterpret_cast<u32x4*>(lds + L::off(r + 1, col)) = st.x1[ps];
   }
 }
 
 // ---------------------------------------------------------------------------
-// Column fragment of a row-major LDS tile X (pitch P elements):
-//   f[j] = X[r0 + 8g + j][c0 + c],  j = 0..7,  lane (c, g).
+// Column fragment of an LDS tile X (layout Lds<T, NCOL>):
+//   f[j] = X[r0 + 8g + j][c0 + c],  j = 0..7,  lane (c, g);  r0 % 8 == 0, c0 % 16 == 0.
 // 16-bit types use ds_read_b64_tr_b16: within each 16-lane group, lane i gets
 // element i%4 of the 8-byte chunk read by lane 4j + i/4, so pointing lane i at
 // X[rb + i/4][c0 + 4(i%4)] delivers X[rb + j][c0 + i] for j = 0..3; two reads
-// (rb = r0+8g and r0+8g+4) give the eight rows.  fp32 gathers eight words.
+// (rb = r0+8g and r0+8g+4, which share swz) give the eight rows.  fp32
+// gathers eight words.
 // ---------------------------------------------------------------------------
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
-template <typename T, int P>
+template <typename T, int NCOL>
 __device__ __forceinline__ typename Elem<T>::frag load_frag_tr(const T* X, int r0, int c0) {
+  typedef Lds<T, NCOL> L;
   const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
   typename Elem<T>::frag f;
   if constexpr (sizeof(T) == 2) {
-    const T* a0 = X + (r0 + 8 * g + (c >> 2)) * P + c0 + 4 * (c & 3);
+    const T* a0 = X + L::off(r0 + 8 * g + (c >> 2), c0 + 4 * (c & 3));
     const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(a0));
-    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(a0 + 4 * P));
+    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(a0 + 4 * L::kRowPitch));
     i16x4 both[2] = {lo, hi};
     __builtin_memcpy(&f, both, 16);
   } else {
-    const T* a0 = X + (r0 + 8 * g) * P + c0 + c;
+    const T* a0 = X + L::off(r0 + 8 * g, c0 + c);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) f[j] = a0[j * P];
+    for (int j = 0; j < 8; ++j) f[j] = a0[j * L::kRowPitch];
   }
   return f;
 }
@@ -381,25 +418,48 @@ __device__ __forceinline__ typename Elem<T>::frag load_frag_tr(const T* X, int r
 //   y: per k-block B fragments built from a score tile;
 //   acc[dsub] holds d = 16*dsub + 4*g + i for this lane's stationary row.
 // ---------------------------------------------------------------------------
+// Both products issue their fragment reads in batches of eight (one k-half of
+// the streamed tile for mm_s, all of D = 64 for mm_d) ahead of the MFMAs that
+// consume them; the scheduling barrier keeps the compiler from sinking each
+// read next to its MFMA.
 template <typename T, int D>
 __device__ __forceinline__ void mm_d(Tile& out, const T* rows, const typename Elem<T>::frag* sta) {
-  constexpr int P = Lds<T, D>::kRowPitch;
+  typedef Lds<T, D> L;
+  typedef typename Elem<T>::frag frag;
   const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  constexpr int KS = D / 32;
+  constexpr int AB = (TTT_MM_BATCH && sizeof(T) == 2) ? (KS <= 2 ? 4 : 2) : 1;  // subtiles per batch
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    const T* rp = rows + sigma(a, c) * P + 8 * g;
+  for (int a0 = 0; a0 < 4; a0 += AB) {
+    frag x[AB][KS];
 #pragma unroll
-    for (int ks = 0; ks < D / 32; ++ks) out.q[a] = Elem<T>::mma(out.q[a], load_frag<T>(rp + 32 * ks), sta[ks]);
+    for (int a = 0; a < AB; ++a)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) x[a][ks] = load_frag<T>(rows + L::off(sigma(a0 + a, c), 32 * ks + 8 * g));
+    if constexpr (AB > 1) __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int a = 0; a < AB; ++a)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) out.q[a0 + a] = Elem<T>::mma(out.q[a0 + a], x[a][ks], sta[ks]);
   }
 }
 
 template <typename T, int D>
 __device__ __forceinline__ void mm_s(f32x4* acc, const T* X, const typename Elem<T>::frag* y) {
-  constexpr int P = Lds<T, D>::kRowPitch;
+  typedef typename Elem<T>::frag frag;
+  constexpr int NB = (TTT_MM_BATCH && sizeof(T) == 2) ? 8 : 1;  // fragments per batch
+  constexpr int DSN = D / 16;
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
+  for (int i0 = 0; i0 < 2 * DSN; i0 += NB) {
+    frag x[NB];
 #pragma unroll
-    for (int ds = 0; ds < D / 16; ++ds) acc[ds] = Elem<T>::mma(acc[ds], load_frag_tr<T, P>(X, 32 * kb, 16 * ds), y[kb]);
+    for (int i = 0; i < NB; ++i) x[i] = load_frag_tr<T, D>(X, 32 * ((i0 + i) / DSN), 16 * ((i0 + i) % DSN));
+    if constexpr (NB > 1) __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int kb = (i0 + i) / DSN, ds = (i0 + i) % DSN;
+      acc[ds] = Elem<T>::mma(acc[ds], x[i], y[kb]);
+    }
   }
 }
 

@@ -41,27 +41,6 @@
 
 namespace ttt {
 
-template <typename T>
-__device__ __forceinline__ void gg_load_p_frags(typename Elem<T>::frag* f, const T* pm, int n0, int T_, bool row_ok,
-                                                bool full) {
-  const int g = (threadIdx.x & 63) >> 4;
-  if (full) {  // every row and column of the tile is inside T (uniform)
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) f[kb] = load_frag<T>(pm + n0 + stream_index(kb, g, 0));
-    return;
-  }
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
-    const int n = n0 + stream_index(kb, g, 0);
-    if (row_ok && n + 8 <= T_) {
-      f[kb] = load_frag<T>(pm + n);
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) f[kb][j] = (row_ok && n + j < T_) ? pm[n + j] : Elem<T>::cvt(0.f);
-    }
-  }
-}
-
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool LOADP, bool GDO>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TTT_GG_WAVES_PER_EU)))
@@ -125,7 +104,7 @@ void k_gg_row(Params a) {
     stage_load<T, D>(s1, V + (int64_t)n0 * a.v.st, a.v.st, T_ - n0, D);
     stage_load<T, D>(s2, gK + (int64_t)n0 * a.gk.st, a.gk.st, T_ - n0, D);
     stage_load<T, D>(s3, gV + (int64_t)n0 * a.gv.st, a.gv.st, T_ - n0, D);
-    if constexpr (LOADP) gg_load_p_frags<T>(pn, Pm, n0, T_, row_ok, mb * kBlk + kBlk <= T_ && n0 + kBlk <= T_);
+    if constexpr (LOADP) load_p_frags<T>(pn, Pm, n0, T_);
   };
   load_tile(cr.t0);
   for (int nb = cr.t0; nb < cr.t1; ++nb) {
@@ -326,7 +305,7 @@ void k_gg_col(Params a) {
     if constexpr (LOADP) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const frag f = load_frag_tr<T, LP::kRowPitch>(sP, 32 * kb, 16 * w);
+        const frag f = load_frag_tr<T, kBlk>(sP, 32 * kb, 16 * w);
 #pragma unroll
         for (int j = 0; j < 8; ++j) p.set(kb, j, E::f32(f[j]));
       }

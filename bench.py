@@ -34,19 +34,65 @@ METRIC = "fwd+bwd+grad-grad ms at T=8k/16k d=64 fp16 causal; MFMA/HBM % of peak"
 REFERENCE_H100_MS = {"C3": 4.054, "C4_16k": 13.649}  # artifacts/gradgrad_sweep.csv (reduced grad-grad)
 
 
-def make_step(cfg: workloads.Config, x):
+def _two_stage_sum(t: torch.Tensor) -> torch.Tensor:
+    """Sum as 256 row sums then one 256-element sum: torch's single-output
+    reduction over a large tensor clears a semaphore buffer with a memset,
+    which must not be recorded into a HIP graph; this form launches two reduce
+    kernels and no memset.  Its gradient is the same all-ones broadcast."""
+    return t.reshape(256, -1).sum(1).sum()
+
+
+def make_step(cfg: workloads.Config, x, graph_safe: bool = False):
     q, k, v = (x[n].requires_grad_(True) for n in ("q", "k", "v"))
     do, rq, rk, rv = x["do"], x["rq"], x["rk"], x["rv"]
+    red = _two_stage_sum if graph_safe else torch.sum
 
     def step():
         o = triton_attention(q, k, v, causal=cfg.causal, bwd_mode=cfg.bwd_mode)
         dq, dk, dv = torch.autograd.grad(o, (q, k, v), do, create_graph=cfg.gradgrad)
         if not cfg.gradgrad:
-            return dq
-        s = (dq * rq).sum() + (dk * rk).sum() + (dv * rv).sum()
+            return (dq,)
+        s = red(dq * rq) + red(dk * rk) + red(dv * rv)
         return torch.autograd.grad(s, (q, k, v))
 
     return step
+
+
+def graph_steps(cfg: workloads.Config, x, steps: int, warmup: int, checks: int = 3) -> float:
+    """ms per step of the same step replayed from a HIP graph (captured once;
+    every replay reruns every kernel from the resident inputs).  Before timing,
+    `checks` replays, each followed by eager steps and a synchronisation, are
+    compared bitwise with the eager result; a mismatch raises."""
+    step = make_step(cfg, x, graph_safe=True)
+    side = torch.cuda.Stream()  # default priority
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    ref = [t.clone() for t in step()]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = step()
+    for i in range(checks):
+        graph.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(out, ref):
+            if not torch.equal(a, b):
+                raise RuntimeError(f"graph replay {i} differs from the eager step")
+        step()  # eager work between replays
+        torch.cuda.synchronize()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    del graph
+    return ms
 
 
 def time_steps(step, steps: int, warmup: int) -> float:
@@ -165,6 +211,7 @@ def main():
     ap.add_argument("--config", default="C3", choices=sorted(workloads.CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the T=16k point and forward-only metrics")
+    ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay of the step")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="also run a plain device copy of this many MiB (counter calibration for rocprof)")
     args = ap.parse_args()
@@ -186,6 +233,7 @@ def main():
     step = make_step(cfg, x)
     ms = time_steps(step, args.steps, args.warmup)
     ktimes = kernel_times(step)
+    graph_ms = graph_steps(cfg, x, args.steps, args.warmup) if not args.no_graph else None
     roof = workloads.roofline_us(cfg)
 
     out = {
@@ -209,6 +257,7 @@ def main():
         "tflops": round(roof["flops"] / (ms * 1e-3) / 1e12, 3),
         "step_roofline_us": round(roof["roofline_us"], 2),
         "step_roofline_frac": round(roof["roofline_us"] * 1e-3 / ms, 5),
+        "graph_ms_per_step": None if graph_ms is None else round(graph_ms, 4),
         "kernel_us": {k: round(v * 1e3, 2) for k, v in sorted(ktimes.items())},
         "kernel_sum_us": round(sum(ktimes.values()) * 1e3, 2),
         "roofline": roofline_entry(cfg, ktimes),

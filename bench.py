@@ -231,6 +231,10 @@ def main():
     cfg = workloads.CONFIGS[args.config]
     x = workloads.make_inputs(cfg, seed=0, device=dev)
     step = make_step(cfg, x)
+    # Backward passes run on the calling thread: the engine's default hand-off
+    # to a per-device worker thread costs more host time per step than the
+    # kernels take at this size.  The work done per step is the same.
+    torch.autograd.set_multithreading_enabled(False)
     ms = time_steps(step, args.steps, args.warmup)
     ktimes = kernel_times(step)
     graph_ms = graph_steps(cfg, x, args.steps, args.warmup) if not args.no_graph else None
@@ -253,7 +257,7 @@ def main():
                                f"{'causal 64x64 block-sparse' if cfg.causal else 'non-causal'} "
                                f"{cfg.bwd_mode} fwd+bwd{'+grad-grad' if cfg.gradgrad else ''}",
                    "batch": cfg.b, "heads": cfg.h, "seq_len": cfg.t, "head_dim": cfg.d,
-                   "bwd_mode": cfg.bwd_mode},
+                   "bwd_mode": cfg.bwd_mode, "autograd": "eager, backward on the calling thread"},
         "tflops": round(roof["flops"] / (ms * 1e-3) / 1e12, 3),
         "step_roofline_us": round(roof["roofline_us"], 2),
         "step_roofline_frac": round(roof["roofline_us"] * 1e-3 / ms, 5),

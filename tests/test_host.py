@@ -73,22 +73,72 @@ def test_validation_errors_without_gpu():
                                  None, 0, None) == 1
 
 
+def _slice_workgroups(n, c, causal):
+    """Workgroups of one (b,h) slice with chunks of c tiles, by brute force."""
+    return sum(-(-ln // c) for ln in (range(1, n + 1) if causal else [n] * n))
+
+
+def _simulated_chunk(nblk, causal, bh, slots, min_chunk=4):
+    """Independent restatement of the library's split chooser: list-schedule
+    the grid (x = block + nblk*chunk, y = b*h; heaviest block first) onto
+    `slots` workgroup slots spread round-robin over 8 XCDs, cost = makespan +
+    0.015 per non-empty workgroup, each non-empty workgroup taking its tiles
+    + 0.5 and an empty one 0.05."""
+    import heapq
+
+    def cost(c):
+        per = max(1, slots // 8)
+        heaps = [[0.0] * per for _ in range(8)]
+        end, used, idx = 0.0, 0, 0
+        k = -(-nblk // c)
+        for _ in range(bh):
+            for ch in range(k):
+                for b in range(nblk):
+                    ln = nblk - b if causal else nblk
+                    t = max(0, min(c, ln - ch * c))
+                    h = heaps[idx % 8]
+                    f = heapq.heappop(h) + (t + 0.5 if t else 0.05)
+                    heapq.heappush(h, f)
+                    end, used, idx = max(end, f), used + (t > 0), idx + 1
+        return end + 0.015 * used
+
+    if bh * nblk >= slots:
+        return nblk
+    best_c, best = nblk, cost(nblk)
+    c = min(min_chunk, nblk)
+    while c < nblk:
+        if bh * _slice_workgroups(nblk, c, causal) <= 16 * slots:
+            v = cost(c)
+            if v < best:
+                best_c, best = c, v
+        c = c + 1 if c < 64 else c + max(1, c // 32)
+    return best_c
+
+
 def test_workspace_sizes():
-    # C3: 128 blocks, 8256 active tiles.  Forward and grad-grad aim at 1024
-    # workgroups: chunk ceil(8256/1024) = 9 tiles -> 15 chunks; the first
-    # backward aims at 512: chunk 17 -> 8 chunks.  Forward partials = 1 acc x 64
-    # + 2 scalars per row.
-    c3 = _prob(seqlen=8192)
-    assert _lib.workspace_bytes(c3, _lib.ENTRY_FWD) == 128 * 15 * 64 * (64 + 2) * 4
-    assert _lib.workspace_bytes(c3, _lib.ENTRY_GG_ROW) == 128 * 15 * 64 * (4 * 64 + 3) * 4
-    assert _lib.workspace_bytes(c3, _lib.ENTRY_GG, True) == 128 * 15 * 64 * (7 * 64 + 3) * 4
-    assert _lib.workspace_bytes(c3, _lib.ENTRY_BWD) == 128 * 8 * 64 * (2 * 64) * 4
+    # Without a GPU the split assumes 256 CUs x 2 workgroups, 90% usable = 460
+    # slots.  Partial accumulators per chunk: nacc x 64 x D fp32 + nsc scalars
+    # per row (forward 1 acc + 2, dQ 1, dK/dV 2, GQ 4 + 3, GQ+GdO 7 + 3).
+    slots = 460
+    for (t, causal, bh) in [(8192, 1, 1), (16384, 1, 1), (8192, 0, 1), (4096, 1, 2), (2048, 1, 1)]:
+        nblk = t // 64
+        c = _simulated_chunk(nblk, bool(causal), bh, slots)
+        k = -(-nblk // c)
+        pr = _prob(seqlen=t, causal=causal, heads=bh)
+        parts = bh * nblk * k if k > 1 else 0
+        assert _lib.workspace_bytes(pr, _lib.ENTRY_FWD) == parts * 64 * (64 + 2) * 4, (t, causal, bh, c)
+        assert _lib.workspace_bytes(pr, _lib.ENTRY_GG_ROW) == parts * 64 * (4 * 64 + 3) * 4
+        assert _lib.workspace_bytes(pr, _lib.ENTRY_GG, True) == parts * 64 * (7 * 64 + 3) * 4
+        assert _lib.workspace_bytes(pr, _lib.ENTRY_BWD) == parts * 64 * (2 * 64) * 4
+    # C3: one round of 21-tile chunks (455 workgroups in the 460 slots; 20
+    # tiles would need 476 and spill into a second round)
+    assert _simulated_chunk(128, True, 1, slots) == 21 and _slice_workgroups(128, 21, True) == 455
+    assert _slice_workgroups(128, 20, True) == 476
     # C5 fills the chip with blocks alone: no split, no workspace
     c5 = _prob(batch=4, heads=16, seqlen=8192, head_dim=128, dtype=1)
     assert all(_lib.workspace_bytes(c5, e) == 0 for e in range(8))
-    # no chunk is shorter than 4 tiles: 4 blocks never split, 5 blocks split once
+    # no chunk is shorter than 4 tiles: 4 blocks never split; split_chunk forces a length
     assert _lib.workspace_bytes(_prob(seqlen=256), _lib.ENTRY_GG_COL) == 0
-    assert _lib.workspace_bytes(_prob(seqlen=300), _lib.ENTRY_GG_COL) == 5 * 2 * 64 * 128 * 4
     assert _lib.workspace_bytes(_prob(seqlen=300, split_chunk=2), _lib.ENTRY_GG_COL) == 5 * 3 * 64 * 128 * 4
     assert _lib.load().ttt_attn_workspace_size(ctypes.byref(_prob()), 99, 0) == -1
 

@@ -372,6 +372,26 @@ static hipError_t launch_rowsum_t(const Params& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <typename T, int D>
+static int occupancy_dq_t(bool load_p) {
+  return load_p ? occupancy_of(k_bwd_dq<T, D, true>) : occupancy_of(k_bwd_dq<T, D, false>);
+}
+
+template <typename T, int D>
+static int occupancy_dkdv_t(bool load_p) {
+  return load_p ? occupancy_of(k_bwd_dkdv<T, D, true, false>) : occupancy_of(k_bwd_dkdv<T, D, false, false>);
+}
+
+int occupancy_dq(int dtype, int D, bool load_p) {
+  DISPATCH_DTYPE_D(dtype, D, return occupancy_dq_t<ElemT, kD>(load_p));
+  return 0;
+}
+
+int occupancy_dkdv(int dtype, int D, bool load_p) {
+  DISPATCH_DTYPE_D(dtype, D, return occupancy_dkdv_t<ElemT, kD>(load_p));
+  return 0;
+}
+
 hipError_t launch_bwd_dq(int dtype, int D, const Params& a, bool load_p, hipStream_t st) {
   DISPATCH_DTYPE_D(dtype, D, return launch_dq_t<ElemT, kD>(dtype, a, load_p, st));
   return hipErrorInvalidValue;

@@ -6,10 +6,17 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <functional>
 #include <initializer_list>
+#include <map>
+#include <mutex>
+#include <queue>
+#include <tuple>
+#include <vector>
 
 #include "../../include/ttt_attn.h"
 #include "ttt_launch.h"
@@ -26,20 +33,26 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
-// Workgroups the split aims for, per kernel family, on an MI355X (256 CUs):
-// the light forward/backward kernels keep several workgroups resident per CU,
-// the register-heavy grad-grad kernels two.
-#ifndef TTT_TARGET_FWD
-#define TTT_TARGET_FWD 1024
+// The split of a streamed loop into chunks is chosen by simulating how the
+// hardware would run the launch: workgroups go to the XCDs round-robin in
+// launch order and, within an XCD, to whichever of its slots frees first.
+// The simulated makespan plus a small per-workgroup cost (partials, combine)
+// is minimised over the chunk length.  TTT_SLOT_FILL is the share (percent)
+// of the nominal slots (CUs x workgroups per CU from the occupancy
+// calculator) the simulation assumes usable.  The constants were fitted to
+// MI355X sweeps of every kernel family at T = 8192 and 16384, where they pick
+// the measured fastest chunk length.  Without a device (workspace queries on
+// a host with no GPU) the slots default to kFallbackCus x kFallbackPerCu.
+#ifndef TTT_SLOT_FILL
+#define TTT_SLOT_FILL 90
 #endif
-#ifndef TTT_TARGET_BWD
-#define TTT_TARGET_BWD 512
-#endif
-#ifndef TTT_TARGET_GG
-#define TTT_TARGET_GG 1024
-#endif
-constexpr int64_t kFamTarget[] = {TTT_TARGET_FWD, TTT_TARGET_FWD, TTT_TARGET_BWD, TTT_TARGET_BWD,
-                                  TTT_TARGET_GG, TTT_TARGET_GG, TTT_TARGET_GG};
+constexpr int kXcds = 8;
+constexpr double kWgOverheadTiles = 0.5;   // per workgroup, in tile times
+constexpr double kEmptyWgTiles = 0.05;     // a workgroup whose chunk is empty
+constexpr double kWgCostTiles = 0.015;     // per workgroup, added to the makespan
+constexpr int64_t kMaxSimWorkgroups = 16;  // x slots: larger grids are not considered
+constexpr int kFallbackCus = 256;
+constexpr int kFallbackPerCu = 2;
 // Chunks shorter than this are not worth a combine pass.
 constexpr int kMinChunk = 4;
 
@@ -86,22 +99,134 @@ struct Split {
   int nblk, chunk, nchunk_max;
 };
 
-// Tiles per workgroup: enough workgroups to fill the chip, no chunk shorter
-// than kMinChunk, no split at all when the blocks alone fill it.
-Split choose_split(const ttt_problem* pr, int fam) {
+// CUs of the current device (cached per device), or 0 without one.
+int device_cus(int* dev_out) {
+  static std::atomic<int> no_device{0};
+  static std::atomic<int> cus[16];
+  if (no_device.load(std::memory_order_relaxed)) return 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) {
+    (void)hipGetLastError();
+    no_device.store(1, std::memory_order_relaxed);
+    return 0;
+  }
+  *dev_out = dev;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+      (void)hipGetLastError();
+      no_device.store(1, std::memory_order_relaxed);
+      return 0;
+    }
+    cus[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// Workgroup slots of family `fam`'s kernel (variant load_p) on the current
+// device; cached per (device, family, dtype, head dim, variant).
+int64_t family_slots(const ttt_problem* pr, int fam, bool load_p) {
+  static std::atomic<int> per_cu[16][7][3][2][2];
+  int dev = 0;
+  const int cus = device_cus(&dev);
+  if (cus == 0) return (int64_t)kFallbackCus * kFallbackPerCu * TTT_SLOT_FILL / 100;
+  const int dt = pr->dtype, ds = pr->head_dim == 128 ? 1 : 0, lp = load_p ? 1 : 0;
+  int n = per_cu[dev][fam][dt][ds][lp].load(std::memory_order_relaxed);
+  if (n == 0) {
+    const int D = (int)pr->head_dim;
+    switch (fam) {
+      case ttt::kFamFwdOnline: n = ttt::occupancy_fwd(dt, D, false); break;
+      case ttt::kFamFwdP: n = ttt::occupancy_fwd(dt, D, true); break;
+      case ttt::kFamDq: n = ttt::occupancy_dq(dt, D, load_p); break;
+      case ttt::kFamDkdv: n = ttt::occupancy_dkdv(dt, D, load_p); break;
+      case ttt::kFamGgRow: n = ttt::occupancy_gg_row(dt, D, load_p, false); break;
+      case ttt::kFamGgRowGdo: n = ttt::occupancy_gg_row(dt, D, load_p, true); break;
+      default: n = ttt::occupancy_gg_col(dt, D, load_p); break;
+    }
+    if (n <= 0) n = kFallbackPerCu;
+    per_cu[dev][fam][dt][ds][lp].store(n, std::memory_order_relaxed);
+  }
+  return std::max<int64_t>(1, (int64_t)cus * n * TTT_SLOT_FILL / 100);
+}
+
+// Workgroups of one (b,h) slice when every block's streamed range is cut
+// into chunks of c tiles: blocks have 1..n tiles (causal) or n tiles each.
+int64_t slice_workgroups(int64_t n, int64_t c, bool causal) {
+  const int64_t k = (n + c - 1) / c;  // chunks of the longest block
+  return causal ? k * n - c * k * (k - 1) / 2 : k * n;
+}
+
+// Simulated makespan (tile times) of a launch: grid x = block + nblk*chunk,
+// y = (b,h); block i (launch order) has nblk - i tiles (causal, heaviest
+// first) or nblk; `slots` usable workgroup slots spread over kXcds XCDs.
+double simulate_launch(int64_t nblk, int64_t c, bool causal, int64_t bh, int64_t slots, int64_t* nonempty) {
+  const int64_t per = std::max<int64_t>(1, slots / kXcds);
+  std::vector<std::priority_queue<double, std::vector<double>, std::greater<double>>> xcd(kXcds);
+  for (auto& q : xcd)
+    for (int64_t i = 0; i < per; ++i) q.push(0.0);
+  const int64_t k = (nblk + c - 1) / c;
+  double end = 0.0;
+  int64_t idx = 0, used = 0;
+  for (int64_t y = 0; y < bh; ++y)
+    for (int64_t ch = 0; ch < k; ++ch)
+      for (int64_t b = 0; b < nblk; ++b, ++idx) {
+        const int64_t len = causal ? nblk - b : nblk;
+        const int64_t t = std::max<int64_t>(0, std::min(c, len - ch * c));
+        auto& q = xcd[idx % kXcds];
+        const double f = q.top() + (t > 0 ? (double)t + kWgOverheadTiles : kEmptyWgTiles);
+        q.pop();
+        q.push(f);
+        end = std::max(end, f);
+        used += t > 0;
+      }
+  *nonempty = used;
+  return end;
+}
+
+// Tiles per workgroup (see above).  No split when the blocks alone fill the
+// slots; chunks are at least kMinChunk tiles.  Cached per shape.
+int64_t best_chunk(int64_t nblk, bool causal, int64_t bh, int64_t slots) {
+  static std::mutex mu;
+  static std::map<std::tuple<int64_t, int, int64_t, int64_t>, int64_t> cache;
+  const auto key = std::make_tuple(nblk, causal ? 1 : 0, bh, slots);
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    const auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+  }
+  int64_t best_c = nblk;
+  double best = 0.0;
+  {
+    int64_t used = 0;
+    best = simulate_launch(nblk, nblk, causal, bh, slots, &used) + kWgCostTiles * used;
+  }
+  // candidates: every length up to 64 tiles, then steps of ~3%
+  for (int64_t c = std::min<int64_t>(kMinChunk, nblk); c < nblk; c = c < 64 ? c + 1 : c + std::max<int64_t>(1, c / 32)) {
+    if (bh * slice_workgroups(nblk, c, causal) > kMaxSimWorkgroups * slots) continue;
+    int64_t used = 0;
+    const double cost = simulate_launch(nblk, c, causal, bh, slots, &used) + kWgCostTiles * used;
+    if (cost < best) {
+      best = cost;
+      best_c = c;
+    }
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  cache[key] = best_c;
+  return best_c;
+}
+
+Split choose_split(const ttt_problem* pr, int fam, bool load_p) {
   Split s;
   s.nblk = (int)((pr->seqlen + ttt::kBlk - 1) / ttt::kBlk);
   const int64_t bh = pr->batch * pr->heads;
-  int c;
+  int64_t c;
   if (pr->split_chunk > 0) {
     c = pr->split_chunk;
   } else {
-    const int64_t tiles = pr->causal ? (int64_t)s.nblk * (s.nblk + 1) / 2 : (int64_t)s.nblk * s.nblk;
-    const int64_t total = bh * tiles;
-    const int64_t target = kFamTarget[fam];
-    c = (int)std::max<int64_t>(kMinChunk, (total + target - 1) / target);
+    const int64_t slots = family_slots(pr, fam, load_p);
+    c = bh * s.nblk >= slots ? s.nblk : best_chunk(s.nblk, pr->causal != 0, bh, slots);
   }
-  s.chunk = std::min(c, s.nblk);
+  s.chunk = (int)std::min<int64_t>(c, s.nblk);
   s.nchunk_max = (s.nblk + s.chunk - 1) / s.chunk;
   return s;
 }
@@ -125,7 +250,12 @@ int64_t family_bytes(const ttt_problem* pr, const Split& s, int fam) {
   return parts * ttt::kBlk * (ttt::kFamNacc[fam] * pr->head_dim + ttt::kFamNsc[fam]) * (int64_t)sizeof(float);
 }
 
-int64_t fam_bytes(const ttt_problem* pr, int fam) { return family_bytes(pr, choose_split(pr, fam), fam); }
+// Workspace of a family: the larger of its two variants' (with and without
+// P), since a workspace query does not say which one will run.
+int64_t fam_bytes(const ttt_problem* pr, int fam) {
+  return std::max(family_bytes(pr, choose_split(pr, fam, false), fam),
+                  family_bytes(pr, choose_split(pr, fam, true), fam));
+}
 
 int64_t entry_bytes(const ttt_problem* pr, int entry, bool gdo) {
   if (entry == TTT_ENTRY_BWD) return std::max(fam_bytes(pr, ttt::kFamDq), fam_bytes(pr, ttt::kFamDkdv));
@@ -148,8 +278,8 @@ ttt::Params base_params(const ttt_problem* pr) {
 }
 
 // Attach the split and the workspace for kernel family `fam`.
-int attach_split(const ttt_problem* pr, int fam, void* ws, int64_t ws_bytes, ttt::Params* a) {
-  const Split s = choose_split(pr, fam);
+int attach_split(const ttt_problem* pr, int fam, bool load_p, void* ws, int64_t ws_bytes, ttt::Params* a) {
+  const Split s = choose_split(pr, fam, load_p);
   a->chunk = s.chunk;
   a->nchunk_max = s.nchunk_max;
   const int64_t need = family_bytes(pr, s, fam);
@@ -216,7 +346,7 @@ int ttt_attn_fwd(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, co
   a.lse = lse;
   const bool wp = has_p(p);
   if (wp) TRY(take_view(pr, p, "p", &a.p));
-  TRY(attach_split(pr, wp ? ttt::kFamFwdP : ttt::kFamFwdOnline, workspace, workspace_bytes, &a));
+  TRY(attach_split(pr, wp ? ttt::kFamFwdP : ttt::kFamFwdOnline, wp, workspace, workspace_bytes, &a));
   return launched(ttt::launch_fwd(pr->dtype, (int)pr->head_dim, a, wp, (hipStream_t)stream), "ttt_attn_fwd");
 }
 
@@ -242,7 +372,7 @@ int ttt_attn_bwd_dq(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
   a.rowsum_in = rowsum_in;
   a.rowsum_out = rowsum_out;
   if (!rowsum_in) TRY(take_view(pr, o, "o (needed to form D without rowsum_in)", &a.o));
-  TRY(attach_split(pr, ttt::kFamDq, workspace, workspace_bytes, &a));
+  TRY(attach_split(pr, ttt::kFamDq, lp, workspace, workspace_bytes, &a));
   return launched(ttt::launch_bwd_dq(pr->dtype, (int)pr->head_dim, a, lp, (hipStream_t)stream),
                   "ttt_attn_bwd_dq");
 }
@@ -271,7 +401,7 @@ int ttt_attn_bwd_dkdv(const ttt_problem* pr, const ttt_view* q, const ttt_view* 
   TRY(check_stats({lse, rowsum}));
   a.lse = const_cast<float*>(lse);
   a.rowsum_in = rowsum;
-  TRY(attach_split(pr, ttt::kFamDkdv, workspace, workspace_bytes, &a));
+  TRY(attach_split(pr, ttt::kFamDkdv, lp, workspace, workspace_bytes, &a));
   return launched(ttt::launch_bwd_dkdv(pr->dtype, (int)pr->head_dim, a, lp, dv_only, (hipStream_t)stream),
                   "ttt_attn_bwd_dkdv");
 }
@@ -327,7 +457,7 @@ int ttt_attn_gg_row(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
   a.rowsum_in = rowsum;
   a.e = e_out;
   a.f = f_out;
-  TRY(attach_split(pr, gdo ? ttt::kFamGgRowGdo : ttt::kFamGgRow, workspace, workspace_bytes, &a));
+  TRY(attach_split(pr, gdo ? ttt::kFamGgRowGdo : ttt::kFamGgRow, lp, workspace, workspace_bytes, &a));
   return launched(ttt::launch_gg_row(pr->dtype, (int)pr->head_dim, a, lp, gdo, (hipStream_t)stream),
                   "ttt_attn_gg_row");
 }
@@ -357,7 +487,7 @@ int ttt_attn_gg_col(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
   a.rowsum_in = rowsum;
   a.e = const_cast<float*>(e_in);
   a.f = const_cast<float*>(f_in);
-  TRY(attach_split(pr, ttt::kFamGgCol, workspace, workspace_bytes, &a));
+  TRY(attach_split(pr, ttt::kFamGgCol, lp, workspace, workspace_bytes, &a));
   return launched(ttt::launch_gg_col(pr->dtype, (int)pr->head_dim, a, lp, (hipStream_t)stream),
                   "ttt_attn_gg_col");
 }

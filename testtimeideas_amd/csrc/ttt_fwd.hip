@@ -21,6 +21,8 @@
 //
 // Reference semantics: ttt_kernels/triton_attention.py:18-25 (math path),
 // :51-59 (P path), kernels :87-256.
+#include <algorithm>
+
 #include "ttt_common.h"
 #include "ttt_launch.h"
 
@@ -317,6 +319,17 @@ static hipError_t launch_fwd_t(int dtype, const Params& a, bool write_p, hipStre
     if (a.nchunk_max > 1) return launch_combine_fwd(dtype, D, a, st);
   }
   return hipGetLastError();
+}
+
+template <typename T, int D>
+static int occupancy_fwd_t(bool write_p) {
+  if (!write_p) return occupancy_of(k_fwd_online<T, D>);
+  return std::min(occupancy_of(k_fwd_stats<T, D>), occupancy_of(k_fwd_p<T, D>));
+}
+
+int occupancy_fwd(int dtype, int D, bool write_p) {
+  DISPATCH_DTYPE_D(dtype, D, return occupancy_fwd_t<ElemT, kD>(write_p));
+  return 0;
 }
 
 hipError_t launch_fwd(int dtype, int D, const Params& a, bool write_p, hipStream_t st) {

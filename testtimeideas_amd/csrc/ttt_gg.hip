@@ -406,6 +406,28 @@ static hipError_t launch_gg_col_t(int dtype, const Params& a, bool load_p, hipSt
   return hipGetLastError();
 }
 
+template <typename T, int D>
+static int occupancy_gg_row_t(bool load_p, bool gdo) {
+  if (load_p)
+    return gdo ? occupancy_of(k_gg_row<T, D, true, true>) : occupancy_of(k_gg_row<T, D, true, false>);
+  return gdo ? occupancy_of(k_gg_row<T, D, false, true>) : occupancy_of(k_gg_row<T, D, false, false>);
+}
+
+template <typename T, int D>
+static int occupancy_gg_col_t(bool load_p) {
+  return load_p ? occupancy_of(k_gg_col<T, D, true>) : occupancy_of(k_gg_col<T, D, false>);
+}
+
+int occupancy_gg_row(int dtype, int D, bool load_p, bool gdo) {
+  DISPATCH_DTYPE_D(dtype, D, return occupancy_gg_row_t<ElemT, kD>(load_p, gdo));
+  return 0;
+}
+
+int occupancy_gg_col(int dtype, int D, bool load_p) {
+  DISPATCH_DTYPE_D(dtype, D, return occupancy_gg_col_t<ElemT, kD>(load_p));
+  return 0;
+}
+
 hipError_t launch_gg_row(int dtype, int D, const Params& a, bool load_p, bool want_gdout, hipStream_t st) {
   DISPATCH_DTYPE_D(dtype, D, return launch_gg_row_t<ElemT, kD>(dtype, a, load_p, want_gdout, st));
   return hipErrorInvalidValue;

@@ -38,6 +38,27 @@ enum : int { kFamFwdOnline = 0, kFamFwdP = 1, kFamDq = 2, kFamDkdv = 3, kFamGgRo
 constexpr int kFamNacc[] = {1, 1, 1, 2, 4, 7, 2};
 constexpr int kFamNsc[] = {2, 2, 0, 0, 3, 3, 0};
 
+// Workgroups of a kernel that one CU holds at once (HIP occupancy calculator
+// on the current device); 0 when it cannot be queried.
+template <typename K>
+inline int occupancy_of(K kernel) {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(kernel), kThreads, 0) !=
+      hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return n;
+}
+
+// Occupancy of the kernels a launch of each family runs (the smaller one when
+// it runs two).
+int occupancy_fwd(int dtype, int D, bool write_p);
+int occupancy_dq(int dtype, int D, bool load_p);
+int occupancy_dkdv(int dtype, int D, bool load_p);
+int occupancy_gg_row(int dtype, int D, bool load_p, bool gdo);
+int occupancy_gg_col(int dtype, int D, bool load_p);
+
 hipError_t launch_fwd(int dtype, int D, const Params& a, bool write_p, hipStream_t st);
 hipError_t launch_combine_sum(int dtype, int D, const Params& a, int which, hipStream_t st);
 hipError_t launch_combine_fwd(int dtype, int D, const Params& a, hipStream_t st);

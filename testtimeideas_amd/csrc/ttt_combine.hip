@@ -9,8 +9,8 @@
 //
 // A block's 64 x D outputs are covered by D/16 workgroups; thread t of
 // workgroup `sub` owns one 4-wide slot: slot = 256*sub + t, row slot/(D/4),
-// columns 4*(slot % (D/4)) .. +3.  Loads of all accumulators of a chunk are
-// issued together and the chunk loop is unrolled; the sums still run in chunk
+// columns 4*(slot % (D/4)) .. +3.  A thread issues the loads of all
+// accumulators of up to kBatch chunks together; the sums still run in chunk
 // order.
 #include "ttt_common.h"
 #include "ttt_launch.h"
@@ -35,6 +35,12 @@ __device__ __forceinline__ int block_nch(const Params& a, int blk, int nblk, boo
   return (hi - lo + a.chunk - 1) / a.chunk;
 }
 
+// Chunks whose loads a thread issues together before adding them.  The
+// loads of a batch are unconditional (chunk indices past nch-1 repeat the
+// last chunk) so that none waits for another; the adds still run in chunk
+// order 0, 1, ..., nch-1.
+constexpr int kBatch = 8;
+
 // out[i] = sum over chunks k (in order) of accumulator a0 + i at (r, d0..d0+3).
 template <int D, int NA>
 __device__ __forceinline__ void sum_parts(f32x4* out, const float* ws, int64_t p0, int nch, int nacc, int a0,
@@ -43,13 +49,42 @@ __device__ __forceinline__ void sum_parts(f32x4* out, const float* ws, int64_t p
   for (int i = 0; i < NA; ++i) out[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   const float* base = ws + (p0 * nacc + a0) * kBlk * D + r * D + d0;
   const int64_t step = (int64_t)nacc * kBlk * D;
-#pragma unroll 4
-  for (int k = 0; k < nch; ++k) {
-    f32x4 x[NA];
+  for (int k0 = 0; k0 < nch; k0 += kBatch) {
+    f32x4 x[kBatch][NA];
 #pragma unroll
-    for (int i = 0; i < NA; ++i) x[i] = *reinterpret_cast<const f32x4*>(base + k * step + i * kBlk * D);
+    for (int u = 0; u < kBatch; ++u) {
+      const int k = min(k0 + u, nch - 1);
 #pragma unroll
-    for (int i = 0; i < NA; ++i) out[i] += x[i];
+      for (int i = 0; i < NA; ++i) x[u][i] = *reinterpret_cast<const f32x4*>(base + k * step + i * kBlk * D);
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      if (k0 + u < nch) {
+#pragma unroll
+        for (int i = 0; i < NA; ++i) out[i] += x[u][i];
+      }
+  }
+}
+
+// s[j] = sum over chunks k (in order) of row scalar j (of NS) at row r.
+template <int NS>
+__device__ __forceinline__ void sum_scalars(float* s, const float* ws_sc, int64_t p0, int nch, int r) {
+#pragma unroll
+  for (int j = 0; j < NS; ++j) s[j] = 0.f;
+  for (int k0 = 0; k0 < nch; k0 += kBatch) {
+    float x[kBatch][NS];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int k = min(k0 + u, nch - 1);
+#pragma unroll
+      for (int j = 0; j < NS; ++j) x[u][j] = ws_sc[(p0 + k) * NS * kBlk + j * kBlk + r];
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      if (k0 + u < nch) {
+#pragma unroll
+        for (int j = 0; j < NS; ++j) s[j] += x[u][j];
+      }
   }
 }
 
@@ -110,14 +145,32 @@ __global__ __launch_bounds__(kThreads) void k_combine_fwd(Params a) {
   if (row >= T_) return;
   const int64_t p0 = part_index(a, bh, nblk, cs.blk, 0);
   float mm = -INFINITY;
-  for (int k = 0; k < nch; ++k) mm = fmaxf(mm, a.ws_sc[(p0 + k) * 2 * kBlk + r]);
+  for (int k0 = 0; k0 < nch; k0 += kBatch) {
+    float x[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) x[u] = a.ws_sc[(p0 + min(k0 + u, nch - 1)) * 2 * kBlk + r];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) mm = fmaxf(mm, x[u]);  // repeats of the last chunk leave the max
+  }
   float ll = 0.f;
   f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-  for (int k = 0; k < nch; ++k) {
-    const float wk = fast_exp2(a.ws_sc[(p0 + k) * 2 * kBlk + r] - mm);
-    ll += a.ws_sc[(p0 + k) * 2 * kBlk + kBlk + r] * wk;
-    v += wk * *reinterpret_cast<const f32x4*>(a.ws_acc + (p0 + k) * kBlk * D + r * D + cs.d0);
+  for (int k0 = 0; k0 < nch; k0 += kBatch) {
+    float mk[kBatch], lk[kBatch];
+    f32x4 xk[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int64_t k = p0 + min(k0 + u, nch - 1);
+      mk[u] = a.ws_sc[k * 2 * kBlk + r];
+      lk[u] = a.ws_sc[k * 2 * kBlk + kBlk + r];
+      xk[u] = *reinterpret_cast<const f32x4*>(a.ws_acc + k * kBlk * D + r * D + cs.d0);
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      if (k0 + u < nch) {
+        const float wk = fast_exp2(mk[u] - mm);
+        ll += lk[u] * wk;
+        v += wk * xk[u];
+      }
   }
   store_slot<T>(a.o, b, h, row, cs.d0, v * (1.f / ll));
   if (cs.d0 == 0) a.lse[(int64_t)bh * T_ + row] = (mm + __log2f(ll)) * kLn2;
@@ -140,13 +193,9 @@ __global__ __launch_bounds__(kThreads) void k_combine_gg_row(Params a) {
   const int row = cs.blk * kBlk + r;
   if (row >= T_) return;
   const int64_t p0 = part_index(a, bh, nblk, cs.blk, 0);
-  float ev = 0.f, xv = 0.f, dv = 0.f;
-  for (int k = 0; k < nch; ++k) {
-    const float* sc = a.ws_sc + (p0 + k) * 3 * kBlk + r;
-    ev += sc[0];
-    xv += sc[kBlk];
-    dv += sc[2 * kBlk];
-  }
+  float sc[3];
+  sum_scalars<3>(sc, a.ws_sc, p0, nch, r);
+  const float ev = sc[0], xv = sc[1], dv = sc[2];
   const float fv = xv - ev * dv;
   f32x4 t[4];
   sum_parts<D, 4>(t, a.ws_acc, p0, nch, NACC, 0, r, cs.d0);

@@ -463,6 +463,41 @@ __device__ __forceinline__ void mm_s(f32x4* acc, const T* X, const typename Elem
   }
 }
 
+// Half-tile products for kernels that walk a streamed tile in its two 32-row
+// halves (kb = 0, 1; compile-time after unrolling): mm_d_half forms subtiles
+// a = 2kb, 2kb+1 of mm_d's output, mm_s_half adds k-block kb of mm_s.  Work on
+// one half does not depend on the other, so the second half's products can
+// run while the first half's elementwise work does.
+template <typename T, int D>
+__device__ __forceinline__ void mm_d_half(Tile& out, int kb, const T* rows, const typename Elem<T>::frag* sta) {
+  typedef Lds<T, D> L;
+  typedef typename Elem<T>::frag frag;
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  constexpr int KS = D / 32;
+  frag x[2][KS];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) x[a][ks] = load_frag<T>(rows + L::off(sigma(2 * kb + a, c), 32 * ks + 8 * g));
+  if constexpr (TTT_MM_BATCH && sizeof(T) == 2) __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) out.q[2 * kb + a] = Elem<T>::mma(out.q[2 * kb + a], x[a][ks], sta[ks]);
+}
+
+template <typename T, int D>
+__device__ __forceinline__ void mm_s_half(f32x4* acc, int kb, const T* X, typename Elem<T>::frag y) {
+  typedef typename Elem<T>::frag frag;
+  constexpr int DSN = D / 16;
+  frag x[DSN];
+#pragma unroll
+  for (int ds = 0; ds < DSN; ++ds) x[ds] = load_frag_tr<T, D>(X, 32 * kb, 16 * ds);
+  if constexpr (TTT_MM_BATCH && sizeof(T) == 2) __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int ds = 0; ds < DSN; ++ds) acc[ds] = Elem<T>::mma(acc[ds], x[ds], y);
+}
+
 // Reductions over the four lane groups (same c), with the gfx950 VALU lane
 // swaps: permlane16_swap(x, x) returns, in each lane, the pair {x[l], x[l^16]}
 // (order depending on the lane's 16-lane row); permlane32_swap does the same
@@ -534,6 +569,81 @@ __device__ __forceinline__ void stat_read8(float* v, const float* lds, int st, i
 #pragma unroll
   for (int j = 0; j < 4; ++j) { v[j] = a[j]; v[4 + j] = b[j]; }
 }
+
+// ---------------------------------------------------------------------------
+// Direct global -> LDS staging (16-bit types).  global_load_lds_dwordx4 writes
+// lane i's 16 bytes to LDS at (wave's base) + 16 i, so one wave instruction
+// fills 1 KiB of a tile linearly; pinned on the GPU with an in-bounds probe.
+// A lane therefore fetches the logical (row, chunk) stored at its LDS bytes:
+// row = byte / row_bytes, chunk = (byte % row_bytes) / 16 ^ swz(row).  Wave w
+// issues the tile's instructions w, w + 4, ...  The loads bypass registers and
+// complete on vmcnt; readers wait for them (dma_wait) and meet at a barrier.
+// As with stage_load, rows at or beyond rows_valid and chunks at or beyond
+// cols_valid read from row 0 / chunk 0 (finite data that consumers mask).
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+template <typename T, int NCOL>
+struct TileDma {  // for the unpadded (chunk-permuted) layout only: Lds<T, NCOL>::kSwizzle
+  typedef Lds<T, NCOL> L;
+  static constexpr int kRowBytes = NCOL * (int)sizeof(T);
+  static constexpr int kInstr = kBlk * kRowBytes / 1024;  // wave instructions per tile
+  static constexpr int kPerWave = kInstr / 4;
+  static_assert(kPerWave * 4 == kInstr, "tile shape");
+  int row[kPerWave], col[kPerWave];  // this lane's logical row and first column per instruction
+  __device__ __forceinline__ TileDma() {
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int q = 0; q < kPerWave; ++q) {
+      const int byte = 1024 * (w + 4 * q) + 16 * lane;
+      const int r = byte / kRowBytes;
+      row[q] = r;
+      col[q] = (((byte % kRowBytes) / 16) ^ L::swz(r)) * L::kChunk;
+    }
+  }
+  // Element offsets (row stride ld) of this lane's fetches for an interior tile.
+  __device__ __forceinline__ void offsets(int* off, int64_t ld) const {
+#pragma unroll
+    for (int q = 0; q < kPerWave; ++q) off[q] = (int)((int64_t)row[q] * ld + col[q]);
+  }
+  // Issue the loads of the tile at g into lds.  `off` from offsets(); ragged
+  // tiles (uniform) recompute them with row/column clamping.
+  __device__ __forceinline__ void load(T* lds, const T* g, const int* off, int64_t ld, int rows_valid,
+                                       int cols_valid) const {
+    const int w = threadIdx.x >> 6;
+    const bool ragged = rows_valid < kBlk || cols_valid < NCOL;
+#pragma unroll
+    for (int q = 0; q < kPerWave; ++q) {
+      int o = off[q];
+      if (ragged) {
+        const int r = row[q] < rows_valid ? row[q] : 0;
+        const int c = col[q] < cols_valid ? col[q] : 0;
+        o = (int)((int64_t)r * ld + c);
+      }
+#if defined(__HIP_DEVICE_COMPILE__)  // the builtin exists only for the gfx950 target
+      __builtin_amdgcn_global_load_lds(g + o, (lds_void_t*)(reinterpret_cast<char*>(lds) + 1024 * (w + 4 * q)),
+                                       16, 0, 0);
+#endif
+    }
+  }
+};
+
+// Row statistics through the 4-byte form: wave w < NS fetches statistic w of
+// the tile's rows into lds[w][0..63] (rows at or beyond rows_valid read row 0).
+template <int NS>
+__device__ __forceinline__ void stat_dma(float* lds, const float* s0, const float* s1, const float* s2,
+                                         const float* s3, int m0, int rows_valid) {
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (w >= NS) return;
+  const float* src = w == 0 ? s0 : w == 1 ? s1 : w == 2 ? s2 : s3;
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(src + m0 + (lane < rows_valid ? lane : 0), (lds_void_t*)(lds + kBlk * w), 4,
+                                   0, 0);
+#endif
+}
+
+// Wait for this wave's direct loads (then meet the other waves at a barrier).
+__device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // Eight consecutive fp32 values v[0..7] = src[idx0 .. idx0+7], zero past n.
 // `fast` (uniform) asserts idx0 + 8 <= n and a 16-byte aligned src + idx0.

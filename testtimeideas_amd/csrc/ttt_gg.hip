@@ -38,6 +38,9 @@
 #ifndef TTT_GG_WAVES_PER_EU
 #define TTT_GG_WAVES_PER_EU 2
 #endif
+#ifndef TTT_GG_COL_WAVES_PER_EU
+#define TTT_GG_COL_WAVES_PER_EU TTT_GG_WAVES_PER_EU
+#endif
 
 namespace ttt {
 
@@ -226,19 +229,23 @@ void k_gg_row(Params a) {
 
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool LOADP>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TTT_GG_WAVES_PER_EU)))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TTT_GG_COL_WAVES_PER_EU)))
 void k_gg_col(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
   typedef Lds<T, kBlk> LP;
-  __shared__ __align__(16) T sQ[L::kRowElems];
-  __shared__ __align__(16) T sgQ[L::kRowElems];
-  __shared__ __align__(16) T sdO[L::kRowElems];
-  __shared__ __align__(16) T sP[LOADP ? LP::kRowElems : 8];
+  // 16-bit types stream tiles straight into two LDS buffers (TileDma); fp32
+  // stages them through registers into one.
+  constexpr bool kDma = L::kSwizzle && D == 64;  // at D = 128 two buffers would halve the occupancy
+  constexpr int kBuf = kDma ? 2 : 1;
+  __shared__ __align__(16) T sQ[kBuf][L::kRowElems];
+  __shared__ __align__(16) T sgQ[kBuf][L::kRowElems];
+  __shared__ __align__(16) T sdO[kBuf][L::kRowElems];
+  __shared__ __align__(16) T sP[kBuf][LOADP ? LP::kRowElems : 8];
   // Staged row statistics of the streamed tile: D, E, F, then lse (recompute).
   constexpr int kNS = LOADP ? 3 : 4;
-  __shared__ __align__(16) float sS[kNS * kBlk];
+  __shared__ __align__(16) float sS[kBuf][kNS * kBlk];
 
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
@@ -278,7 +285,7 @@ void k_gg_col(Params a) {
 #pragma unroll
   for (int i = 0; i < D / 16; ++i) acc_gk[i] = acc_gv[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  Stage<T, D> s0, s1, s2;
+  Stage<T, D> s0, s1, s2;  // register staging (fp32 only)
   Stage<T, kBlk> sp;
   float stv;
   auto load_tile = [&](int mb) {
@@ -289,33 +296,68 @@ void k_gg_col(Params a) {
     if constexpr (LOADP) stage_load<T, kBlk>(sp, Pb + (int64_t)m0 * a.p.st + n0, a.p.st, T_ - m0, T_ - n0);
     stv = stat_load<kNS>(rs, ev, fv, lse, m0, T_ - m0);
   };
-  load_tile(cr.t0);
+  // Direct path: per-lane fetch offsets of an interior tile, computed once.
+  TileDma<T, D> dd;
+  TileDma<T, kBlk> dp_;
+  int oQ[TileDma<T, D>::kPerWave], ogQ[TileDma<T, D>::kPerWave], odO[TileDma<T, D>::kPerWave];
+  int oP[TileDma<T, kBlk>::kPerWave];
+  auto dma_tile = [&](int mb, int buf) {
+    if constexpr (kDma) {
+      const int m0 = mb * kBlk;
+      dd.load(sQ[buf], Q + (int64_t)m0 * a.q.st, oQ, a.q.st, T_ - m0, D);
+      dd.load(sgQ[buf], gQ + (int64_t)m0 * a.gq.st, ogQ, a.gq.st, T_ - m0, D);
+      dd.load(sdO[buf], dO + (int64_t)m0 * a.dout.st, odO, a.dout.st, T_ - m0, D);
+      if constexpr (LOADP) dp_.load(sP[buf], Pb + (int64_t)m0 * a.p.st + n0, oP, a.p.st, T_ - m0, T_ - n0);
+      stat_dma<kNS>(sS[buf], rs, ev, fv, lse, m0, T_ - m0);
+    }
+  };
+  if constexpr (kDma) {
+    dd.offsets(oQ, a.q.st);
+    dd.offsets(ogQ, a.gq.st);
+    dd.offsets(odO, a.dout.st);
+    if constexpr (LOADP) dp_.offsets(oP, a.p.st);
+    dma_tile(cr.t0, 0);
+  } else {
+    load_tile(cr.t0);
+  }
   for (int mb = cr.t0; mb < cr.t1; ++mb) {
     const int m0 = mb * kBlk;
-    __syncthreads();
-    stage_store_rows<T, D>(s0, sQ);
-    stage_store_rows<T, D>(s1, sgQ);
-    stage_store_rows<T, D>(s2, sdO);
-    if constexpr (LOADP) stage_store_rows<T, kBlk>(sp, sP);
-    stat_store<kNS>(stv, sS);
-    __syncthreads();
-    if (mb + 1 < cr.t1) load_tile(mb + 1);
+    const int cur = kDma ? ((mb - cr.t0) & 1) : 0;
+    if constexpr (kDma) {
+      dma_wait();  // this wave's loads of tile mb
+      __syncthreads();  // everyone's, and everyone is done with the other buffer
+      if (mb + 1 < cr.t1) dma_tile(mb + 1, cur ^ 1);
+    } else {
+      __syncthreads();
+      stage_store_rows<T, D>(s0, sQ[0]);
+      stage_store_rows<T, D>(s1, sgQ[0]);
+      stage_store_rows<T, D>(s2, sdO[0]);
+      if constexpr (LOADP) stage_store_rows<T, kBlk>(sp, sP[0]);
+      stat_store<kNS>(stv, sS[0]);
+      __syncthreads();
+      if (mb + 1 < cr.t1) load_tile(mb + 1);
+    }
+    const T* cQ = sQ[cur];
+    const T* cgQ = sgQ[cur];
+    const T* cdO = sdO[cur];
+    const T* cP = sP[cur];
+    const float* cS = sS[cur];
 
     Tile p, dp, gds, gp1;
     if constexpr (LOADP) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const frag f = load_frag_tr<T, kBlk>(sP, 32 * kb, 16 * w);
+        const frag f = load_frag_tr<T, kBlk>(cP, 32 * kb, 16 * w);
 #pragma unroll
         for (int j = 0; j < 8; ++j) p.set(kb, j, E::f32(f[j]));
       }
     } else {
       p.zero();
-      mm_d<T, D>(p, sQ, kf);
+      mm_d<T, D>(p, cQ, kf);
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         float l2[8];
-        stat_read8(l2, sS, 3, kb);
+        stat_read8(l2, cS, 3, kb);
 #pragma unroll
         for (int j = 0; j < 8; ++j) p.set(kb, j, fast_exp2(p.at(kb, j) * a.scale_log2 - l2[j] * kLog2e));
       }
@@ -332,18 +374,18 @@ void k_gg_col(Params a) {
     dp.zero();
     gds.zero();
     gp1.zero();
-    mm_d<T, D>(dp, sdO, vf);
-    mm_d<T, D>(gds, sgQ, kf);
-    mm_d<T, D>(gds, sQ, gkf);
-    mm_d<T, D>(gp1, sdO, gvf);
-
-    frag dsf[2], gsf[2], gdpf[2];
+    // The streamed tile in two halves: products over d for half kb, its
+    // elementwise terms, then its contributions to GK and GV.
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
+      mm_d_half<T, D>(dp, kb, cdO, vf);
+      mm_d_half<T, D>(gds, kb, cgQ, kf);
+      mm_d_half<T, D>(gds, kb, cQ, gkf);
+      mm_d_half<T, D>(gp1, kb, cdO, gvf);
       float d8[8], e8[8], f8[8];
-      stat_read8(d8, sS, 0, kb);
-      stat_read8(e8, sS, 1, kb);
-      stat_read8(f8, sS, 2, kb);
+      stat_read8(d8, cS, 0, kb);
+      stat_read8(e8, cS, 1, kb);
+      stat_read8(f8, cS, 2, kb);
       float vds[8], vgs[8], vgdp[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -356,13 +398,10 @@ void k_gg_col(Params a) {
         vgdp[j] = P * (gd - e8[j]);
         vgs[j] = P * (gp - f8[j]);
       }
-      dsf[kb] = vals_frag<T>(vds);
-      gsf[kb] = vals_frag<T>(vgs);
-      gdpf[kb] = vals_frag<T>(vgdp);
+      mm_s_half<T, D>(acc_gk, kb, cgQ, vals_frag<T>(vds));
+      mm_s_half<T, D>(acc_gk, kb, cQ, vals_frag<T>(vgs));
+      mm_s_half<T, D>(acc_gv, kb, cdO, vals_frag<T>(vgdp));
     }
-    mm_s<T, D>(acc_gk, sgQ, dsf);
-    mm_s<T, D>(acc_gk, sQ, gsf);
-    mm_s<T, D>(acc_gv, sdO, gdpf);
   }
   if (cr.nch == 1) {
     store_acc_rows<T, D>(at<T>(a.gk_out, b, h), a.gk_out.st, n, T_, acc_gk, s);

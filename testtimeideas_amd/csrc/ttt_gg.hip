@@ -52,10 +52,14 @@ void k_gg_row(Params a) {
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
   constexpr int NACC = GDO ? 7 : 4;
-  __shared__ __align__(16) T sK[L::kRowElems];
-  __shared__ __align__(16) T sV[L::kRowElems];
-  __shared__ __align__(16) T sgK[L::kRowElems];
-  __shared__ __align__(16) T sgV[L::kRowElems];
+  // 16-bit types at D = 64 stream tiles straight into two LDS buffers
+  // (TileDma); the rest stage them through registers into one.
+  constexpr bool kDma = L::kSwizzle && D == 64;
+  constexpr int kBuf = kDma ? 2 : 1;
+  __shared__ __align__(16) T sK[kBuf][L::kRowElems];
+  __shared__ __align__(16) T sV[kBuf][L::kRowElems];
+  __shared__ __align__(16) T sgK[kBuf][L::kRowElems];
+  __shared__ __align__(16) T sgV[kBuf][L::kRowElems];
 
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
@@ -99,7 +103,7 @@ void k_gg_row(Params a) {
   }
   float e_acc = 0.f, x_acc = 0.f, d_acc = 0.f;
 
-  Stage<T, D> s0, s1, s2, s3;
+  Stage<T, D> s0, s1, s2, s3;  // register staging (not kDma)
   frag pn[2];
   auto load_tile = [&](int nb) {
     const int n0 = nb * kBlk;
@@ -109,15 +113,46 @@ void k_gg_row(Params a) {
     stage_load<T, D>(s3, gV + (int64_t)n0 * a.gv.st, a.gv.st, T_ - n0, D);
     if constexpr (LOADP) load_p_frags<T>(pn, Pm, n0, T_);
   };
-  load_tile(cr.t0);
+  TileDma<T, D> dd;
+  int oK[TileDma<T, D>::kPerWave], oV[TileDma<T, D>::kPerWave];
+  int ogK[TileDma<T, D>::kPerWave], ogV[TileDma<T, D>::kPerWave];
+  auto dma_tile = [&](int nb, int buf) {
+    if constexpr (kDma) {
+      const int n0 = nb * kBlk;
+      dd.load(sK[buf], K + (int64_t)n0 * a.k.st, oK, a.k.st, T_ - n0, D);
+      dd.load(sV[buf], V + (int64_t)n0 * a.v.st, oV, a.v.st, T_ - n0, D);
+      dd.load(sgK[buf], gK + (int64_t)n0 * a.gk.st, ogK, a.gk.st, T_ - n0, D);
+      dd.load(sgV[buf], gV + (int64_t)n0 * a.gv.st, ogV, a.gv.st, T_ - n0, D);
+      if constexpr (LOADP) load_p_frags<T>(pn, Pm, n0, T_);
+    }
+  };
+  if constexpr (kDma) {
+    dd.offsets(oK, a.k.st);
+    dd.offsets(oV, a.v.st);
+    dd.offsets(ogK, a.gk.st);
+    dd.offsets(ogV, a.gv.st);
+    dma_tile(cr.t0, 0);
+  } else {
+    load_tile(cr.t0);
+  }
   for (int nb = cr.t0; nb < cr.t1; ++nb) {
     const int n0 = nb * kBlk;
-    __syncthreads();
-    stage_store_rows<T, D>(s0, sK);
-    stage_store_rows<T, D>(s1, sV);
-    stage_store_rows<T, D>(s2, sgK);
-    stage_store_rows<T, D>(s3, sgV);
-    __syncthreads();
+    const int cur = kDma ? ((nb - cr.t0) & 1) : 0;
+    if constexpr (kDma) {
+      dma_wait();  // this wave's loads of tile nb (LDS tiles and P fragments)
+      __syncthreads();  // everyone's, and everyone is done with the other buffer
+    } else {
+      __syncthreads();
+      stage_store_rows<T, D>(s0, sK[0]);
+      stage_store_rows<T, D>(s1, sV[0]);
+      stage_store_rows<T, D>(s2, sgK[0]);
+      stage_store_rows<T, D>(s3, sgV[0]);
+      __syncthreads();
+    }
+    const T* cK = sK[cur];
+    const T* cV = sV[cur];
+    const T* cgK = sgK[cur];
+    const T* cgV = sgV[cur];
     Tile p, dp, gds, gp1;
     if constexpr (LOADP) {
 #pragma unroll
@@ -125,10 +160,15 @@ void k_gg_row(Params a) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) p.set(kb, j, E::f32(pn[kb][j]));
     }
-    if (nb + 1 < cr.t1) load_tile(nb + 1);
+    if (nb + 1 < cr.t1) {
+      if constexpr (kDma)
+        dma_tile(nb + 1, cur ^ 1);
+      else
+        load_tile(nb + 1);
+    }
     if constexpr (!LOADP) {
       p.zero();
-      mm_d<T, D>(p, sK, qf);
+      mm_d<T, D>(p, cK, qf);
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -146,10 +186,10 @@ void k_gg_row(Params a) {
     dp.zero();
     gds.zero();
     gp1.zero();
-    mm_d<T, D>(dp, sV, dof);
-    mm_d<T, D>(gds, sgK, qf);
-    mm_d<T, D>(gds, sK, gqf);
-    mm_d<T, D>(gp1, sgV, dof);
+    mm_d<T, D>(dp, cV, dof);
+    mm_d<T, D>(gds, cgK, qf);
+    mm_d<T, D>(gds, cK, gqf);
+    mm_d<T, D>(gp1, cgV, dof);
 
     frag dsf[2], z1f[2], z2f[2], pf[2], z4f[2];
 #pragma unroll
@@ -177,14 +217,14 @@ void k_gg_row(Params a) {
       pf[kb] = tile_frag<T>(p, kb);
       if constexpr (GDO) z4f[kb] = vals_frag<T>(vz4);
     }
-    mm_s<T, D>(a1, sgK, dsf);
-    mm_s<T, D>(a2, sK, z1f);
-    mm_s<T, D>(a3, sK, z2f);
-    mm_s<T, D>(a4, sK, pf);
+    mm_s<T, D>(a1, cgK, dsf);
+    mm_s<T, D>(a2, cK, z1f);
+    mm_s<T, D>(a3, cK, z2f);
+    mm_s<T, D>(a4, cK, pf);
     if constexpr (GDO) {
-      mm_s<T, D>(b1, sgV, pf);
-      mm_s<T, D>(b2, sV, z4f);
-      mm_s<T, D>(b3, sV, pf);
+      mm_s<T, D>(b1, cgV, pf);
+      mm_s<T, D>(b2, cV, z4f);
+      mm_s<T, D>(b3, cV, pf);
     }
   }
   const float Ev = group_sum(e_acc);

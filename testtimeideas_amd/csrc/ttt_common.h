@@ -621,8 +621,10 @@ struct TileDma {  // for the unpadded (chunk-permuted) layout only: Lds<T, NCOL>
         o = (int)((int64_t)r * ld + c);
       }
 #if defined(__HIP_DEVICE_COMPILE__)  // the builtin exists only for the gfx950 target
-      __builtin_amdgcn_global_load_lds(g + o, (lds_void_t*)(reinterpret_cast<char*>(lds) + 1024 * (w + 4 * q)),
-                                       16, 0, 0);
+      // uniform base + unsigned 32-bit byte offset: the saddr + voffset form
+      const char* src = reinterpret_cast<const char*>(g) + (uint32_t)o * (uint32_t)sizeof(T);
+      __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(reinterpret_cast<char*>(lds) + 1024 * (w + 4 * q)), 16,
+                                       0, 0);
 #endif
     }
   }
@@ -633,17 +635,26 @@ struct TileDma {  // for the unpadded (chunk-permuted) layout only: Lds<T, NCOL>
 template <int NS>
 __device__ __forceinline__ void stat_dma(float* lds, const float* s0, const float* s1, const float* s2,
                                          const float* s3, int m0, int rows_valid) {
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;  // w: uniform
   if (w >= NS) return;
   const float* src = w == 0 ? s0 : w == 1 ? s1 : w == 2 ? s2 : s3;
 #if defined(__HIP_DEVICE_COMPILE__)
-  __builtin_amdgcn_global_load_lds(src + m0 + (lane < rows_valid ? lane : 0), (lds_void_t*)(lds + kBlk * w), 4,
-                                   0, 0);
+  const char* p = reinterpret_cast<const char*>(src + m0) + (uint32_t)(lane < rows_valid ? lane : 0) * 4u;
+  __builtin_amdgcn_global_load_lds(p, (lds_void_t*)(lds + kBlk * w), 4, 0, 0);
 #endif
 }
 
 // Wait for this wave's direct loads (then meet the other waves at a barrier).
+// The compiler also waits for outstanding direct loads before any LDS read it
+// cannot prove disjoint from their destination, so kernels keep the two
+// buffers in distinct arrays and give each loop step a compile-time buffer
+// role (Parity<0>, Parity<1>).
 __device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+template <int P>
+struct Parity {
+  static constexpr int value = P;
+};
 
 // Eight consecutive fp32 values v[0..7] = src[idx0 .. idx0+7], zero past n.
 // `fast` (uniform) asserts idx0 + 8 <= n and a 16-byte aligned src + idx0.

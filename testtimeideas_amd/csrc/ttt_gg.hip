@@ -275,17 +275,33 @@ void k_gg_col(Params a) {
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
   typedef Lds<T, kBlk> LP;
-  // 16-bit types stream tiles straight into two LDS buffers (TileDma); fp32
-  // stages them through registers into one.
-  constexpr bool kDma = L::kSwizzle && D == 64;  // at D = 128 two buffers would halve the occupancy
-  constexpr int kBuf = kDma ? 2 : 1;
-  __shared__ __align__(16) T sQ[kBuf][L::kRowElems];
-  __shared__ __align__(16) T sgQ[kBuf][L::kRowElems];
-  __shared__ __align__(16) T sdO[kBuf][L::kRowElems];
-  __shared__ __align__(16) T sP[kBuf][LOADP ? LP::kRowElems : 8];
-  // Staged row statistics of the streamed tile: D, E, F, then lse (recompute).
-  constexpr int kNS = LOADP ? 3 : 4;
-  __shared__ __align__(16) float sS[kBuf][kNS * kBlk];
+  // 16-bit types at D = 64 stream tiles straight into two LDS buffers
+  // (TileDma), set 0 and set 1, in distinct arrays with a compile-time role per
+  // loop step; the rest stage them through registers into set 0.
+  constexpr bool kDma = L::kSwizzle && D == 64;
+  constexpr int kNS = LOADP ? 3 : 4;  // staged row statistics: D, E, F, then lse (recompute)
+  constexpr int kE1 = kDma ? L::kRowElems : 8;
+  constexpr int kP0 = LOADP ? LP::kRowElems : 8, kP1 = (LOADP && kDma) ? LP::kRowElems : 8;
+  __shared__ __align__(16) T sQ0[L::kRowElems];
+  __shared__ __align__(16) T sgQ0[L::kRowElems];
+  __shared__ __align__(16) T sdO0[L::kRowElems];
+  __shared__ __align__(16) T sP0[kP0];
+  __shared__ __align__(16) float sS0[kNS * kBlk];
+  __shared__ __align__(16) T sQ1[kE1];
+  __shared__ __align__(16) T sgQ1[kE1];
+  __shared__ __align__(16) T sdO1[kE1];
+  __shared__ __align__(16) T sP1[kP1];
+  __shared__ __align__(16) float sS1[kDma ? kNS * kBlk : 4];
+  struct Bufs {
+    T *q, *gq, *dout, *p;
+    float* st;
+  };
+  auto bufs = [&](auto par) __attribute__((always_inline)) -> Bufs {
+    if constexpr (decltype(par)::value == 0)
+      return Bufs{sQ0, sgQ0, sdO0, sP0, sS0};
+    else
+      return Bufs{sQ1, sgQ1, sdO1, sP1, sS1};
+  };
 
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
@@ -325,79 +341,24 @@ void k_gg_col(Params a) {
 #pragma unroll
   for (int i = 0; i < D / 16; ++i) acc_gk[i] = acc_gv[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  Stage<T, D> s0, s1, s2;  // register staging (fp32 only)
-  Stage<T, kBlk> sp;
-  float stv;
-  auto load_tile = [&](int mb) {
+  // One streamed tile (query block mb) from the staged buffers cb.
+  auto compute = [&](int mb, const Bufs& cb) __attribute__((always_inline)) {
     const int m0 = mb * kBlk;
-    stage_load<T, D>(s0, Q + (int64_t)m0 * a.q.st, a.q.st, T_ - m0, D);
-    stage_load<T, D>(s1, gQ + (int64_t)m0 * a.gq.st, a.gq.st, T_ - m0, D);
-    stage_load<T, D>(s2, dO + (int64_t)m0 * a.dout.st, a.dout.st, T_ - m0, D);
-    if constexpr (LOADP) stage_load<T, kBlk>(sp, Pb + (int64_t)m0 * a.p.st + n0, a.p.st, T_ - m0, T_ - n0);
-    stv = stat_load<kNS>(rs, ev, fv, lse, m0, T_ - m0);
-  };
-  // Direct path: per-lane fetch offsets of an interior tile, computed once.
-  TileDma<T, D> dd;
-  TileDma<T, kBlk> dp_;
-  int oQ[TileDma<T, D>::kPerWave], ogQ[TileDma<T, D>::kPerWave], odO[TileDma<T, D>::kPerWave];
-  int oP[TileDma<T, kBlk>::kPerWave];
-  auto dma_tile = [&](int mb, int buf) {
-    if constexpr (kDma) {
-      const int m0 = mb * kBlk;
-      dd.load(sQ[buf], Q + (int64_t)m0 * a.q.st, oQ, a.q.st, T_ - m0, D);
-      dd.load(sgQ[buf], gQ + (int64_t)m0 * a.gq.st, ogQ, a.gq.st, T_ - m0, D);
-      dd.load(sdO[buf], dO + (int64_t)m0 * a.dout.st, odO, a.dout.st, T_ - m0, D);
-      if constexpr (LOADP) dp_.load(sP[buf], Pb + (int64_t)m0 * a.p.st + n0, oP, a.p.st, T_ - m0, T_ - n0);
-      stat_dma<kNS>(sS[buf], rs, ev, fv, lse, m0, T_ - m0);
-    }
-  };
-  if constexpr (kDma) {
-    dd.offsets(oQ, a.q.st);
-    dd.offsets(ogQ, a.gq.st);
-    dd.offsets(odO, a.dout.st);
-    if constexpr (LOADP) dp_.offsets(oP, a.p.st);
-    dma_tile(cr.t0, 0);
-  } else {
-    load_tile(cr.t0);
-  }
-  for (int mb = cr.t0; mb < cr.t1; ++mb) {
-    const int m0 = mb * kBlk;
-    const int cur = kDma ? ((mb - cr.t0) & 1) : 0;
-    if constexpr (kDma) {
-      dma_wait();  // this wave's loads of tile mb
-      __syncthreads();  // everyone's, and everyone is done with the other buffer
-      if (mb + 1 < cr.t1) dma_tile(mb + 1, cur ^ 1);
-    } else {
-      __syncthreads();
-      stage_store_rows<T, D>(s0, sQ[0]);
-      stage_store_rows<T, D>(s1, sgQ[0]);
-      stage_store_rows<T, D>(s2, sdO[0]);
-      if constexpr (LOADP) stage_store_rows<T, kBlk>(sp, sP[0]);
-      stat_store<kNS>(stv, sS[0]);
-      __syncthreads();
-      if (mb + 1 < cr.t1) load_tile(mb + 1);
-    }
-    const T* cQ = sQ[cur];
-    const T* cgQ = sgQ[cur];
-    const T* cdO = sdO[cur];
-    const T* cP = sP[cur];
-    const float* cS = sS[cur];
-
     Tile p, dp, gds, gp1;
     if constexpr (LOADP) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const frag f = load_frag_tr<T, kBlk>(cP, 32 * kb, 16 * w);
+        const frag f = load_frag_tr<T, kBlk>(cb.p, 32 * kb, 16 * w);
 #pragma unroll
         for (int j = 0; j < 8; ++j) p.set(kb, j, E::f32(f[j]));
       }
     } else {
       p.zero();
-      mm_d<T, D>(p, cQ, kf);
+      mm_d<T, D>(p, cb.q, kf);
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         float l2[8];
-        stat_read8(l2, cS, 3, kb);
+        stat_read8(l2, cb.st, 3, kb);
 #pragma unroll
         for (int j = 0; j < 8; ++j) p.set(kb, j, fast_exp2(p.at(kb, j) * a.scale_log2 - l2[j] * kLog2e));
       }
@@ -418,14 +379,14 @@ void k_gg_col(Params a) {
     // elementwise terms, then its contributions to GK and GV.
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      mm_d_half<T, D>(dp, kb, cdO, vf);
-      mm_d_half<T, D>(gds, kb, cgQ, kf);
-      mm_d_half<T, D>(gds, kb, cQ, gkf);
-      mm_d_half<T, D>(gp1, kb, cdO, gvf);
+      mm_d_half<T, D>(dp, kb, cb.dout, vf);
+      mm_d_half<T, D>(gds, kb, cb.gq, kf);
+      mm_d_half<T, D>(gds, kb, cb.q, gkf);
+      mm_d_half<T, D>(gp1, kb, cb.dout, gvf);
       float d8[8], e8[8], f8[8];
-      stat_read8(d8, cS, 0, kb);
-      stat_read8(e8, cS, 1, kb);
-      stat_read8(f8, cS, 2, kb);
+      stat_read8(d8, cb.st, 0, kb);
+      stat_read8(e8, cb.st, 1, kb);
+      stat_read8(f8, cb.st, 2, kb);
       float vds[8], vgs[8], vgdp[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -438,9 +399,66 @@ void k_gg_col(Params a) {
         vgdp[j] = P * (gd - e8[j]);
         vgs[j] = P * (gp - f8[j]);
       }
-      mm_s_half<T, D>(acc_gk, kb, cgQ, vals_frag<T>(vds));
-      mm_s_half<T, D>(acc_gk, kb, cQ, vals_frag<T>(vgs));
-      mm_s_half<T, D>(acc_gv, kb, cdO, vals_frag<T>(vgdp));
+      mm_s_half<T, D>(acc_gk, kb, cb.gq, vals_frag<T>(vds));
+      mm_s_half<T, D>(acc_gk, kb, cb.q, vals_frag<T>(vgs));
+      mm_s_half<T, D>(acc_gv, kb, cb.dout, vals_frag<T>(vgdp));
+    }
+  };
+
+  if constexpr (kDma) {
+    // Per-lane fetch offsets of an interior tile, computed once.
+    const TileDma<T, D> dd;
+    const TileDma<T, kBlk> dpt;
+    int oQ[TileDma<T, D>::kPerWave], ogQ[TileDma<T, D>::kPerWave], odO[TileDma<T, D>::kPerWave];
+    int oP[TileDma<T, kBlk>::kPerWave];
+    dd.offsets(oQ, a.q.st);
+    dd.offsets(ogQ, a.gq.st);
+    dd.offsets(odO, a.dout.st);
+    if constexpr (LOADP) dpt.offsets(oP, a.p.st);
+    auto dma_tile = [&](int mb, const Bufs& wb) __attribute__((always_inline)) {
+      const int m0 = mb * kBlk;
+      dd.load(wb.q, Q + (int64_t)m0 * a.q.st, oQ, a.q.st, T_ - m0, D);
+      dd.load(wb.gq, gQ + (int64_t)m0 * a.gq.st, ogQ, a.gq.st, T_ - m0, D);
+      dd.load(wb.dout, dO + (int64_t)m0 * a.dout.st, odO, a.dout.st, T_ - m0, D);
+      if constexpr (LOADP) dpt.load(wb.p, Pb + (int64_t)m0 * a.p.st + n0, oP, a.p.st, T_ - m0, T_ - n0);
+      stat_dma<kNS>(wb.st, rs, ev, fv, lse, m0, T_ - m0);
+    };
+    // Step over tile mb from buffer set P while the next tile streams into set 1-P.
+    auto step = [&](auto par, int mb) __attribute__((always_inline)) {
+      constexpr int P = decltype(par)::value;
+      dma_wait();       // this wave's loads of tile mb
+      __syncthreads();  // everyone's, and everyone is done with the other set
+      if (mb + 1 < cr.t1) dma_tile(mb + 1, bufs(Parity<1 - P>{}));
+      compute(mb, bufs(Parity<P>{}));
+    };
+    dma_tile(cr.t0, bufs(Parity<0>{}));
+    for (int mb = cr.t0; mb < cr.t1; mb += 2) {
+      step(Parity<0>{}, mb);
+      if (mb + 1 < cr.t1) step(Parity<1>{}, mb + 1);
+    }
+  } else {
+    Stage<T, D> s0, s1, s2;
+    Stage<T, kBlk> sp;
+    float stv;
+    auto load_tile = [&](int mb) __attribute__((always_inline)) {
+      const int m0 = mb * kBlk;
+      stage_load<T, D>(s0, Q + (int64_t)m0 * a.q.st, a.q.st, T_ - m0, D);
+      stage_load<T, D>(s1, gQ + (int64_t)m0 * a.gq.st, a.gq.st, T_ - m0, D);
+      stage_load<T, D>(s2, dO + (int64_t)m0 * a.dout.st, a.dout.st, T_ - m0, D);
+      if constexpr (LOADP) stage_load<T, kBlk>(sp, Pb + (int64_t)m0 * a.p.st + n0, a.p.st, T_ - m0, T_ - n0);
+      stv = stat_load<kNS>(rs, ev, fv, lse, m0, T_ - m0);
+    };
+    load_tile(cr.t0);
+    for (int mb = cr.t0; mb < cr.t1; ++mb) {
+      __syncthreads();
+      stage_store_rows<T, D>(s0, sQ0);
+      stage_store_rows<T, D>(s1, sgQ0);
+      stage_store_rows<T, D>(s2, sdO0);
+      if constexpr (LOADP) stage_store_rows<T, kBlk>(sp, sP0);
+      stat_store<kNS>(stv, sS0);
+      __syncthreads();
+      if (mb + 1 < cr.t1) load_tile(mb + 1);
+      compute(mb, bufs(Parity<0>{}));
     }
   }
   if (cr.nch == 1) {

@@ -24,9 +24,11 @@
  *     and the T stride (in bytes) must be 16-byte aligned.
  *   - P is a [B,H,T,T] matrix described by a ttt_view whose stride_t is the row
  *     stride; the column dimension must be contiguous and the row stride (in
- *     bytes) 16-byte aligned.  With causal=1 only the lower block triangle of
+ *     bytes) 16-byte aligned.  Rows are read in runs of 8 elements, so the
+ *     storage must extend to column T rounded up to 8 of the last row.  With causal=1 only the lower block triangle of
  *     64x64 tiles (block column <= block row) is written or read; the other
- *     tiles are never touched.
+ *     tiles are never touched.  A window narrows this to the tiles that hold
+ *     a visible key of some row.
  *   - Row statistics (lse, rowsum, E, F) are contiguous fp32 [B*H*T] arrays,
  *     index (b*H + h)*T + t.  lse is the natural-log log-sum-exp of the scaled
  *     scores of each row.
@@ -34,7 +36,8 @@
  *     fp32-accumulated MFMA on the input dtype.
  *
  * The computed quantities (per (b,h) slice, s = scale):
- *   S = s*Q*K^T (causal: entries with col > row are -inf), P = softmax(S),
+ *   S = s*Q*K^T + bias (causal: entries with col > row are -inf; window:
+ *   entries with col < lo(row) too), P = softmax(S),
  *   O = P*V;  D = rowsum(dO o O);  dV = P^T*dO;  dP = dO*V^T;
  *   dS = P o (dP - D);  dQ = s*dS*K;  dK = s*dS^T*Q.
  *   Double backward with cotangents gQ, gK, gV on (dQ, dK, dV):
@@ -79,6 +82,27 @@ typedef enum ttt_entry {
   TTT_ENTRY_GG = 7
 } ttt_entry;
 
+/* A strided [B,H,T,X] operand (X = D, or T for P). Strides are in elements. */
+typedef struct ttt_view {
+  void* data;
+  int64_t stride_b;
+  int64_t stride_h;
+  int64_t stride_t;
+} ttt_view;
+
+/* Key windows (ttt_problem.window_kind).  Query row m sees keys n with
+ * lo(m) <= n <= m:
+ *   TTT_WINDOW_SLIDING  lo(m) = m - W + 1 — make_window_mask(T, W),
+ *                       cloud_ttt_e2e/ttt_e2e/utils.py:40-54;
+ *   TTT_WINDOW_LOCAL    rows in chunks of W, chunk c sees keys from
+ *                       min(T, (c+1)W) - W — WindowedSelfAttention's chunked
+ *                       loop, cloud_ttt_e2e/ttt_e2e/attention.py:111-128,
+ *                       with the mask of :56-69, as one problem.            */
+typedef enum ttt_window_kind {
+  TTT_WINDOW_SLIDING = 0,
+  TTT_WINDOW_LOCAL = 1
+} ttt_window_kind;
+
 /* Problem description shared by every entry point. */
 typedef struct ttt_problem {
   int32_t dtype;    /* ttt_dtype                                  */
@@ -89,15 +113,19 @@ typedef struct ttt_problem {
   int64_t head_dim; /* D: 64 or 128                               */
   float scale;      /* softmax scale s                            */
   int32_t split_chunk; /* tiles per workgroup; 0 = automatic      */
+  int32_t window;      /* W >= 0; 0 = none.  W > 0 needs causal=1;
+                          W >= seqlen is the same as no window     */
+  int32_t window_kind; /* ttt_window_kind                          */
+  ttt_view bias;       /* additive score bias, [B,H,T,T] in the input
+                          dtype, data NULL = none.  Any stride may be
+                          0 (broadcast); columns are contiguous; the
+                          base and the nonzero strides (in bytes) are
+                          16-byte aligned; rows are read like P's.
+                          The bias enters S before the softmax and,
+                          like a mask, receives no gradient.  A row
+                          left with no finite score gives NaN, as
+                          softmax does.                           */
 } ttt_problem;
-
-/* A strided [B,H,T,X] operand (X = D, or T for P). Strides are in elements. */
-typedef struct ttt_view {
-  void* data;
-  int64_t stride_b;
-  int64_t stride_h;
-  int64_t stride_t;
-} ttt_view;
 
 /* Library version (major*10000 + minor*100 + patch). */
 int ttt_version(void);

@@ -17,24 +17,26 @@ def _zeros(r: int, c: int) -> Mat:
     return [[0.0] * c for _ in range(r)]
 
 
-def forward(q: Mat, k: Mat, v: Mat, causal: bool, scale: float) -> Tuple[Mat, Mat]:
-    t, d = len(q), len(q[0])
-    p = _zeros(t, t)
+def forward(q: Mat, k: Mat, v: Mat, causal: bool, scale: float, bias: Mat = None) -> Tuple[Mat, Mat]:
+    """(O, P); bias: an additive [Tq][Tk] score bias (entries may be -inf)."""
+    t, tk, d = len(q), len(k), len(q[0])
+    p = _zeros(t, tk)
     o = _zeros(t, d)
     for m in range(t):
         row = []
-        for n in range(t):
+        for n in range(tk):
             if causal and n > m:
                 row.append(-math.inf)
             else:
-                row.append(scale * sum(q[m][x] * k[n][x] for x in range(d)))
+                x = scale * sum(q[m][x] * k[n][x] for x in range(d))
+                row.append(x + bias[m][n] if bias is not None else x)
         mx = max(row)
         ex = [0.0 if r == -math.inf else math.exp(r - mx) for r in row]
         z = sum(ex)
-        for n in range(t):
+        for n in range(tk):
             p[m][n] = ex[n] / z
         for x in range(d):
-            o[m][x] = sum(p[m][n] * v[n][x] for n in range(t))
+            o[m][x] = sum(p[m][n] * v[n][x] for n in range(tk))
     return o, p
 
 

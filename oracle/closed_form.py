@@ -17,6 +17,9 @@ dV (through P and dO), dP (through dO and V) and P (through S):
   GQ  = s (dS gK + gS K)               GK = s (dS^T gQ + gS^T Q)
   GV  = gdP^T dO                       GdO = P gV + gdP V
 
+An additive score bias (a constant) enters only through P, so the same
+formulas hold with one.
+
 This is the reference's recompute-mode second derivative
 (ttt_kernels/triton_attention.py:416-420), i.e. ATen's double backward of the
 math path (:18-25), written out.
@@ -36,9 +39,15 @@ def _mask(t: int) -> np.ndarray:
     return np.triu(np.ones((t, t), dtype=bool), 1)
 
 
-def forward(q, k, v, causal: bool, scale: float) -> Dict[str, np.ndarray]:
+def forward(q, k, v, causal: bool, scale: float, bias=None) -> Dict[str, np.ndarray]:
+    """bias: an additive score bias broadcastable to [..., Tq, Tk] (entries
+    may be -inf), added before the causal mask and the softmax, as the
+    reference TTT model's ``_attention`` does
+    (cloud_ttt_e2e/ttt_e2e/attention.py:9-18)."""
     q, k, v = (np.asarray(x, dtype=np.float64) for x in (q, k, v))
     s = scale * (q @ _t(k))
+    if bias is not None:
+        s = s + np.asarray(bias, dtype=np.float64)
     if causal:
         s = np.where(_mask(s.shape[-1]), -np.inf, s)
     mx = s.max(axis=-1, keepdims=True)
@@ -48,9 +57,9 @@ def forward(q, k, v, causal: bool, scale: float) -> Dict[str, np.ndarray]:
     return {"o": p @ v, "p": p, "lse": (mx + np.log(l))[..., 0]}
 
 
-def backward(q, k, v, do, causal: bool, scale: float) -> Dict[str, np.ndarray]:
+def backward(q, k, v, do, causal: bool, scale: float, bias=None) -> Dict[str, np.ndarray]:
     q, k, v, do = (np.asarray(x, dtype=np.float64) for x in (q, k, v, do))
-    f = forward(q, k, v, causal, scale)
+    f = forward(q, k, v, causal, scale, bias)
     p, o = f["p"], f["o"]
     dp = do @ _t(v)
     dd = (p * dp).sum(axis=-1, keepdims=True)
@@ -59,9 +68,9 @@ def backward(q, k, v, do, causal: bool, scale: float) -> Dict[str, np.ndarray]:
             "dv": _t(p) @ do, "rowsum": dd[..., 0], "ds": ds, "dp": dp}
 
 
-def double_backward(q, k, v, do, gq, gk, gv, causal: bool, scale: float) -> Dict[str, np.ndarray]:
+def double_backward(q, k, v, do, gq, gk, gv, causal: bool, scale: float, bias=None) -> Dict[str, np.ndarray]:
     q, k, v, do, gq, gk, gv = (np.asarray(x, dtype=np.float64) for x in (q, k, v, do, gq, gk, gv))
-    b = backward(q, k, v, do, causal, scale)
+    b = backward(q, k, v, do, causal, scale, bias)
     p, dp, ds = b["p"], b["dp"], b["ds"]
     dd = b["rowsum"][..., None]
     gds = scale * (gq @ _t(k) + q @ _t(gk))

@@ -7,6 +7,7 @@ steps follow the two harness forms the reference and its baseline use.
 """
 from __future__ import annotations
 
+import math
 from typing import Dict, Optional
 
 import torch
@@ -43,17 +44,29 @@ def lse_math(q, k, causal: bool, scale: float):
     return torch.logsumexp(scores, dim=-1)
 
 
+def attention_masked(q, k, v, attn_mask):
+    """softmax(q k^T / sqrt(d) + attn_mask) v, the reference TTT model's
+    ``_attention`` (cloud_ttt_e2e/ttt_e2e/attention.py:9-18); q [..,Lq,D],
+    k, v [..,Lk,D], attn_mask broadcastable to [..,Lq,Lk] or None."""
+    scores = torch.matmul(q, k.transpose(-2, -1)) * (1.0 / math.sqrt(q.size(-1)))
+    if attn_mask is not None:
+        scores = scores + attn_mask
+    return torch.matmul(torch.softmax(scores, dim=-1), v)
+
+
 def gradgrad_step(q, k, v, do, rq, rk, rv, causal: bool, scale: float,
-                  do_requires_grad: bool = False) -> Dict[str, Optional[torch.Tensor]]:
+                  do_requires_grad: bool = False, attn_mask=None) -> Dict[str, Optional[torch.Tensor]]:
     """The BASELINE cotangent form of one step on the math path:
 
         O = attn(q, k, v)
         dQ, dK, dV = grad(O, (q, k, v), dO, create_graph=True)
         GQ, GK, GV (, GdO) = grad(sum(dQ*rq + dK*rk + dV*rv), (q, k, v (, dO)))
+
+    With attn_mask, attn is ``attention_masked`` (scale 1/sqrt(d)) instead.
     """
     q, k, v = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
     do = do.detach().clone().requires_grad_(do_requires_grad)
-    o = attention_math(q, k, v, causal, scale)
+    o = attention_math(q, k, v, causal, scale) if attn_mask is None else attention_masked(q, k, v, attn_mask)
     dq, dk, dv = torch.autograd.grad(o, (q, k, v), do, create_graph=True)
     s = (dq * rq).sum() + (dk * rk).sum() + (dv * rv).sum()
     wrt = (q, k, v, do) if do_requires_grad else (q, k, v)

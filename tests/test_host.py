@@ -33,10 +33,11 @@ def test_library_exports_every_declared_symbol():
 
 
 def _prob(**kw):
-    d = dict(dtype=0, causal=1, batch=1, heads=1, seqlen=128, head_dim=64, scale=0.125, split_chunk=0)
+    d = dict(dtype=0, causal=1, batch=1, heads=1, seqlen=128, head_dim=64, scale=0.125, split_chunk=0, window=0,
+             window_kind=0)
     d.update(kw)
     return _lib._Problem(d["dtype"], d["causal"], d["batch"], d["heads"], d["seqlen"], d["head_dim"],
-                         d["scale"], d["split_chunk"])
+                         d["scale"], d["split_chunk"], d["window"], d["window_kind"])
 
 
 def _v(addr=0x10000, st=64):
@@ -78,23 +79,54 @@ def _slice_workgroups(n, c, causal):
     return sum(-(-ln // c) for ln in (range(1, n + 1) if causal else [n] * n))
 
 
-def _simulated_chunk(nblk, causal, bh, slots, min_chunk=4):
+def _visible(t, causal, window=0, kind=0):
+    """[T, T] bool: query i sees key j, from the mask definitions (a window
+    of T or more is none)."""
+    i = np.arange(t)[:, None]
+    j = np.arange(t)[None, :]
+    vis = np.ones((t, t), bool) if not causal else j <= i
+    if 0 < window < t:
+        lo = i - window + 1 if kind == 0 else np.minimum(t, (i // window + 1) * window) - window
+        vis = vis & (j >= lo)
+    return vis
+
+
+def _block_tiles(t, causal, window=0, kind=0, col=False):
+    """Streamed tiles of each block in launch order, by brute force: the
+    span between the first and last tile holding a visible pair (row kernels
+    issue the last row block first when causal)."""
+    vis = _visible(t, causal, window, kind)
+    nblk = -(-t // 64)
+    out = []
+    for i in range(nblk):
+        b = i if col or not causal else nblk - 1 - i
+        strip = vis[:, b * 64:(b + 1) * 64] if col else vis[b * 64:(b + 1) * 64, :]
+        hit = strip.any(axis=1 if col else 0)
+        tiles = sorted({n // 64 for n in np.nonzero(hit)[0]})
+        out.append(tiles[-1] - tiles[0] + 1)
+    return out
+
+
+def _simulated_chunk(nblk, causal, bh, slots, min_chunk=4, lengths=None):
     """Independent restatement of the library's split chooser: list-schedule
-    the grid (x = block + nblk*chunk, y = b*h; heaviest block first) onto
-    `slots` workgroup slots spread round-robin over 8 XCDs, cost = makespan +
-    0.015 per non-empty workgroup, each non-empty workgroup taking its tiles
-    + 0.5 and an empty one 0.05."""
+    the grid (x = block + nblk*chunk, y = b*h; blocks in launch order with
+    `lengths` tiles, by default nblk..1 when causal) onto `slots` workgroup
+    slots spread round-robin over 8 XCDs, cost = makespan + 0.015 per
+    non-empty workgroup, each non-empty workgroup taking its tiles + 0.5 and
+    an empty one 0.05."""
     import heapq
+
+    lens = lengths or ([nblk - b for b in range(nblk)] if causal else [nblk] * nblk)
+    lmax = max(lens)
 
     def cost(c):
         per = max(1, slots // 8)
         heaps = [[0.0] * per for _ in range(8)]
         end, used, idx = 0.0, 0, 0
-        k = -(-nblk // c)
+        k = -(-lmax // c)
         for _ in range(bh):
             for ch in range(k):
-                for b in range(nblk):
-                    ln = nblk - b if causal else nblk
+                for ln in lens:
                     t = max(0, min(c, ln - ch * c))
                     h = heaps[idx % 8]
                     f = heapq.heappop(h) + (t + 0.5 if t else 0.05)
@@ -103,16 +135,70 @@ def _simulated_chunk(nblk, causal, bh, slots, min_chunk=4):
         return end + 0.015 * used
 
     if bh * nblk >= slots:
-        return nblk
-    best_c, best = nblk, cost(nblk)
-    c = min(min_chunk, nblk)
-    while c < nblk:
-        if bh * _slice_workgroups(nblk, c, causal) <= 16 * slots:
+        return lmax
+    best_c, best = lmax, cost(lmax)
+    c = min(min_chunk, lmax)
+    while c < lmax:
+        if bh * sum(-(-ln // c) for ln in lens) <= 16 * slots:
             v = cost(c)
             if v < best:
                 best_c, best = c, v
         c = c + 1 if c < 64 else c + max(1, c // 32)
     return best_c
+
+
+@pytest.mark.parametrize("t,window,kind", [(8192, 512, 1), (8192, 512, 0), (1100, 512, 1), (1100, 300, 0),
+                                           (4096, 64, 0), (4096, 100, 1), (2048, 4096, 0)])
+def test_window_workspace_matches_brute_force_ranges(t, window, kind):
+    """The library's tile ranges under a window (seen through the workspace
+    it asks for) equal the brute-force spans of visible pairs."""
+    slots = 460
+    nblk = -(-t // 64)
+    for col, entry, nacc_nsc in ((False, _lib.ENTRY_FWD, 64 + 2), (True, _lib.ENTRY_GG_COL, 2 * 64)):
+        lens = _block_tiles(t, True, window, kind, col)
+        c = _simulated_chunk(nblk, True, 1, slots, lengths=lens)
+        k = -(-max(lens) // min(c, max(lens)))
+        pr = _prob(seqlen=t, window=window, window_kind=kind)
+        parts = nblk * k if k > 1 else 0
+        assert _lib.workspace_bytes(pr, entry) == parts * 64 * nacc_nsc * 4, (col, lens[:4], c)
+    # plain causal: the brute-force spans are nblk, nblk-1, ..., 1 (rows) and the same (columns)
+    assert _block_tiles(640, True) == list(range(10, 0, -1)) == _block_tiles(640, True, col=True)
+
+
+def test_window_and_bias_validation():
+    lib = _lib.load()
+    assert _fwd_rc(_prob(window=-1)) == 1
+    assert _fwd_rc(_prob(window=16, causal=0)) == 1
+    assert b"causal" in lib.ttt_last_error()
+    assert _fwd_rc(_prob(window=16, window_kind=5)) == 1
+    pr = _prob()
+    pr.bias = _lib._View(0x10002, 0, 0, 128)
+    assert _fwd_rc(pr) == 1 and b"bias" in lib.ttt_last_error()
+    pr.bias = _lib._View(0x10000, 0, 0, 100)
+    assert _fwd_rc(pr) == 1 and b"bias" in lib.ttt_last_error()
+    pr.bias = _lib._View(0x10000, -128, 0, 128)
+    assert _fwd_rc(pr) == 1
+    # a window of T or more is none: the same workspace as plain causal
+    big = _prob(seqlen=8192)
+    assert _lib.workspace_bytes(_prob(seqlen=8192, window=8192), _lib.ENTRY_GG) == \
+        _lib.workspace_bytes(big, _lib.ENTRY_GG)
+
+
+def test_prep_bias_layouts():
+    """Bias operands: broadcast dims keep stride 0, rows whose storage ends
+    short of 16 bytes are copied into padded rows, aligned ones are used as
+    they are."""
+    m = torch.zeros(512, 512, dtype=torch.float16)
+    out = _lib.prep_bias(m, 2, 8, 512, torch.float16, "cpu")
+    assert out.shape == (2, 8, 512, 512) and out.stride()[:2] == (0, 0) and out.data_ptr() == m.data_ptr()
+    odd = torch.randn(1, 1, 100, 100).half()
+    out = _lib.prep_bias(odd, 1, 2, 100, torch.float16, "cpu")
+    assert out.stride(2) == 104 and torch.equal(out[0, 1], odd[0, 0])
+    kp = torch.zeros(3, 1, 1, 64)  # key padding mask, fp32 -> fp16
+    out = _lib.prep_bias(kp, 3, 4, 64, torch.float16, "cpu")
+    assert out.dtype == torch.float16 and out.stride()[1:3] == (0, 0)
+    with pytest.raises(ValueError):
+        _lib.prep_bias(torch.zeros(5, 7), 1, 1, 8, torch.float16, "cpu")
 
 
 def test_workspace_sizes():

@@ -15,6 +15,7 @@ from __future__ import annotations
 
 import contextlib
 import ctypes
+import dataclasses
 import os
 from typing import Dict, List, Optional, Tuple
 
@@ -30,6 +31,15 @@ class ExtensionMissingError(RuntimeError):
     """libttt_attn.so has not been built (run ``__graft_entry__.build()``)."""
 
 
+class _View(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("stride_b", ctypes.c_int64),
+        ("stride_h", ctypes.c_int64),
+        ("stride_t", ctypes.c_int64),
+    ]
+
+
 class _Problem(ctypes.Structure):
     _fields_ = [
         ("dtype", ctypes.c_int32),
@@ -40,16 +50,35 @@ class _Problem(ctypes.Structure):
         ("head_dim", ctypes.c_int64),
         ("scale", ctypes.c_float),
         ("split_chunk", ctypes.c_int32),
+        ("window", ctypes.c_int32),
+        ("window_kind", ctypes.c_int32),
+        ("bias", _View),
     ]
 
 
-class _View(ctypes.Structure):
-    _fields_ = [
-        ("data", ctypes.c_void_p),
-        ("stride_b", ctypes.c_int64),
-        ("stride_h", ctypes.c_int64),
-        ("stride_t", ctypes.c_int64),
-    ]
+# ttt_window_kind (include/ttt_attn.h)
+WINDOW_SLIDING, WINDOW_LOCAL = 0, 1
+
+
+@dataclasses.dataclass(frozen=True)
+class Mask:
+    """Which scores a problem masks.
+
+    causal: keys after the query are masked.  window (> 0, needs causal): a
+    key window of kind WINDOW_SLIDING (query m sees keys m-W+1..m,
+    cloud_ttt_e2e/ttt_e2e/utils.py:40-54) or WINDOW_LOCAL (the chunked loop
+    of cloud_ttt_e2e/ttt_e2e/attention.py:111-128 as one problem).  bias: an
+    additive score bias already in kernel layout (see ``prep_bias``), or None.
+    """
+    causal: bool = False
+    window: int = 0
+    window_kind: int = WINDOW_SLIDING
+    bias: Optional[torch.Tensor] = None
+
+
+def as_mask(m) -> Mask:
+    """A Mask, given a Mask or a plain causal flag."""
+    return m if isinstance(m, Mask) else Mask(causal=bool(m))
 
 
 _P = ctypes.POINTER
@@ -196,6 +225,17 @@ def prep(t: torch.Tensor, d_pad: int) -> torch.Tensor:
     return t.contiguous()
 
 
+def prep_rows(t: torch.Tensor, d_pad: int, front: int, back: int) -> torch.Tensor:
+    """``prep`` plus `front` zero rows before and `back` zero rows after the T
+    dimension (copies only when there is padding to add)."""
+    if front == 0 and back == 0:
+        return prep(t, d_pad)
+    b, h, n, d = t.shape
+    out = t.new_zeros((b, h, front + n + back, d_pad))
+    out[:, :, front:front + n, :d] = t
+    return out
+
+
 def check_inputs(*ts: torch.Tensor) -> None:
     ref = ts[0]
     if ref.dim() != 4:
@@ -230,16 +270,54 @@ def split_chunk(n: int):
         _split_chunk = prev
 
 
-def _problem(x: torch.Tensor, causal: bool, scale: float) -> _Problem:
+def _problem(x: torch.Tensor, mask, scale: float) -> _Problem:
     b, h, t, d = x.shape
-    return _Problem(_DTYPE_CODE[x.dtype], 1 if causal else 0, b, h, t, d, float(scale), _split_chunk)
+    m = as_mask(mask)
+    bv = _View(None, 0, 0, 0)
+    if m.bias is not None:
+        s = m.bias.stride()
+        bv = _View(m.bias.data_ptr(), s[0], s[1], s[2])
+    return _Problem(_DTYPE_CODE[x.dtype], 1 if m.causal else 0, b, h, t, d, float(scale), _split_chunk,
+                    int(m.window), int(m.window_kind), bv)
+
+
+def prep_bias(bias: torch.Tensor, b: int, h: int, t: int, dtype: torch.dtype, device) -> torch.Tensor:
+    """An additive score bias broadcastable to [b,h,t,t] as the kernels read
+    it: `dtype` (the input dtype), an expanded [b,h,t,t] view whose broadcast
+    dimensions have stride 0, unit column stride, 16-byte aligned base and
+    strides, and rows readable up to t rounded up to 8 elements.  Copies only when the given
+    tensor does not already satisfy this.  The bias receives no gradient."""
+    x = bias.detach()
+    if x.dtype != dtype:
+        x = x.to(dtype)
+    if x.device != torch.device(device):
+        x = x.to(device)
+    if x.dim() > 4:
+        raise ValueError(f"attn_mask of shape {tuple(bias.shape)} does not broadcast to [B, H, T, T]")
+    while x.dim() < 4:
+        x = x.unsqueeze(0)
+    try:
+        full = x.expand(b, h, t, t)
+    except RuntimeError as e:
+        raise ValueError(f"attn_mask of shape {tuple(bias.shape)} does not broadcast to "
+                         f"{(b, h, t, t)}") from e
+    eb = x.element_size()
+    tp = (t + ROW_READ - 1) // ROW_READ * ROW_READ
+    if (full.stride(-1) == 1 and full.data_ptr() % 16 == 0
+            and all((s * eb) % 16 == 0 for s in full.stride()[:3]) and _rows_readable(full)):
+        return full
+    keep = tuple(1 if x.size(i) == 1 else n for i, n in enumerate((b, h, t)))
+    buf = torch.empty(keep + (tp,), dtype=x.dtype, device=x.device)
+    buf[..., :t].copy_(x.expand(keep + (t,)))
+    return buf[..., :t].expand(b, h, t, t)
 
 
 _ws_sizes: Dict[tuple, int] = {}
 
 
 def workspace_bytes(pr: _Problem, entry: int, gdo: bool = False) -> int:
-    key = (pr.dtype, pr.causal, pr.batch, pr.heads, pr.seqlen, pr.head_dim, pr.split_chunk, entry, gdo)
+    key = (pr.dtype, pr.causal, pr.batch, pr.heads, pr.seqlen, pr.head_dim, pr.split_chunk, pr.window,
+           pr.window_kind, pr.bias.data is not None, entry, gdo)
     n = _ws_sizes.get(key)
     if n is None:
         n = int(load().ttt_attn_workspace_size(ctypes.byref(pr), entry, 1 if gdo else 0))
@@ -258,11 +336,25 @@ def _workspace(pr: _Problem, entry: int, device, gdo: bool = False):
     return buf.data_ptr(), n, buf
 
 
+# The kernels read rows of P and of the bias in runs of 8 elements from
+# multiples of 8, so a row is read up to T rounded up to 8 elements.
+ROW_READ = 8
+
+
+def _rows_readable(x: torch.Tensor) -> bool:
+    """The last element the kernels read of a [B,H,T,N] operand (row T-1 of
+    the last (b, h), column roundup(N, 8) - 1) lies inside its storage."""
+    n = x.size(-1)
+    span = (n + ROW_READ - 1) // ROW_READ * ROW_READ
+    last = x.storage_offset() + sum((d - 1) * st for d, st in zip(x.shape[:-1], x.stride()[:-1])) + span
+    return last * x.element_size() <= x.untyped_storage().nbytes()
+
+
 def alloc_p(like: torch.Tensor) -> torch.Tensor:
-    """[B,H,T,T] P buffer whose rows start on 16-byte boundaries."""
+    """[B,H,T,T] P buffer whose rows start on 16-byte boundaries and hold T
+    rounded up to 8 elements."""
     b, h, t, _ = like.shape
-    per = 16 // like.element_size()
-    tp = (t + per - 1) // per * per
+    tp = (t + ROW_READ - 1) // ROW_READ * ROW_READ
     buf = torch.empty((b, h, t, tp), dtype=like.dtype, device=like.device)
     return buf if tp == t else buf[..., :t]
 
@@ -274,7 +366,7 @@ def _stats(like: torch.Tensor) -> torch.Tensor:
 
 def prep_p(p: torch.Tensor) -> torch.Tensor:
     if p.stride(-1) == 1 and p.data_ptr() % 16 == 0 and all(
-            (s * p.element_size()) % 16 == 0 for s in p.stride()[:-1]):
+            (s * p.element_size()) % 16 == 0 for s in p.stride()[:-1]) and _rows_readable(p):
         return p
     out = alloc_p(p)
     out.copy_(p)
@@ -286,9 +378,10 @@ def _empty_like_out(x: torch.Tensor) -> torch.Tensor:
 
 
 # ---------------------------------------------------------------------------
-# Tensor-level entry points (inputs already padded and validated).
+# Tensor-level entry points (inputs already padded and validated).  `mask` is
+# a Mask, or a bool for a plain causal flag.
 # ---------------------------------------------------------------------------
-def fwd(q, k, v, causal: bool, scale: float, want_p: bool):
+def fwd(q, k, v, mask, scale: float, want_p: bool):
     """Forward: O, LSE and (save_p) P.  Reference: TritonAttentionFn.forward,
     ttt_kernels/triton_attention.py:261-337 (P path :51-59, :270-273)."""
     o = _empty_like_out(q)
@@ -296,14 +389,14 @@ def fwd(q, k, v, causal: bool, scale: float, want_p: bool):
     p = alloc_p(q) if want_p else None
     if q.numel() == 0:
         return o, lse, p
-    pr = _problem(q, causal, scale)
+    pr = _problem(q, mask, scale)
     wp, wn, _wbuf = _workspace(pr, ENTRY_FWD_P if want_p else ENTRY_FWD, q.device)
     _timed("ttt_attn_fwd", ctypes.byref(pr), _view(q), _view(k), _view(v), _view(o), lse.data_ptr(),
            _view(p), wp, wn, _stream())
     return o, lse, p
 
 
-def bwd(q, k, v, o, do, lse, p, causal: bool, scale: float):
+def bwd(q, k, v, o, do, lse, p, mask, scale: float):
     """First backward: dQ, dK, dV and the row statistic D = rowsum(dO o O).
     Reference: TritonAttentionFn.backward, triton_attention.py:351-379 and
     :416-420; launchers backward_stubs.py:154-181, 224-255, 362-425."""
@@ -313,7 +406,7 @@ def bwd(q, k, v, o, do, lse, p, causal: bool, scale: float):
     rowsum = _stats(q)
     if q.numel() == 0:
         return dq, dk, dv, rowsum
-    prob = _problem(q, causal, scale)
+    prob = _problem(q, mask, scale)
     pr = ctypes.byref(prob)
     st = _stream()
     lse_p = _fptr(lse)
@@ -329,43 +422,43 @@ def bwd(q, k, v, o, do, lse, p, causal: bool, scale: float):
     return dq, dk, dv, rowsum
 
 
-def bwd_dq(q, k, v, do, p, lse, rowsum, causal: bool, scale: float, o=None):
+def bwd_dq(q, k, v, do, p, lse, rowsum, mask, scale: float, o=None):
     """dQ alone (D from rowsum, or formed from O).  Reference: _attn_bwd_dq_kernel,
     backward_stubs.py:259-309."""
     dq = _empty_like_out(q)
     if q.numel() == 0:
         return dq
-    prob = _problem(q, causal, scale)
+    prob = _problem(q, mask, scale)
     wp, wn, _wbuf = _workspace(prob, ENTRY_BWD_DQ, q.device)
     _timed("ttt_attn_bwd_dq", ctypes.byref(prob), _view(q), _view(k), _view(v), _view(o), _view(do),
            _fptr(lse), _view(p), _fptr(rowsum), None, _view(dq), wp, wn, _stream())
     return dq
 
 
-def bwd_dkdv(q, k, v, do, p, lse, rowsum, causal: bool, scale: float, want_dk: bool = True):
+def bwd_dkdv(q, k, v, do, p, lse, rowsum, mask, scale: float, want_dk: bool = True):
     """dK and dV (or dV alone).  Reference: backward_stubs.py:22-181, 313-359."""
     dk = _empty_like_out(do) if want_dk else None
     dv = _empty_like_out(do)
     if do.numel() == 0:
         return dk, dv
-    prob = _problem(do, causal, scale)
+    prob = _problem(do, mask, scale)
     wp, wn, _wbuf = _workspace(prob, ENTRY_BWD_DKDV, do.device)
     _timed("ttt_attn_bwd_dkdv", ctypes.byref(prob), _view(q), _view(k), _view(v), _view(do), _fptr(lse),
            _view(p), _fptr(rowsum), _view(dk), _view(dv), wp, wn, _stream())
     return dk, dv
 
 
-def rowsum_from_p(p, do, v, causal: bool):
+def rowsum_from_p(p, do, v, mask):
     """rowsum = sum_n P o (dO V^T).  Reference: backward_stubs.py:184-255."""
     rs = _stats(do)
     if do.numel() == 0:
         return rs
-    pr = ctypes.byref(_problem(do, causal, 1.0))
+    pr = ctypes.byref(_problem(do, mask, 1.0))
     _timed("ttt_attn_bwd_rowsum", pr, _view(p), _view(do), _view(v), rs.data_ptr(), _stream())
     return rs
 
 
-def gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, causal: bool, scale: float, want_gdo: bool):
+def gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, mask, scale: float, want_gdo: bool):
     """Double backward: (GQ, GK, GV, GdO or None).  Reference stubs
     backward_stubs.py:539-548; torch version :434-514 (corrected)."""
     gq_out = _empty_like_out(q)
@@ -376,7 +469,7 @@ def gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, causal: bool, scale: float, want
     f = _stats(q)
     if q.numel() == 0:
         return gq_out, gk_out, gv_out, gdo
-    prob = _problem(q, causal, scale)
+    prob = _problem(q, mask, scale)
     pr = ctypes.byref(prob)
     st = _stream()
     lse_p = _fptr(lse)

@@ -13,7 +13,10 @@
 // kernels load the lane's 8-element row fragments straight from HBM; column
 // kernels stage the 64x64 P tile in LDS and read it by columns);
 // LOADP = false recomputes P = exp2(s*log2e*QK^T - lse*log2e) per tile.
-// Causal: fully masked tiles are skipped, diagonal tiles masked per element.
+// Causal: fully masked tiles are skipped, diagonal tiles masked per element;
+// a key window likewise (RowMask / ColMask).  Recomputed P adds the additive
+// bias when there is one (saved P already holds it).  XM instantiates the
+// window/bias code.
 // The next tile's loads are issued before the current tile's math.
 //
 // Reference semantics: ttt_kernels/triton_attention.py:364-378 (save_p torch
@@ -48,7 +51,7 @@ __device__ __forceinline__ void frags_to_tile(Tile& p, const typename Elem<T>::f
 }
 
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool LOADP>
+template <typename T, int D, bool LOADP, bool XM>
 __global__ __launch_bounds__(kThreads) void k_bwd_dq(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
@@ -61,12 +64,16 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dq(Params a) {
   const int bi = blockIdx.x % nblk, ch = blockIdx.x / nblk;
   const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
   const int mb = a.causal ? (nblk - 1 - bi) : bi;
-  const Chunk cr = chunk_of(0, row_block_hi(mb, nblk, a.causal), ch, a.chunk);
+  const Range rg = row_block_range(mb, nblk, T_, a.causal, XM ? a.win : 0, a.win_kind);
+  const Chunk cr = chunk_of(rg.lo, rg.hi, ch, a.chunk);
   if (ch >= cr.nch) return;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c = lane & 15, g = lane >> 4;
   const int rl = 16 * w + c;
   const int m = mb * kBlk + rl;
   const bool row_ok = m < T_;
+  const RowMask<XM> mk(a, mb, m);
+  const T* brow =
+      (XM && !LOADP && a.bias.p) ? at<const T>(a.bias, b, h) + (int64_t)(row_ok ? m : 0) * a.bias.st : nullptr;
 
   const T* Q = at<const T>(a.q, b, h);
   const T* K = at<const T>(a.k, b, h);
@@ -116,19 +123,14 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dq(Params a) {
     if constexpr (!LOADP) {
       p.zero();
       mm_d<T, D>(p, sK, qf);
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) p.set(kb, j, fast_exp2(p.at(kb, j) * a.scale_log2 - lse2));
+      recompute_p_row<T, XM>(p, a, brow, n0, lse2);
     }
-    if ((a.causal && nb == mb) || (n0 + kBlk > T_)) {
+    if (mk.tile(nb)) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int n = n0 + stream_index(kb, g, j);
-          if (n >= T_ || (a.causal && n > m)) p.set(kb, j, 0.f);
-        }
+        for (int j = 0; j < 8; ++j)
+          p.set(kb, j, mk.masked(n0 + stream_index(kb, g, j)) ? 0.f : p.at(kb, j));
     }
     Tile dp;
     dp.zero();
@@ -150,7 +152,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dq(Params a) {
 }
 
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool LOADP, bool DV_ONLY>
+template <typename T, int D, bool LOADP, bool DV_ONLY, bool XM>
 __global__ __launch_bounds__(kThreads) void k_bwd_dkdv(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
@@ -170,12 +172,15 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dkdv(Params a) {
   const int nblk = (T_ + kBlk - 1) / kBlk;
   const int nb = blockIdx.x % nblk, ch = blockIdx.x / nblk;  // causal: column 0 has the most tiles
   const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
-  const Chunk cr = chunk_of(col_block_lo(nb, a.causal), nblk, ch, a.chunk);
+  const Range rg = col_block_range(nb, nblk, T_, a.causal, XM ? a.win : 0, a.win_kind);
+  const Chunk cr = chunk_of(rg.lo, rg.hi, ch, a.chunk);
   if (ch >= cr.nch) return;
   const int n0 = nb * kBlk;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c = lane & 15, g = lane >> 4;
   const int cl = 16 * w + c;
   const int n = n0 + cl;
+  const ColMask<XM> mk(a, nb, n);
+  const T* bcol = (XM && !LOADP && a.bias.p) ? at<const T>(a.bias, b, h) + (n < T_ ? n : 0) : nullptr;
 
   const T* Q = at<const T>(a.q, b, h);
   const T* K = at<const T>(a.k, b, h);
@@ -229,22 +234,14 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dkdv(Params a) {
     } else {
       p.zero();
       mm_d<T, D>(p, sQ, kf);
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        float l2[8];
-        stat_read8(l2, sS, kSL, kb);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) p.set(kb, j, fast_exp2(p.at(kb, j) * a.scale_log2 - l2[j] * kLog2e));
-      }
+      recompute_p_col<T, XM>(p, a, bcol, m0, sS, kSL);
     }
-    if ((a.causal && mb == nb) || (m0 + kBlk > T_) || (n0 + kBlk > T_)) {
+    if (mk.tile(mb)) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int mm = m0 + stream_index(kb, g, j);
-          if (mm >= T_ || n >= T_ || (a.causal && n > mm)) p.set(kb, j, 0.f);
-        }
+        for (int j = 0; j < 8; ++j)
+          p.set(kb, j, mk.masked(m0 + stream_index(kb, g, j)) ? 0.f : p.at(kb, j));
     }
     frag pf[2];
 #pragma unroll
@@ -279,7 +276,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dkdv(Params a) {
 // ---------------------------------------------------------------------------
 // rowsum[m] = sum_n P[m,n] * (dO*V^T)[m,n]; causal skips tiles past the
 // diagonal (they hold zeros in the math path).
-template <typename T, int D>
+template <typename T, int D, bool XM>
 __global__ __launch_bounds__(kThreads) void k_bwd_rowsum(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
@@ -302,25 +299,26 @@ __global__ __launch_bounds__(kThreads) void k_bwd_rowsum(Params a) {
   for (int ks = 0; ks < D / 32; ++ks) dof[ks] = load_frag_row<T>(dO, a.dout.st, m, T_, 32 * ks + 8 * g);
 
   float sum = 0.f;
-  const int n_end = row_block_hi(mb, nblk, a.causal);
+  const Range rg = row_block_range(mb, nblk, T_, a.causal, XM ? a.win : 0, a.win_kind);
+  const RowMask<XM> mk(a, mb, m);
   Stage<T, D> stV;
-  stage_load<T, D>(stV, V, a.v.st, T_, D);
-  for (int nb = 0; nb < n_end; ++nb) {
+  stage_load<T, D>(stV, V + (int64_t)rg.lo * kBlk * a.v.st, a.v.st, T_ - rg.lo * kBlk, D);
+  for (int nb = rg.lo; nb < rg.hi; ++nb) {
     const int n0 = nb * kBlk;
     __syncthreads();
     stage_store_rows<T, D>(stV, sV);
     __syncthreads();
-    if (nb + 1 < n_end) stage_load<T, D>(stV, V + (int64_t)(n0 + kBlk) * a.v.st, a.v.st, T_ - n0 - kBlk, D);
+    if (nb + 1 < rg.hi) stage_load<T, D>(stV, V + (int64_t)(n0 + kBlk) * a.v.st, a.v.st, T_ - n0 - kBlk, D);
     frag pr[2];
     load_p_frags<T>(pr, Pm, n0, T_);
     Tile p, dp;
     frags_to_tile<T>(p, pr);
-    if (n0 + kBlk > T_) {
+    if (mk.tile(nb)) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-          if (n0 + stream_index(kb, g, j) >= T_) p.set(kb, j, 0.f);
+          p.set(kb, j, mk.masked(n0 + stream_index(kb, g, j)) ? 0.f : p.at(kb, j));
     }
     dp.zero();
     mm_d<T, D>(dp, sV, dof);
@@ -334,33 +332,49 @@ __global__ __launch_bounds__(kThreads) void k_bwd_rowsum(Params a) {
 }
 
 // ---------------------------------------------------------------------------
+template <typename T, int D, bool XM>
+static void launch_dq_x(const Params& a, bool load_p, dim3 grid, hipStream_t st) {
+  if (load_p)
+    hipLaunchKernelGGL((k_bwd_dq<T, D, true, XM>), grid, dim3(kThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL((k_bwd_dq<T, D, false, XM>), grid, dim3(kThreads), 0, st, a);
+}
+
 template <typename T, int D>
 static hipError_t launch_dq_t(int dtype, const Params& a, bool load_p, hipStream_t st) {
   const int nblk = (a.T + kBlk - 1) / kBlk;
   dim3 grid(nblk * a.nchunk_max, a.B * a.H);
-  if (load_p)
-    hipLaunchKernelGGL((k_bwd_dq<T, D, true>), grid, dim3(kThreads), 0, st, a);
+  if (extended_mask(a))
+    launch_dq_x<T, D, true>(a, load_p, grid, st);
   else
-    hipLaunchKernelGGL((k_bwd_dq<T, D, false>), grid, dim3(kThreads), 0, st, a);
+    launch_dq_x<T, D, false>(a, load_p, grid, st);
   if (a.nchunk_max > 1) return launch_combine_sum(dtype, D, a, kOutDQ, st);
   return hipGetLastError();
+}
+
+template <typename T, int D, bool XM>
+static void launch_dkdv_x(const Params& a, bool load_p, bool dv_only, dim3 grid, hipStream_t st) {
+  if (load_p) {
+    if (dv_only)
+      hipLaunchKernelGGL((k_bwd_dkdv<T, D, true, true, XM>), grid, dim3(kThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((k_bwd_dkdv<T, D, true, false, XM>), grid, dim3(kThreads), 0, st, a);
+  } else {
+    if (dv_only)
+      hipLaunchKernelGGL((k_bwd_dkdv<T, D, false, true, XM>), grid, dim3(kThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((k_bwd_dkdv<T, D, false, false, XM>), grid, dim3(kThreads), 0, st, a);
+  }
 }
 
 template <typename T, int D>
 static hipError_t launch_dkdv_t(int dtype, const Params& a, bool load_p, bool dv_only, hipStream_t st) {
   const int nblk = (a.T + kBlk - 1) / kBlk;
   dim3 grid(nblk * a.nchunk_max, a.B * a.H);
-  if (load_p) {
-    if (dv_only)
-      hipLaunchKernelGGL((k_bwd_dkdv<T, D, true, true>), grid, dim3(kThreads), 0, st, a);
-    else
-      hipLaunchKernelGGL((k_bwd_dkdv<T, D, true, false>), grid, dim3(kThreads), 0, st, a);
-  } else {
-    if (dv_only)
-      hipLaunchKernelGGL((k_bwd_dkdv<T, D, false, true>), grid, dim3(kThreads), 0, st, a);
-    else
-      hipLaunchKernelGGL((k_bwd_dkdv<T, D, false, false>), grid, dim3(kThreads), 0, st, a);
-  }
+  if (extended_mask(a))
+    launch_dkdv_x<T, D, true>(a, load_p, dv_only, grid, st);
+  else
+    launch_dkdv_x<T, D, false>(a, load_p, dv_only, grid, st);
   if (a.nchunk_max > 1) return launch_combine_sum(dtype, D, a, dv_only ? kOutDV : kOutDKDV, st);
   return hipGetLastError();
 }
@@ -368,27 +382,33 @@ static hipError_t launch_dkdv_t(int dtype, const Params& a, bool load_p, bool dv
 template <typename T, int D>
 static hipError_t launch_rowsum_t(const Params& a, hipStream_t st) {
   dim3 grid((a.T + kBlk - 1) / kBlk, a.B * a.H);
-  hipLaunchKernelGGL((k_bwd_rowsum<T, D>), grid, dim3(kThreads), 0, st, a);
+  if (extended_mask(a))
+    hipLaunchKernelGGL((k_bwd_rowsum<T, D, true>), grid, dim3(kThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL((k_bwd_rowsum<T, D, false>), grid, dim3(kThreads), 0, st, a);
   return hipGetLastError();
 }
 
-template <typename T, int D>
+template <typename T, int D, bool XM>
 static int occupancy_dq_t(bool load_p) {
-  return load_p ? occupancy_of(k_bwd_dq<T, D, true>) : occupancy_of(k_bwd_dq<T, D, false>);
+  return load_p ? occupancy_of(k_bwd_dq<T, D, true, XM>) : occupancy_of(k_bwd_dq<T, D, false, XM>);
 }
 
-template <typename T, int D>
+template <typename T, int D, bool XM>
 static int occupancy_dkdv_t(bool load_p) {
-  return load_p ? occupancy_of(k_bwd_dkdv<T, D, true, false>) : occupancy_of(k_bwd_dkdv<T, D, false, false>);
+  return load_p ? occupancy_of(k_bwd_dkdv<T, D, true, false, XM>)
+                : occupancy_of(k_bwd_dkdv<T, D, false, false, XM>);
 }
 
-int occupancy_dq(int dtype, int D, bool load_p) {
-  DISPATCH_DTYPE_D(dtype, D, return occupancy_dq_t<ElemT, kD>(load_p));
+int occupancy_dq(int dtype, int D, bool load_p, bool xm) {
+  if (xm) DISPATCH_DTYPE_D(dtype, D, return occupancy_dq_t<ElemT, kD, true>(load_p));
+  else DISPATCH_DTYPE_D(dtype, D, return occupancy_dq_t<ElemT, kD, false>(load_p));
   return 0;
 }
 
-int occupancy_dkdv(int dtype, int D, bool load_p) {
-  DISPATCH_DTYPE_D(dtype, D, return occupancy_dkdv_t<ElemT, kD>(load_p));
+int occupancy_dkdv(int dtype, int D, bool load_p, bool xm) {
+  if (xm) DISPATCH_DTYPE_D(dtype, D, return occupancy_dkdv_t<ElemT, kD, true>(load_p));
+  else DISPATCH_DTYPE_D(dtype, D, return occupancy_dkdv_t<ElemT, kD, false>(load_p));
   return 0;
 }
 

@@ -92,8 +92,24 @@ int check_problem(const ttt_problem* pr) {
     return fail(TTT_ERR_INVALID_ARGUMENT, "seqlen %lld exceeds 2^24", (long long)pr->seqlen);
   if (pr->causal != 0 && pr->causal != 1) return fail(TTT_ERR_INVALID_ARGUMENT, "causal must be 0 or 1");
   if (pr->split_chunk < 0) return fail(TTT_ERR_INVALID_ARGUMENT, "split_chunk must be >= 0");
+  if (pr->window < 0) return fail(TTT_ERR_INVALID_ARGUMENT, "window must be >= 0");
+  if (pr->window > 0 && pr->causal != 1) return fail(TTT_ERR_INVALID_ARGUMENT, "a window needs causal=1");
+  if (pr->window_kind != TTT_WINDOW_SLIDING && pr->window_kind != TTT_WINDOW_LOCAL)
+    return fail(TTT_ERR_INVALID_ARGUMENT, "window_kind %d is not sliding (0) or local (1)", pr->window_kind);
+  if (pr->bias.data) {
+    const int64_t eb = (int64_t)elem_bytes(pr->dtype);
+    if (!aligned16(pr->bias.data)) return fail(TTT_ERR_INVALID_ARGUMENT, "bias: base pointer not 16-byte aligned");
+    for (const int64_t st : {pr->bias.stride_b, pr->bias.stride_h, pr->bias.stride_t})
+      if (st < 0 || (st * eb) % 16 != 0)
+        return fail(TTT_ERR_INVALID_ARGUMENT, "bias: strides must be >= 0 and multiples of 16 bytes");
+  }
   return TTT_OK;
 }
+
+// The window the kernels apply: W >= T sees every earlier key, i.e. none.
+int eff_window(const ttt_problem* pr) { return pr->window > 0 && pr->window < pr->seqlen ? pr->window : 0; }
+
+bool has_xm(const ttt_problem* pr) { return eff_window(pr) > 0 || pr->bias.data != nullptr; }
 
 struct Split {
   int nblk, chunk, nchunk_max;
@@ -126,52 +142,72 @@ int device_cus(int* dev_out) {
 // Workgroup slots of family `fam`'s kernel (variant load_p) on the current
 // device; cached per (device, family, dtype, head dim, variant).
 int64_t family_slots(const ttt_problem* pr, int fam, bool load_p) {
-  static std::atomic<int> per_cu[16][7][3][2][2];
+  static std::atomic<int> per_cu[16][7][3][2][2][2];
   int dev = 0;
   const int cus = device_cus(&dev);
   if (cus == 0) return (int64_t)kFallbackCus * kFallbackPerCu * TTT_SLOT_FILL / 100;
   const int dt = pr->dtype, ds = pr->head_dim == 128 ? 1 : 0, lp = load_p ? 1 : 0;
-  int n = per_cu[dev][fam][dt][ds][lp].load(std::memory_order_relaxed);
+  const bool xm = has_xm(pr);
+  int n = per_cu[dev][fam][dt][ds][lp][xm].load(std::memory_order_relaxed);
   if (n == 0) {
     const int D = (int)pr->head_dim;
     switch (fam) {
-      case ttt::kFamFwdOnline: n = ttt::occupancy_fwd(dt, D, false); break;
-      case ttt::kFamFwdP: n = ttt::occupancy_fwd(dt, D, true); break;
-      case ttt::kFamDq: n = ttt::occupancy_dq(dt, D, load_p); break;
-      case ttt::kFamDkdv: n = ttt::occupancy_dkdv(dt, D, load_p); break;
-      case ttt::kFamGgRow: n = ttt::occupancy_gg_row(dt, D, load_p, false); break;
-      case ttt::kFamGgRowGdo: n = ttt::occupancy_gg_row(dt, D, load_p, true); break;
-      default: n = ttt::occupancy_gg_col(dt, D, load_p); break;
+      case ttt::kFamFwdOnline: n = ttt::occupancy_fwd(dt, D, false, xm); break;
+      case ttt::kFamFwdP: n = ttt::occupancy_fwd(dt, D, true, xm); break;
+      case ttt::kFamDq: n = ttt::occupancy_dq(dt, D, load_p, xm); break;
+      case ttt::kFamDkdv: n = ttt::occupancy_dkdv(dt, D, load_p, xm); break;
+      case ttt::kFamGgRow: n = ttt::occupancy_gg_row(dt, D, load_p, false, xm); break;
+      case ttt::kFamGgRowGdo: n = ttt::occupancy_gg_row(dt, D, load_p, true, xm); break;
+      default: n = ttt::occupancy_gg_col(dt, D, load_p, xm); break;
     }
     if (n <= 0) n = kFallbackPerCu;
-    per_cu[dev][fam][dt][ds][lp].store(n, std::memory_order_relaxed);
+    per_cu[dev][fam][dt][ds][lp][xm].store(n, std::memory_order_relaxed);
   }
   return std::max<int64_t>(1, (int64_t)cus * n * TTT_SLOT_FILL / 100);
 }
 
+bool column_family(int fam) { return fam == ttt::kFamDkdv || fam == ttt::kFamGgCol; }
+
+// Streamed tiles of each block of a slice in launch order: row kernels issue
+// row block nblk-1-i first when causal (block i otherwise), column kernels
+// column block i.  Plain causal gives nblk, nblk-1, ..., 1.
+std::vector<int64_t> block_tiles(const ttt_problem* pr, bool col) {
+  const int T = (int)pr->seqlen, nblk = (T + ttt::kBlk - 1) / ttt::kBlk;
+  const int W = eff_window(pr), kind = pr->window_kind, causal = pr->causal;
+  std::vector<int64_t> len(nblk);
+  for (int i = 0; i < nblk; ++i) {
+    const ttt::Range r = col ? ttt::col_block_range(i, nblk, T, causal, W, kind)
+                             : ttt::row_block_range(causal ? nblk - 1 - i : i, nblk, T, causal, W, kind);
+    len[i] = r.hi - r.lo;
+  }
+  return len;
+}
+
 // Workgroups of one (b,h) slice when every block's streamed range is cut
-// into chunks of c tiles: blocks have 1..n tiles (causal) or n tiles each.
-int64_t slice_workgroups(int64_t n, int64_t c, bool causal) {
-  const int64_t k = (n + c - 1) / c;  // chunks of the longest block
-  return causal ? k * n - c * k * (k - 1) / 2 : k * n;
+// into chunks of c tiles.
+int64_t slice_workgroups(const std::vector<int64_t>& len, int64_t c) {
+  int64_t n = 0;
+  for (const int64_t l : len) n += (l + c - 1) / c;
+  return n;
 }
 
 // Simulated makespan (tile times) of a launch: grid x = block + nblk*chunk,
-// y = (b,h); block i (launch order) has nblk - i tiles (causal, heaviest
-// first) or nblk; `slots` usable workgroup slots spread over kXcds XCDs.
-double simulate_launch(int64_t nblk, int64_t c, bool causal, int64_t bh, int64_t slots, int64_t* nonempty) {
+// y = (b,h); block i (launch order) has len[i] tiles; `slots` usable
+// workgroup slots spread over kXcds XCDs.
+double simulate_launch(const std::vector<int64_t>& len, int64_t c, int64_t bh, int64_t slots, int64_t* nonempty) {
   const int64_t per = std::max<int64_t>(1, slots / kXcds);
   std::vector<std::priority_queue<double, std::vector<double>, std::greater<double>>> xcd(kXcds);
   for (auto& q : xcd)
     for (int64_t i = 0; i < per; ++i) q.push(0.0);
-  const int64_t k = (nblk + c - 1) / c;
+  const int64_t nblk = (int64_t)len.size();
+  const int64_t lmax = *std::max_element(len.begin(), len.end());
+  const int64_t k = (lmax + c - 1) / c;
   double end = 0.0;
   int64_t idx = 0, used = 0;
   for (int64_t y = 0; y < bh; ++y)
     for (int64_t ch = 0; ch < k; ++ch)
       for (int64_t b = 0; b < nblk; ++b, ++idx) {
-        const int64_t len = causal ? nblk - b : nblk;
-        const int64_t t = std::max<int64_t>(0, std::min(c, len - ch * c));
+        const int64_t t = std::max<int64_t>(0, std::min(c, len[b] - ch * c));
         auto& q = xcd[idx % kXcds];
         const double f = q.top() + (t > 0 ? (double)t + kWgOverheadTiles : kEmptyWgTiles);
         q.pop();
@@ -185,26 +221,28 @@ double simulate_launch(int64_t nblk, int64_t c, bool causal, int64_t bh, int64_t
 
 // Tiles per workgroup (see above).  No split when the blocks alone fill the
 // slots; chunks are at least kMinChunk tiles.  Cached per shape.
-int64_t best_chunk(int64_t nblk, bool causal, int64_t bh, int64_t slots) {
+int64_t best_chunk(const ttt_problem* pr, const std::vector<int64_t>& len, bool col, int64_t bh, int64_t slots) {
   static std::mutex mu;
-  static std::map<std::tuple<int64_t, int, int64_t, int64_t>, int64_t> cache;
-  const auto key = std::make_tuple(nblk, causal ? 1 : 0, bh, slots);
+  static std::map<std::tuple<int64_t, int, int, int, int, int64_t, int64_t>, int64_t> cache;
+  const auto key = std::make_tuple((int64_t)pr->seqlen, pr->causal, eff_window(pr), pr->window_kind, col ? 1 : 0,
+                                   bh, slots);
   {
     std::lock_guard<std::mutex> lock(mu);
     const auto it = cache.find(key);
     if (it != cache.end()) return it->second;
   }
-  int64_t best_c = nblk;
+  const int64_t lmax = *std::max_element(len.begin(), len.end());
+  int64_t best_c = lmax;
   double best = 0.0;
   {
     int64_t used = 0;
-    best = simulate_launch(nblk, nblk, causal, bh, slots, &used) + kWgCostTiles * used;
+    best = simulate_launch(len, lmax, bh, slots, &used) + kWgCostTiles * used;
   }
   // candidates: every length up to 64 tiles, then steps of ~3%
-  for (int64_t c = std::min<int64_t>(kMinChunk, nblk); c < nblk; c = c < 64 ? c + 1 : c + std::max<int64_t>(1, c / 32)) {
-    if (bh * slice_workgroups(nblk, c, causal) > kMaxSimWorkgroups * slots) continue;
+  for (int64_t c = std::min<int64_t>(kMinChunk, lmax); c < lmax; c = c < 64 ? c + 1 : c + std::max<int64_t>(1, c / 32)) {
+    if (bh * slice_workgroups(len, c) > kMaxSimWorkgroups * slots) continue;
     int64_t used = 0;
-    const double cost = simulate_launch(nblk, c, causal, bh, slots, &used) + kWgCostTiles * used;
+    const double cost = simulate_launch(len, c, bh, slots, &used) + kWgCostTiles * used;
     if (cost < best) {
       best = cost;
       best_c = c;
@@ -219,15 +257,18 @@ Split choose_split(const ttt_problem* pr, int fam, bool load_p) {
   Split s;
   s.nblk = (int)((pr->seqlen + ttt::kBlk - 1) / ttt::kBlk);
   const int64_t bh = pr->batch * pr->heads;
+  const bool col = column_family(fam);
+  const std::vector<int64_t> len = block_tiles(pr, col);
+  const int64_t lmax = *std::max_element(len.begin(), len.end());
   int64_t c;
   if (pr->split_chunk > 0) {
     c = pr->split_chunk;
   } else {
     const int64_t slots = family_slots(pr, fam, load_p);
-    c = bh * s.nblk >= slots ? s.nblk : best_chunk(s.nblk, pr->causal != 0, bh, slots);
+    c = bh * s.nblk >= slots ? lmax : best_chunk(pr, len, col, bh, slots);
   }
-  s.chunk = (int)std::min<int64_t>(c, s.nblk);
-  s.nchunk_max = (s.nblk + s.chunk - 1) / s.chunk;
+  s.chunk = (int)std::min<int64_t>(c, lmax);
+  s.nchunk_max = (int)((lmax + s.chunk - 1) / s.chunk);
   return s;
 }
 
@@ -272,6 +313,12 @@ ttt::Params base_params(const ttt_problem* pr) {
   a.H = (int)pr->heads;
   a.T = (int)pr->seqlen;
   a.causal = pr->causal;
+  a.win = eff_window(pr);
+  a.win_kind = pr->window_kind;
+  a.bias.p = pr->bias.data;
+  a.bias.sb = pr->bias.stride_b;
+  a.bias.sh = pr->bias.stride_h;
+  a.bias.st = pr->bias.stride_t;
   a.scale = pr->scale;
   a.scale_log2 = pr->scale * ttt::kLog2e;
   return a;

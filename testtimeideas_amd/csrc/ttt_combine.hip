@@ -30,9 +30,9 @@ struct CombineSlot {
 };
 
 __device__ __forceinline__ int block_nch(const Params& a, int blk, int nblk, bool col) {
-  const int lo = col ? col_block_lo(blk, a.causal) : 0;
-  const int hi = col ? nblk : row_block_hi(blk, nblk, a.causal);
-  return (hi - lo + a.chunk - 1) / a.chunk;
+  const Range r = col ? col_block_range(blk, nblk, a.T, a.causal, a.win, a.win_kind)
+                      : row_block_range(blk, nblk, a.T, a.causal, a.win, a.win_kind);
+  return (r.hi - r.lo + a.chunk - 1) / a.chunk;
 }
 
 // Chunks whose loads a thread issues together before adding them.  The

@@ -72,6 +72,8 @@ struct View {
 struct Params {
   int B, H, T;
   int causal;
+  int win, win_kind;  // key window (0: none; else 0 < win < T, with causal), kWin*
+  View bias;          // additive score bias [B,H,T,T] (p == nullptr: none); strides may be 0
   float scale;       // s
   float scale_log2;  // s * log2(e): scores are kept in base-2 units
   View q, k, v, o, dout;
@@ -104,9 +106,98 @@ __device__ __forceinline__ Chunk chunk_of(int lo, int hi, int ch, int chunk) {
   return r;
 }
 
-// Tile range of a row block (query rows) and of a column block (key rows).
-__device__ __forceinline__ int row_block_hi(int mb, int nblk, int causal) { return causal ? mb + 1 : nblk; }
-__device__ __forceinline__ int col_block_lo(int nb, int causal) { return causal ? nb : 0; }
+// ---------------------------------------------------------------------------
+// Masks.  Query row m sees key n iff n < T, n <= m (causal), n >= win_lo(m)
+// (window), and the additive bias, if any, leaves the score finite.  Window
+// kinds (a window implies causal; the host passes 0 < W < T, a window of T or
+// more being plain causal):
+//   kWinSliding  win_lo(m) = m - W + 1: the sliding window of
+//                cloud_ttt_e2e/ttt_e2e/utils.py:40-54 (make_window_mask).
+//   kWinLocal    rows in chunks of W; the keys of chunk c begin at
+//                min(T, (c+1)*W) - W: the chunked loop of
+//                cloud_ttt_e2e/ttt_e2e/attention.py:111-128 with the mask of
+//                :56-69 (full chunks attend within themselves, a last partial
+//                chunk to the last W keys).
+// win_lo is non-decreasing in m, so win_hi(n), the last row that sees key n,
+// is well defined and row m sees key n <=> win_lo(m) <= n <=> m <= win_hi(n).
+// ---------------------------------------------------------------------------
+enum : int { kWinSliding = 0, kWinLocal = 1 };
+
+__host__ __device__ __forceinline__ int win_lo(int m, int T, int W, int kind) {
+  if (W <= 0) return 0;
+  if (kind == kWinSliding) return m - W + 1 > 0 ? m - W + 1 : 0;
+  const int end = (m / W + 1) * W;  // <= m + W < 2T: no overflow
+  const int lo = (end < T ? end : T) - W;
+  return lo > 0 ? lo : 0;
+}
+
+__host__ __device__ __forceinline__ int win_hi(int n, int T, int W, int kind) {
+  if (W <= 0) return T - 1;
+  if (kind == kWinSliding) return n + W - 1 < T - 1 ? n + W - 1 : T - 1;
+  if (n >= T - W) return T - 1;  // the last chunk (partial or not) starts at T - W
+  return (n / W + 1) * W - 1;
+}
+
+// Streamed tiles [lo, hi) of row block mb (key tiles) and of column block nb
+// (query tiles).  W = 0 gives the causal / full ranges.
+struct Range {
+  int lo, hi;
+};
+
+__host__ __device__ __forceinline__ Range row_block_range(int mb, int nblk, int T, int causal, int W, int kind) {
+  Range r;
+  r.lo = win_lo(mb * kBlk, T, W, kind) / kBlk;
+  r.hi = causal ? mb + 1 : nblk;
+  return r;
+}
+
+__host__ __device__ __forceinline__ Range col_block_range(int nb, int nblk, int T, int causal, int W, int kind) {
+  const int last = nb * kBlk + kBlk - 1 < T - 1 ? nb * kBlk + kBlk - 1 : T - 1;
+  Range r;
+  r.lo = causal ? nb : 0;
+  r.hi = win_hi(last, T, W, kind) / kBlk + 1;
+  return r;
+}
+
+// Per-lane mask of a row-block kernel (stationary query row m).  XM: the
+// problem has a window or a bias (other kernels compile W = 0 in).
+template <bool XM>
+struct RowMask {
+  int m, mb, T, causal, lo, lo_last;
+  __device__ __forceinline__ RowMask(const Params& a, int mb_, int m_) : m(m_), mb(mb_), T(a.T), causal(a.causal) {
+    const int W = XM ? a.win : 0;
+    lo = win_lo(m, T, W, a.win_kind);
+    const int last = mb * kBlk + kBlk - 1 < T - 1 ? mb * kBlk + kBlk - 1 : T - 1;
+    lo_last = win_lo(last, T, W, a.win_kind);
+  }
+  // Key tile nb holds a masked key of some row of the block.
+  __device__ __forceinline__ bool tile(int nb) const {
+    return (causal && nb == mb) || (nb * kBlk + kBlk > T) || (XM && nb * kBlk < lo_last);
+  }
+  // Branch-free (bitwise ops): callers select with it.
+  __device__ __forceinline__ bool masked(int n) const {
+    return (n >= T) | ((causal != 0) & (n > m)) | (XM & (n < lo));
+  }
+};
+
+// Per-lane mask of a column-block kernel (stationary key row n).
+template <bool XM>
+struct ColMask {
+  int n, nb, T, causal, hi, hi_first;
+  __device__ __forceinline__ ColMask(const Params& a, int nb_, int n_) : n(n_), nb(nb_), T(a.T), causal(a.causal) {
+    const int W = XM ? a.win : 0;
+    hi = win_hi(n, T, W, a.win_kind);
+    hi_first = win_hi(nb * kBlk, T, W, a.win_kind);
+  }
+  // Query tile mb holds a masked pair of this block.
+  __device__ __forceinline__ bool tile(int mb) const {
+    return (causal && mb == nb) || (mb * kBlk + kBlk > T) || (nb * kBlk + kBlk > T) ||
+           (XM && mb * kBlk + kBlk - 1 > hi_first);
+  }
+  __device__ __forceinline__ bool masked(int mm) const {
+    return (mm >= T) | (n >= T) | ((causal != 0) & (n > mm)) | (XM & (mm > hi));
+  }
+};
 
 __device__ __forceinline__ int64_t part_index(const Params& a, int bh, int nblk, int blk, int ch) {
   return ((int64_t)bh * nblk + blk) * a.nchunk_max + ch;
@@ -360,6 +451,38 @@ __device__ __forceinline__ void load_p_frags(typename Elem<T>::frag* f, const T*
     const int n = n0 + stream_index(kb, g, 0);
     f[kb] = load_frag<T>(pm + (n < T_ ? n : 0));
   }
+}
+
+// Additive bias, in base-2 units, onto a streamed tile of a row-block kernel:
+// row pointer brow (this lane's stationary row), columns as load_p_frags
+// (same row-storage contract as P).
+template <typename T>
+__device__ __forceinline__ void add_bias_row(Tile& s, const T* brow, int n0, int T_) {
+  typename Elem<T>::frag f[2];
+  load_p_frags<T>(f, brow, n0, T_);
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s.set(kb, j, s.at(kb, j) + Elem<T>::f32(f[kb][j]) * kLog2e);
+}
+
+// The same for a column-block kernel: bcol points at this lane's key column
+// of row 0; streamed rows m0 + stream_index(kb, g, j) (rows >= T read row 0).
+template <typename T>
+__device__ __forceinline__ void add_bias_col(Tile& s, const T* bcol, int64_t st, int m0, int T_) {
+  const int g = (threadIdx.x & 63) >> 4;
+  float v[2][8];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int mm = m0 + stream_index(kb, g, j);
+      v[kb][j] = Elem<T>::f32(bcol[(int64_t)(mm < T_ ? mm : 0) * st]);
+    }
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s.set(kb, j, s.at(kb, j) + v[kb][j] * kLog2e);
 }
 
 // Write staged registers to an LDS tile (layout of Lds<T, NCOL>).
@@ -674,6 +797,62 @@ __device__ __forceinline__ void load_vec8(float* v, const float* src, int idx0, 
   } else {
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] = (idx0 + j < n) ? src[idx0 + j] : 0.f;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// P = exp2(s*log2e*x [+ bias*log2e] - lse2) from raw scores x of a row-block
+// tile (brow: this lane's bias row, or nullptr).
+template <typename T, bool XM>
+__device__ __forceinline__ void recompute_p_row(Tile& p, const Params& a, const T* brow, int n0, float lse2) {
+  if constexpr (XM) {
+    if (brow) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) p.set(kb, j, p.at(kb, j) * a.scale_log2);
+      add_bias_row<T>(p, brow, n0, a.T);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) p.set(kb, j, fast_exp2(p.at(kb, j) - lse2));
+      return;
+    }
+  }
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) p.set(kb, j, fast_exp2(p.at(kb, j) * a.scale_log2 - lse2));
+}
+
+// The same for a column-block tile: l2 holds lse2 of the streamed rows of
+// k-block kb; bcol is this lane's bias column (or nullptr).
+template <typename T, bool XM>
+__device__ __forceinline__ void recompute_p_col(Tile& p, const Params& a, const T* bcol, int m0, const float* sS,
+                                                int slot) {
+  if constexpr (XM) {
+    if (bcol) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) p.set(kb, j, p.at(kb, j) * a.scale_log2);
+      add_bias_col<T>(p, bcol, a.bias.st, m0, a.T);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        float l2[8];
+        stat_read8(l2, sS, slot, kb);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) p.set(kb, j, fast_exp2(p.at(kb, j) - l2[j] * kLog2e));
+      }
+      return;
+    }
+  }
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    float l2[8];
+    stat_read8(l2, sS, slot, kb);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) p.set(kb, j, fast_exp2(p.at(kb, j) * a.scale_log2 - l2[j] * kLog2e));
   }
 }
 

@@ -15,9 +15,12 @@
 //                 returns the cached probabilities.                (save_p)
 //
 // Causal: key tiles past the diagonal are skipped; the diagonal tile is masked
-// per element (key > query).  Row blocks are issued heaviest first.  Blocks
-// split into several chunks are finished by the combine kernels of
-// ttt_combine.hip.
+// per element (key > query).  A key window also skips the tiles before the
+// block's first visible key and masks the tiles it cuts.  An additive bias is
+// added to the base-2 scores of every tile.  The window and bias code is a
+// separate instantiation (XM), so plain problems run the kernels without it.
+// Row blocks are issued heaviest first.  Blocks split into several chunks are
+// finished by the combine kernels of ttt_combine.hip.
 //
 // Reference semantics: ttt_kernels/triton_attention.py:18-25 (math path),
 // :51-59 (P path), kernels :87-256.
@@ -29,26 +32,28 @@
 namespace ttt {
 
 // Scores of key tile nb (rows sK) for query row m, in base-2 units; masked
-// entries are -inf.
-template <typename T, int D>
+// entries are -inf.  brow: this row of the additive bias, or nullptr.
+template <typename T, int D, bool XM>
 __device__ __forceinline__ void fwd_scores(Tile& s, const T* sK, const typename Elem<T>::frag* qf,
-                                           const Params& a, int nb, int mb, int m) {
+                                           const Params& a, const RowMask<XM>& mk, const T* brow, int nb) {
   const int g = (threadIdx.x & 63) >> 4;
   s.zero();
   mm_d<T, D>(s, sK, qf);
   const int n0 = nb * kBlk;
-  const bool need_mask = (a.causal && nb == mb) || (n0 + kBlk > a.T);
+  const bool need_mask = mk.tile(nb);
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      float x = s.at(kb, j) * a.scale_log2;
-      if (need_mask) {
-        const int n = n0 + stream_index(kb, g, j);
-        if (n >= a.T || (a.causal && n > m)) x = -INFINITY;
-      }
-      s.set(kb, j, x);
-    }
+    for (int j = 0; j < 8; ++j) s.set(kb, j, s.at(kb, j) * a.scale_log2);
+  if constexpr (XM)
+    if (brow) add_bias_row<T>(s, brow, n0, a.T);
+  if (need_mask) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        s.set(kb, j, mk.masked(n0 + stream_index(kb, g, j)) ? -INFINITY : s.at(kb, j));
+  }
 }
 
 __device__ __forceinline__ float tile_max(const Tile& s) {
@@ -61,7 +66,7 @@ __device__ __forceinline__ float tile_max(const Tile& s) {
 }
 
 // ---------------------------------------------------------------------------
-template <typename T, int D>
+template <typename T, int D, bool XM>
 __global__ __launch_bounds__(kThreads) void k_fwd_online(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
@@ -74,11 +79,14 @@ __global__ __launch_bounds__(kThreads) void k_fwd_online(Params a) {
   const int bi = blockIdx.x % nblk, ch = blockIdx.x / nblk;
   const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
   const int mb = a.causal ? (nblk - 1 - bi) : bi;
-  const Chunk cr = chunk_of(0, row_block_hi(mb, nblk, a.causal), ch, a.chunk);
+  const Range rg = row_block_range(mb, nblk, T_, a.causal, XM ? a.win : 0, a.win_kind);
+  const Chunk cr = chunk_of(rg.lo, rg.hi, ch, a.chunk);
   if (ch >= cr.nch) return;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c = lane & 15, g = lane >> 4;
   const int rl = 16 * w + c;  // row within the block
   const int m = mb * kBlk + rl;
+  const RowMask<XM> mk(a, mb, m);
+  const T* brow = (XM && a.bias.p) ? at<const T>(a.bias, b, h) + (int64_t)(m < T_ ? m : 0) * a.bias.st : nullptr;
 
   const T* Q = at<const T>(a.q, b, h);
   const T* K = at<const T>(a.k, b, h);
@@ -106,9 +114,11 @@ __global__ __launch_bounds__(kThreads) void k_fwd_online(Params a) {
       stage_load<T, D>(stV, V + (int64_t)n1 * a.v.st, a.v.st, T_ - n1, D);
     }
     Tile s;
-    fwd_scores<T, D>(s, sK, qf, a, nb, mb, m);
+    fwd_scores<T, D, XM>(s, sK, qf, a, mk, brow, nb);
     const float mnew = fmaxf(mx, tile_max(s));
-    const float alpha = fast_exp2(mx - mnew);
+    // A window can mask a row's every key of a tile so far: shift by 0 then.
+    const float msh = (XM && mnew == -INFINITY) ? 0.f : mnew;
+    const float alpha = fast_exp2(mx - msh);
     float ts = 0.f;
     frag pf[2];
 #pragma unroll
@@ -116,7 +126,7 @@ __global__ __launch_bounds__(kThreads) void k_fwd_online(Params a) {
       float pv[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        pv[j] = fast_exp2(s.at(kb, j) - mnew);
+        pv[j] = fast_exp2(s.at(kb, j) - msh);
         ts += pv[j];
       }
       pf[kb] = vals_frag<T>(pv);
@@ -144,7 +154,7 @@ __global__ __launch_bounds__(kThreads) void k_fwd_online(Params a) {
 }
 
 // ---------------------------------------------------------------------------
-template <typename T, int D>
+template <typename T, int D, bool XM>
 __global__ __launch_bounds__(kThreads) void k_fwd_stats(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
@@ -156,11 +166,14 @@ __global__ __launch_bounds__(kThreads) void k_fwd_stats(Params a) {
   const int bi = blockIdx.x % nblk, ch = blockIdx.x / nblk;
   const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
   const int mb = a.causal ? (nblk - 1 - bi) : bi;
-  const Chunk cr = chunk_of(0, row_block_hi(mb, nblk, a.causal), ch, a.chunk);
+  const Range rg = row_block_range(mb, nblk, T_, a.causal, XM ? a.win : 0, a.win_kind);
+  const Chunk cr = chunk_of(rg.lo, rg.hi, ch, a.chunk);
   if (ch >= cr.nch) return;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c = lane & 15, g = lane >> 4;
   const int rl = 16 * w + c;
   const int m = mb * kBlk + rl;
+  const RowMask<XM> mk(a, mb, m);
+  const T* brow = (XM && a.bias.p) ? at<const T>(a.bias, b, h) + (int64_t)(m < T_ ? m : 0) * a.bias.st : nullptr;
 
   const T* Q = at<const T>(a.q, b, h);
   const T* K = at<const T>(a.k, b, h);
@@ -180,7 +193,7 @@ __global__ __launch_bounds__(kThreads) void k_fwd_stats(Params a) {
       stage_load<T, D>(stK, K + (int64_t)n1 * a.k.st, a.k.st, T_ - n1, D);
     }
     Tile s;
-    fwd_scores<T, D>(s, sK, qf, a, nb, mb, m);
+    fwd_scores<T, D, XM>(s, sK, qf, a, mk, brow, nb);
     // Per-lane running max and sum over this lane's columns; combined across
     // the four lane groups after the loop.  A lane whose columns are all
     // masked so far keeps max -inf and sum 0 (shift by 0 avoids -inf - -inf).
@@ -200,8 +213,10 @@ __global__ __launch_bounds__(kThreads) void k_fwd_stats(Params a) {
     mx = mnew;
   }
   {
-    const float mrow = group_max(mx);  // finite: every row has a valid column in tile 0
-    l = group_sum(l * fast_exp2(mx - mrow));
+    // Finite without a window (every row sees a key of its first tile); with
+    // one a chunk can miss all of a row's keys, and then max -inf, sum 0.
+    const float mrow = group_max(mx);
+    l = group_sum(l * fast_exp2(mx - ((XM && mrow == -INFINITY) ? 0.f : mrow)));
     mx = mrow;
   }
   if (g != 0) return;
@@ -215,7 +230,7 @@ __global__ __launch_bounds__(kThreads) void k_fwd_stats(Params a) {
 }
 
 // ---------------------------------------------------------------------------
-template <typename T, int D>
+template <typename T, int D, bool XM>
 __global__ __launch_bounds__(kThreads) void k_fwd_p(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
@@ -228,11 +243,14 @@ __global__ __launch_bounds__(kThreads) void k_fwd_p(Params a) {
   const int bi = blockIdx.x % nblk, ch = blockIdx.x / nblk;
   const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
   const int mb = a.causal ? (nblk - 1 - bi) : bi;
-  const Chunk cr = chunk_of(0, row_block_hi(mb, nblk, a.causal), ch, a.chunk);
+  const Range rg = row_block_range(mb, nblk, T_, a.causal, XM ? a.win : 0, a.win_kind);
+  const Chunk cr = chunk_of(rg.lo, rg.hi, ch, a.chunk);
   if (ch >= cr.nch) return;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c = lane & 15, g = lane >> 4;
   const int rl = 16 * w + c;
   const int m = mb * kBlk + rl;
+  const RowMask<XM> mk(a, mb, m);
+  const T* brow = (XM && a.bias.p) ? at<const T>(a.bias, b, h) + (int64_t)(m < T_ ? m : 0) * a.bias.st : nullptr;
   const int64_t ridx = (int64_t)bh * T_ + m;
 
   // Row LSE (base 2) from the statistics pass.
@@ -276,7 +294,7 @@ __global__ __launch_bounds__(kThreads) void k_fwd_p(Params a) {
       stage_load<T, D>(stV, V + (int64_t)n1 * a.v.st, a.v.st, T_ - n1, D);
     }
     Tile s;
-    fwd_scores<T, D>(s, sK, qf, a, nb, mb, m);
+    fwd_scores<T, D, XM>(s, sK, qf, a, mk, brow, nb);
     const int n0 = nb * kBlk;
     frag pf[2];
 #pragma unroll
@@ -306,29 +324,38 @@ __global__ __launch_bounds__(kThreads) void k_fwd_p(Params a) {
 }
 
 // ---------------------------------------------------------------------------
+template <typename T, int D, bool XM>
+static void launch_fwd_x(const Params& a, bool write_p, dim3 grid, hipStream_t st) {
+  if (write_p) {
+    hipLaunchKernelGGL((k_fwd_stats<T, D, XM>), grid, dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL((k_fwd_p<T, D, XM>), grid, dim3(kThreads), 0, st, a);
+  } else {
+    hipLaunchKernelGGL((k_fwd_online<T, D, XM>), grid, dim3(kThreads), 0, st, a);
+  }
+}
+
 template <typename T, int D>
 static hipError_t launch_fwd_t(int dtype, const Params& a, bool write_p, hipStream_t st) {
   const int nblk = (a.T + kBlk - 1) / kBlk;
   dim3 grid(nblk * a.nchunk_max, a.B * a.H);
-  if (write_p) {
-    hipLaunchKernelGGL((k_fwd_stats<T, D>), grid, dim3(kThreads), 0, st, a);
-    hipLaunchKernelGGL((k_fwd_p<T, D>), grid, dim3(kThreads), 0, st, a);
-    if (a.nchunk_max > 1) return launch_combine_sum(dtype, D, a, kOutO, st);
-  } else {
-    hipLaunchKernelGGL((k_fwd_online<T, D>), grid, dim3(kThreads), 0, st, a);
-    if (a.nchunk_max > 1) return launch_combine_fwd(dtype, D, a, st);
-  }
+  if (extended_mask(a))
+    launch_fwd_x<T, D, true>(a, write_p, grid, st);
+  else
+    launch_fwd_x<T, D, false>(a, write_p, grid, st);
+  if (a.nchunk_max > 1)
+    return write_p ? launch_combine_sum(dtype, D, a, kOutO, st) : launch_combine_fwd(dtype, D, a, st);
   return hipGetLastError();
 }
 
-template <typename T, int D>
+template <typename T, int D, bool XM>
 static int occupancy_fwd_t(bool write_p) {
-  if (!write_p) return occupancy_of(k_fwd_online<T, D>);
-  return std::min(occupancy_of(k_fwd_stats<T, D>), occupancy_of(k_fwd_p<T, D>));
+  if (!write_p) return occupancy_of(k_fwd_online<T, D, XM>);
+  return std::min(occupancy_of(k_fwd_stats<T, D, XM>), occupancy_of(k_fwd_p<T, D, XM>));
 }
 
-int occupancy_fwd(int dtype, int D, bool write_p) {
-  DISPATCH_DTYPE_D(dtype, D, return occupancy_fwd_t<ElemT, kD>(write_p));
+int occupancy_fwd(int dtype, int D, bool write_p, bool xm) {
+  if (xm) DISPATCH_DTYPE_D(dtype, D, return occupancy_fwd_t<ElemT, kD, true>(write_p));
+  else DISPATCH_DTYPE_D(dtype, D, return occupancy_fwd_t<ElemT, kD, false>(write_p));
   return 0;
 }
 

@@ -45,7 +45,7 @@
 namespace ttt {
 
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool LOADP, bool GDO>
+template <typename T, int D, bool LOADP, bool GDO, bool XM>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TTT_GG_WAVES_PER_EU)))
 void k_gg_row(Params a) {
   typedef Elem<T> E;
@@ -66,12 +66,16 @@ void k_gg_row(Params a) {
   const int bi = blockIdx.x % nblk, ch = blockIdx.x / nblk;
   const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
   const int mb = a.causal ? (nblk - 1 - bi) : bi;
-  const Chunk cr = chunk_of(0, row_block_hi(mb, nblk, a.causal), ch, a.chunk);
+  const Range rg = row_block_range(mb, nblk, T_, a.causal, XM ? a.win : 0, a.win_kind);
+  const Chunk cr = chunk_of(rg.lo, rg.hi, ch, a.chunk);
   if (ch >= cr.nch) return;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c = lane & 15, g = lane >> 4;
   const int rl = 16 * w + c;
   const int m = mb * kBlk + rl;
   const bool row_ok = m < T_;
+  const RowMask<XM> mk(a, mb, m);
+  const T* brow =
+      (XM && !LOADP && a.bias.p) ? at<const T>(a.bias, b, h) + (int64_t)(row_ok ? m : 0) * a.bias.st : nullptr;
 
   const T* Q = at<const T>(a.q, b, h);
   const T* K = at<const T>(a.k, b, h);
@@ -169,19 +173,14 @@ void k_gg_row(Params a) {
     if constexpr (!LOADP) {
       p.zero();
       mm_d<T, D>(p, cK, qf);
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) p.set(kb, j, fast_exp2(p.at(kb, j) * a.scale_log2 - lse2));
+      recompute_p_row<T, XM>(p, a, brow, n0, lse2);
     }
-    if ((a.causal && nb == mb) || (n0 + kBlk > T_)) {
+    if (mk.tile(nb)) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int n = n0 + stream_index(kb, g, j);
-          if (n >= T_ || (a.causal && n > m)) p.set(kb, j, 0.f);
-        }
+        for (int j = 0; j < 8; ++j)
+          p.set(kb, j, mk.masked(n0 + stream_index(kb, g, j)) ? 0.f : p.at(kb, j));
     }
     dp.zero();
     gds.zero();
@@ -268,7 +267,7 @@ void k_gg_row(Params a) {
 }
 
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool LOADP>
+template <typename T, int D, bool LOADP, bool XM>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TTT_GG_COL_WAVES_PER_EU)))
 void k_gg_col(Params a) {
   typedef Elem<T> E;
@@ -307,12 +306,15 @@ void k_gg_col(Params a) {
   const int nblk = (T_ + kBlk - 1) / kBlk;
   const int nb = blockIdx.x % nblk, ch = blockIdx.x / nblk;
   const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
-  const Chunk cr = chunk_of(col_block_lo(nb, a.causal), nblk, ch, a.chunk);
+  const Range rg = col_block_range(nb, nblk, T_, a.causal, XM ? a.win : 0, a.win_kind);
+  const Chunk cr = chunk_of(rg.lo, rg.hi, ch, a.chunk);
   if (ch >= cr.nch) return;
   const int n0 = nb * kBlk;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c = lane & 15, g = lane >> 4;
   const int cl = 16 * w + c;
   const int n = n0 + cl;
+  const ColMask<XM> mk(a, nb, n);
+  const T* bcol = (XM && !LOADP && a.bias.p) ? at<const T>(a.bias, b, h) + (n < T_ ? n : 0) : nullptr;
 
   const T* Q = at<const T>(a.q, b, h);
   const T* K = at<const T>(a.k, b, h);
@@ -355,22 +357,14 @@ void k_gg_col(Params a) {
     } else {
       p.zero();
       mm_d<T, D>(p, cb.q, kf);
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        float l2[8];
-        stat_read8(l2, cb.st, 3, kb);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) p.set(kb, j, fast_exp2(p.at(kb, j) * a.scale_log2 - l2[j] * kLog2e));
-      }
+      recompute_p_col<T, XM>(p, a, bcol, m0, cb.st, 3);
     }
-    if ((a.causal && mb == nb) || (m0 + kBlk > T_) || (n0 + kBlk > T_)) {
+    if (mk.tile(mb)) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int mm = m0 + stream_index(kb, g, j);
-          if (mm >= T_ || n >= T_ || (a.causal && n > mm)) p.set(kb, j, 0.f);
-        }
+        for (int j = 0; j < 8; ++j)
+          p.set(kb, j, mk.masked(m0 + stream_index(kb, g, j)) ? 0.f : p.at(kb, j));
     }
     dp.zero();
     gds.zero();
@@ -472,21 +466,29 @@ void k_gg_col(Params a) {
 }
 
 // ---------------------------------------------------------------------------
+template <typename T, int D, bool XM>
+static void launch_gg_row_x(const Params& a, bool load_p, bool gdo, dim3 grid, hipStream_t st) {
+  if (load_p) {
+    if (gdo)
+      hipLaunchKernelGGL((k_gg_row<T, D, true, true, XM>), grid, dim3(kThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((k_gg_row<T, D, true, false, XM>), grid, dim3(kThreads), 0, st, a);
+  } else {
+    if (gdo)
+      hipLaunchKernelGGL((k_gg_row<T, D, false, true, XM>), grid, dim3(kThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((k_gg_row<T, D, false, false, XM>), grid, dim3(kThreads), 0, st, a);
+  }
+}
+
 template <typename T, int D>
 static hipError_t launch_gg_row_t(int dtype, const Params& a, bool load_p, bool gdo, hipStream_t st) {
   const int nblk = (a.T + kBlk - 1) / kBlk;
   dim3 grid(nblk * a.nchunk_max, a.B * a.H);
-  if (load_p) {
-    if (gdo)
-      hipLaunchKernelGGL((k_gg_row<T, D, true, true>), grid, dim3(kThreads), 0, st, a);
-    else
-      hipLaunchKernelGGL((k_gg_row<T, D, true, false>), grid, dim3(kThreads), 0, st, a);
-  } else {
-    if (gdo)
-      hipLaunchKernelGGL((k_gg_row<T, D, false, true>), grid, dim3(kThreads), 0, st, a);
-    else
-      hipLaunchKernelGGL((k_gg_row<T, D, false, false>), grid, dim3(kThreads), 0, st, a);
-  }
+  if (extended_mask(a))
+    launch_gg_row_x<T, D, true>(a, load_p, gdo, grid, st);
+  else
+    launch_gg_row_x<T, D, false>(a, load_p, gdo, grid, st);
   if (a.nchunk_max > 1) return launch_combine_gg_row(dtype, D, a, gdo, st);
   return hipGetLastError();
 }
@@ -495,33 +497,43 @@ template <typename T, int D>
 static hipError_t launch_gg_col_t(int dtype, const Params& a, bool load_p, hipStream_t st) {
   const int nblk = (a.T + kBlk - 1) / kBlk;
   dim3 grid(nblk * a.nchunk_max, a.B * a.H);
-  if (load_p)
-    hipLaunchKernelGGL((k_gg_col<T, D, true>), grid, dim3(kThreads), 0, st, a);
-  else
-    hipLaunchKernelGGL((k_gg_col<T, D, false>), grid, dim3(kThreads), 0, st, a);
+  const bool xm = extended_mask(a);
+  if (load_p) {
+    if (xm)
+      hipLaunchKernelGGL((k_gg_col<T, D, true, true>), grid, dim3(kThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((k_gg_col<T, D, true, false>), grid, dim3(kThreads), 0, st, a);
+  } else {
+    if (xm)
+      hipLaunchKernelGGL((k_gg_col<T, D, false, true>), grid, dim3(kThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((k_gg_col<T, D, false, false>), grid, dim3(kThreads), 0, st, a);
+  }
   if (a.nchunk_max > 1) return launch_combine_sum(dtype, D, a, kOutGKGV, st);
   return hipGetLastError();
 }
 
-template <typename T, int D>
+template <typename T, int D, bool XM>
 static int occupancy_gg_row_t(bool load_p, bool gdo) {
   if (load_p)
-    return gdo ? occupancy_of(k_gg_row<T, D, true, true>) : occupancy_of(k_gg_row<T, D, true, false>);
-  return gdo ? occupancy_of(k_gg_row<T, D, false, true>) : occupancy_of(k_gg_row<T, D, false, false>);
+    return gdo ? occupancy_of(k_gg_row<T, D, true, true, XM>) : occupancy_of(k_gg_row<T, D, true, false, XM>);
+  return gdo ? occupancy_of(k_gg_row<T, D, false, true, XM>) : occupancy_of(k_gg_row<T, D, false, false, XM>);
 }
 
-template <typename T, int D>
+template <typename T, int D, bool XM>
 static int occupancy_gg_col_t(bool load_p) {
-  return load_p ? occupancy_of(k_gg_col<T, D, true>) : occupancy_of(k_gg_col<T, D, false>);
+  return load_p ? occupancy_of(k_gg_col<T, D, true, XM>) : occupancy_of(k_gg_col<T, D, false, XM>);
 }
 
-int occupancy_gg_row(int dtype, int D, bool load_p, bool gdo) {
-  DISPATCH_DTYPE_D(dtype, D, return occupancy_gg_row_t<ElemT, kD>(load_p, gdo));
+int occupancy_gg_row(int dtype, int D, bool load_p, bool gdo, bool xm) {
+  if (xm) DISPATCH_DTYPE_D(dtype, D, return occupancy_gg_row_t<ElemT, kD, true>(load_p, gdo));
+  else DISPATCH_DTYPE_D(dtype, D, return occupancy_gg_row_t<ElemT, kD, false>(load_p, gdo));
   return 0;
 }
 
-int occupancy_gg_col(int dtype, int D, bool load_p) {
-  DISPATCH_DTYPE_D(dtype, D, return occupancy_gg_col_t<ElemT, kD>(load_p));
+int occupancy_gg_col(int dtype, int D, bool load_p, bool xm) {
+  if (xm) DISPATCH_DTYPE_D(dtype, D, return occupancy_gg_col_t<ElemT, kD, true>(load_p));
+  else DISPATCH_DTYPE_D(dtype, D, return occupancy_gg_col_t<ElemT, kD, false>(load_p));
   return 0;
 }
 

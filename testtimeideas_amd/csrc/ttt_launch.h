@@ -51,13 +51,17 @@ inline int occupancy_of(K kernel) {
   return n;
 }
 
+// The problem has a key window or an additive bias: launches run the kernels'
+// XM instantiation.
+inline bool extended_mask(const Params& a) { return a.win > 0 || a.bias.p != nullptr; }
+
 // Occupancy of the kernels a launch of each family runs (the smaller one when
-// it runs two).
-int occupancy_fwd(int dtype, int D, bool write_p);
-int occupancy_dq(int dtype, int D, bool load_p);
-int occupancy_dkdv(int dtype, int D, bool load_p);
-int occupancy_gg_row(int dtype, int D, bool load_p, bool gdo);
-int occupancy_gg_col(int dtype, int D, bool load_p);
+// it runs two); xm selects the window/bias instantiation.
+int occupancy_fwd(int dtype, int D, bool write_p, bool xm);
+int occupancy_dq(int dtype, int D, bool load_p, bool xm);
+int occupancy_dkdv(int dtype, int D, bool load_p, bool xm);
+int occupancy_gg_row(int dtype, int D, bool load_p, bool gdo, bool xm);
+int occupancy_gg_col(int dtype, int D, bool load_p, bool xm);
 
 hipError_t launch_fwd(int dtype, int D, const Params& a, bool write_p, hipStream_t st);
 hipError_t launch_combine_sum(int dtype, int D, const Params& a, int which, hipStream_t st);

@@ -40,8 +40,37 @@ RECOMPUTE_MODES = ("recompute", "recompute_manual", "recompute_sdp", "recompute_
 BWD_MODES = RECOMPUTE_MODES + SAVE_P_MODES + ("custom",)
 
 
-def _unpad(t: Optional[torch.Tensor], d: int) -> Optional[torch.Tensor]:
-    return t if t is None or t.size(-1) == d else t[..., :d]
+class Layout:
+    """How a problem's operands map onto the kernels' square [B, H, T, Dp]
+    operands: the head dim is zero-padded to Dp (64 or 128); with fewer
+    queries than keys, query-side tensors (q, O, dO and their gradients) get
+    `qpad` zero rows in front; with more queries than keys, key-side tensors
+    (k, v and their gradients) get `kpad` zero rows at the end.  Zero query
+    rows (q = dO = 0, cotangent 0) contribute nothing to any gradient, and
+    padded keys are masked by the bias, so the results on the real rows are
+    those of the rectangular problem."""
+
+    def __init__(self, d: int, qpad: int = 0, kpad: int = 0):
+        self.d = d
+        self.dpad = _lib.padded_head_dim(d)
+        self.qpad = qpad
+        self.kpad = kpad
+
+    def q(self, t: torch.Tensor) -> torch.Tensor:
+        return _lib.prep_rows(t, self.dpad, self.qpad, 0)
+
+    def k(self, t: torch.Tensor) -> torch.Tensor:
+        return _lib.prep_rows(t, self.dpad, 0, self.kpad)
+
+    def uq(self, t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+        if t is None or (self.qpad == 0 and t.size(-1) == self.d):
+            return t
+        return t[..., self.qpad:, :self.d]
+
+    def uk(self, t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+        if t is None or (self.kpad == 0 and t.size(-1) == self.d):
+            return t
+        return t[..., :t.size(-2) - self.kpad, :self.d]
 
 
 def mode_kind(bwd_mode: str) -> str:
@@ -59,31 +88,62 @@ class _AttnBwdFn(torch.autograd.Function):
     double backward."""
 
     @staticmethod
-    def forward(ctx, q, k, v, do, qp, kp, vp, op, lse, p, causal, scale):
-        d = q.size(-1)
-        dop = _lib.prep(do, qp.size(-1))
-        dq, dk, dv, rowsum = _lib.bwd(qp, kp, vp, op, dop, lse, p, causal, scale)
+    def forward(ctx, q, k, v, do, qp, kp, vp, op, lse, p, mask, scale, lay):
+        dop = lay.q(do)
+        dq, dk, dv, rowsum = _lib.bwd(qp, kp, vp, op, dop, lse, p, mask, scale)
         ctx.save_for_backward(qp, kp, vp, dop, lse, p, rowsum)
-        ctx.causal = causal
+        ctx.mask = mask
         ctx.scale = scale
-        ctx.d = d
-        return _unpad(dq, d), _unpad(dk, d), _unpad(dv, d)
+        ctx.lay = lay
+        return lay.uq(dq), lay.uk(dk), lay.uk(dv)
 
     @staticmethod
     @once_differentiable
     def backward(ctx, gdq, gdk, gdv):
         qp, kp, vp, dop, lse, p, rowsum = ctx.saved_tensors
-        d, dpad = ctx.d, qp.size(-1)
-        g1, g2, g3 = (_lib.prep(g.to(qp.dtype), dpad) for g in (gdq, gdk, gdv))
+        lay = ctx.lay
+        g1 = lay.q(gdq.to(qp.dtype))
+        g2, g3 = (lay.k(g.to(qp.dtype)) for g in (gdk, gdv))
         want_gdo = ctx.needs_input_grad[3]
-        gq, gk, gv, gdo = _lib.gg(qp, kp, vp, dop, lse, p, rowsum, g1, g2, g3, ctx.causal, ctx.scale,
-                                  want_gdo)
+        gq, gk, gv, gdo = _lib.gg(qp, kp, vp, dop, lse, p, rowsum, g1, g2, g3, ctx.mask, ctx.scale, want_gdo)
         need = ctx.needs_input_grad
-        return (_unpad(gq, d) if need[0] else None,
-                _unpad(gk, d) if need[1] else None,
-                _unpad(gv, d) if need[2] else None,
-                _unpad(gdo, d) if want_gdo else None,
-                None, None, None, None, None, None, None, None)
+        return (lay.uq(gq) if need[0] else None,
+                lay.uk(gk) if need[1] else None,
+                lay.uk(gv) if need[2] else None,
+                lay.uq(gdo) if want_gdo else None,
+                None, None, None, None, None, None, None, None, None)
+
+
+def attn_forward(ctx, q, k, v, mask: "_lib.Mask", scale: float, bwd_mode: str, lay: Layout) -> torch.Tensor:
+    """Forward of an attention Function: runs the kernels on the laid-out
+    operands and keeps what the backward needs on ctx."""
+    ctx.mask = mask
+    ctx.scale = scale
+    ctx.bwd_mode = bwd_mode
+    ctx.lay = lay
+    kind = mode_kind(bwd_mode)
+    qp = lay.q(q)
+    kp, vp = lay.k(k), lay.k(v)
+    op, lse, p = _lib.fwd(qp, kp, vp, mask, scale, want_p=(kind == "save_p"))
+    ctx.save_for_backward(q, k, v, qp, kp, vp, op, lse, p)
+    ctx.saved_probs = () if p is None else (p,)
+    return lay.uq(op)
+
+
+def attn_backward(ctx, grad_out: torch.Tensor):
+    """(dq, dk, dv) of an attention Function.  Under create_graph=True
+    (grad mode on in the backward) they come from _AttnBwdFn, whose backward
+    is the exact double backward; otherwise straight from the kernels."""
+    q, k, v, qp, kp, vp, op, lse, p = ctx.saved_tensors
+    mask, scale, lay = ctx.mask, ctx.scale, ctx.lay
+    if torch.is_grad_enabled():
+        # The kernel operands go in detached: the closed-form double backward
+        # already covers every dependence on q, k, v, so no gradient may flow
+        # into O (an output of this node) or into the saved inputs a second time.
+        return _AttnBwdFn.apply(q, k, v, grad_out, qp.detach(), kp.detach(), vp.detach(), op.detach(), lse, p,
+                                mask, scale, lay)
+    dq, dk, dv, _ = _lib.bwd(qp, kp, vp, op, lay.q(grad_out), lse, p, mask, scale)
+    return lay.uq(dq), lay.uk(dk), lay.uk(dv)
 
 
 class TritonAttentionFn(torch.autograd.Function):
@@ -97,37 +157,18 @@ class TritonAttentionFn(torch.autograd.Function):
         if scale is None:
             scale = 1.0 / math.sqrt(q.size(-1))
         ctx.causal = causal
-        ctx.scale = scale
-        ctx.bwd_mode = bwd_mode
-        kind = mode_kind(bwd_mode)
-        d = q.size(-1)
-        dpad = _lib.padded_head_dim(d)
-        qp, kp, vp = (_lib.prep(t, dpad) for t in (q, k, v))
-        op, lse, p = _lib.fwd(qp, kp, vp, causal, scale, want_p=(kind == "save_p"))
-        ctx.save_for_backward(q, k, v, qp, kp, vp, op, lse, p)
-        ctx.saved_probs = () if p is None else (p,)
-        return _unpad(op, d)
+        return attn_forward(ctx, q, k, v, _lib.Mask(causal=bool(causal)), scale, bwd_mode, Layout(q.size(-1)))
 
     @staticmethod
     def backward(ctx, grad_out: torch.Tensor):
-        q, k, v, qp, kp, vp, op, lse, p = ctx.saved_tensors
-        causal, scale = ctx.causal, ctx.scale
         if ctx.bwd_mode == "custom":
+            q, k, v = ctx.saved_tensors[:3]
+            causal, scale = ctx.causal, ctx.scale
             dq = backward_stubs.triton_attn_bwd_dq(q, k, v, grad_out, causal=causal, scale=scale)
             dk = backward_stubs.triton_attn_bwd_dk(q, k, v, grad_out, causal=causal, scale=scale)
             dv = backward_stubs.triton_attn_bwd_dv(q, k, v, grad_out, causal=causal, scale=scale)
             return dq, dk, dv, None, None, None
-        if torch.is_grad_enabled():
-            # The kernel operands go in detached: the closed-form double backward
-            # already covers every dependence on q, k, v, so no gradient may flow
-            # into O (an output of this node) or into the saved inputs a second time.
-            dq, dk, dv = _AttnBwdFn.apply(q, k, v, grad_out, qp.detach(), kp.detach(), vp.detach(),
-                                          op.detach(), lse, p, causal, scale)
-        else:
-            d = q.size(-1)
-            dop = _lib.prep(grad_out, qp.size(-1))
-            dq, dk, dv, _ = _lib.bwd(qp, kp, vp, op, dop, lse, p, causal, scale)
-            dq, dk, dv = _unpad(dq, d), _unpad(dk, d), _unpad(dv, d)
+        dq, dk, dv = attn_backward(ctx, grad_out)
         return dq, dk, dv, None, None, None
 
 

@@ -28,6 +28,7 @@ if ROOT not in sys.path:
 import torch  # noqa: E402
 
 from testtimeideas_amd import _lib, workloads  # noqa: E402
+from testtimeideas_amd.ttt_e2e import windowed_attention  # noqa: E402
 from ttt_kernels import triton_attention  # noqa: E402
 
 METRIC = "fwd+bwd+grad-grad ms at T=8k/16k d=64 fp16 causal; MFMA/HBM % of peak"
@@ -47,8 +48,13 @@ def make_step(cfg: workloads.Config, x, graph_safe: bool = False):
     do, rq, rk, rv = x["do"], x["rq"], x["rk"], x["rv"]
     red = _two_stage_sum if graph_safe else torch.sum
 
+    def attend():
+        if cfg.window:
+            return windowed_attention(q, k, v, cfg.window, local=cfg.window_kind == "local", bwd_mode=cfg.bwd_mode)
+        return triton_attention(q, k, v, causal=cfg.causal, bwd_mode=cfg.bwd_mode)
+
     def step():
-        o = triton_attention(q, k, v, causal=cfg.causal, bwd_mode=cfg.bwd_mode)
+        o = attend()
         dq, dk, dv = torch.autograd.grad(o, (q, k, v), do, create_graph=cfg.gradgrad)
         if not cfg.gradgrad:
             return (dq,)
@@ -115,7 +121,12 @@ def kernel_times(step, reps: int = 10):
         return _lib.mean_ms(rec)
 
 
-def roofline_entry(cfg, ktimes, with_p=True):
+SAVE_P = ("save_p", "save_p_triton", "save_p_triton_bwd", "save_p_triton_full")
+
+
+def roofline_entry(cfg, ktimes, with_p=None):
+    if with_p is None:
+        with_p = cfg.bwd_mode in SAVE_P
     name = max(ktimes, key=ktimes.get)
     model = workloads.kernel_model(name, cfg, with_p)
     dur_s = ktimes[name] * 1e-3
@@ -181,16 +192,25 @@ def cpu_baseline(cfg: workloads.Config, budget_s: float = 20.0):
     torch.set_num_threads(threads)
     x = workloads.make_inputs(cfg, seed=0)
     args = [x[n] for n in ("q", "k", "v", "do", "rq", "rk", "rv")]
-    math_path.gradgrad_step(*args, cfg.causal, cfg.scale)  # warmup
+    if cfg.window:
+        # the reference's chunk loop (WindowedSelfAttention) through its masked math, with autograd
+        def run():
+            return math_path.window_gradgrad_step(*args, cfg.window)
+        what = f"the reference's {cfg.window}-row chunk loop of masked math with autograd"
+    else:
+        def run():
+            return math_path.gradgrad_step(*args, cfg.causal, cfg.scale)
+        what = "torch CPU math path with autograd"
+    run()  # warmup
     times = []
     while not times or (sum(times) < budget_s * 1e3 and len(times) < 20):
         t0 = time.perf_counter()
-        math_path.gradgrad_step(*args, cfg.causal, cfg.scale)
+        run()
         times.append((time.perf_counter() - t0) * 1e3)
     return {"value": round(statistics.median(times), 3), "unit": "ms", "cores": threads, "kind": "port",
             "sample": f"{len(times)} full {cfg.name} steps (b{cfg.b} h{cfg.h} T{cfg.t} d{cfg.d} {cfg.dtype} "
-                      f"causal={cfg.causal}) after 1 warmup, median; torch CPU math path with autograd; "
-                      f"{threads} threads on {_cpu_model()}"}
+                      f"causal={cfg.causal}{f' window={cfg.window}' if cfg.window else ''}) after 1 warmup, "
+                      f"median; {what}; {threads} threads on {_cpu_model()}"}
 
 
 def copy_calibration(mb: int, reps: int = 5) -> None:
@@ -255,9 +275,11 @@ def main():
         "data": "synthetic N(0,1) q,k,v,dO,rq,rk,rv from a seeded CPU generator",
         "config": {"workload": f"{cfg.name}: b{cfg.b} h{cfg.h} T{cfg.t} d{cfg.d} {cfg.dtype} "
                                f"{'causal 64x64 block-sparse' if cfg.causal else 'non-causal'} "
+                               f"{f'{cfg.window_kind} window {cfg.window} ' if cfg.window else ''}"
                                f"{cfg.bwd_mode} fwd+bwd{'+grad-grad' if cfg.gradgrad else ''}",
                    "batch": cfg.b, "heads": cfg.h, "seq_len": cfg.t, "head_dim": cfg.d,
-                   "bwd_mode": cfg.bwd_mode, "autograd": "eager, backward on the calling thread"},
+                   "window": cfg.window or None, "bwd_mode": cfg.bwd_mode,
+                   "autograd": "eager, backward on the calling thread"},
         "tflops": round(roof["flops"] / (ms * 1e-3) / 1e12, 3),
         "step_roofline_us": round(roof["roofline_us"], 2),
         "step_roofline_frac": round(roof["roofline_us"] * 1e-3 / ms, 5),
@@ -284,6 +306,12 @@ def main():
         fwd_flops = 4.0 * cfg.b * cfg.h * cfg.d * workloads.active_area(cfg.t, cfg.causal)
         out["fwd_lse_us"] = round(fwd_ms * 1e3, 2)
         out["fwd_lse_mfma_frac"] = round(fwd_flops / (fwd_ms * 1e-3) / (workloads.PEAK_TFLOPS["f16"] * 1e12), 4)
+        # the reference TTT model's windowed attention (one launch per pass for its chunk loop)
+        for name in ("TTT_W512", "TTT_W512_8K"):
+            cw = workloads.CONFIGS[name]
+            xw = workloads.make_inputs(cw, seed=0, device=dev)
+            out[name.lower() + "_ms"] = round(time_steps(make_step(cw, xw), max(5, args.steps // 2), 3), 4)
+            del xw
 
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(cfg)

@@ -88,3 +88,37 @@ def harness_step(q, k, v, causal: bool, scale: float) -> Dict[str, torch.Tensor]
     gg = torch.autograd.grad(s, (q, k, v))
     return {"o": o.detach(), "dq": grads[0].detach(), "dk": grads[1].detach(), "dv": grads[2].detach(),
             "gq": gg[0], "gk": gg[1], "gv": gg[2]}
+
+
+def window_chunks_attention(q, k, v, window: int):
+    """The attention of WindowedSelfAttention.forward for T > window, as the
+    reference computes it (cloud_ttt_e2e/ttt_e2e/attention.py:111-128): query
+    chunks [s, e) of `window` rows against keys [max(0, e - window), e), each
+    with the local mask of :56-69 through ``attention_masked``, outputs
+    concatenated.  Differentiable (torch autograd); T <= window is causal."""
+    t = q.size(-2)
+    if t <= window:
+        i = torch.arange(t)
+        mask = torch.zeros((t, t), dtype=q.dtype).masked_fill(i[None, :] > i[:, None], float("-inf"))
+        return attention_masked(q, k, v, mask)
+    outs = []
+    for start in range(0, t, window):
+        end = min(t, start + window)
+        kv = max(0, end - window)
+        qi = torch.arange(start, end)[:, None]
+        kj = torch.arange(kv, end)[None, :]
+        mask = torch.zeros((end - start, end - kv), dtype=q.dtype)
+        mask = mask.masked_fill((kj > qi) | (qi - kj >= window), float("-inf"))
+        outs.append(attention_masked(q[..., start:end, :], k[..., kv:end, :], v[..., kv:end, :], mask))
+    return torch.cat(outs, dim=-2)
+
+
+def window_gradgrad_step(q, k, v, do, rq, rk, rv, window: int) -> Dict[str, torch.Tensor]:
+    """``gradgrad_step``'s BASELINE form over ``window_chunks_attention``."""
+    q, k, v = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    o = window_chunks_attention(q, k, v, window)
+    dq, dk, dv = torch.autograd.grad(o, (q, k, v), do, create_graph=True)
+    s = (dq * rq).sum() + (dk * rk).sum() + (dv * rv).sum()
+    g = torch.autograd.grad(s, (q, k, v))
+    return {"o": o.detach(), "dq": dq.detach(), "dk": dk.detach(), "dv": dv.detach(),
+            "gq": g[0], "gk": g[1], "gv": g[2]}

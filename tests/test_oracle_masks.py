@@ -119,3 +119,16 @@ def test_planted_mask_mistakes_fail():
     no_overlap = np.where((j > i) | (j < (i // 3) * 3), NEG, 0.0)  # last chunk sees only itself
     loop = masks.chunked_loop(q, k, v, 3, 0.5)
     assert not np.allclose(loop["o"], cf.forward(q, k, v, False, 0.5, no_overlap)["o"], atol=1e-6)
+
+
+@pytest.mark.parametrize("t,w", [(300, 128), (100, 128), (129, 64)])
+def test_torch_window_loop_equals_numpy_loop(t, w):
+    """math_path.window_gradgrad_step (torch autograd through the reference's
+    chunk loop, the CPU baseline's workload) equals the closed forms per chunk."""
+    g = torch.Generator().manual_seed(t)
+    q, k, v, do, rq, rk, rv = (torch.randn((2, t, 8), generator=g, dtype=torch.float64) for _ in range(7))
+    a = math_path.window_gradgrad_step(q, k, v, do, rq, rk, rv, w)
+    b = masks.chunked_loop(q.numpy(), k.numpy(), v.numpy(), w, 1.0 / np.sqrt(8), do.numpy(), rq.numpy(),
+                           rk.numpy(), rv.numpy())
+    for n in ("o", "dq", "dk", "dv", "gq", "gk", "gv"):
+        assert np.allclose(a[n].numpy(), b[n], atol=1e-12), n

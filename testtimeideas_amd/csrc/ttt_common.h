@@ -72,8 +72,6 @@ struct View {
 struct Params {
   int B, H, T;
   int causal;
-  int win, win_kind;  // key window (0: none; else 0 < win < T, with causal), kWin*
-  View bias;          // additive score bias [B,H,T,T] (p == nullptr: none); strides may be 0
   float scale;       // s
   float scale_log2;  // s * log2(e): scores are kept in base-2 units
   View q, k, v, o, dout;
@@ -91,6 +89,9 @@ struct Params {
   int nchunk_max;            // chunks of the longest block
   float* ws_acc;             // [BH][nblk][nchunk_max][nacc][64][D] partial accumulators
   float* ws_sc;              // [BH][nblk][nchunk_max][nsc][64] partial row scalars
+  // masks beyond causality (last, so the fields above keep their offsets)
+  int win, win_kind;  // key window (0: none; else 0 < win < T, with causal), kWin*
+  View bias;          // additive score bias [B,H,T,T] (p == nullptr: none); strides may be 0
 };
 
 // Streamed tiles [t0, t1) of chunk `ch` of a block whose tiles are [lo, hi).

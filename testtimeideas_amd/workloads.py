@@ -42,6 +42,8 @@ class Config:
     qkv_scale: float = 1.0
     gradgrad: bool = True
     bwd_mode: str = "save_p_triton_full"
+    window: int = 0           # key window (needs causal); 0 = none
+    window_kind: str = "local"  # "local": WindowedSelfAttention's chunks; "sliding": make_window_mask
 
     @property
     def torch_dtype(self) -> torch.dtype:
@@ -58,6 +60,12 @@ CONFIGS: Dict[str, Config] = {
     "C3": Config("C3", 1, 1, 8192, 64, "fp16", True),
     "C4_16k": Config("C4_16k", 1, 1, 16384, 64, "fp16", True),
     "C5": Config("C5", 4, 16, 8192, 128, "bf16", True, qkv_scale=0.5),
+    # The reference TTT model's attention (cloud_ttt_e2e/configs/meta_8k_v2.yaml: batch 8, d_model 384,
+    # 6 heads, window 512, inner-loop chunks of 1024 tokens, fp32): WindowedSelfAttention on one chunk,
+    # differentiated twice by the meta-gradient.
+    "TTT_W512": Config("TTT_W512", 8, 6, 1024, 64, "fp32", True, bwd_mode="recompute", window=512),
+    # The same attention over a whole 8k sequence in bf16 (the prefix pass's shape).
+    "TTT_W512_8K": Config("TTT_W512_8K", 8, 6, 8192, 64, "bf16", True, bwd_mode="recompute", window=512),
 }
 
 
@@ -81,21 +89,42 @@ def make_inputs(cfg: Config, seed: int = 0, device: Optional[torch.device] = Non
     return out
 
 
-def active_area(t: int, causal: bool, blk: int = 64) -> int:
+def _window_lo(m: int, t: int, w: int, kind: str) -> int:
+    """First key query m sees under a window (0 without one)."""
+    if w <= 0 or w >= t:
+        return 0
+    if kind == "sliding":
+        return max(0, m - w + 1)
+    return max(0, min(t, (m // w + 1) * w) - w)
+
+
+def active_area(t: int, causal: bool, blk: int = 64, window: int = 0, kind: str = "local") -> int:
+    """Elements of the 64x64 score tiles the kernels process: all, the lower
+    block triangle (causal), or, with a window, the tiles between each row
+    block's first visible key and its diagonal."""
     if not causal:
         return t * t
     nb = (t + blk - 1) // blk
-    return blk * blk * nb * (nb + 1) // 2
+    if window <= 0 or window >= t:
+        return blk * blk * nb * (nb + 1) // 2
+    return blk * blk * sum(mb - _window_lo(mb * blk, t, window, kind) // blk + 1 for mb in range(nb))
+
+
+def cfg_area(cfg: Config) -> int:
+    return active_area(cfg.t, cfg.causal, window=cfg.window, kind=cfg.window_kind)
 
 
 def step_flops(cfg: Config) -> float:
     c = 28 if cfg.gradgrad else 12
-    return float(c * cfg.b * cfg.h * cfg.d * active_area(cfg.t, cfg.causal))
+    return float(c * cfg.b * cfg.h * cfg.d * cfg_area(cfg))
 
 
 def step_bytes(cfg: Config) -> float:
     e = torch.tensor([], dtype=cfg.torch_dtype).element_size()
-    bh, a, t, d = cfg.b * cfg.h, active_area(cfg.t, cfg.causal), cfg.t, cfg.d
+    bh, a, t, d = cfg.b * cfg.h, cfg_area(cfg), cfg.t, cfg.d
+    if cfg.bwd_mode not in ("save_p", "save_p_triton", "save_p_triton_bwd", "save_p_triton_full"):
+        # recompute: no P in HBM; q, k, v, o, dO, cotangents and gradients, LSE, D, E, F
+        return float(21 * e * bh * t * d + 16 * bh * t) if cfg.gradgrad else float(11 * e * bh * t * d + 8 * bh * t)
     if cfg.gradgrad:
         return float(3 * e * bh * a + 21 * e * bh * t * d + 12 * bh * t)
     return float(2 * e * bh * a + 11 * e * bh * t * d + 8 * bh * t)
@@ -138,7 +167,7 @@ def kernel_model(name: str, cfg: Config, with_p: bool) -> Dict[str, float]:
     key = name + ("/p" if with_p else "")
     c, ppass, ntd, nvec = _KERNEL[key]
     e = torch.tensor([], dtype=cfg.torch_dtype).element_size()
-    bh, a = cfg.b * cfg.h, active_area(cfg.t, cfg.causal)
+    bh, a = cfg.b * cfg.h, cfg_area(cfg)
     flops = float(c * bh * cfg.d * a)
     byts = float(ppass * e * bh * a + ntd * e * bh * cfg.t * cfg.d + 4 * nvec * bh * cfg.t)
     tag = DTYPE_TAG[cfg.torch_dtype]

@@ -34,20 +34,32 @@
 #include "ttt_launch.h"
 
 // Waves per SIMD the grad-grad kernels are compiled for (registers are
-// limited to 512 / this per lane).
+// limited to 512 / this per lane): two at D = 64 (16-bit types; and fp32 in
+// the column kernel, whose few spills cost less than half the waves), one
+// otherwise, where two spill heavily (fp32 fragments take twice the
+// registers, D = 128 twice the accumulators).  Measured on MI355X: C5 (bf16,
+// D = 128) grad-grad 43.8 -> 14.9 ms, fp32 D = 64 row pass 352 -> 268 us.
 #ifndef TTT_GG_WAVES_PER_EU
 #define TTT_GG_WAVES_PER_EU 2
 #endif
 #ifndef TTT_GG_COL_WAVES_PER_EU
 #define TTT_GG_COL_WAVES_PER_EU TTT_GG_WAVES_PER_EU
 #endif
+#ifndef TTT_GG_WIDE_WAVES_PER_EU
+#define TTT_GG_WIDE_WAVES_PER_EU 1
+#endif
 
 namespace ttt {
 
+template <typename T, int D, int NARROW, bool COL>
+struct GgWaves {
+  static constexpr int value = ((sizeof(T) == 2 || COL) && D == 64) ? NARROW : TTT_GG_WIDE_WAVES_PER_EU;
+};
+
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool LOADP, bool GDO, bool XM>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TTT_GG_WAVES_PER_EU)))
-void k_gg_row(Params a) {
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::value))) void k_gg_row(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
@@ -268,8 +280,8 @@ void k_gg_row(Params a) {
 
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool LOADP, bool XM>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(TTT_GG_COL_WAVES_PER_EU)))
-void k_gg_col(Params a) {
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_COL_WAVES_PER_EU, true>::value))) void k_gg_col(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;

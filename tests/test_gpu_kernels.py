@@ -186,3 +186,18 @@ def test_split_matches_unsplit():
         b = _run(xs, True, 0.125, True)
     for n in ("o", "dq", "dk", "dv", "gq", "gk", "gv", "gdo", "lse", "rowsum"):
         assert (a[n] - b[n]).abs().max().item() < 1e-5, n
+
+
+@pytest.mark.parametrize("b,h", [(2, 4), (1, 16)])
+@pytest.mark.parametrize("save_p", [True, False])
+@pytest.mark.parametrize("chunk", [0, 2])
+def test_slices_divisible_by_eight(b, h, save_p, chunk):
+    """B*H a multiple of 8: each slice's workgroups run on one XCD (the
+    kernels remap the grid); results must be the same as per-slice math."""
+    dt = torch.float16
+    t = 200
+    xs = _inputs(b, h, t, 64, dt, seed=b * 10 + h)
+    print(f"[case] slices b={b} h={h} save_p={save_p} chunk={chunk}", flush=True)
+    with _lib.split_chunk(chunk):
+        out = _run(xs, True, 0.125, save_p)
+    _compare(out, _ref(xs, True, 0.125), dt, True, t)

@@ -111,7 +111,8 @@ def _simulated_chunk(nblk, causal, bh, slots, min_chunk=4, lengths=None):
     """Independent restatement of the library's split chooser: list-schedule
     the grid (x = block + nblk*chunk, y = b*h; blocks in launch order with
     `lengths` tiles, by default nblk..1 when causal) onto `slots` workgroup
-    slots spread round-robin over 8 XCDs, cost = makespan + 0.015 per
+    slots spread round-robin over 8 XCDs (slice y to XCD y % 8 when b*h is a
+    multiple of 8), cost = makespan + 0.015 per
     non-empty workgroup, each non-empty workgroup taking its tiles + 0.5 and
     an empty one 0.05."""
     import heapq
@@ -124,11 +125,11 @@ def _simulated_chunk(nblk, causal, bh, slots, min_chunk=4, lengths=None):
         heaps = [[0.0] * per for _ in range(8)]
         end, used, idx = 0.0, 0, 0
         k = -(-lmax // c)
-        for _ in range(bh):
+        for y in range(bh):
             for ch in range(k):
                 for ln in lens:
                     t = max(0, min(c, ln - ch * c))
-                    h = heaps[idx % 8]
+                    h = heaps[y % 8 if bh % 8 == 0 else idx % 8]
                     f = heapq.heappop(h) + (t + 0.5 if t else 0.05)
                     heapq.heappush(h, f)
                     end, used, idx = max(end, f), used + (t > 0), idx + 1

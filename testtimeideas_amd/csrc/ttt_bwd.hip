@@ -61,8 +61,9 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dq(Params a) {
 
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
-  const int bi = blockIdx.x % nblk, ch = blockIdx.x / nblk;
-  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+  const Slot sl = grid_slot();
+  const int bi = sl.x % nblk, ch = sl.x / nblk;
+  const int bh = sl.y, b = bh / a.H, h = bh % a.H;
   const int mb = a.causal ? (nblk - 1 - bi) : bi;
   const Range rg = row_block_range(mb, nblk, T_, a.causal, XM ? a.win : 0, a.win_kind);
   const Chunk cr = chunk_of(rg.lo, rg.hi, ch, a.chunk);
@@ -170,8 +171,9 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dkdv(Params a) {
 
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
-  const int nb = blockIdx.x % nblk, ch = blockIdx.x / nblk;  // causal: column 0 has the most tiles
-  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+  const Slot sl = grid_slot();
+  const int nb = sl.x % nblk, ch = sl.x / nblk;  // causal: column 0 has the most tiles
+  const int bh = sl.y, b = bh / a.H, h = bh % a.H;
   const Range rg = col_block_range(nb, nblk, T_, a.causal, XM ? a.win : 0, a.win_kind);
   const Chunk cr = chunk_of(rg.lo, rg.hi, ch, a.chunk);
   if (ch >= cr.nch) return;
@@ -284,9 +286,10 @@ __global__ __launch_bounds__(kThreads) void k_bwd_rowsum(Params a) {
   __shared__ __align__(16) T sV[L::kRowElems];
 
   const int T_ = a.T;
-  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+  const Slot sl = grid_slot();
+  const int bh = sl.y, b = bh / a.H, h = bh % a.H;
   const int nblk = (T_ + kBlk - 1) / kBlk;
-  const int mb = a.causal ? (nblk - 1 - (int)blockIdx.x) : (int)blockIdx.x;
+  const int mb = a.causal ? (nblk - 1 - sl.x) : sl.x;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c = lane & 15, g = lane >> 4;
   const int m = mb * kBlk + 16 * w + c;
   const bool row_ok = m < T_;

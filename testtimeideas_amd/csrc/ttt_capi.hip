@@ -193,7 +193,9 @@ int64_t slice_workgroups(const std::vector<int64_t>& len, int64_t c) {
 
 // Simulated makespan (tile times) of a launch: grid x = block + nblk*chunk,
 // y = (b,h); block i (launch order) has len[i] tiles; `slots` usable
-// workgroup slots spread over kXcds XCDs.
+// workgroup slots spread over kXcds XCDs.  Workgroups go to the XCDs
+// round-robin in launch order, or slice y to XCD y % 8 when the slices divide
+// evenly (the kernels' grid_slot).
 double simulate_launch(const std::vector<int64_t>& len, int64_t c, int64_t bh, int64_t slots, int64_t* nonempty) {
   const int64_t per = std::max<int64_t>(1, slots / kXcds);
   std::vector<std::priority_queue<double, std::vector<double>, std::greater<double>>> xcd(kXcds);
@@ -202,13 +204,14 @@ double simulate_launch(const std::vector<int64_t>& len, int64_t c, int64_t bh, i
   const int64_t nblk = (int64_t)len.size();
   const int64_t lmax = *std::max_element(len.begin(), len.end());
   const int64_t k = (lmax + c - 1) / c;
+  const bool by_slice = TTT_XCD_SLICES && bh % kXcds == 0;
   double end = 0.0;
   int64_t idx = 0, used = 0;
   for (int64_t y = 0; y < bh; ++y)
     for (int64_t ch = 0; ch < k; ++ch)
       for (int64_t b = 0; b < nblk; ++b, ++idx) {
         const int64_t t = std::max<int64_t>(0, std::min(c, len[b] - ch * c));
-        auto& q = xcd[idx % kXcds];
+        auto& q = xcd[by_slice ? y % kXcds : idx % kXcds];
         const double f = q.top() + (t > 0 ? (double)t + kWgOverheadTiles : kEmptyWgTiles);
         q.pop();
         q.push(f);

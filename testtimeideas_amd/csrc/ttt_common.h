@@ -94,6 +94,34 @@ struct Params {
   View bias;          // additive score bias [B,H,T,T] (p == nullptr: none); strides may be 0
 };
 
+// Logical grid position (x, slice y) of this workgroup.  The hardware hands
+// workgroups to the 8 XCDs round-robin in linear launch order (x fastest).
+// When the slices divide evenly by 8, slice y runs on XCD y % 8, so the tiles
+// the blocks of one slice share are fetched into one XCD's L2 instead of
+// eight; each XCD still takes its slices' blocks in launch order, and the
+// mapping is a bijection of the grid.  TTT_XCD_SLICES=0 keeps the launch order.
+#ifndef TTT_XCD_SLICES
+#define TTT_XCD_SLICES 1
+#endif
+struct Slot {
+  int x, y;
+};
+
+__device__ __forceinline__ Slot grid_slot() {
+  Slot s;
+  const int gx = gridDim.x, gy = gridDim.y;
+  if (!TTT_XCD_SLICES || (gy & 7) != 0) {
+    s.x = blockIdx.x;
+    s.y = blockIdx.y;
+    return s;
+  }
+  const int lin = blockIdx.x + gx * blockIdx.y;
+  const int i = lin >> 3;
+  s.x = i % gx;
+  s.y = 8 * (i / gx) + (lin & 7);
+  return s;
+}
+
 // Streamed tiles [t0, t1) of chunk `ch` of a block whose tiles are [lo, hi).
 struct Chunk {
   int t0, t1, nch;

@@ -76,8 +76,9 @@ __global__ __launch_bounds__(kThreads) void k_fwd_online(Params a) {
 
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
-  const int bi = blockIdx.x % nblk, ch = blockIdx.x / nblk;
-  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+  const Slot sl = grid_slot();
+  const int bi = sl.x % nblk, ch = sl.x / nblk;
+  const int bh = sl.y, b = bh / a.H, h = bh % a.H;
   const int mb = a.causal ? (nblk - 1 - bi) : bi;
   const Range rg = row_block_range(mb, nblk, T_, a.causal, XM ? a.win : 0, a.win_kind);
   const Chunk cr = chunk_of(rg.lo, rg.hi, ch, a.chunk);
@@ -163,8 +164,9 @@ __global__ __launch_bounds__(kThreads) void k_fwd_stats(Params a) {
 
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
-  const int bi = blockIdx.x % nblk, ch = blockIdx.x / nblk;
-  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+  const Slot sl = grid_slot();
+  const int bi = sl.x % nblk, ch = sl.x / nblk;
+  const int bh = sl.y, b = bh / a.H, h = bh % a.H;
   const int mb = a.causal ? (nblk - 1 - bi) : bi;
   const Range rg = row_block_range(mb, nblk, T_, a.causal, XM ? a.win : 0, a.win_kind);
   const Chunk cr = chunk_of(rg.lo, rg.hi, ch, a.chunk);
@@ -240,8 +242,9 @@ __global__ __launch_bounds__(kThreads) void k_fwd_p(Params a) {
 
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
-  const int bi = blockIdx.x % nblk, ch = blockIdx.x / nblk;
-  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+  const Slot sl = grid_slot();
+  const int bi = sl.x % nblk, ch = sl.x / nblk;
+  const int bh = sl.y, b = bh / a.H, h = bh % a.H;
   const int mb = a.causal ? (nblk - 1 - bi) : bi;
   const Range rg = row_block_range(mb, nblk, T_, a.causal, XM ? a.win : 0, a.win_kind);
   const Chunk cr = chunk_of(rg.lo, rg.hi, ch, a.chunk);

@@ -75,8 +75,9 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
 
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
-  const int bi = blockIdx.x % nblk, ch = blockIdx.x / nblk;
-  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+  const Slot sl = grid_slot();
+  const int bi = sl.x % nblk, ch = sl.x / nblk;
+  const int bh = sl.y, b = bh / a.H, h = bh % a.H;
   const int mb = a.causal ? (nblk - 1 - bi) : bi;
   const Range rg = row_block_range(mb, nblk, T_, a.causal, XM ? a.win : 0, a.win_kind);
   const Chunk cr = chunk_of(rg.lo, rg.hi, ch, a.chunk);
@@ -316,8 +317,9 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_COL_WAVES_PER_EU, true>:
 
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
-  const int nb = blockIdx.x % nblk, ch = blockIdx.x / nblk;
-  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+  const Slot sl = grid_slot();
+  const int nb = sl.x % nblk, ch = sl.x / nblk;
+  const int bh = sl.y, b = bh / a.H, h = bh % a.H;
   const Range rg = col_block_range(nb, nblk, T_, a.causal, XM ? a.win : 0, a.win_kind);
   const Chunk cr = chunk_of(rg.lo, rg.hi, ch, a.chunk);
   if (ch >= cr.nch) return;

@@ -213,6 +213,59 @@ def cpu_baseline(cfg: workloads.Config, budget_s: float = 20.0):
                       f"median; {what}; {threads} threads on {_cpu_model()}"}
 
 
+# The reference's meta-training configuration (cloud_ttt_e2e/configs/meta_8k_v2.yaml) and its H100 rate
+# (cloud_ttt_e2e/meta_8k_v2.log: 1.26-1.28 s/it over 5000 iterations).
+META_8K = dict(vocab_size=512, num_keys=64, max_seq_len=8192, context_len=6144, query_len=2048, window_size=512,
+               d_model=384, n_heads=6, n_layers=8, d_ff=1536, suffix_layers=2, dual_mlp=True,
+               ttt_param_filter="mlp_fast", chunk_size=1024, far_frac=0.75, batch_size=8, lr=5e-4, inner_steps=4,
+               inner_lr=0.1)
+META_8K_H100_S_PER_IT = 1.27
+
+
+def meta_bench(steps: int, warmup: int, dev) -> dict:
+    """Seconds per meta-training iteration of the reference TTT model at
+    meta_8k_v2 on this GPU, timed as the reference's loop is
+    (scripts/train_meta.py:133-160): synthetic batch, meta_step, backward of
+    the outer loss through every inner update, AdamW step."""
+    from testtimeideas_amd.ttt_e2e import data, meta
+    from testtimeideas_amd.ttt_e2e.model import ModelConfig, TTTModel
+    c = META_8K
+    torch.manual_seed(1337)
+    model = TTTModel(ModelConfig(vocab_size=c["vocab_size"], max_seq_len=c["max_seq_len"],
+                                 window_size=c["window_size"], d_model=c["d_model"], n_heads=c["n_heads"],
+                                 n_layers=c["n_layers"], d_ff=c["d_ff"], suffix_layers=c["suffix_layers"],
+                                 dual_mlp=c["dual_mlp"])).to(dev)
+    opt = torch.optim.AdamW(model.parameters(), lr=c["lr"], weight_decay=0.0)
+    gen = torch.Generator().manual_seed(1337)
+
+    def it():
+        bt = data.generate_kv_batch(c["batch_size"], c["context_len"], c["query_len"], c["vocab_size"],
+                                    num_keys=c["num_keys"], device=dev, pad_to=c["max_seq_len"],
+                                    far_frac=c["far_frac"], generator=gen)
+        inner, outer = meta.meta_step(model, bt.input_ids, bt.targets, bt.inner_mask, bt.outer_mask,
+                                      inner_lr=c["inner_lr"], inner_steps=c["inner_steps"],
+                                      param_filter=c["ttt_param_filter"], chunk_size=c["chunk_size"])
+        opt.zero_grad(set_to_none=True)
+        outer.backward()
+        opt.step()
+        return inner, outer
+
+    for _ in range(warmup):
+        it()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        inner, outer = it()
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    return {"s_per_it": round(statistics.median(times), 4), "iterations": steps, "warmup": warmup,
+            "inner_loss": round(float(inner), 4), "outer_loss": round(float(outer), 4),
+            "reference_h100_s_per_it": META_8K_H100_S_PER_IT,
+            "config": "meta_8k_v2: b8 T8192 d_model 384 6 heads 8 layers (2 suffix) window 512 chunks 1024, "
+                      "4 inner steps on mlp_fast, fp32, AdamW"}
+
+
 def copy_calibration(mb: int, reps: int = 5) -> None:
     """A plain device copy of `mb` MiB (read mb, write mb), for scaling rocprof's
     FETCH_SIZE / WRITE_SIZE counters to bytes."""
@@ -228,7 +281,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="C3", choices=sorted(workloads.CONFIGS))
+    ap.add_argument("--config", default="C3", choices=sorted(workloads.CONFIGS) + ["META_8K"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the T=16k point and forward-only metrics")
     ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay of the step")
@@ -248,6 +301,16 @@ def main():
     dev = torch.device("cuda", 0)
     if args.copy_mb:
         copy_calibration(args.copy_mb)
+    if args.config == "META_8K":
+        torch.autograd.set_multithreading_enabled(False)
+        r = meta_bench(args.steps, args.warmup, dev)
+        print(json.dumps({"metric": "meta-train s/it (reference TTT model, meta_8k_v2)", "value": r["s_per_it"],
+                          "unit": "s/it", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                          "ms_per_step": round(r["s_per_it"] * 1e3, 2), "higher_is_better": False,
+                          "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+                          "data": "synthetic key-value batches (the reference's generator, restated)",
+                          "config": {"workload": r["config"]}, "meta": r}), flush=True)
+        return
     cfg = workloads.CONFIGS[args.config]
     x = workloads.make_inputs(cfg, seed=0, device=dev)
     step = make_step(cfg, x)
@@ -312,6 +375,8 @@ def main():
             xw = workloads.make_inputs(cw, seed=0, device=dev)
             out[name.lower() + "_ms"] = round(time_steps(make_step(cw, xw), max(5, args.steps // 2), 3), 4)
             del xw
+        # the whole meta-training iteration of the reference TTT model (one GPU)
+        out["meta_8k"] = meta_bench(3, 1, dev)
 
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(cfg)

@@ -32,6 +32,15 @@ def test_library_exports_every_declared_symbol():
     assert lib.ttt_version() >= 200
 
 
+def test_torch_binding_loads():
+    """The torch binding of the fused entry points is built next to the
+    library and exposes them (no call: there is no GPU here)."""
+    mod = _lib.ext()
+    assert os.path.dirname(mod.__file__) == os.path.dirname(_lib.LIB_PATH)
+    for name in ("fwd", "bwd", "gg"):
+        assert callable(getattr(mod, name))
+
+
 def _prob(**kw):
     d = dict(dtype=0, causal=1, batch=1, heads=1, seqlen=128, head_dim=64, scale=0.125, split_chunk=0, window=0,
              window_kind=0)

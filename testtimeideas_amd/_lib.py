@@ -16,6 +16,7 @@ from __future__ import annotations
 import contextlib
 import ctypes
 import dataclasses
+import importlib.util
 import os
 from typing import Dict, List, Optional, Tuple
 
@@ -23,6 +24,10 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libttt_attn.so")
+# torch binding of the three fused entry points (csrc/ttt_torch.cpp): the same
+# C calls with the per-call Python work (views, outputs, workspace, stream)
+# done in C++.  The per-kernel entry points and the launchers stay on ctypes.
+EXT_PATH = os.path.join(_HERE, "_ttt_torch.so")
 
 _DTYPE_CODE = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 
@@ -128,6 +133,24 @@ def load() -> ctypes.CDLL:
     lib.ttt_attn_workspace_size.restype = ctypes.c_int64
     _lib = lib
     return lib
+
+
+_ext_mod = None
+
+
+def ext():
+    """The torch binding module (loaded once, after libttt_attn.so)."""
+    global _ext_mod
+    if _ext_mod is None:
+        load()
+        if not os.path.exists(EXT_PATH):
+            raise ExtensionMissingError(
+                f"{EXT_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'`")
+        spec = importlib.util.spec_from_file_location("testtimeideas_amd._ttt_torch", EXT_PATH)
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        _ext_mod = mod
+    return _ext_mod
 
 
 def _call(name: str, *args) -> None:
@@ -384,6 +407,11 @@ def _empty_like_out(x: torch.Tensor) -> torch.Tensor:
 def fwd(q, k, v, mask, scale: float, want_p: bool):
     """Forward: O, LSE and (save_p) P.  Reference: TritonAttentionFn.forward,
     ttt_kernels/triton_attention.py:261-337 (P path :51-59, :270-273)."""
+    if q.numel() and _timing is None:
+        m = as_mask(mask)
+        o, lse, p = ext().fwd(q, k, v, m.causal, float(scale), bool(want_p), _split_chunk, int(m.window),
+                              int(m.window_kind), m.bias)
+        return o, lse, p
     o = _empty_like_out(q)
     lse = _stats(q)
     p = alloc_p(q) if want_p else None
@@ -400,6 +428,11 @@ def bwd(q, k, v, o, do, lse, p, mask, scale: float):
     """First backward: dQ, dK, dV and the row statistic D = rowsum(dO o O).
     Reference: TritonAttentionFn.backward, triton_attention.py:351-379 and
     :416-420; launchers backward_stubs.py:154-181, 224-255, 362-425."""
+    if q.numel() and _timing is None:
+        m = as_mask(mask)
+        dq, dk, dv, rowsum = ext().bwd(q, k, v, o, do, lse, p, m.causal, float(scale), _split_chunk, int(m.window),
+                                       int(m.window_kind), m.bias)
+        return dq, dk, dv, rowsum
     dq = _empty_like_out(q)
     dk = _empty_like_out(k)
     dv = _empty_like_out(v)
@@ -461,6 +494,12 @@ def rowsum_from_p(p, do, v, mask):
 def gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, mask, scale: float, want_gdo: bool):
     """Double backward: (GQ, GK, GV, GdO or None).  Reference stubs
     backward_stubs.py:539-548; torch version :434-514 (corrected)."""
+    if q.numel() and _timing is None:
+        m = as_mask(mask)
+        gq_out, gk_out, gv_out, gdo = ext().gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, m.causal, float(scale),
+                                               bool(want_gdo), _split_chunk, int(m.window), int(m.window_kind),
+                                               m.bias)
+        return gq_out, gk_out, gv_out, gdo
     gq_out = _empty_like_out(q)
     gk_out = _empty_like_out(k)
     gv_out = _empty_like_out(v)

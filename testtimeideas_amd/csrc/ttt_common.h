@@ -615,6 +615,52 @@ __device__ __forceinline__ void mm_s(f32x4* acc, const T* X, const typename Elem
   }
 }
 
+// mm_s for two or three products over the same tile X (acc_n += y_n . X):
+// each fragment of X is read from LDS once and feeds every product.
+template <typename T, int D>
+__device__ __forceinline__ void mm_s2(f32x4* acc0, const typename Elem<T>::frag* y0, f32x4* acc1,
+                                      const typename Elem<T>::frag* y1, const T* X) {
+  typedef typename Elem<T>::frag frag;
+  constexpr int NB = (TTT_MM_BATCH && sizeof(T) == 2) ? 8 : 1;
+  constexpr int DSN = D / 16;
+#pragma unroll
+  for (int i0 = 0; i0 < 2 * DSN; i0 += NB) {
+    frag x[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) x[i] = load_frag_tr<T, D>(X, 32 * ((i0 + i) / DSN), 16 * ((i0 + i) % DSN));
+    if constexpr (NB > 1) __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int kb = (i0 + i) / DSN, ds = (i0 + i) % DSN;
+      acc0[ds] = Elem<T>::mma(acc0[ds], x[i], y0[kb]);
+      acc1[ds] = Elem<T>::mma(acc1[ds], x[i], y1[kb]);
+    }
+  }
+}
+
+template <typename T, int D>
+__device__ __forceinline__ void mm_s3(f32x4* acc0, const typename Elem<T>::frag* y0, f32x4* acc1,
+                                      const typename Elem<T>::frag* y1, f32x4* acc2,
+                                      const typename Elem<T>::frag* y2, const T* X) {
+  typedef typename Elem<T>::frag frag;
+  constexpr int NB = (TTT_MM_BATCH && sizeof(T) == 2) ? 8 : 1;
+  constexpr int DSN = D / 16;
+#pragma unroll
+  for (int i0 = 0; i0 < 2 * DSN; i0 += NB) {
+    frag x[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) x[i] = load_frag_tr<T, D>(X, 32 * ((i0 + i) / DSN), 16 * ((i0 + i) % DSN));
+    if constexpr (NB > 1) __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int kb = (i0 + i) / DSN, ds = (i0 + i) % DSN;
+      acc0[ds] = Elem<T>::mma(acc0[ds], x[i], y0[kb]);
+      acc1[ds] = Elem<T>::mma(acc1[ds], x[i], y1[kb]);
+      acc2[ds] = Elem<T>::mma(acc2[ds], x[i], y2[kb]);
+    }
+  }
+}
+
 // Half-tile products for kernels that walk a streamed tile in its two 32-row
 // halves (kb = 0, 1; compile-time after unrolling): mm_d_half forms subtiles
 // a = 2kb, 2kb+1 of mm_d's output, mm_s_half adds k-block kb of mm_s.  Work on
@@ -636,6 +682,30 @@ __device__ __forceinline__ void mm_d_half(Tile& out, int kb, const T* rows, cons
   for (int a = 0; a < 2; ++a)
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) out.q[2 * kb + a] = Elem<T>::mma(out.q[2 * kb + a], x[a][ks], sta[ks]);
+}
+
+// mm_d_half for two products over the same rows (out0 from sta0, out1 from
+// sta1), reading each row fragment once.
+template <typename T, int D>
+__device__ __forceinline__ void mm_d2_half(Tile& out0, Tile& out1, int kb, const T* rows,
+                                           const typename Elem<T>::frag* sta0, const typename Elem<T>::frag* sta1) {
+  typedef Lds<T, D> L;
+  typedef typename Elem<T>::frag frag;
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  constexpr int KS = D / 32;
+  frag x[2][KS];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) x[a][ks] = load_frag<T>(rows + L::off(sigma(2 * kb + a, c), 32 * ks + 8 * g));
+  if constexpr (TTT_MM_BATCH && sizeof(T) == 2) __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      out0.q[2 * kb + a] = Elem<T>::mma(out0.q[2 * kb + a], x[a][ks], sta0[ks]);
+      out1.q[2 * kb + a] = Elem<T>::mma(out1.q[2 * kb + a], x[a][ks], sta1[ks]);
+    }
 }
 
 template <typename T, int D>

@@ -29,6 +29,12 @@
 #include "ttt_common.h"
 #include "ttt_launch.h"
 
+// Tiles of K and V a forward kernel loads ahead of the one it computes
+// (measured on MI355X: 2 and 3 were no faster than 1).
+#ifndef TTT_FWD_PREFETCH
+#define TTT_FWD_PREFETCH 1
+#endif
+
 namespace ttt {
 
 // Scores of key tile nb (rows sK) for query row m, in base-2 units; masked
@@ -101,19 +107,24 @@ __global__ __launch_bounds__(kThreads) void k_fwd_online(Params a) {
   for (int i = 0; i < D / 16; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   float mx = -INFINITY, l = 0.f;
 
-  Stage<T, D> stK, stV;
-  stage_load<T, D>(stK, K + (int64_t)cr.t0 * kBlk * a.k.st, a.k.st, T_ - cr.t0 * kBlk, D);
-  stage_load<T, D>(stV, V + (int64_t)cr.t0 * kBlk * a.v.st, a.v.st, T_ - cr.t0 * kBlk, D);
-  for (int nb = cr.t0; nb < cr.t1; ++nb) {
+  // Register stages for the next kPre tiles' K and V (loads issued kPre
+  // tiles ahead of their use).
+  constexpr int kPre = TTT_FWD_PREFETCH;
+  Stage<T, D> stK[kPre], stV[kPre];
+  auto load_kv = [&](int nb, Stage<T, D>& sk, Stage<T, D>& sv) __attribute__((always_inline)) {
+    const int n1 = nb * kBlk;
+    stage_load<T, D>(sk, K + (int64_t)n1 * a.k.st, a.k.st, T_ - n1, D);
+    stage_load<T, D>(sv, V + (int64_t)n1 * a.v.st, a.v.st, T_ - n1, D);
+  };
+#pragma unroll
+  for (int i = 0; i < kPre; ++i)
+    if (i == 0 || cr.t0 + i < cr.t1) load_kv(cr.t0 + i, stK[i], stV[i]);
+  auto tile = [&](int nb, Stage<T, D>& sk, Stage<T, D>& sv) __attribute__((always_inline)) {
     __syncthreads();
-    stage_store_rows<T, D>(stK, sK);
-    stage_store_rows<T, D>(stV, sV);
+    stage_store_rows<T, D>(sk, sK);
+    stage_store_rows<T, D>(sv, sV);
     __syncthreads();
-    if (nb + 1 < cr.t1) {
-      const int n1 = (nb + 1) * kBlk;
-      stage_load<T, D>(stK, K + (int64_t)n1 * a.k.st, a.k.st, T_ - n1, D);
-      stage_load<T, D>(stV, V + (int64_t)n1 * a.v.st, a.v.st, T_ - n1, D);
-    }
+    if (nb + kPre < cr.t1) load_kv(nb + kPre, sk, sv);
     Tile s;
     fwd_scores<T, D, XM>(s, sK, qf, a, mk, brow, nb);
     const float mnew = fmaxf(mx, tile_max(s));
@@ -137,6 +148,11 @@ __global__ __launch_bounds__(kThreads) void k_fwd_online(Params a) {
 #pragma unroll
     for (int i = 0; i < D / 16; ++i) acc[i] *= alpha;
     mm_s<T, D>(acc, sV, pf);
+  };
+  for (int nb = cr.t0; nb < cr.t1; nb += kPre) {
+#pragma unroll
+    for (int i = 0; i < kPre; ++i)
+      if (i == 0 || nb + i < cr.t1) tile(nb + i, stK[i], stV[i]);
   }
 
   l = group_sum(l);
@@ -184,16 +200,20 @@ __global__ __launch_bounds__(kThreads) void k_fwd_stats(Params a) {
   for (int ks = 0; ks < D / 32; ++ks) qf[ks] = load_frag_row<T>(Q, a.q.st, m, T_, 32 * ks + 8 * g);
 
   float mx = -INFINITY, l = 0.f;
-  Stage<T, D> stK;
-  stage_load<T, D>(stK, K + (int64_t)cr.t0 * kBlk * a.k.st, a.k.st, T_ - cr.t0 * kBlk, D);
-  for (int nb = cr.t0; nb < cr.t1; ++nb) {
+  constexpr int kPre = TTT_FWD_PREFETCH;
+  Stage<T, D> stK[kPre];
+  auto load_k = [&](int nb, Stage<T, D>& sk) __attribute__((always_inline)) {
+    const int n1 = nb * kBlk;
+    stage_load<T, D>(sk, K + (int64_t)n1 * a.k.st, a.k.st, T_ - n1, D);
+  };
+#pragma unroll
+  for (int i = 0; i < kPre; ++i)
+    if (i == 0 || cr.t0 + i < cr.t1) load_k(cr.t0 + i, stK[i]);
+  auto tile = [&](int nb, Stage<T, D>& sk) __attribute__((always_inline)) {
     __syncthreads();
-    stage_store_rows<T, D>(stK, sK);
+    stage_store_rows<T, D>(sk, sK);
     __syncthreads();
-    if (nb + 1 < cr.t1) {
-      const int n1 = (nb + 1) * kBlk;
-      stage_load<T, D>(stK, K + (int64_t)n1 * a.k.st, a.k.st, T_ - n1, D);
-    }
+    if (nb + kPre < cr.t1) load_k(nb + kPre, sk);
     Tile s;
     fwd_scores<T, D, XM>(s, sK, qf, a, mk, brow, nb);
     // Per-lane running max and sum over this lane's columns; combined across
@@ -213,6 +233,11 @@ __global__ __launch_bounds__(kThreads) void k_fwd_stats(Params a) {
       for (int j = 0; j < 8; ++j) ts += fast_exp2(s.at(kb, j) - shift);
     l = l * fast_exp2(mx - shift) + ts;
     mx = mnew;
+  };
+  for (int nb = cr.t0; nb < cr.t1; nb += kPre) {
+#pragma unroll
+    for (int i = 0; i < kPre; ++i)
+      if (i == 0 || nb + i < cr.t1) tile(nb + i, stK[i]);
   }
   {
     // Finite without a window (every row sees a key of its first tile); with
@@ -283,19 +308,24 @@ __global__ __launch_bounds__(kThreads) void k_fwd_p(Params a) {
 #pragma unroll
   for (int i = 0; i < D / 16; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  Stage<T, D> stK, stV;
-  stage_load<T, D>(stK, K + (int64_t)cr.t0 * kBlk * a.k.st, a.k.st, T_ - cr.t0 * kBlk, D);
-  stage_load<T, D>(stV, V + (int64_t)cr.t0 * kBlk * a.v.st, a.v.st, T_ - cr.t0 * kBlk, D);
-  for (int nb = cr.t0; nb < cr.t1; ++nb) {
+  // Register stages for the next kPre tiles' K and V (loads issued kPre
+  // tiles ahead of their use).
+  constexpr int kPre = TTT_FWD_PREFETCH;
+  Stage<T, D> stK[kPre], stV[kPre];
+  auto load_kv = [&](int nb, Stage<T, D>& sk, Stage<T, D>& sv) __attribute__((always_inline)) {
+    const int n1 = nb * kBlk;
+    stage_load<T, D>(sk, K + (int64_t)n1 * a.k.st, a.k.st, T_ - n1, D);
+    stage_load<T, D>(sv, V + (int64_t)n1 * a.v.st, a.v.st, T_ - n1, D);
+  };
+#pragma unroll
+  for (int i = 0; i < kPre; ++i)
+    if (i == 0 || cr.t0 + i < cr.t1) load_kv(cr.t0 + i, stK[i], stV[i]);
+  auto tile = [&](int nb, Stage<T, D>& sk, Stage<T, D>& sv) __attribute__((always_inline)) {
     __syncthreads();
-    stage_store_rows<T, D>(stK, sK);
-    stage_store_rows<T, D>(stV, sV);
+    stage_store_rows<T, D>(sk, sK);
+    stage_store_rows<T, D>(sv, sV);
     __syncthreads();
-    if (nb + 1 < cr.t1) {
-      const int n1 = (nb + 1) * kBlk;
-      stage_load<T, D>(stK, K + (int64_t)n1 * a.k.st, a.k.st, T_ - n1, D);
-      stage_load<T, D>(stV, V + (int64_t)n1 * a.v.st, a.v.st, T_ - n1, D);
-    }
+    if (nb + kPre < cr.t1) load_kv(nb + kPre, sk, sv);
     Tile s;
     fwd_scores<T, D, XM>(s, sK, qf, a, mk, brow, nb);
     const int n0 = nb * kBlk;
@@ -318,6 +348,11 @@ __global__ __launch_bounds__(kThreads) void k_fwd_p(Params a) {
       }
     }
     mm_s<T, D>(acc, sV, pf);
+  };
+  for (int nb = cr.t0; nb < cr.t1; nb += kPre) {
+#pragma unroll
+    for (int i = 0; i < kPre; ++i)
+      if (i == 0 || nb + i < cr.t1) tile(nb + i, stK[i], stV[i]);
   }
   if (cr.nch == 1) {
     store_acc_rows<T, D>(at<T>(a.o, b, h), a.o.st, m, T_, acc, 1.f);

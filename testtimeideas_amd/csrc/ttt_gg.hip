@@ -45,6 +45,11 @@
 #ifndef TTT_GG_COL_WAVES_PER_EU
 #define TTT_GG_COL_WAVES_PER_EU TTT_GG_WAVES_PER_EU
 #endif
+// Products that stream the same LDS tile read each fragment once (1) or
+// once per product (0).
+#ifndef TTT_GG_SHARED_READS
+#define TTT_GG_SHARED_READS 1
+#endif
 #ifndef TTT_GG_WIDE_WAVES_PER_EU
 #define TTT_GG_WIDE_WAVES_PER_EU 1
 #endif
@@ -230,13 +235,16 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
       if constexpr (GDO) z4f[kb] = vals_frag<T>(vz4);
     }
     mm_s<T, D>(a1, cgK, dsf);
+#if TTT_GG_SHARED_READS
+    mm_s3<T, D>(a2, z1f, a3, z2f, a4, pf, cK);
+#else
     mm_s<T, D>(a2, cK, z1f);
     mm_s<T, D>(a3, cK, z2f);
     mm_s<T, D>(a4, cK, pf);
+#endif
     if constexpr (GDO) {
       mm_s<T, D>(b1, cgV, pf);
-      mm_s<T, D>(b2, cV, z4f);
-      mm_s<T, D>(b3, cV, pf);
+      mm_s2<T, D>(b2, z4f, b3, pf, cV);
     }
   }
   const float Ev = group_sum(e_acc);
@@ -387,10 +395,14 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_COL_WAVES_PER_EU, true>:
     // elementwise terms, then its contributions to GK and GV.
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
+#if TTT_GG_SHARED_READS
+      mm_d2_half<T, D>(dp, gp1, kb, cb.dout, vf, gvf);
+#else
       mm_d_half<T, D>(dp, kb, cb.dout, vf);
+      mm_d_half<T, D>(gp1, kb, cb.dout, gvf);
+#endif
       mm_d_half<T, D>(gds, kb, cb.gq, kf);
       mm_d_half<T, D>(gds, kb, cb.q, gkf);
-      mm_d_half<T, D>(gp1, kb, cb.dout, gvf);
       float d8[8], e8[8], f8[8];
       stat_read8(d8, cb.st, 0, kb);
       stat_read8(e8, cb.st, 1, kb);

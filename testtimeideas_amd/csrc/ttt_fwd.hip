@@ -34,6 +34,15 @@
 #ifndef TTT_FWD_PREFETCH
 #define TTT_FWD_PREFETCH 1
 #endif
+// Key tiles per barrier round of the statistics pass and of the P pass
+// (measured on MI355X: two make the statistics pass 3 us faster at C3 and
+// leave C5 unchanged; the P pass is slower with two).
+#ifndef TTT_FWD_STATS_TILES
+#define TTT_FWD_STATS_TILES 2
+#endif
+#ifndef TTT_FWD_P_TILES
+#define TTT_FWD_P_TILES 1
+#endif
 
 namespace ttt {
 
@@ -176,7 +185,10 @@ __global__ __launch_bounds__(kThreads) void k_fwd_stats(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
-  __shared__ __align__(16) T sK[L::kRowElems];
+  // R key tiles per round: one pair of barriers and R independent score
+  // products per round.
+  constexpr int R = TTT_FWD_STATS_TILES;
+  __shared__ __align__(16) T sK[R][L::kRowElems];
 
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
@@ -200,44 +212,56 @@ __global__ __launch_bounds__(kThreads) void k_fwd_stats(Params a) {
   for (int ks = 0; ks < D / 32; ++ks) qf[ks] = load_frag_row<T>(Q, a.q.st, m, T_, 32 * ks + 8 * g);
 
   float mx = -INFINITY, l = 0.f;
-  constexpr int kPre = TTT_FWD_PREFETCH;
-  Stage<T, D> stK[kPre];
+  Stage<T, D> stK[R];
+  // Tiles past the chunk load its last tile again (unconditional loads; the
+  // round masks them out).
   auto load_k = [&](int nb, Stage<T, D>& sk) __attribute__((always_inline)) {
-    const int n1 = nb * kBlk;
+    const int n1 = (nb < cr.t1 ? nb : cr.t1 - 1) * kBlk;
     stage_load<T, D>(sk, K + (int64_t)n1 * a.k.st, a.k.st, T_ - n1, D);
   };
 #pragma unroll
-  for (int i = 0; i < kPre; ++i)
-    if (i == 0 || cr.t0 + i < cr.t1) load_k(cr.t0 + i, stK[i]);
-  auto tile = [&](int nb, Stage<T, D>& sk) __attribute__((always_inline)) {
+  for (int i = 0; i < R; ++i) load_k(cr.t0 + i, stK[i]);
+  for (int nb = cr.t0; nb < cr.t1; nb += R) {
     __syncthreads();
-    stage_store_rows<T, D>(sk, sK);
+#pragma unroll
+    for (int i = 0; i < R; ++i) stage_store_rows<T, D>(stK[i], sK[i]);
     __syncthreads();
-    if (nb + kPre < cr.t1) load_k(nb + kPre, sk);
-    Tile s;
-    fwd_scores<T, D, XM>(s, sK, qf, a, mk, brow, nb);
+    if (nb + R < cr.t1) {
+#pragma unroll
+      for (int i = 0; i < R; ++i) load_k(nb + R + i, stK[i]);
+    }
+    Tile s[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      fwd_scores<T, D, XM>(s[i], sK[i], qf, a, mk, brow, nb + i);
+      if (i > 0 && nb + i >= cr.t1) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) s[i].set(kb, j, -INFINITY);
+      }
+    }
     // Per-lane running max and sum over this lane's columns; combined across
     // the four lane groups after the loop.  A lane whose columns are all
     // masked so far keeps max -inf and sum 0 (shift by 0 avoids -inf - -inf).
     float tmax = -INFINITY;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int i = 0; i < R; ++i)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) tmax = fmaxf(tmax, s.at(kb, j));
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) tmax = fmaxf(tmax, s[i].at(kb, j));
     const float mnew = fmaxf(mx, tmax);
     const float shift = mnew == -INFINITY ? 0.f : mnew;
     float ts = 0.f;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int i = 0; i < R; ++i)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) ts += fast_exp2(s.at(kb, j) - shift);
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ts += fast_exp2(s[i].at(kb, j) - shift);
     l = l * fast_exp2(mx - shift) + ts;
     mx = mnew;
-  };
-  for (int nb = cr.t0; nb < cr.t1; nb += kPre) {
-#pragma unroll
-    for (int i = 0; i < kPre; ++i)
-      if (i == 0 || nb + i < cr.t1) tile(nb + i, stK[i]);
   }
   {
     // Finite without a window (every row sees a key of its first tile); with
@@ -262,8 +286,10 @@ __global__ __launch_bounds__(kThreads) void k_fwd_p(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
-  __shared__ __align__(16) T sK[L::kRowElems];
-  __shared__ __align__(16) T sV[L::kRowElems];
+  // R key tiles per barrier round (as in k_fwd_stats).
+  constexpr int R = TTT_FWD_P_TILES;
+  __shared__ __align__(16) T sK[R][L::kRowElems];
+  __shared__ __align__(16) T sV[R][L::kRowElems];
 
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
@@ -308,51 +334,54 @@ __global__ __launch_bounds__(kThreads) void k_fwd_p(Params a) {
 #pragma unroll
   for (int i = 0; i < D / 16; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Register stages for the next kPre tiles' K and V (loads issued kPre
-  // tiles ahead of their use).
-  constexpr int kPre = TTT_FWD_PREFETCH;
-  Stage<T, D> stK[kPre], stV[kPre];
+  Stage<T, D> stK[R], stV[R];
+  // Tiles past the chunk load its last tile again (unconditional loads); their
+  // P is neither stored nor accumulated.
   auto load_kv = [&](int nb, Stage<T, D>& sk, Stage<T, D>& sv) __attribute__((always_inline)) {
-    const int n1 = nb * kBlk;
+    const int n1 = (nb < cr.t1 ? nb : cr.t1 - 1) * kBlk;
     stage_load<T, D>(sk, K + (int64_t)n1 * a.k.st, a.k.st, T_ - n1, D);
     stage_load<T, D>(sv, V + (int64_t)n1 * a.v.st, a.v.st, T_ - n1, D);
   };
 #pragma unroll
-  for (int i = 0; i < kPre; ++i)
-    if (i == 0 || cr.t0 + i < cr.t1) load_kv(cr.t0 + i, stK[i], stV[i]);
-  auto tile = [&](int nb, Stage<T, D>& sk, Stage<T, D>& sv) __attribute__((always_inline)) {
+  for (int i = 0; i < R; ++i) load_kv(cr.t0 + i, stK[i], stV[i]);
+  for (int nb = cr.t0; nb < cr.t1; nb += R) {
     __syncthreads();
-    stage_store_rows<T, D>(sk, sK);
-    stage_store_rows<T, D>(sv, sV);
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      stage_store_rows<T, D>(stK[i], sK[i]);
+      stage_store_rows<T, D>(stV[i], sV[i]);
+    }
     __syncthreads();
-    if (nb + kPre < cr.t1) load_kv(nb + kPre, sk, sv);
-    Tile s;
-    fwd_scores<T, D, XM>(s, sK, qf, a, mk, brow, nb);
-    const int n0 = nb * kBlk;
-    frag pf[2];
+    if (nb + R < cr.t1) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      float pv[8];
+      for (int i = 0; i < R; ++i) load_kv(nb + R + i, stK[i], stV[i]);
+    }
 #pragma unroll
-      for (int j = 0; j < 8; ++j) pv[j] = E::f32(E::cvt(fast_exp2(s.at(kb, j) - lse2)));
-      pf[kb] = vals_frag<T>(pv);
-      if (m < T_) {
-        const int n = n0 + stream_index(kb, g, 0);
-        if (n + 8 <= T_) {
-          store8<T>(Pm + n, pv);
-        } else {
+    for (int i = 0; i < R; ++i) {
+      const bool valid = i == 0 || nb + i < cr.t1;
+      Tile s;
+      fwd_scores<T, D, XM>(s, sK[i], qf, a, mk, brow, nb + i);
+      const int n0 = (nb + i) * kBlk;
+      frag pf[2];
 #pragma unroll
-          for (int j = 0; j < 8; ++j)
-            if (n + j < T_) Pm[n + j] = E::cvt(pv[j]);
+      for (int kb = 0; kb < 2; ++kb) {
+        float pv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pv[j] = valid ? E::f32(E::cvt(fast_exp2(s.at(kb, j) - lse2))) : 0.f;
+        pf[kb] = vals_frag<T>(pv);
+        if (valid && m < T_) {
+          const int n = n0 + stream_index(kb, g, 0);
+          if (n + 8 <= T_) {
+            store8<T>(Pm + n, pv);
+          } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+              if (n + j < T_) Pm[n + j] = E::cvt(pv[j]);
+          }
         }
       }
+      mm_s<T, D>(acc, sV[i], pf);
     }
-    mm_s<T, D>(acc, sV, pf);
-  };
-  for (int nb = cr.t0; nb < cr.t1; nb += kPre) {
-#pragma unroll
-    for (int i = 0; i < kPre; ++i)
-      if (i == 0 || nb + i < cr.t1) tile(nb + i, stK[i], stV[i]);
   }
   if (cr.nch == 1) {
     store_acc_rows<T, D>(at<T>(a.o, b, h), a.o.st, m, T_, acc, 1.f);

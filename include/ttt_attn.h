@@ -141,6 +141,15 @@ const char* ttt_last_error(void);
 int64_t ttt_attn_workspace_size(const ttt_problem* pr, int32_t entry, int32_t want_gdout);
 
 /*
+ * The split a single-family entry (FWD, FWD_P, BWD_DQ, BWD_DKDV, GG_ROW,
+ * GG_COL) would use for this problem on the current device: tiles per
+ * workgroup, chunks of the longest block, and the workgroup slots assumed.
+ * Any output pointer may be NULL.  Diagnostics; no reference counterpart.
+ */
+int ttt_attn_split_info(const ttt_problem* pr, int32_t entry, int32_t load_p, int32_t want_gdout,
+                        int32_t* chunk, int32_t* nchunk_max, int64_t* slots);
+
+/*
  * Forward.  Writes O and lse; if p != NULL (and p->data != NULL) also writes
  * P = softmax(S) rounded to the input dtype, and computes O from that rounded
  * P (two passes over K: row statistics, then P and P*V).  With p == NULL it

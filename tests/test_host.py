@@ -175,6 +175,16 @@ def test_window_workspace_matches_brute_force_ranges(t, window, kind):
     assert _block_tiles(640, True) == list(range(10, 0, -1)) == _block_tiles(640, True, col=True)
 
 
+def test_split_info_matches_workspace():
+    """ttt_attn_split_info reports the split the workspace is sized for (no
+    GPU here: 256 CUs x 2 workgroups, 90 % usable)."""
+    pr = _prob(seqlen=8192)
+    assert _lib.split_info(pr, _lib.ENTRY_GG_ROW, True) == (21, 7, 460)
+    assert _lib.workspace_bytes(pr, _lib.ENTRY_GG_ROW) == 128 * 7 * 64 * (4 * 64 + 3) * 4
+    with pytest.raises(RuntimeError, match="single kernel family"):
+        _lib.split_info(pr, _lib.ENTRY_GG, True)
+
+
 def test_window_and_bias_validation():
     lib = _lib.load()
     assert _fwd_rc(_prob(window=-1)) == 1

@@ -131,6 +131,9 @@ def load() -> ctypes.CDLL:
     lib.ttt_version.restype = ctypes.c_int
     lib.ttt_attn_workspace_size.argtypes = [_P(_Problem), ctypes.c_int32, ctypes.c_int32]
     lib.ttt_attn_workspace_size.restype = ctypes.c_int64
+    lib.ttt_attn_split_info.argtypes = [_P(_Problem), ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                        _P(ctypes.c_int32), _P(ctypes.c_int32), _P(ctypes.c_int64)]
+    lib.ttt_attn_split_info.restype = ctypes.c_int
     _lib = lib
     return lib
 
@@ -527,6 +530,15 @@ def gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, mask, scale: float, want_gdo: bo
     return gq_out, gk_out, gv_out, gdo
 
 
+def split_info(pr: _Problem, entry: int, load_p: bool, gdo: bool = False) -> Tuple[int, int, int]:
+    """(tiles per workgroup, chunks of the longest block, workgroup slots) the
+    library would use for `entry` on the current device."""
+    c, n, sl = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64()
+    _call("ttt_attn_split_info", ctypes.byref(pr), entry, 1 if load_p else 0, 1 if gdo else 0, ctypes.byref(c),
+          ctypes.byref(n), ctypes.byref(sl))
+    return c.value, n.value, sl.value
+
+
 def exported_symbols() -> List[str]:
     """Names of the C entry points this binding uses (for ABI checks)."""
-    return list(_SIGS) + ["ttt_last_error", "ttt_version", "ttt_attn_workspace_size"]
+    return list(_SIGS) + ["ttt_last_error", "ttt_version", "ttt_attn_workspace_size", "ttt_attn_split_info"]

@@ -382,6 +382,18 @@ int64_t ttt_attn_workspace_size(const ttt_problem* pr, int32_t entry, int32_t wa
   return entry_bytes(pr, entry, want_gdout != 0);
 }
 
+int ttt_attn_split_info(const ttt_problem* pr, int32_t entry, int32_t load_p, int32_t want_gdout, int32_t* chunk,
+                        int32_t* nchunk_max, int64_t* slots) {
+  TRY(check_problem(pr));
+  const int fam = family_of(entry, want_gdout != 0);
+  if (fam < 0) return fail(TTT_ERR_INVALID_ARGUMENT, "entry %d is not a single kernel family", entry);
+  const Split s = choose_split(pr, fam, load_p != 0);
+  if (chunk) *chunk = s.chunk;
+  if (nchunk_max) *nchunk_max = s.nchunk_max;
+  if (slots) *slots = family_slots(pr, fam, load_p != 0);
+  return TTT_OK;
+}
+
 int ttt_attn_fwd(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
                  const ttt_view* o, float* lse, const ttt_view* p, void* workspace, int64_t workspace_bytes,
                  void* stream) {

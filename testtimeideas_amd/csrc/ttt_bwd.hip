@@ -124,7 +124,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dq(Params a) {
     if constexpr (!LOADP) {
       p.zero();
       mm_d<T, D>(p, sK, qf);
-      recompute_p_row<T, XM>(p, a, brow, n0, lse2);
+      recompute_p_row<T, XM>(p, a, brow, n0, lse2, a.scale_log2);
     }
     if (mk.tile(nb)) {
 #pragma unroll
@@ -236,7 +236,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dkdv(Params a) {
     } else {
       p.zero();
       mm_d<T, D>(p, sQ, kf);
-      recompute_p_col<T, XM>(p, a, bcol, m0, sS, kSL);
+      recompute_p_col<T, XM>(p, a, bcol, m0, sS, kSL, a.scale_log2);
     }
     if (mk.tile(mb)) {
 #pragma unroll

@@ -902,14 +902,17 @@ __device__ __forceinline__ void load_vec8(float* v, const float* src, int idx0, 
 // ---------------------------------------------------------------------------
 // P = exp2(s*log2e*x [+ bias*log2e] - lse2) from raw scores x of a row-block
 // tile (brow: this lane's bias row, or nullptr).
+// sl2 converts raw scores to base-2 units: s*log2(e), or log2(e) when the
+// stationary fragments were scaled by s beforehand.
 template <typename T, bool XM>
-__device__ __forceinline__ void recompute_p_row(Tile& p, const Params& a, const T* brow, int n0, float lse2) {
+__device__ __forceinline__ void recompute_p_row(Tile& p, const Params& a, const T* brow, int n0, float lse2,
+                                                float sl2) {
   if constexpr (XM) {
     if (brow) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) p.set(kb, j, p.at(kb, j) * a.scale_log2);
+        for (int j = 0; j < 8; ++j) p.set(kb, j, p.at(kb, j) * sl2);
       add_bias_row<T>(p, brow, n0, a.T);
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -921,20 +924,20 @@ __device__ __forceinline__ void recompute_p_row(Tile& p, const Params& a, const 
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) p.set(kb, j, fast_exp2(p.at(kb, j) * a.scale_log2 - lse2));
+    for (int j = 0; j < 8; ++j) p.set(kb, j, fast_exp2(p.at(kb, j) * sl2 - lse2));
 }
 
 // The same for a column-block tile: l2 holds lse2 of the streamed rows of
 // k-block kb; bcol is this lane's bias column (or nullptr).
 template <typename T, bool XM>
 __device__ __forceinline__ void recompute_p_col(Tile& p, const Params& a, const T* bcol, int m0, const float* sS,
-                                                int slot) {
+                                                int slot, float sl2) {
   if constexpr (XM) {
     if (bcol) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) p.set(kb, j, p.at(kb, j) * a.scale_log2);
+        for (int j = 0; j < 8; ++j) p.set(kb, j, p.at(kb, j) * sl2);
       add_bias_col<T>(p, bcol, a.bias.st, m0, a.T);
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
@@ -951,8 +954,17 @@ __device__ __forceinline__ void recompute_p_col(Tile& p, const Params& a, const 
     float l2[8];
     stat_read8(l2, sS, slot, kb);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) p.set(kb, j, fast_exp2(p.at(kb, j) * a.scale_log2 - l2[j] * kLog2e));
+    for (int j = 0; j < 8; ++j) p.set(kb, j, fast_exp2(p.at(kb, j) * sl2 - l2[j] * kLog2e));
   }
+}
+
+// A fragment with every element multiplied by s (rounded to the element type).
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::frag scale_frag(typename Elem<T>::frag f, float s) {
+  float v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = Elem<T>::f32(f[j]) * s;
+  return vals_frag<T>(v);
 }
 
 }  // namespace ttt

@@ -45,6 +45,12 @@
 #ifndef TTT_GG_COL_WAVES_PER_EU
 #define TTT_GG_COL_WAVES_PER_EU TTT_GG_WAVES_PER_EU
 #endif
+// The stationary Q, gQ (row pass) and K, gK (column pass) fragments are
+// scaled by s once (1), so the score products come out in units of s and the
+// per-element multiplications by s drop out, or not (0).
+#ifndef TTT_GG_PRESCALE
+#define TTT_GG_PRESCALE 1
+#endif
 // Products that stream the same LDS tile read each fragment once (1) or
 // once per product (0).
 #ifndef TTT_GG_SHARED_READS
@@ -108,6 +114,10 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
   for (int ks = 0; ks < D / 32; ++ks) {
     qf[ks] = load_frag_row<T>(Q, a.q.st, m, T_, 32 * ks + 8 * g);
     gqf[ks] = load_frag_row<T>(gQ, a.gq.st, m, T_, 32 * ks + 8 * g);
+    if constexpr (TTT_GG_PRESCALE) {
+      qf[ks] = scale_frag<T>(qf[ks], a.scale);
+      gqf[ks] = scale_frag<T>(gqf[ks], a.scale);
+    }
     dof[ks] = load_frag_row<T>(dO, a.dout.st, m, T_, 32 * ks + 8 * g);
   }
   const int64_t ridx = (int64_t)bh * T_ + m;
@@ -115,6 +125,7 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
   const float lse2 = (!LOADP && row_ok) ? a.lse[ridx] * kLog2e : 0.f;
   const T* Pm = LOADP ? at<const T>(a.p, b, h) + (int64_t)(row_ok ? m : 0) * a.p.st : nullptr;
   const float s = a.scale;
+  const float kSl2 = TTT_GG_PRESCALE ? kLog2e : a.scale_log2;  // raw score -> base 2
 
   f32x4 a1[D / 16], a2[D / 16], a3[D / 16], a4[D / 16];
   f32x4 b1[GDO ? D / 16 : 1], b2[GDO ? D / 16 : 1], b3[GDO ? D / 16 : 1];
@@ -191,7 +202,7 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
     if constexpr (!LOADP) {
       p.zero();
       mm_d<T, D>(p, cK, qf);
-      recompute_p_row<T, XM>(p, a, brow, n0, lse2);
+      recompute_p_row<T, XM>(p, a, brow, n0, lse2, kSl2);
     }
     if (mk.tile(nb)) {
 #pragma unroll
@@ -215,11 +226,11 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float P = p.at(kb, j);
-        const float gd = s * gds.at(kb, j);
+        const float gd = TTT_GG_PRESCALE ? gds.at(kb, j) : s * gds.at(kb, j);
         const float dpv = dp.at(kb, j);
-        const float ds = P * (dpv - Dm);
-        const float z1 = P * gp1.at(kb, j) + gd * ds;
         const float z2 = P * dpv;
+        const float ds = z2 - P * Dm;  // P o (dP - D)
+        const float z1 = P * gp1.at(kb, j) + gd * ds;
         e_acc += gd * P;
         x_acc += z1;
         d_acc += z2;
@@ -351,12 +362,17 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_COL_WAVES_PER_EU, true>:
   const float* fv = a.f + (int64_t)bh * T_;
   const float* lse = LOADP ? nullptr : a.lse + (int64_t)bh * T_;
   const float s = a.scale;
+  const float kSl2 = TTT_GG_PRESCALE ? kLog2e : a.scale_log2;  // raw score -> base 2
 
   frag kf[D / 32], gkf[D / 32], vf[D / 32], gvf[D / 32];
 #pragma unroll
   for (int ks = 0; ks < D / 32; ++ks) {
     kf[ks] = load_frag_row<T>(K, a.k.st, n, T_, 32 * ks + 8 * g);
     gkf[ks] = load_frag_row<T>(gK, a.gk.st, n, T_, 32 * ks + 8 * g);
+    if constexpr (TTT_GG_PRESCALE) {
+      kf[ks] = scale_frag<T>(kf[ks], a.scale);
+      gkf[ks] = scale_frag<T>(gkf[ks], a.scale);
+    }
     vf[ks] = load_frag_row<T>(V, a.v.st, n, T_, 32 * ks + 8 * g);
     gvf[ks] = load_frag_row<T>(gV, a.gv.st, n, T_, 32 * ks + 8 * g);
   }
@@ -379,7 +395,7 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_COL_WAVES_PER_EU, true>:
     } else {
       p.zero();
       mm_d<T, D>(p, cb.q, kf);
-      recompute_p_col<T, XM>(p, a, bcol, m0, cb.st, 3);
+      recompute_p_col<T, XM>(p, a, bcol, m0, cb.st, 3, kSl2);
     }
     if (mk.tile(mb)) {
 #pragma unroll
@@ -412,7 +428,7 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_COL_WAVES_PER_EU, true>:
       for (int j = 0; j < 8; ++j) {
         const float P = p.at(kb, j);
         const float dpv = dp.at(kb, j);
-        const float gd = s * gds.at(kb, j);
+        const float gd = TTT_GG_PRESCALE ? gds.at(kb, j) : s * gds.at(kb, j);
         const float dmd = dpv - d8[j];
         const float gp = gp1.at(kb, j) + gd * dmd - e8[j] * dpv;
         vds[j] = P * dmd;

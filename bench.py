@@ -43,7 +43,14 @@ def _two_stage_sum(t: torch.Tensor) -> torch.Tensor:
     return t.reshape(256, -1).sum(1).sum()
 
 
-def make_step(cfg: workloads.Config, x, graph_safe: bool = False):
+def make_step(cfg: workloads.Config, x, graph_safe: bool = False, scalar_loss: bool = False):
+    """One step: O, then (dQ, dK, dV) with create_graph=True, then the
+    gradient of sum(dQ*rq + dK*rk + dV*rv) with respect to (q, k, v).  By
+    default that last gradient is asked for as the vector-Jacobian product of
+    (dQ, dK, dV) with cotangents (rq, rk, rv), which is the same gradient
+    (the sum is linear in dQ, dK, dV with those coefficients) and launches
+    only the attention kernels; `scalar_loss` instead forms the scalar with
+    torch products and reductions and differentiates it, as a script would."""
     q, k, v = (x[n].requires_grad_(True) for n in ("q", "k", "v"))
     do, rq, rk, rv = x["do"], x["rq"], x["rk"], x["rv"]
     red = _two_stage_sum if graph_safe else torch.sum
@@ -58,6 +65,8 @@ def make_step(cfg: workloads.Config, x, graph_safe: bool = False):
         dq, dk, dv = torch.autograd.grad(o, (q, k, v), do, create_graph=cfg.gradgrad)
         if not cfg.gradgrad:
             return (dq,)
+        if not scalar_loss:
+            return torch.autograd.grad((dq, dk, dv), (q, k, v), (rq, rk, rv))
         s = red(dq * rq) + red(dk * rk) + red(dv * rv)
         return torch.autograd.grad(s, (q, k, v))
 
@@ -319,6 +328,8 @@ def main():
     # kernels take at this size.  The work done per step is the same.
     torch.autograd.set_multithreading_enabled(False)
     ms = time_steps(step, args.steps, args.warmup)
+    # the same step with the scalar sum(dQ*rq + dK*rk + dV*rv) formed and differentiated
+    ms_scalar = time_steps(make_step(cfg, x, scalar_loss=True), args.steps, args.warmup) if cfg.gradgrad else None
     ktimes = kernel_times(step)
     graph_ms = graph_steps(cfg, x, args.steps, args.warmup) if not args.no_graph else None
     roof = workloads.roofline_us(cfg)
@@ -347,6 +358,7 @@ def main():
         "step_roofline_us": round(roof["roofline_us"], 2),
         "step_roofline_frac": round(roof["roofline_us"] * 1e-3 / ms, 5),
         "graph_ms_per_step": None if graph_ms is None else round(graph_ms, 4),
+        "scalar_loss_ms_per_step": None if ms_scalar is None else round(ms_scalar, 4),
         "kernel_us": {k: round(v * 1e3, 2) for k, v in sorted(ktimes.items())},
         "kernel_sum_us": round(sum(ktimes.values()) * 1e3, 2),
         "roofline": roofline_entry(cfg, ktimes),

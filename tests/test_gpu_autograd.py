@@ -159,3 +159,22 @@ def test_c1_golden_fixture_fp32():
     got = _gpu_step(xs, False, None, "save_p_triton_full", do_requires_grad=True)
     for n in ("o", "dq", "dk", "dv", "gq", "gk", "gv", "gdo"):
         check(n, got[n], f[f"out_{n}"], torch.float32)
+
+
+@pytest.mark.parametrize("mode", ["save_p_triton_full", "recompute"])
+def test_cotangent_form_equals_scalar_loss(mode):
+    """The gradient of sum(dQ*rq + dK*rk + dV*rv) asked for as the
+    vector-Jacobian product of (dQ, dK, dV) with cotangents (rq, rk, rv) is
+    the gradient of the scalar: the scalar's backward hands the double
+    backward 1*rq, 1*rk, 1*rv, which are rq, rk, rv exactly, so the two
+    results agree bitwise."""
+    print(f"cotangent form mode={mode}", flush=True)
+    q, k, v, do, rq, rk, rv = (x.cuda() for x in _inputs(1, 2, 384, 64, torch.float16, seed=5))
+    q, k, v = (t.requires_grad_(True) for t in (q, k, v))
+    o = triton_attention(q, k, v, causal=True, bwd_mode=mode)
+    dq, dk, dv = torch.autograd.grad(o, (q, k, v), do, create_graph=True)
+    vjp = torch.autograd.grad((dq, dk, dv), (q, k, v), (rq, rk, rv), retain_graph=True)
+    s = (dq * rq).sum() + (dk * rk).sum() + (dv * rv).sum()
+    scalar = torch.autograd.grad(s, (q, k, v))
+    for name, a, b in zip(("gq", "gk", "gv"), vjp, scalar):
+        assert torch.equal(a, b), name

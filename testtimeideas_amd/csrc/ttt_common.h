@@ -482,6 +482,20 @@ __device__ __forceinline__ void load_p_frags(typename Elem<T>::frag* f, const T*
   }
 }
 
+// The same fragments through a running pointer: pl = this lane's row of P at
+// column n0 + stream_index(0, g, 0).  Full tiles load from pl directly; the
+// ragged last tile clamps as load_p_frags (row pointer pm).
+template <typename T>
+__device__ __forceinline__ void load_p_frags_run(typename Elem<T>::frag* f, const T* pl, const T* pm, int n0,
+                                                 int T_) {
+  if (n0 + kBlk <= T_) {
+    f[0] = load_frag<T>(pl);
+    f[1] = load_frag<T>(pl + 32);
+  } else {
+    load_p_frags<T>(f, pm, n0, T_);
+  }
+}
+
 // Additive bias, in base-2 units, onto a streamed tile of a row-block kernel:
 // row pointer brow (this lane's stationary row), columns as load_p_frags
 // (same row-storage contract as P).
@@ -813,8 +827,10 @@ struct TileDma {  // for the unpadded (chunk-permuted) layout only: Lds<T, NCOL>
   static constexpr int kPerWave = kInstr / 4;
   static_assert(kPerWave * 4 == kInstr, "tile shape");
   int row[kPerWave], col[kPerWave];  // this lane's logical row and first column per instruction
+  int wslice;                         // 1024 * wave index, uniform
   __device__ __forceinline__ TileDma() {
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    wslice = 1024 * __builtin_amdgcn_readfirstlane(w);
 #pragma unroll
     for (int q = 0; q < kPerWave; ++q) {
       const int byte = 1024 * (w + 4 * q) + 16 * lane;
@@ -823,32 +839,41 @@ struct TileDma {  // for the unpadded (chunk-permuted) layout only: Lds<T, NCOL>
       col[q] = (((byte % kRowBytes) / 16) ^ L::swz(r)) * L::kChunk;
     }
   }
-  // Element offsets (row stride ld) of this lane's fetches for an interior tile.
+  // Byte offsets (row stride ld elements) of this lane's fetches for an
+  // interior tile.
   __device__ __forceinline__ void offsets(int* off, int64_t ld) const {
 #pragma unroll
-    for (int q = 0; q < kPerWave; ++q) off[q] = (int)((int64_t)row[q] * ld + col[q]);
+    for (int q = 0; q < kPerWave; ++q) off[q] = (int)(((int64_t)row[q] * ld + col[q]) * (int64_t)sizeof(T));
   }
   // Issue the loads of the tile at g into lds.  `off` from offsets(); ragged
   // tiles (uniform) recompute them with row/column clamping.
   __device__ __forceinline__ void load(T* lds, const T* g, const int* off, int64_t ld, int rows_valid,
                                        int cols_valid) const {
-    const int w = threadIdx.x >> 6;
-    const bool ragged = rows_valid < kBlk || cols_valid < NCOL;
+    if (rows_valid < kBlk || cols_valid < NCOL)
+      load_ragged(lds, g, ld, rows_valid, cols_valid);
+    else
+      load_full(lds, g, off);
+  }
+  // An interior tile (every row and column valid).
+  __device__ __forceinline__ void load_full(T* lds, const T* g, const int* off) const {
+#pragma unroll
+    for (int q = 0; q < kPerWave; ++q) issue(lds, g, off[q], q);
+  }
+  __device__ __forceinline__ void load_ragged(T* lds, const T* g, int64_t ld, int rows_valid, int cols_valid) const {
 #pragma unroll
     for (int q = 0; q < kPerWave; ++q) {
-      int o = off[q];
-      if (ragged) {
-        const int r = row[q] < rows_valid ? row[q] : 0;
-        const int c = col[q] < cols_valid ? col[q] : 0;
-        o = (int)((int64_t)r * ld + c);
-      }
-#if defined(__HIP_DEVICE_COMPILE__)  // the builtin exists only for the gfx950 target
-      // uniform base + unsigned 32-bit byte offset: the saddr + voffset form
-      const char* src = reinterpret_cast<const char*>(g) + (uint32_t)o * (uint32_t)sizeof(T);
-      __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(reinterpret_cast<char*>(lds) + 1024 * (w + 4 * q)), 16,
-                                       0, 0);
-#endif
+      const int r = row[q] < rows_valid ? row[q] : 0;
+      const int c = col[q] < cols_valid ? col[q] : 0;
+      issue(lds, g, (int)(((int64_t)r * ld + c) * (int64_t)sizeof(T)), q);
     }
+  }
+  // One 16-byte-per-lane load into the 1 KB slice (wave + 4q) of lds, in the
+  // saddr + voffset form: uniform base g, unsigned 32-bit byte offset.
+  __device__ __forceinline__ void issue(T* lds, const T* g, int byte_off, int q) const {
+#if defined(__HIP_DEVICE_COMPILE__)  // the builtin exists only for the gfx950 target
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(g) + (uint32_t)byte_off,
+                                     (lds_void_t*)(reinterpret_cast<char*>(lds) + wslice + 4096 * q), 16, 0, 0);
+#endif
   }
 };
 

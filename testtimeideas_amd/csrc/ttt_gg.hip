@@ -136,15 +136,31 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
   }
   float e_acc = 0.f, x_acc = 0.f, d_acc = 0.f;
 
+  // Tiles are fetched in order t0, t0 + 1, ... through running pointers
+  // (advanced one tile per fetch) rather than from the tile index.
+  const int64_t t0r = (int64_t)cr.t0 * kBlk;
+  const T* Kn = K + t0r * a.k.st;
+  const T* Vn = V + t0r * a.v.st;
+  const T* gKn = gK + t0r * a.gk.st;
+  const T* gVn = gV + t0r * a.gv.st;
+  const T* Pn = LOADP ? Pm + t0r + stream_index(0, g, 0) : nullptr;
+  auto advance = [&]() {
+    Kn += kBlk * a.k.st;
+    Vn += kBlk * a.v.st;
+    gKn += kBlk * a.gk.st;
+    gVn += kBlk * a.gv.st;
+    if constexpr (LOADP) Pn += kBlk;
+  };
   Stage<T, D> s0, s1, s2, s3;  // register staging (not kDma)
   frag pn[2];
   auto load_tile = [&](int nb) {
     const int n0 = nb * kBlk;
-    stage_load<T, D>(s0, K + (int64_t)n0 * a.k.st, a.k.st, T_ - n0, D);
-    stage_load<T, D>(s1, V + (int64_t)n0 * a.v.st, a.v.st, T_ - n0, D);
-    stage_load<T, D>(s2, gK + (int64_t)n0 * a.gk.st, a.gk.st, T_ - n0, D);
-    stage_load<T, D>(s3, gV + (int64_t)n0 * a.gv.st, a.gv.st, T_ - n0, D);
-    if constexpr (LOADP) load_p_frags<T>(pn, Pm, n0, T_);
+    stage_load<T, D>(s0, Kn, a.k.st, T_ - n0, D);
+    stage_load<T, D>(s1, Vn, a.v.st, T_ - n0, D);
+    stage_load<T, D>(s2, gKn, a.gk.st, T_ - n0, D);
+    stage_load<T, D>(s3, gVn, a.gv.st, T_ - n0, D);
+    if constexpr (LOADP) load_p_frags_run<T>(pn, Pn, Pm, n0, T_);
+    advance();
   };
   TileDma<T, D> dd;
   int oK[TileDma<T, D>::kPerWave], oV[TileDma<T, D>::kPerWave];
@@ -152,11 +168,23 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
   auto dma_tile = [&](int nb, int buf) {
     if constexpr (kDma) {
       const int n0 = nb * kBlk;
-      dd.load(sK[buf], K + (int64_t)n0 * a.k.st, oK, a.k.st, T_ - n0, D);
-      dd.load(sV[buf], V + (int64_t)n0 * a.v.st, oV, a.v.st, T_ - n0, D);
-      dd.load(sgK[buf], gK + (int64_t)n0 * a.gk.st, ogK, a.gk.st, T_ - n0, D);
-      dd.load(sgV[buf], gV + (int64_t)n0 * a.gv.st, ogV, a.gv.st, T_ - n0, D);
-      if constexpr (LOADP) load_p_frags<T>(pn, Pm, n0, T_);
+      if (n0 + kBlk <= T_) {  // uniform: one test per tile for all four tiles and P
+        dd.load_full(sK[buf], Kn, oK);
+        dd.load_full(sV[buf], Vn, oV);
+        dd.load_full(sgK[buf], gKn, ogK);
+        dd.load_full(sgV[buf], gVn, ogV);
+        if constexpr (LOADP) {
+          pn[0] = load_frag<T>(Pn);
+          pn[1] = load_frag<T>(Pn + 32);
+        }
+      } else {
+        dd.load_ragged(sK[buf], Kn, a.k.st, T_ - n0, D);
+        dd.load_ragged(sV[buf], Vn, a.v.st, T_ - n0, D);
+        dd.load_ragged(sgK[buf], gKn, a.gk.st, T_ - n0, D);
+        dd.load_ragged(sgV[buf], gVn, a.gv.st, T_ - n0, D);
+        if constexpr (LOADP) load_p_frags<T>(pn, Pm, n0, T_);
+      }
+      advance();
     }
   };
   if constexpr (kDma) {
@@ -451,13 +479,32 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_COL_WAVES_PER_EU, true>:
     dd.offsets(ogQ, a.gq.st);
     dd.offsets(odO, a.dout.st);
     if constexpr (LOADP) dpt.offsets(oP, a.p.st);
+    // Tiles are fetched in order t0, t0 + 1, ... through running pointers
+    // (advanced one tile per fetch) rather than from the tile index.
+    const int64_t t0r = (int64_t)cr.t0 * kBlk;
+    const T* Qn = Q + t0r * a.q.st;
+    const T* gQn = gQ + t0r * a.gq.st;
+    const T* dOn = dO + t0r * a.dout.st;
+    const T* Pn = LOADP ? Pb + t0r * a.p.st + n0 : nullptr;
+    const bool cols_full = n0 + kBlk <= T_;
     auto dma_tile = [&](int mb, const Bufs& wb) __attribute__((always_inline)) {
       const int m0 = mb * kBlk;
-      dd.load(wb.q, Q + (int64_t)m0 * a.q.st, oQ, a.q.st, T_ - m0, D);
-      dd.load(wb.gq, gQ + (int64_t)m0 * a.gq.st, ogQ, a.gq.st, T_ - m0, D);
-      dd.load(wb.dout, dO + (int64_t)m0 * a.dout.st, odO, a.dout.st, T_ - m0, D);
-      if constexpr (LOADP) dpt.load(wb.p, Pb + (int64_t)m0 * a.p.st + n0, oP, a.p.st, T_ - m0, T_ - n0);
+      if (m0 + kBlk <= T_ && cols_full) {  // uniform: one test per tile
+        dd.load_full(wb.q, Qn, oQ);
+        dd.load_full(wb.gq, gQn, ogQ);
+        dd.load_full(wb.dout, dOn, odO);
+        if constexpr (LOADP) dpt.load_full(wb.p, Pn, oP);
+      } else {
+        dd.load_ragged(wb.q, Qn, a.q.st, T_ - m0, D);
+        dd.load_ragged(wb.gq, gQn, a.gq.st, T_ - m0, D);
+        dd.load_ragged(wb.dout, dOn, a.dout.st, T_ - m0, D);
+        if constexpr (LOADP) dpt.load_ragged(wb.p, Pn, a.p.st, T_ - m0, T_ - n0);
+      }
       stat_dma<kNS>(wb.st, rs, ev, fv, lse, m0, T_ - m0);
+      Qn += kBlk * a.q.st;
+      gQn += kBlk * a.gq.st;
+      dOn += kBlk * a.dout.st;
+      if constexpr (LOADP) Pn += kBlk * a.p.st;
     };
     // Step over tile mb from buffer set P while the next tile streams into set 1-P.
     auto step = [&](auto par, int mb) __attribute__((always_inline)) {

@@ -52,7 +52,8 @@ __device__ __forceinline__ void frags_to_tile(Tile& p, const typename Elem<T>::f
 
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool LOADP, bool XM>
-__global__ __launch_bounds__(kThreads) void k_bwd_dq(Params a) {
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_BWD_RECOMPUTE && !LOADP && D == 64>::value))) void k_bwd_dq(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
@@ -154,7 +155,8 @@ __global__ __launch_bounds__(kThreads) void k_bwd_dq(Params a) {
 
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool LOADP, bool DV_ONLY, bool XM>
-__global__ __launch_bounds__(kThreads) void k_bwd_dkdv(Params a) {
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_BWD_RECOMPUTE && !LOADP && D == 64>::value))) void k_bwd_dkdv(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;

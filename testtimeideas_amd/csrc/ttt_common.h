@@ -103,6 +103,29 @@ struct Params {
 #ifndef TTT_XCD_SLICES
 #define TTT_XCD_SLICES 1
 #endif
+
+// Where MFMA accumulators live.  A kernel whose register budget is capped at
+// 256 (at least two waves per EU) and whose inline asm names no AGPRs gets
+// its MFMA results in VGPRs, which the elementwise code reads directly; with
+// the full 512-register budget the compiler keeps them in AGPRs and copies
+// each one out (v_accvgpr_read) before use.  AccWaves<true> asks for the
+// first, AccWaves<false> leaves the budget open.  Which is faster depends on
+// the kernel variant (measured), so each kernel chooses per variant; the
+// TTT_VACC_* switches below turn a choice off for A/B timing.
+template <bool VGPR_ACC>
+struct AccWaves {
+  static constexpr int value = VGPR_ACC ? 2 : 1;
+};
+#ifndef TTT_VACC_ONLINE
+#define TTT_VACC_ONLINE 1  // forward with online softmax (recompute modes)
+#endif
+#ifndef TTT_VACC_FWD_WIDE
+#define TTT_VACC_FWD_WIDE 1  // statistics and P passes at D = 128
+#endif
+#ifndef TTT_VACC_BWD_RECOMPUTE
+#define TTT_VACC_BWD_RECOMPUTE 1  // dQ and dK/dV kernels that recompute P, D = 64
+#endif
+
 struct Slot {
   int x, y;
 };

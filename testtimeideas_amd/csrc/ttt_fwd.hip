@@ -82,7 +82,8 @@ __device__ __forceinline__ float tile_max(const Tile& s) {
 
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool XM>
-__global__ __launch_bounds__(kThreads) void k_fwd_online(Params a) {
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_ONLINE>::value))) void k_fwd_online(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
@@ -181,7 +182,8 @@ __global__ __launch_bounds__(kThreads) void k_fwd_online(Params a) {
 
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool XM>
-__global__ __launch_bounds__(kThreads) void k_fwd_stats(Params a) {
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_FWD_WIDE && D == 128>::value))) void k_fwd_stats(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
@@ -282,7 +284,8 @@ __global__ __launch_bounds__(kThreads) void k_fwd_stats(Params a) {
 
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool XM>
-__global__ __launch_bounds__(kThreads) void k_fwd_p(Params a) {
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_FWD_WIDE && D == 128>::value))) void k_fwd_p(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;

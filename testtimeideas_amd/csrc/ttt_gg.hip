@@ -30,8 +30,21 @@
 // of the recompute path, ttt_kernels/triton_attention.py:416-420.  These
 // kernels compute the exact second derivative of the math path
 // (triton_attention.py:18-25) in closed form.
+//
+// The file is compiled once per head dim, TTT_GG_HEAD_DIM = 64 or 128: each
+// object holds that width's kernels, and its entry points carry the width in
+// their names (launch_gg_row64, ...; ttt_launch.h picks by D).  The D = 128
+// object is built with VGPR-form MFMA (-amdgpu-mfma-vgpr-form): its kernels
+// need more than 256 registers, so they cannot take VGPR accumulators by a
+// register cap, and with the flag the compiler still keeps the accumulators
+// in VGPRs and moves only the overflow to AGPRs (C5 grad-grad -5 %).
 #include "ttt_common.h"
 #include "ttt_launch.h"
+
+#ifndef TTT_GG_HEAD_DIM
+#define TTT_GG_HEAD_DIM 64
+#endif
+static_assert(TTT_GG_HEAD_DIM == 64 || TTT_GG_HEAD_DIM == 128, "head dim of this object");
 
 // Waves per SIMD the grad-grad kernels are compiled for (registers are
 // limited to 512 / this per lane): two at D = 64 (16-bit types; and fp32 in
@@ -614,25 +627,41 @@ static int occupancy_gg_col_t(bool load_p) {
   return load_p ? occupancy_of(k_gg_col<T, D, true, XM>) : occupancy_of(k_gg_col<T, D, false, XM>);
 }
 
-int occupancy_gg_row(int dtype, int D, bool load_p, bool gdo, bool xm) {
-  if (xm) DISPATCH_DTYPE_D(dtype, D, return occupancy_gg_row_t<ElemT, kD, true>(load_p, gdo));
-  else DISPATCH_DTYPE_D(dtype, D, return occupancy_gg_row_t<ElemT, kD, false>(load_p, gdo));
+// Entry points of this object's head dim (D is TTT_GG_HEAD_DIM).
+#define TTT_GG_DISPATCH(dtype, ...)                                  \
+  do {                                                               \
+    constexpr int kD = TTT_GG_HEAD_DIM;                              \
+    if ((dtype) == kF16) {                                           \
+      typedef _Float16 ElemT;                                        \
+      __VA_ARGS__;                                                   \
+    } else if ((dtype) == kBF16) {                                   \
+      typedef __bf16 ElemT;                                          \
+      __VA_ARGS__;                                                   \
+    } else if ((dtype) == kF32) {                                    \
+      typedef float ElemT;                                           \
+      __VA_ARGS__;                                                   \
+    }                                                                \
+  } while (0)
+
+int TTT_GG_NAME(occupancy_gg_row)(int dtype, bool load_p, bool gdo, bool xm) {
+  if (xm) TTT_GG_DISPATCH(dtype, return occupancy_gg_row_t<ElemT, kD, true>(load_p, gdo));
+  else TTT_GG_DISPATCH(dtype, return occupancy_gg_row_t<ElemT, kD, false>(load_p, gdo));
   return 0;
 }
 
-int occupancy_gg_col(int dtype, int D, bool load_p, bool xm) {
-  if (xm) DISPATCH_DTYPE_D(dtype, D, return occupancy_gg_col_t<ElemT, kD, true>(load_p));
-  else DISPATCH_DTYPE_D(dtype, D, return occupancy_gg_col_t<ElemT, kD, false>(load_p));
+int TTT_GG_NAME(occupancy_gg_col)(int dtype, bool load_p, bool xm) {
+  if (xm) TTT_GG_DISPATCH(dtype, return occupancy_gg_col_t<ElemT, kD, true>(load_p));
+  else TTT_GG_DISPATCH(dtype, return occupancy_gg_col_t<ElemT, kD, false>(load_p));
   return 0;
 }
 
-hipError_t launch_gg_row(int dtype, int D, const Params& a, bool load_p, bool want_gdout, hipStream_t st) {
-  DISPATCH_DTYPE_D(dtype, D, return launch_gg_row_t<ElemT, kD>(dtype, a, load_p, want_gdout, st));
+hipError_t TTT_GG_NAME(launch_gg_row)(int dtype, const Params& a, bool load_p, bool want_gdout, hipStream_t st) {
+  TTT_GG_DISPATCH(dtype, return launch_gg_row_t<ElemT, kD>(dtype, a, load_p, want_gdout, st));
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_gg_col(int dtype, int D, const Params& a, bool load_p, hipStream_t st) {
-  DISPATCH_DTYPE_D(dtype, D, return launch_gg_col_t<ElemT, kD>(dtype, a, load_p, st));
+hipError_t TTT_GG_NAME(launch_gg_col)(int dtype, const Params& a, bool load_p, hipStream_t st) {
+  TTT_GG_DISPATCH(dtype, return launch_gg_col_t<ElemT, kD>(dtype, a, load_p, st));
   return hipErrorInvalidValue;
 }
 

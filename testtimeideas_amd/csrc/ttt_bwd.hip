@@ -24,6 +24,25 @@
 #include "ttt_common.h"
 #include "ttt_launch.h"
 
+#ifndef TTT_DQ_FULLTILE
+#define TTT_DQ_FULLTILE 1
+#endif
+#ifndef TTT_DQ_PEEL
+#define TTT_DQ_PEEL 1
+#endif
+// Fetch forms, switchable for A/B timing.  FULLTILE: full tiles staged
+// through per-lane offsets computed once (else stage_load's clamped
+// addressing).  PEEL: the last tile peeled off the loop so the next tile's
+// fetch inside it is unconditional (its registers then need no copies across
+// iterations).  In dK/dV both cost registers (up to +24 VGPRs, past an
+// occupancy step at D = 128: C5 dK/dV +20 %), so they are off there.
+#ifndef TTT_DKDV_FULLTILE
+#define TTT_DKDV_FULLTILE 0
+#endif
+#ifndef TTT_DKDV_PEEL
+#define TTT_DKDV_PEEL 0
+#endif
+
 namespace ttt {
 
 // D for this lane's row from the lane's dO fragments and O read in the same
@@ -50,10 +69,21 @@ __device__ __forceinline__ void frags_to_tile(Tile& p, const typename Elem<T>::f
     for (int j = 0; j < 8; ++j) p.set(kb, j, Elem<T>::f32(f[kb][j]));
 }
 
+// Waves per EU the dQ kernel is compiled for: VGPR accumulators (AccWaves)
+// for the D = 64 recompute variants, and for their 16-bit types a cap of 128
+// registers, which keeps four waves per SIMD (the window/bias variant sits
+// right at that boundary; at 132 registers it drops to three, measured
+// TTT_W512_8K dQ 101 -> 113 us).
+template <typename T, int D, bool LOADP>
+struct DqWaves {
+  static constexpr bool kVacc = TTT_VACC_BWD_RECOMPUTE && !LOADP && D == 64;
+  static constexpr int value = kVacc ? (sizeof(T) == 2 ? 4 : AccWaves<true>::value) : AccWaves<false>::value;
+};
+
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool LOADP, bool XM>
 __global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_BWD_RECOMPUTE && !LOADP && D == 64>::value))) void k_bwd_dq(Params a) {
+__attribute__((amdgpu_waves_per_eu(DqWaves<T, D, LOADP>::value))) void k_bwd_dq(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
@@ -103,12 +133,43 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_BWD_RECOMPUTE && !LOADP && 
 #pragma unroll
   for (int i = 0; i < D / 16; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // Key tiles are fetched in order through running pointers; a full tile
+  // uses offsets computed once, a ragged one clamps (stage_load).
   Stage<T, D> stK, stV;
   frag pn[2];
-  stage_load<T, D>(stK, K + (int64_t)cr.t0 * kBlk * a.k.st, a.k.st, T_ - cr.t0 * kBlk, D);
-  stage_load<T, D>(stV, V + (int64_t)cr.t0 * kBlk * a.v.st, a.v.st, T_ - cr.t0 * kBlk, D);
-  if constexpr (LOADP) load_p_frags<T>(pn, Pm, cr.t0 * kBlk, T_);
-  for (int nb = cr.t0; nb < cr.t1; ++nb) {
+  const StageOff<T, D> soK = stage_offsets<T, D>(a.k.st), soV = stage_offsets<T, D>(a.v.st);
+  const T* Kn = K + (int64_t)cr.t0 * kBlk * a.k.st;
+  const T* Vn = V + (int64_t)cr.t0 * kBlk * a.v.st;
+  const T* Pn = LOADP ? Pm + cr.t0 * kBlk + stream_index(0, g, 0) : nullptr;
+  auto fetch = [&](int nb) __attribute__((always_inline)) {
+    const int n1 = nb * kBlk;
+    if constexpr (!LOADP) {
+      // Recompute: tile-indexed clamped loads, measured faster for this
+      // variant than the running-pointer form below.
+      stage_load<T, D>(stK, K + (int64_t)n1 * a.k.st, a.k.st, T_ - n1, D);
+      stage_load<T, D>(stV, V + (int64_t)n1 * a.v.st, a.v.st, T_ - n1, D);
+      return;
+    }
+    if (TTT_DQ_FULLTILE && n1 + kBlk <= T_) {
+      stage_load_full<T, D>(stK, Kn, soK);
+      stage_load_full<T, D>(stV, Vn, soV);
+      if constexpr (LOADP) {
+        pn[0] = load_frag_g<T>(Pn);
+        pn[1] = load_frag_g<T>(Pn + 32);
+      }
+    } else {
+      stage_load<T, D>(stK, Kn, a.k.st, T_ - n1, D);
+      stage_load<T, D>(stV, Vn, a.v.st, T_ - n1, D);
+      if constexpr (LOADP) load_p_frags<T>(pn, Pm, n1, T_);
+    }
+    Kn += kBlk * a.k.st;
+    Vn += kBlk * a.v.st;
+    if constexpr (LOADP) Pn += kBlk;
+  };
+  fetch(cr.t0);
+  // The last tile is peeled off the loop, so inside it the next tile's fetch
+  // is unconditional and its registers need no copies across iterations.
+  auto tile = [&](int nb, auto prefetch) __attribute__((always_inline)) {
     const int n0 = nb * kBlk;
     __syncthreads();
     stage_store_rows<T, D>(stK, sK);
@@ -116,12 +177,9 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_BWD_RECOMPUTE && !LOADP && 
     __syncthreads();
     Tile p;
     if constexpr (LOADP) frags_to_tile<T>(p, pn);
-    if (nb + 1 < cr.t1) {
-      const int n1 = n0 + kBlk;
-      stage_load<T, D>(stK, K + (int64_t)n1 * a.k.st, a.k.st, T_ - n1, D);
-      stage_load<T, D>(stV, V + (int64_t)n1 * a.v.st, a.v.st, T_ - n1, D);
-      if constexpr (LOADP) load_p_frags<T>(pn, Pm, n1, T_);
-    }
+    if constexpr (decltype(prefetch)::value == 1) fetch(nb + 1);
+    if constexpr (decltype(prefetch)::value == 2)
+      if (nb + 1 < cr.t1) fetch(nb + 1);
     if constexpr (!LOADP) {
       p.zero();
       mm_d<T, D>(p, sK, qf);
@@ -146,6 +204,12 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_BWD_RECOMPUTE && !LOADP && 
       dsf[kb] = vals_frag<T>(v);
     }
     mm_s<T, D>(acc, sK, dsf);
+  };
+  if constexpr (TTT_DQ_PEEL && LOADP) {
+    for (int nb = cr.t0; nb + 1 < cr.t1; ++nb) tile(nb, Parity<1>{});
+    tile(cr.t1 - 1, Parity<0>{});
+  } else {
+    for (int nb = cr.t0; nb < cr.t1; ++nb) tile(nb, Parity<2>{});
   }
   if (cr.nch == 1)
     store_acc_rows<T, D>(at<T>(a.dq, b, h), a.dq.st, m, T_, acc, a.scale);
@@ -205,18 +269,38 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_BWD_RECOMPUTE && !LOADP && 
 #pragma unroll
   for (int i = 0; i < D / 16; ++i) acc_dv[i] = acc_dk[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // Query tiles are fetched in order through running pointers; a full tile
+  // uses offsets computed once, a ragged one clamps (stage_load).
   Stage<T, D> stdO, stQ;
   Stage<T, kBlk> stP;
   float stv = 0.f;
-  auto load_tile = [&](int mb) {
+  const StageOff<T, D> sodO = stage_offsets<T, D>(a.dout.st), soQ = stage_offsets<T, D>(a.q.st);
+  const StageOff<T, kBlk> soP = stage_offsets<T, kBlk>(LOADP ? a.p.st : 0);
+  const int64_t t0r = (int64_t)cr.t0 * kBlk;
+  const T* dOn = dO + t0r * a.dout.st;
+  const T* Qn = Q + t0r * a.q.st;
+  const T* Pn = LOADP ? Pb + t0r * a.p.st + n0 : nullptr;
+  const bool cols_full = n0 + kBlk <= T_;
+  auto load_tile = [&](int mb) __attribute__((always_inline)) {
     const int m0 = mb * kBlk;
-    stage_load<T, D>(stdO, dO + (int64_t)m0 * a.dout.st, a.dout.st, T_ - m0, D);
-    if constexpr (kNeedQ) stage_load<T, D>(stQ, Q + (int64_t)m0 * a.q.st, a.q.st, T_ - m0, D);
-    if constexpr (LOADP) stage_load<T, kBlk>(stP, Pb + (int64_t)m0 * a.p.st + n0, a.p.st, T_ - m0, T_ - n0);
+    if (TTT_DKDV_FULLTILE && m0 + kBlk <= T_ && cols_full) {
+      stage_load_full<T, D>(stdO, dOn, sodO);
+      if constexpr (kNeedQ) stage_load_full<T, D>(stQ, Qn, soQ);
+      if constexpr (LOADP) stage_load_full<T, kBlk>(stP, Pn, soP);
+    } else {
+      stage_load<T, D>(stdO, dOn, a.dout.st, T_ - m0, D);
+      if constexpr (kNeedQ) stage_load<T, D>(stQ, Qn, a.q.st, T_ - m0, D);
+      if constexpr (LOADP) stage_load<T, kBlk>(stP, Pn, a.p.st, T_ - m0, T_ - n0);
+    }
     if constexpr (kNS > 0) stv = stat_load<kNS>(DV_ONLY ? lse : rs, lse, nullptr, nullptr, m0, T_ - m0);
+    dOn += kBlk * a.dout.st;
+    if constexpr (kNeedQ) Qn += kBlk * a.q.st;
+    if constexpr (LOADP) Pn += kBlk * a.p.st;
   };
   load_tile(cr.t0);
-  for (int mb = cr.t0; mb < cr.t1; ++mb) {
+  // The last tile is peeled off the loop, so inside it the next tile's fetch
+  // is unconditional.
+  auto tile = [&](int mb, auto prefetch) __attribute__((always_inline)) {
     const int m0 = mb * kBlk;
     __syncthreads();
     stage_store_rows<T, D>(stdO, sdO);
@@ -224,7 +308,9 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_BWD_RECOMPUTE && !LOADP && 
     if constexpr (LOADP) stage_store_rows<T, kBlk>(stP, sP);
     if constexpr (kNS > 0) stat_store<kNS>(stv, sS);
     __syncthreads();
-    if (mb + 1 < cr.t1) load_tile(mb + 1);
+    if constexpr (decltype(prefetch)::value == 1) load_tile(mb + 1);
+    if constexpr (decltype(prefetch)::value == 2)
+      if (mb + 1 < cr.t1) load_tile(mb + 1);
 
     // P(m, n) for streamed m = m0 + 32kb + 8g + j, stationary n.
     Tile p;
@@ -266,7 +352,13 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_BWD_RECOMPUTE && !LOADP && 
       }
       mm_s<T, D>(acc_dk, sQ, dsf);
     }
-  }
+  };
+#if TTT_DKDV_PEEL
+  for (int mb = cr.t0; mb + 1 < cr.t1; ++mb) tile(mb, Parity<1>{});
+  tile(cr.t1 - 1, Parity<0>{});
+#else
+  for (int mb = cr.t0; mb < cr.t1; ++mb) tile(mb, Parity<2>{});
+#endif
   if (cr.nch == 1) {
     store_acc_rows<T, D>(at<T>(a.dv, b, h), a.dv.st, n, T_, acc_dv, 1.f);
     if constexpr (!DV_ONLY) store_acc_rows<T, D>(at<T>(a.dk, b, h), a.dk.st, n, T_, acc_dk, a.scale);

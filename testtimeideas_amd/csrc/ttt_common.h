@@ -120,7 +120,7 @@ struct AccWaves {
 #define TTT_VACC_ONLINE 1  // forward with online softmax (recompute modes)
 #endif
 #ifndef TTT_VACC_FWD_WIDE
-#define TTT_VACC_FWD_WIDE 1  // statistics and P passes at D = 128
+#define TTT_VACC_FWD_WIDE 1  // statistics and P passes at D = 128, 16-bit types
 #endif
 #ifndef TTT_VACC_BWD_RECOMPUTE
 #define TTT_VACC_BWD_RECOMPUTE 1  // dQ and dK/dV kernels that recompute P, D = 64
@@ -322,6 +322,26 @@ __device__ __forceinline__ typename Elem<T>::frag load_frag(const T* p) {
   }
 }
 
+// The same from global memory, through an explicit global address space so
+// that the compiler emits a global (not flat) load: a flat load also counts
+// on lgkmcnt, and every later wait for LDS reads would wait for it too.
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::frag load_frag_g(const T* p) {
+  typedef typename Elem<T>::frag F;
+  typedef __attribute__((address_space(1))) const F gF;
+  typedef __attribute__((address_space(1))) const f32x4 gf32x4;
+  if constexpr (sizeof(T) == 2) {
+    return *(gF*)p;
+  } else {
+    const f32x4 lo = *(gf32x4*)p;
+    const f32x4 hi = *(gf32x4*)(p + 4);
+    F r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { r[j] = lo[j]; r[4 + j] = hi[j]; }
+    return r;
+  }
+}
+
 template <typename T>
 __device__ __forceinline__ typename Elem<T>::frag zero_frag() {
   typename Elem<T>::frag r;
@@ -335,7 +355,7 @@ __device__ __forceinline__ typename Elem<T>::frag zero_frag() {
 template <typename T>
 __device__ __forceinline__ typename Elem<T>::frag load_frag_row(const T* base, int64_t ld, int row,
                                                                 int nrows, int col) {
-  if (row < nrows) return load_frag<T>(base + (int64_t)row * ld + col);
+  if (row < nrows) return load_frag_g<T>(base + (int64_t)row * ld + col);
   return zero_frag<T>();
 }
 
@@ -465,7 +485,13 @@ struct Stage {
   u32x4 x0[kPasses], x1[kPasses];
 };
 
-__device__ __forceinline__ u32x4 load16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+// 16 bytes from global memory.  The explicit global address space keeps the
+// compiler from emitting a flat load where it cannot infer it (a flat load
+// also counts on lgkmcnt, so every later wait for LDS reads would wait for it).
+typedef __attribute__((address_space(1))) const u32x4 global_u32x4;
+__device__ __forceinline__ u32x4 load16(const void* p) {
+  return *(global_u32x4*)p;  // address-space cast (C-style: the only form C++ allows)
+}
 
 // Load a 64 x NCOL tile whose element [0][0] is at g (row stride ld).
 // Every thread issues the same unconditional loads on every tile: rows at or
@@ -491,6 +517,46 @@ __device__ __forceinline__ void stage_load(Stage<T, NCOL>& st, const T* __restri
   }
 }
 
+// Per-lane byte offsets of stage_load's fetches for a full tile (every row
+// and column valid), computed once per kernel: a full tile is then fetched
+// from its uniform base with no per-tile address arithmetic beyond the base.
+template <typename T, int NCOL>
+struct StageOff {
+  int o0[Stage<T, NCOL>::kPasses], o1[Stage<T, NCOL>::kPasses];
+};
+
+template <typename T, int NCOL>
+__device__ __forceinline__ StageOff<T, NCOL> stage_offsets(int64_t ld) {
+  typedef Stage<T, NCOL> S;
+  const int tid = threadIdx.x;
+  const int col = (tid % S::kChunksPerRow) * S::kChunk;
+  StageOff<T, NCOL> so;
+#pragma unroll
+  for (int ps = 0; ps < S::kPasses; ++ps) {
+    const int r = 2 * (tid / S::kChunksPerRow + ps * S::kPairsPerPass);
+    so.o0[ps] = (int)(((int64_t)r * ld + col) * (int64_t)sizeof(T));
+    so.o1[ps] = (int)(((int64_t)(r + 1) * ld + col) * (int64_t)sizeof(T));
+  }
+  return so;
+}
+
+// stage_load of a full tile at g (uniform) through precomputed offsets.  Each
+// offset passes through an empty asm as the 32-bit register it is: otherwise
+// the compiler keeps every offset widened to 64 bits across the loop, which
+// doubles their registers (and costs kernels near a register boundary their
+// occupancy).
+template <typename T, int NCOL>
+__device__ __forceinline__ void stage_load_full(Stage<T, NCOL>& st, const T* g, const StageOff<T, NCOL>& so) {
+  const char* gb = reinterpret_cast<const char*>(g);
+#pragma unroll
+  for (int ps = 0; ps < Stage<T, NCOL>::kPasses; ++ps) {
+    uint32_t o0 = (uint32_t)so.o0[ps], o1 = (uint32_t)so.o1[ps];
+    asm volatile("" : "+v"(o0), "+v"(o1));
+    st.x0[ps] = load16(gb + o0);
+    st.x1[ps] = load16(gb + o1);
+  }
+}
+
 // Raw P fragments of one streamed tile for this lane's stationary row: row pm,
 // columns n0 + 32kb + 8g .. +7.  Unconditional like stage_load: a fragment
 // starting at or beyond T reads column 0 instead, and callers mask columns
@@ -501,7 +567,7 @@ __device__ __forceinline__ void load_p_frags(typename Elem<T>::frag* f, const T*
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
     const int n = n0 + stream_index(kb, g, 0);
-    f[kb] = load_frag<T>(pm + (n < T_ ? n : 0));
+    f[kb] = load_frag_g<T>(pm + (n < T_ ? n : 0));
   }
 }
 
@@ -512,8 +578,8 @@ template <typename T>
 __device__ __forceinline__ void load_p_frags_run(typename Elem<T>::frag* f, const T* pl, const T* pm, int n0,
                                                  int T_) {
   if (n0 + kBlk <= T_) {
-    f[0] = load_frag<T>(pl);
-    f[1] = load_frag<T>(pl + 32);
+    f[0] = load_frag_g<T>(pl);
+    f[1] = load_frag_g<T>(pl + 32);
   } else {
     load_p_frags<T>(f, pm, n0, T_);
   }

@@ -31,6 +31,11 @@
 
 // Tiles of K and V a forward kernel loads ahead of the one it computes
 // (measured on MI355X: 2 and 3 were no faster than 1).
+// Full key tiles are staged through per-lane offsets computed once (1) or
+// through stage_load's clamped addressing like ragged tiles (0).
+#ifndef TTT_FWD_FULLTILE
+#define TTT_FWD_FULLTILE 1
+#endif
 #ifndef TTT_FWD_PREFETCH
 #define TTT_FWD_PREFETCH 1
 #endif
@@ -121,10 +126,18 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_ONLINE>::value))) void k_fw
   // tiles ahead of their use).
   constexpr int kPre = TTT_FWD_PREFETCH;
   Stage<T, D> stK[kPre], stV[kPre];
+  const StageOff<T, D> soK = stage_offsets<T, D>(a.k.st), soV = stage_offsets<T, D>(a.v.st);
   auto load_kv = [&](int nb, Stage<T, D>& sk, Stage<T, D>& sv) __attribute__((always_inline)) {
     const int n1 = nb * kBlk;
-    stage_load<T, D>(sk, K + (int64_t)n1 * a.k.st, a.k.st, T_ - n1, D);
-    stage_load<T, D>(sv, V + (int64_t)n1 * a.v.st, a.v.st, T_ - n1, D);
+    const T* kp = K + (int64_t)n1 * a.k.st;
+    const T* vp = V + (int64_t)n1 * a.v.st;
+    if (TTT_FWD_FULLTILE && D == 64 && n1 + kBlk <= T_) {  // full tile: offsets computed once
+      stage_load_full<T, D>(sk, kp, soK);
+      stage_load_full<T, D>(sv, vp, soV);
+    } else {
+      stage_load<T, D>(sk, kp, a.k.st, T_ - n1, D);
+      stage_load<T, D>(sv, vp, a.v.st, T_ - n1, D);
+    }
   };
 #pragma unroll
   for (int i = 0; i < kPre; ++i)
@@ -183,7 +196,7 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_ONLINE>::value))) void k_fw
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool XM>
 __global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_FWD_WIDE && D == 128>::value))) void k_fwd_stats(Params a) {
+__attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_FWD_WIDE && D == 128 && sizeof(T) == 2>::value))) void k_fwd_stats(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
@@ -217,9 +230,14 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_FWD_WIDE && D == 128>::valu
   Stage<T, D> stK[R];
   // Tiles past the chunk load its last tile again (unconditional loads; the
   // round masks them out).
+  const StageOff<T, D> soK = stage_offsets<T, D>(a.k.st);
   auto load_k = [&](int nb, Stage<T, D>& sk) __attribute__((always_inline)) {
     const int n1 = (nb < cr.t1 ? nb : cr.t1 - 1) * kBlk;
-    stage_load<T, D>(sk, K + (int64_t)n1 * a.k.st, a.k.st, T_ - n1, D);
+    const T* kp = K + (int64_t)n1 * a.k.st;
+    if (TTT_FWD_FULLTILE && D == 64 && n1 + kBlk <= T_)  // full tile: offsets computed once
+      stage_load_full<T, D>(sk, kp, soK);
+    else
+      stage_load<T, D>(sk, kp, a.k.st, T_ - n1, D);
   };
 #pragma unroll
   for (int i = 0; i < R; ++i) load_k(cr.t0 + i, stK[i]);
@@ -285,7 +303,7 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_FWD_WIDE && D == 128>::valu
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool XM>
 __global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_FWD_WIDE && D == 128>::value))) void k_fwd_p(Params a) {
+__attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_FWD_WIDE && D == 128 && sizeof(T) == 2>::value))) void k_fwd_p(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
@@ -340,10 +358,18 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_FWD_WIDE && D == 128>::valu
   Stage<T, D> stK[R], stV[R];
   // Tiles past the chunk load its last tile again (unconditional loads); their
   // P is neither stored nor accumulated.
+  const StageOff<T, D> soK = stage_offsets<T, D>(a.k.st), soV = stage_offsets<T, D>(a.v.st);
   auto load_kv = [&](int nb, Stage<T, D>& sk, Stage<T, D>& sv) __attribute__((always_inline)) {
     const int n1 = (nb < cr.t1 ? nb : cr.t1 - 1) * kBlk;
-    stage_load<T, D>(sk, K + (int64_t)n1 * a.k.st, a.k.st, T_ - n1, D);
-    stage_load<T, D>(sv, V + (int64_t)n1 * a.v.st, a.v.st, T_ - n1, D);
+    const T* kp = K + (int64_t)n1 * a.k.st;
+    const T* vp = V + (int64_t)n1 * a.v.st;
+    if (TTT_FWD_FULLTILE && D == 64 && n1 + kBlk <= T_) {  // full tile: offsets computed once
+      stage_load_full<T, D>(sk, kp, soK);
+      stage_load_full<T, D>(sv, vp, soV);
+    } else {
+      stage_load<T, D>(sk, kp, a.k.st, T_ - n1, D);
+      stage_load<T, D>(sv, vp, a.v.st, T_ - n1, D);
+    }
   };
 #pragma unroll
   for (int i = 0; i < R; ++i) load_kv(cr.t0 + i, stK[i], stV[i]);

@@ -31,18 +31,28 @@
 // kernels compute the exact second derivative of the math path
 // (triton_attention.py:18-25) in closed form.
 //
-// The file is compiled once per head dim, TTT_GG_HEAD_DIM = 64 or 128: each
-// object holds that width's kernels, and its entry points carry the width in
-// their names (launch_gg_row64, ...; ttt_launch.h picks by D).  The D = 128
+// The file is compiled into three objects, each holding one head dim's
+// kernels for some element types: TTT_GG_HEAD_DIM (64 or 128), TTT_GG_TYPES
+// (1: fp16 and bf16, 2: fp32, 3: all three) and TTT_GG_SUFFIX, which names
+// the object's entry points (launch_gg_row64, launch_gg_row128h,
+// launch_gg_row128f; ttt_launch.h picks by D and type).  The 16-bit D = 128
 // object is built with VGPR-form MFMA (-amdgpu-mfma-vgpr-form): its kernels
 // need more than 256 registers, so they cannot take VGPR accumulators by a
 // register cap, and with the flag the compiler still keeps the accumulators
-// in VGPRs and moves only the overflow to AGPRs (C5 grad-grad -5 %).
+// in VGPRs and moves only the overflow to AGPRs (C5 grad-grad -5 %).  fp32 at
+// D = 128 is built without it (ROCm 7.2's compiler crashes on one of those
+// kernels with the flag).
 #include "ttt_common.h"
 #include "ttt_launch.h"
 
 #ifndef TTT_GG_HEAD_DIM
 #define TTT_GG_HEAD_DIM 64
+#endif
+#ifndef TTT_GG_TYPES
+#define TTT_GG_TYPES 3
+#endif
+#ifndef TTT_GG_SUFFIX
+#define TTT_GG_SUFFIX 64
 #endif
 static_assert(TTT_GG_HEAD_DIM == 64 || TTT_GG_HEAD_DIM == 128, "head dim of this object");
 
@@ -187,8 +197,8 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
         dd.load_full(sgK[buf], gKn, ogK);
         dd.load_full(sgV[buf], gVn, ogV);
         if constexpr (LOADP) {
-          pn[0] = load_frag<T>(Pn);
-          pn[1] = load_frag<T>(Pn + 32);
+          pn[0] = load_frag_g<T>(Pn);
+          pn[1] = load_frag_g<T>(Pn + 32);
         }
       } else {
         dd.load_ragged(sK[buf], Kn, a.k.st, T_ - n0, D);
@@ -627,19 +637,25 @@ static int occupancy_gg_col_t(bool load_p) {
   return load_p ? occupancy_of(k_gg_col<T, D, true, XM>) : occupancy_of(k_gg_col<T, D, false, XM>);
 }
 
-// Entry points of this object's head dim (D is TTT_GG_HEAD_DIM).
+// Entry points of this object's head dim and element types (D is
+// TTT_GG_HEAD_DIM; other types fall through to an error return).
 #define TTT_GG_DISPATCH(dtype, ...)                                  \
   do {                                                               \
     constexpr int kD = TTT_GG_HEAD_DIM;                              \
-    if ((dtype) == kF16) {                                           \
-      typedef _Float16 ElemT;                                        \
-      __VA_ARGS__;                                                   \
-    } else if ((dtype) == kBF16) {                                   \
-      typedef __bf16 ElemT;                                          \
-      __VA_ARGS__;                                                   \
-    } else if ((dtype) == kF32) {                                    \
-      typedef float ElemT;                                           \
-      __VA_ARGS__;                                                   \
+    if constexpr ((TTT_GG_TYPES & 1) != 0) {                         \
+      if ((dtype) == kF16) {                                         \
+        typedef _Float16 ElemT;                                      \
+        __VA_ARGS__;                                                 \
+      } else if ((dtype) == kBF16) {                                 \
+        typedef __bf16 ElemT;                                        \
+        __VA_ARGS__;                                                 \
+      }                                                              \
+    }                                                                \
+    if constexpr ((TTT_GG_TYPES & 2) != 0) {                         \
+      if ((dtype) == kF32) {                                         \
+        typedef float ElemT;                                         \
+        __VA_ARGS__;                                                 \
+      }                                                              \
     }                                                                \
   } while (0)
 

@@ -60,20 +60,27 @@ inline bool extended_mask(const Params& a) { return a.win > 0 || a.bias.p != nul
 int occupancy_fwd(int dtype, int D, bool write_p, bool xm);
 int occupancy_dq(int dtype, int D, bool load_p, bool xm);
 int occupancy_dkdv(int dtype, int D, bool load_p, bool xm);
-// Grad-grad entry points, one object per head dim (ttt_gg.hip built twice).
+// Grad-grad entry points: ttt_gg.hip is built into one object per head dim
+// (and, at D = 128, per 16-bit / fp32 types), suffixed 64, 128h and 128f.
 #define TTT_GG_CAT2(a, b) a##b
 #define TTT_GG_CAT(a, b) TTT_GG_CAT2(a, b)
-#define TTT_GG_NAME(name) TTT_GG_CAT(name, TTT_GG_HEAD_DIM)
+#define TTT_GG_NAME(name) TTT_GG_CAT(name, TTT_GG_SUFFIX)
 int occupancy_gg_row64(int dtype, bool load_p, bool gdo, bool xm);
-int occupancy_gg_row128(int dtype, bool load_p, bool gdo, bool xm);
+int occupancy_gg_row128h(int dtype, bool load_p, bool gdo, bool xm);
+int occupancy_gg_row128f(int dtype, bool load_p, bool gdo, bool xm);
 int occupancy_gg_col64(int dtype, bool load_p, bool xm);
-int occupancy_gg_col128(int dtype, bool load_p, bool xm);
+int occupancy_gg_col128h(int dtype, bool load_p, bool xm);
+int occupancy_gg_col128f(int dtype, bool load_p, bool xm);
 inline int occupancy_gg_row(int dtype, int D, bool load_p, bool gdo, bool xm) {
-  return D == 64 ? occupancy_gg_row64(dtype, load_p, gdo, xm)
-                 : D == 128 ? occupancy_gg_row128(dtype, load_p, gdo, xm) : 0;
+  if (D == 64) return occupancy_gg_row64(dtype, load_p, gdo, xm);
+  if (D == 128)
+    return dtype == kF32 ? occupancy_gg_row128f(dtype, load_p, gdo, xm) : occupancy_gg_row128h(dtype, load_p, gdo, xm);
+  return 0;
 }
 inline int occupancy_gg_col(int dtype, int D, bool load_p, bool xm) {
-  return D == 64 ? occupancy_gg_col64(dtype, load_p, xm) : D == 128 ? occupancy_gg_col128(dtype, load_p, xm) : 0;
+  if (D == 64) return occupancy_gg_col64(dtype, load_p, xm);
+  if (D == 128) return dtype == kF32 ? occupancy_gg_col128f(dtype, load_p, xm) : occupancy_gg_col128h(dtype, load_p, xm);
+  return 0;
 }
 
 hipError_t launch_fwd(int dtype, int D, const Params& a, bool write_p, hipStream_t st);
@@ -84,16 +91,22 @@ hipError_t launch_bwd_dq(int dtype, int D, const Params& a, bool load_p, hipStre
 hipError_t launch_bwd_dkdv(int dtype, int D, const Params& a, bool load_p, bool dv_only, hipStream_t st);
 hipError_t launch_bwd_rowsum(int dtype, int D, const Params& a, hipStream_t st);
 hipError_t launch_gg_row64(int dtype, const Params& a, bool load_p, bool want_gdout, hipStream_t st);
-hipError_t launch_gg_row128(int dtype, const Params& a, bool load_p, bool want_gdout, hipStream_t st);
+hipError_t launch_gg_row128h(int dtype, const Params& a, bool load_p, bool want_gdout, hipStream_t st);
+hipError_t launch_gg_row128f(int dtype, const Params& a, bool load_p, bool want_gdout, hipStream_t st);
 hipError_t launch_gg_col64(int dtype, const Params& a, bool load_p, hipStream_t st);
-hipError_t launch_gg_col128(int dtype, const Params& a, bool load_p, hipStream_t st);
+hipError_t launch_gg_col128h(int dtype, const Params& a, bool load_p, hipStream_t st);
+hipError_t launch_gg_col128f(int dtype, const Params& a, bool load_p, hipStream_t st);
 inline hipError_t launch_gg_row(int dtype, int D, const Params& a, bool load_p, bool want_gdout, hipStream_t st) {
-  return D == 64 ? launch_gg_row64(dtype, a, load_p, want_gdout, st)
-                 : D == 128 ? launch_gg_row128(dtype, a, load_p, want_gdout, st) : hipErrorInvalidValue;
+  if (D == 64) return launch_gg_row64(dtype, a, load_p, want_gdout, st);
+  if (D == 128)
+    return dtype == kF32 ? launch_gg_row128f(dtype, a, load_p, want_gdout, st)
+                         : launch_gg_row128h(dtype, a, load_p, want_gdout, st);
+  return hipErrorInvalidValue;
 }
 inline hipError_t launch_gg_col(int dtype, int D, const Params& a, bool load_p, hipStream_t st) {
-  return D == 64 ? launch_gg_col64(dtype, a, load_p, st)
-                 : D == 128 ? launch_gg_col128(dtype, a, load_p, st) : hipErrorInvalidValue;
+  if (D == 64) return launch_gg_col64(dtype, a, load_p, st);
+  if (D == 128) return dtype == kF32 ? launch_gg_col128f(dtype, a, load_p, st) : launch_gg_col128h(dtype, a, load_p, st);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace ttt

@@ -74,6 +74,14 @@ static_assert(TTT_GG_HEAD_DIM == 64 || TTT_GG_HEAD_DIM == 128, "head dim of this
 #ifndef TTT_GG_PRESCALE
 #define TTT_GG_PRESCALE 1
 #endif
+// Row sums X = rowsum(Z1) and D = rowsum(Z2) in the row kernel for 16-bit
+// types: by MFMA against a ones fragment from the Z1, Z2 fragments the
+// products already use (1), or by VALU adds of the fp32 values (0).  The
+// MFMA form takes four MFMAs per tile for 32 adds, and sums the same rounded
+// values that the products with K consume.
+#ifndef TTT_GG_MFMA_ROWSUM
+#define TTT_GG_MFMA_ROWSUM 1
+#endif
 // Products that stream the same LDS tile read each fragment once (1) or
 // once per product (0).
 #ifndef TTT_GG_SHARED_READS
@@ -158,6 +166,15 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
     if constexpr (GDO) b1[i] = b2[i] = b3[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   float e_acc = 0.f, x_acc = 0.f, d_acc = 0.f;
+  // MFMA row sums: lane (c, g) of ones x Z holds rowsum(Z) of stationary row
+  // c in all four accumulator slots.
+  constexpr bool kMfmaSums = TTT_GG_MFMA_ROWSUM && sizeof(T) == 2 && !GDO;  // GdO variants spill with it
+  f32x4 xs4 = f32x4{0.f, 0.f, 0.f, 0.f}, ds4 = f32x4{0.f, 0.f, 0.f, 0.f};
+  frag ones;
+  {
+    const float one8[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+    ones = vals_frag<T>(one8);
+  }
 
   // Tiles are fetched in order t0, t0 + 1, ... through running pointers
   // (advanced one tile per fetch) rather than from the tile index.
@@ -283,8 +300,10 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
         const float ds = z2 - P * Dm;  // P o (dP - D)
         const float z1 = P * gp1.at(kb, j) + gd * ds;
         e_acc += gd * P;
-        x_acc += z1;
-        d_acc += z2;
+        if constexpr (!kMfmaSums) {
+          x_acc += z1;
+          d_acc += z2;
+        }
         vds[j] = ds;
         vz1[j] = z1;
         vz2[j] = z2;
@@ -293,6 +312,10 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
       dsf[kb] = vals_frag<T>(vds);
       z1f[kb] = vals_frag<T>(vz1);
       z2f[kb] = vals_frag<T>(vz2);
+      if constexpr (kMfmaSums) {
+        xs4 = E::mma(xs4, ones, z1f[kb]);
+        ds4 = E::mma(ds4, ones, z2f[kb]);
+      }
       pf[kb] = tile_frag<T>(p, kb);
       if constexpr (GDO) z4f[kb] = vals_frag<T>(vz4);
     }
@@ -310,8 +333,8 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
     }
   }
   const float Ev = group_sum(e_acc);
-  const float Xv = group_sum(x_acc);
-  const float Dv = group_sum(d_acc);
+  const float Xv = kMfmaSums ? xs4[0] : group_sum(x_acc);
+  const float Dv = kMfmaSums ? ds4[0] : group_sum(d_acc);
   if (cr.nch == 1) {
     const float Fv = Xv - Ev * Dv;
     f32x4 gq[D / 16];

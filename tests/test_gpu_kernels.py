@@ -89,6 +89,21 @@ def test_ragged_lengths(t, causal, save_p):
     _compare(out, _ref(xs, causal, scale), dt, causal, t)
 
 
+@pytest.mark.parametrize("scale", [-0.125, 0.0, 0.37])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("save_p", [True, False])
+def test_scale_signs(scale, causal, save_p):
+    """Negative and zero scales take the forward's scaled-score path (the
+    fused raw-score statistics need a positive scale); a positive non-power
+    of two takes the fused one.  Ragged T covers the clamped tiles."""
+    dt = torch.float16
+    t = 100
+    xs = _inputs(1, 2, t, 64, dt, seed=11)
+    print(f"[case] scale={scale} causal={causal} save_p={save_p}", flush=True)
+    out = _run(xs, causal, scale, save_p)
+    _compare(out, _ref(xs, causal, scale), dt, causal, t)
+
+
 @pytest.mark.parametrize("dtype", ["fp32", "fp16"])
 def test_c1_shape_fp32_parity(dtype):
     """C1 shape (b1 h1 T64 d64, non-causal) on the GPU kernels."""

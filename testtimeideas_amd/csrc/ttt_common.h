@@ -322,6 +322,15 @@ __device__ __forceinline__ typename Elem<T>::frag load_frag(const T* p) {
   }
 }
 
+// Store a 16-bit fragment (eight elements, 16-byte aligned) to global memory.
+template <typename T>
+__device__ __forceinline__ void store_frag_g(T* p, const typename Elem<T>::frag& f) {
+  static_assert(sizeof(T) == 2, "16-bit fragments");
+  typedef typename Elem<T>::frag F;
+  typedef __attribute__((address_space(1))) F gF;
+  *(gF*)p = f;
+}
+
 // The same from global memory, through an explicit global address space so
 // that the compiler emits a global (not flat) load: a flat load also counts
 // on lgkmcnt, and every later wait for LDS reads would wait for it too.

@@ -33,6 +33,18 @@
 // (measured on MI355X: 2 and 3 were no faster than 1).
 // Full key tiles are staged through per-lane offsets computed once (1) or
 // through stage_load's clamped addressing like ragged tiles (0).
+// The P pass without a window or bias computes P from raw scores with the
+// scale folded into the exponent's FMA and packs it to T once (1), or goes
+// through the scaled, masked score tile (0).
+// The statistics pass without a window or bias keeps its running max and sum
+// in raw-score units, the scale folded into the exponent's FMA (1), or
+// scales every score first (0).
+#ifndef TTT_FWD_STATS_FUSED
+#define TTT_FWD_STATS_FUSED 1
+#endif
+#ifndef TTT_FWD_P_FUSED
+#define TTT_FWD_P_FUSED 1
+#endif
 #ifndef TTT_FWD_FULLTILE
 #define TTT_FWD_FULLTILE 1
 #endif
@@ -227,6 +239,8 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_FWD_WIDE && D == 128 && siz
   for (int ks = 0; ks < D / 32; ++ks) qf[ks] = load_frag_row<T>(Q, a.q.st, m, T_, 32 * ks + 8 * g);
 
   float mx = -INFINITY, l = 0.f;
+  const float csl = a.scale_log2;
+  const bool raw_units = csl > 0.f;  // uniform; the fused form needs a positive scale
   Stage<T, D> stK[R];
   // Tiles past the chunk load its last tile again (unconditional loads; the
   // round masks them out).
@@ -251,6 +265,45 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_FWD_WIDE && D == 128 && siz
       for (int i = 0; i < R; ++i) load_k(nb + R + i, stK[i]);
     }
     Tile s[R];
+    if constexpr (!XM && TTT_FWD_STATS_FUSED) {
+      if (raw_units) {
+        // Max and sum in raw-score units: exp2(raw * csl - max * csl) with the
+        // scale csl = scale*log2e > 0 folded into one FMA per element.
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+          s[i].zero();
+          mm_d<T, D>(s[i], sK[i], qf);
+          const int n0 = (nb + i) * kBlk;
+          if ((i > 0 && nb + i >= cr.t1) || mk.tile(nb + i)) {
+            const bool past = i > 0 && nb + i >= cr.t1;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+              for (int j = 0; j < 8; ++j)
+                s[i].set(kb, j, (past || mk.masked(n0 + stream_index(kb, g, j))) ? -INFINITY : s[i].at(kb, j));
+          }
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < R; ++i)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) tmax = fmaxf(tmax, s[i].at(kb, j));
+        const float mnew = fmaxf(mx, tmax);
+        const float shift = mnew == -INFINITY ? 0.f : mnew * csl;
+        float ts = 0.f;
+#pragma unroll
+        for (int i = 0; i < R; ++i)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ts += fast_exp2(fmaf(s[i].at(kb, j), csl, -shift));
+        l = l * fast_exp2(mx * csl - shift) + ts;
+        mx = mnew;
+        continue;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       fwd_scores<T, D, XM>(s[i], sK[i], qf, a, mk, brow, nb + i);
@@ -283,6 +336,7 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_FWD_WIDE && D == 128 && siz
     l = l * fast_exp2(mx - shift) + ts;
     mx = mnew;
   }
+  if (!XM && TTT_FWD_STATS_FUSED && raw_units && mx != -INFINITY) mx *= csl;  // back to base-2 units
   {
     // Finite without a window (every row sees a key of its first tile); with
     // one a chunk can miss all of a row's keys, and then max -inf, sum 0.
@@ -388,24 +442,63 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_FWD_WIDE && D == 128 && siz
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       const bool valid = i == 0 || nb + i < cr.t1;
-      Tile s;
-      fwd_scores<T, D, XM>(s, sK[i], qf, a, mk, brow, nb + i);
       const int n0 = (nb + i) * kBlk;
       frag pf[2];
+      if constexpr (!XM && sizeof(T) == 2 && TTT_FWD_P_FUSED) {
+        // Raw scores; P = exp2(raw * scale*log2e - lse) in one FMA, masked
+        // entries selected to 0 afterwards, and one rounding to T gives both
+        // the MFMA fragment and the stored P.
+        Tile s;
+        s.zero();
+        mm_d<T, D>(s, sK[i], qf);
+        const bool need_mask = mk.tile(nb + i);
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        float pv[8];
+        for (int kb = 0; kb < 2; ++kb) {
+          float pv[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) pv[j] = valid ? E::f32(E::cvt(fast_exp2(s.at(kb, j) - lse2))) : 0.f;
-        pf[kb] = vals_frag<T>(pv);
-        if (valid && m < T_) {
-          const int n = n0 + stream_index(kb, g, 0);
-          if (n + 8 <= T_) {
-            store8<T>(Pm + n, pv);
-          } else {
+          for (int j = 0; j < 8; ++j) pv[j] = valid ? fast_exp2(fmaf(s.at(kb, j), a.scale_log2, -lse2)) : 0.f;
+          if (need_mask) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-              if (n + j < T_) Pm[n + j] = E::cvt(pv[j]);
+            for (int j = 0; j < 8; ++j) pv[j] = mk.masked(n0 + stream_index(kb, g, j)) ? 0.f : pv[j];
+          }
+          pf[kb] = vals_frag<T>(pv);
+          if (valid && m < T_) {
+            const int n = n0 + stream_index(kb, g, 0);
+            if (n + 8 <= T_) {
+              store_frag_g<T>(Pm + n, pf[kb]);
+            } else {
+              // Ragged last tile: the stored halves taken from the packed
+              // fragment's words (element access would make the compiler
+              // build the fragment element by element).
+              u32x4 raw;
+              __builtin_memcpy(&raw, &pf[kb], 16);
+#pragma unroll
+              for (int j = 0; j < 8; ++j)
+                if (n + j < T_) {
+                  const uint16_t h = (uint16_t)(raw[j >> 1] >> (16 * (j & 1)));
+                  __builtin_memcpy(Pm + n + j, &h, 2);
+                }
+            }
+          }
+        }
+      } else {
+        Tile s;
+        fwd_scores<T, D, XM>(s, sK[i], qf, a, mk, brow, nb + i);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          float pv[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) pv[j] = valid ? E::f32(E::cvt(fast_exp2(s.at(kb, j) - lse2))) : 0.f;
+          pf[kb] = vals_frag<T>(pv);
+          if (valid && m < T_) {
+            const int n = n0 + stream_index(kb, g, 0);
+            if (n + 8 <= T_) {
+              store8<T>(Pm + n, pv);
+            } else {
+#pragma unroll
+              for (int j = 0; j < 8; ++j)
+                if (n + j < T_) Pm[n + j] = E::cvt(pv[j]);
+            }
           }
         }
       }

@@ -31,17 +31,19 @@
 // kernels compute the exact second derivative of the math path
 // (triton_attention.py:18-25) in closed form.
 //
-// The file is compiled into three objects, each holding one head dim's
-// kernels for some element types: TTT_GG_HEAD_DIM (64 or 128), TTT_GG_TYPES
-// (1: fp16 and bf16, 2: fp32, 3: all three) and TTT_GG_SUFFIX, which names
-// the object's entry points (launch_gg_row64, launch_gg_row128h,
-// launch_gg_row128f; ttt_launch.h picks by D and type).  The 16-bit D = 128
-// object is built with VGPR-form MFMA (-amdgpu-mfma-vgpr-form): its kernels
-// need more than 256 registers, so they cannot take VGPR accumulators by a
-// register cap, and with the flag the compiler still keeps the accumulators
-// in VGPRs and moves only the overflow to AGPRs (C5 grad-grad -5 %).  fp32 at
-// D = 128 is built without it (ROCm 7.2's compiler crashes on one of those
-// kernels with the flag).
+// The file is compiled into four objects, each holding one head dim's
+// kernels for some element types and variants: TTT_GG_HEAD_DIM (64 or 128),
+// TTT_GG_TYPES (1: fp16 and bf16, 2: fp32, 3: all three), TTT_GG_ROW_GDO and
+// TTT_GG_COL (below), and TTT_GG_SUFFIX, which names the object's entry
+// points (launch_gg_row64, launch_gg_row128h, launch_gg_row128hg,
+// launch_gg_row128f; ttt_launch.h picks by D, type and GdO).  The 16-bit
+// D = 128 row (without GdO) and column kernels are built with VGPR-form MFMA
+// (-amdgpu-mfma-vgpr-form): they need more than 256 registers, so they cannot
+// take VGPR accumulators by a register cap, and with the flag the compiler
+// still keeps the accumulators in VGPRs and moves only the overflow to AGPRs
+// (C5 grad-grad -5 %).  The heaviest kernels (D = 128 with GdO, and fp32 at
+// D = 128) are built without it: ROCm 7.2's compiler crashes on some of them
+// with the flag.
 #include "ttt_common.h"
 #include "ttt_launch.h"
 
@@ -53,6 +55,14 @@
 #endif
 #ifndef TTT_GG_SUFFIX
 #define TTT_GG_SUFFIX 64
+#endif
+// Which row-kernel variants (1: without GdO, 2: with GdO, 3: both) and
+// whether the column kernels are in this object.
+#ifndef TTT_GG_ROW_GDO
+#define TTT_GG_ROW_GDO 3
+#endif
+#ifndef TTT_GG_COL
+#define TTT_GG_COL 1
 #endif
 static_assert(TTT_GG_HEAD_DIM == 64 || TTT_GG_HEAD_DIM == 128, "head dim of this object");
 
@@ -602,28 +612,36 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_COL_WAVES_PER_EU, true>:
 
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool XM>
-static void launch_gg_row_x(const Params& a, bool load_p, bool gdo, dim3 grid, hipStream_t st) {
-  if (load_p) {
-    if (gdo)
-      hipLaunchKernelGGL((k_gg_row<T, D, true, true, XM>), grid, dim3(kThreads), 0, st, a);
-    else
-      hipLaunchKernelGGL((k_gg_row<T, D, true, false, XM>), grid, dim3(kThreads), 0, st, a);
+// False when the variant asked for is not in this object (ttt_launch.h
+// routes each variant to the object that has it).
+static bool launch_gg_row_x(const Params& a, bool load_p, bool gdo, dim3 grid, hipStream_t st) {
+  if (gdo) {
+    if constexpr ((TTT_GG_ROW_GDO & 2) != 0) {
+      if (load_p)
+        hipLaunchKernelGGL((k_gg_row<T, D, true, true, XM>), grid, dim3(kThreads), 0, st, a);
+      else
+        hipLaunchKernelGGL((k_gg_row<T, D, false, true, XM>), grid, dim3(kThreads), 0, st, a);
+      return true;
+    }
   } else {
-    if (gdo)
-      hipLaunchKernelGGL((k_gg_row<T, D, false, true, XM>), grid, dim3(kThreads), 0, st, a);
-    else
-      hipLaunchKernelGGL((k_gg_row<T, D, false, false, XM>), grid, dim3(kThreads), 0, st, a);
+    if constexpr ((TTT_GG_ROW_GDO & 1) != 0) {
+      if (load_p)
+        hipLaunchKernelGGL((k_gg_row<T, D, true, false, XM>), grid, dim3(kThreads), 0, st, a);
+      else
+        hipLaunchKernelGGL((k_gg_row<T, D, false, false, XM>), grid, dim3(kThreads), 0, st, a);
+      return true;
+    }
   }
+  return false;
 }
 
 template <typename T, int D>
 static hipError_t launch_gg_row_t(int dtype, const Params& a, bool load_p, bool gdo, hipStream_t st) {
   const int nblk = (a.T + kBlk - 1) / kBlk;
   dim3 grid(nblk * a.nchunk_max, a.B * a.H);
-  if (extended_mask(a))
-    launch_gg_row_x<T, D, true>(a, load_p, gdo, grid, st);
-  else
-    launch_gg_row_x<T, D, false>(a, load_p, gdo, grid, st);
+  const bool ok = extended_mask(a) ? launch_gg_row_x<T, D, true>(a, load_p, gdo, grid, st)
+                                    : launch_gg_row_x<T, D, false>(a, load_p, gdo, grid, st);
+  if (!ok) return hipErrorInvalidDeviceFunction;
   if (a.nchunk_max > 1) return launch_combine_gg_row(dtype, D, a, gdo, st);
   return hipGetLastError();
 }
@@ -650,9 +668,14 @@ static hipError_t launch_gg_col_t(int dtype, const Params& a, bool load_p, hipSt
 
 template <typename T, int D, bool XM>
 static int occupancy_gg_row_t(bool load_p, bool gdo) {
-  if (load_p)
-    return gdo ? occupancy_of(k_gg_row<T, D, true, true, XM>) : occupancy_of(k_gg_row<T, D, true, false, XM>);
-  return gdo ? occupancy_of(k_gg_row<T, D, false, true, XM>) : occupancy_of(k_gg_row<T, D, false, false, XM>);
+  if (gdo) {
+    if constexpr ((TTT_GG_ROW_GDO & 2) != 0)
+      return load_p ? occupancy_of(k_gg_row<T, D, true, true, XM>) : occupancy_of(k_gg_row<T, D, false, true, XM>);
+  } else {
+    if constexpr ((TTT_GG_ROW_GDO & 1) != 0)
+      return load_p ? occupancy_of(k_gg_row<T, D, true, false, XM>) : occupancy_of(k_gg_row<T, D, false, false, XM>);
+  }
+  return 0;
 }
 
 template <typename T, int D, bool XM>
@@ -688,20 +711,22 @@ int TTT_GG_NAME(occupancy_gg_row)(int dtype, bool load_p, bool gdo, bool xm) {
   return 0;
 }
 
+hipError_t TTT_GG_NAME(launch_gg_row)(int dtype, const Params& a, bool load_p, bool want_gdout, hipStream_t st) {
+  TTT_GG_DISPATCH(dtype, return launch_gg_row_t<ElemT, kD>(dtype, a, load_p, want_gdout, st));
+  return hipErrorInvalidValue;
+}
+
+#if TTT_GG_COL
 int TTT_GG_NAME(occupancy_gg_col)(int dtype, bool load_p, bool xm) {
   if (xm) TTT_GG_DISPATCH(dtype, return occupancy_gg_col_t<ElemT, kD, true>(load_p));
   else TTT_GG_DISPATCH(dtype, return occupancy_gg_col_t<ElemT, kD, false>(load_p));
   return 0;
 }
 
-hipError_t TTT_GG_NAME(launch_gg_row)(int dtype, const Params& a, bool load_p, bool want_gdout, hipStream_t st) {
-  TTT_GG_DISPATCH(dtype, return launch_gg_row_t<ElemT, kD>(dtype, a, load_p, want_gdout, st));
-  return hipErrorInvalidValue;
-}
-
 hipError_t TTT_GG_NAME(launch_gg_col)(int dtype, const Params& a, bool load_p, hipStream_t st) {
   TTT_GG_DISPATCH(dtype, return launch_gg_col_t<ElemT, kD>(dtype, a, load_p, st));
   return hipErrorInvalidValue;
 }
+#endif
 
 }  // namespace ttt

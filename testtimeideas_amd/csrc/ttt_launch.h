@@ -61,12 +61,14 @@ int occupancy_fwd(int dtype, int D, bool write_p, bool xm);
 int occupancy_dq(int dtype, int D, bool load_p, bool xm);
 int occupancy_dkdv(int dtype, int D, bool load_p, bool xm);
 // Grad-grad entry points: ttt_gg.hip is built into one object per head dim
-// (and, at D = 128, per 16-bit / fp32 types), suffixed 64, 128h and 128f.
+// (and, at D = 128, per 16-bit / 16-bit with GdO / fp32), suffixed 64, 128h,
+// 128hg and 128f.
 #define TTT_GG_CAT2(a, b) a##b
 #define TTT_GG_CAT(a, b) TTT_GG_CAT2(a, b)
 #define TTT_GG_NAME(name) TTT_GG_CAT(name, TTT_GG_SUFFIX)
 int occupancy_gg_row64(int dtype, bool load_p, bool gdo, bool xm);
 int occupancy_gg_row128h(int dtype, bool load_p, bool gdo, bool xm);
+int occupancy_gg_row128hg(int dtype, bool load_p, bool gdo, bool xm);
 int occupancy_gg_row128f(int dtype, bool load_p, bool gdo, bool xm);
 int occupancy_gg_col64(int dtype, bool load_p, bool xm);
 int occupancy_gg_col128h(int dtype, bool load_p, bool xm);
@@ -74,7 +76,9 @@ int occupancy_gg_col128f(int dtype, bool load_p, bool xm);
 inline int occupancy_gg_row(int dtype, int D, bool load_p, bool gdo, bool xm) {
   if (D == 64) return occupancy_gg_row64(dtype, load_p, gdo, xm);
   if (D == 128)
-    return dtype == kF32 ? occupancy_gg_row128f(dtype, load_p, gdo, xm) : occupancy_gg_row128h(dtype, load_p, gdo, xm);
+    return dtype == kF32 ? occupancy_gg_row128f(dtype, load_p, gdo, xm)
+           : gdo         ? occupancy_gg_row128hg(dtype, load_p, gdo, xm)
+                         : occupancy_gg_row128h(dtype, load_p, gdo, xm);
   return 0;
 }
 inline int occupancy_gg_col(int dtype, int D, bool load_p, bool xm) {
@@ -92,6 +96,7 @@ hipError_t launch_bwd_dkdv(int dtype, int D, const Params& a, bool load_p, bool 
 hipError_t launch_bwd_rowsum(int dtype, int D, const Params& a, hipStream_t st);
 hipError_t launch_gg_row64(int dtype, const Params& a, bool load_p, bool want_gdout, hipStream_t st);
 hipError_t launch_gg_row128h(int dtype, const Params& a, bool load_p, bool want_gdout, hipStream_t st);
+hipError_t launch_gg_row128hg(int dtype, const Params& a, bool load_p, bool want_gdout, hipStream_t st);
 hipError_t launch_gg_row128f(int dtype, const Params& a, bool load_p, bool want_gdout, hipStream_t st);
 hipError_t launch_gg_col64(int dtype, const Params& a, bool load_p, hipStream_t st);
 hipError_t launch_gg_col128h(int dtype, const Params& a, bool load_p, hipStream_t st);
@@ -100,6 +105,7 @@ inline hipError_t launch_gg_row(int dtype, int D, const Params& a, bool load_p, 
   if (D == 64) return launch_gg_row64(dtype, a, load_p, want_gdout, st);
   if (D == 128)
     return dtype == kF32 ? launch_gg_row128f(dtype, a, load_p, want_gdout, st)
+           : want_gdout  ? launch_gg_row128hg(dtype, a, load_p, want_gdout, st)
                          : launch_gg_row128h(dtype, a, load_p, want_gdout, st);
   return hipErrorInvalidValue;
 }

@@ -989,6 +989,26 @@ __device__ __forceinline__ void stat_dma(float* lds, const float* s0, const floa
 #endif
 }
 
+// The same with the per-wave choices made once: wave w < NS fetches
+// statistic w (pointer and LDS slice fixed per wave, uniform).
+template <int NS>
+struct StatDma {
+  const float* src;  // this wave's statistic, or null (w >= NS)
+  int w;
+  __device__ __forceinline__ StatDma(const float* s0, const float* s1, const float* s2, const float* s3) {
+    w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    src = w >= NS ? nullptr : w == 0 ? s0 : w == 1 ? s1 : w == 2 ? s2 : s3;
+  }
+  __device__ __forceinline__ void load(float* lds, int m0, int rows_valid) const {
+    if (w >= NS) return;
+#if defined(__HIP_DEVICE_COMPILE__)
+    const int lane = threadIdx.x & 63;
+    const char* p = reinterpret_cast<const char*>(src + m0) + (uint32_t)(lane < rows_valid ? lane : 0) * 4u;
+    __builtin_amdgcn_global_load_lds(p, (lds_void_t*)(lds + kBlk * w), 4, 0, 0);
+#endif
+  }
+};
+
 // Wait for this wave's direct loads (then meet the other waves at a barrier).
 // The compiler also waits for outstanding direct loads before any LDS read it
 // cannot prove disjoint from their destination, so kernels keep the two

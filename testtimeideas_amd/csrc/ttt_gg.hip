@@ -543,6 +543,7 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_COL_WAVES_PER_EU, true>:
     const T* dOn = dO + t0r * a.dout.st;
     const T* Pn = LOADP ? Pb + t0r * a.p.st + n0 : nullptr;
     const bool cols_full = n0 + kBlk <= T_;
+    const StatDma<kNS> sdma(rs, ev, fv, lse);
     auto dma_tile = [&](int mb, const Bufs& wb) __attribute__((always_inline)) {
       const int m0 = mb * kBlk;
       if (m0 + kBlk <= T_ && cols_full) {  // uniform: one test per tile
@@ -556,7 +557,7 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_COL_WAVES_PER_EU, true>:
         dd.load_ragged(wb.dout, dOn, a.dout.st, T_ - m0, D);
         if constexpr (LOADP) dpt.load_ragged(wb.p, Pn, a.p.st, T_ - m0, T_ - n0);
       }
-      stat_dma<kNS>(wb.st, rs, ev, fv, lse, m0, T_ - m0);
+      sdma.load(wb.st, m0, T_ - m0);
       Qn += kBlk * a.q.st;
       gQn += kBlk * a.gq.st;
       dOn += kBlk * a.dout.st;

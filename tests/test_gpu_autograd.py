@@ -54,13 +54,15 @@ def test_modes_gradgrad(mode, causal):
         check(n, got[n], ref[n], torch.float16)
 
 
+@pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("mode", ["save_p_triton_full", "recompute"])
-def test_gdo_when_do_requires_grad(dtype, mode):
-    xs = _inputs(2, 1, 96, 64, dtype, seed=12)
-    print(f"[case] gdo dtype={dtype} mode={mode}", flush=True)
-    got = _gpu_step(xs, True, 0.125, mode, do_requires_grad=True)
-    ref = _cpu_ref(xs, True, 0.125, do_requires_grad=True)
+def test_gdo_when_do_requires_grad(dtype, mode, d):
+    xs = _inputs(2, 1, 96, d, dtype, seed=12)
+    scale = 1.0 / math.sqrt(d)
+    print(f"[case] gdo dtype={dtype} mode={mode} d={d}", flush=True)
+    got = _gpu_step(xs, True, scale, mode, do_requires_grad=True)
+    ref = _cpu_ref(xs, True, scale, do_requires_grad=True)
     for n in ("o", "dq", "dk", "dv", "gq", "gk", "gv", "gdo"):
         check(n, got[n], ref[n], dtype)
 

@@ -92,6 +92,11 @@ static_assert(TTT_GG_HEAD_DIM == 64 || TTT_GG_HEAD_DIM == 128, "head dim of this
 #ifndef TTT_GG_MFMA_ROWSUM
 #define TTT_GG_MFMA_ROWSUM 1
 #endif
+// The column kernel streams 16-bit D = 128 tiles by direct loads too (1), or
+// through registers (0).
+#ifndef TTT_GG_COL_DMA_WIDE
+#define TTT_GG_COL_DMA_WIDE 1
+#endif
 // Products that stream the same LDS tile read each fragment once (1) or
 // once per product (0).
 #ifndef TTT_GG_SHARED_READS
@@ -393,7 +398,7 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_COL_WAVES_PER_EU, true>:
   // 16-bit types at D = 64 stream tiles straight into two LDS buffers
   // (TileDma), set 0 and set 1, in distinct arrays with a compile-time role per
   // loop step; the rest stage them through registers into set 0.
-  constexpr bool kDma = L::kSwizzle && D == 64;
+  constexpr bool kDma = L::kSwizzle && (D == 64 || TTT_GG_COL_DMA_WIDE);
   constexpr int kNS = LOADP ? 3 : 4;  // staged row statistics: D, E, F, then lse (recompute)
   constexpr int kE1 = kDma ? L::kRowElems : 8;
   constexpr int kP0 = LOADP ? LP::kRowElems : 8, kP1 = (LOADP && kDma) ? LP::kRowElems : 8;

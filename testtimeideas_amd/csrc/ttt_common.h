@@ -1014,7 +1014,15 @@ struct StatDma {
 // cannot prove disjoint from their destination, so kernels keep the two
 // buffers in distinct arrays and give each loop step a compile-time buffer
 // role (Parity<0>, Parity<1>).
-__device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// The builtin (not inline asm), so that the compiler's own wait insertion
+// knows these loads are complete: after an asm wait it still counts them as
+// pending and waits again at their first use, which by then comes after the
+// next tile's loads (and waits for those too).  0x0F70: vmcnt(0), expcnt and
+// lgkmcnt left at their maxima.
+__device__ __forceinline__ void dma_wait() {
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
 
 template <int P>
 struct Parity {

@@ -92,8 +92,12 @@ static_assert(TTT_GG_HEAD_DIM == 64 || TTT_GG_HEAD_DIM == 128, "head dim of this
 #ifndef TTT_GG_MFMA_ROWSUM
 #define TTT_GG_MFMA_ROWSUM 1
 #endif
-// The column kernel streams 16-bit D = 128 tiles by direct loads too (1), or
-// through registers (0).
+// The row kernel (TTT_GG_ROW_DMA_WIDE) and the column kernel
+// (TTT_GG_COL_DMA_WIDE) stream 16-bit D = 128 tiles by direct loads too (1),
+// or through registers (0).
+#ifndef TTT_GG_ROW_DMA_WIDE
+#define TTT_GG_ROW_DMA_WIDE 1
+#endif
 #ifndef TTT_GG_COL_DMA_WIDE
 #define TTT_GG_COL_DMA_WIDE 1
 #endif
@@ -121,14 +125,29 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
   constexpr int NACC = GDO ? 7 : 4;
-  // 16-bit types at D = 64 stream tiles straight into two LDS buffers
-  // (TileDma); the rest stage them through registers into one.
+  // 16-bit types stream tiles straight into LDS (TileDma): at D = 64 into two
+  // buffers of one array per operand, picked at run time; at D = 128 into two
+  // buffer sets in distinct arrays with a compile-time role per loop step
+  // (kPar), so that the current tile's LDS reads need not wait for the next
+  // tile's loads (with one workgroup per CU at D = 128 nothing else would hide
+  // that wait).  The rest stage tiles through registers into one buffer.
   constexpr bool kDma = L::kSwizzle && D == 64;
+  constexpr bool kPar = L::kSwizzle && D == 128 && TTT_GG_ROW_DMA_WIDE;
   constexpr int kBuf = kDma ? 2 : 1;
-  __shared__ __align__(16) T sK[kBuf][L::kRowElems];
-  __shared__ __align__(16) T sV[kBuf][L::kRowElems];
-  __shared__ __align__(16) T sgK[kBuf][L::kRowElems];
-  __shared__ __align__(16) T sgV[kBuf][L::kRowElems];
+  constexpr int kE = kPar ? 8 : L::kRowElems;  // the run-time-indexed arrays (unused with kPar)
+  __shared__ __align__(16) T sK[kBuf][kE];
+  __shared__ __align__(16) T sV[kBuf][kE];
+  __shared__ __align__(16) T sgK[kBuf][kE];
+  __shared__ __align__(16) T sgV[kBuf][kE];
+  constexpr int kPE = kPar ? L::kRowElems : 8;
+  __shared__ __align__(16) T pK0[kPE];
+  __shared__ __align__(16) T pV0[kPE];
+  __shared__ __align__(16) T pgK0[kPE];
+  __shared__ __align__(16) T pgV0[kPE];
+  __shared__ __align__(16) T pK1[kPE];
+  __shared__ __align__(16) T pV1[kPE];
+  __shared__ __align__(16) T pgK1[kPE];
+  __shared__ __align__(16) T pgV1[kPE];
 
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
@@ -242,46 +261,12 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
       advance();
     }
   };
-  if constexpr (kDma) {
-    dd.offsets(oK, a.k.st);
-    dd.offsets(oV, a.v.st);
-    dd.offsets(ogK, a.gk.st);
-    dd.offsets(ogV, a.gv.st);
-    dma_tile(cr.t0, 0);
-  } else {
-    load_tile(cr.t0);
-  }
-  for (int nb = cr.t0; nb < cr.t1; ++nb) {
+  // One streamed tile (key block nb) from LDS tiles cK, cV, cgK, cgV; with
+  // LOADP, p already holds its probabilities.
+  auto tile_body = [&](int nb, const T* cK, const T* cV, const T* cgK, const T* cgV, Tile& p)
+      __attribute__((always_inline)) {
     const int n0 = nb * kBlk;
-    const int cur = kDma ? ((nb - cr.t0) & 1) : 0;
-    if constexpr (kDma) {
-      dma_wait();  // this wave's loads of tile nb (LDS tiles and P fragments)
-      __syncthreads();  // everyone's, and everyone is done with the other buffer
-    } else {
-      __syncthreads();
-      stage_store_rows<T, D>(s0, sK[0]);
-      stage_store_rows<T, D>(s1, sV[0]);
-      stage_store_rows<T, D>(s2, sgK[0]);
-      stage_store_rows<T, D>(s3, sgV[0]);
-      __syncthreads();
-    }
-    const T* cK = sK[cur];
-    const T* cV = sV[cur];
-    const T* cgK = sgK[cur];
-    const T* cgV = sgV[cur];
-    Tile p, dp, gds, gp1;
-    if constexpr (LOADP) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) p.set(kb, j, E::f32(pn[kb][j]));
-    }
-    if (nb + 1 < cr.t1) {
-      if constexpr (kDma)
-        dma_tile(nb + 1, cur ^ 1);
-      else
-        load_tile(nb + 1);
-    }
+    Tile dp, gds, gp1;
     if constexpr (!LOADP) {
       p.zero();
       mm_d<T, D>(p, cK, qf);
@@ -345,6 +330,100 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
     if constexpr (GDO) {
       mm_s<T, D>(b1, cgV, pf);
       mm_s2<T, D>(b2, z4f, b3, pf, cV);
+    }
+  };
+  auto p_from_frags = [&](Tile& p) __attribute__((always_inline)) {
+    if constexpr (LOADP) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) p.set(kb, j, E::f32(pn[kb][j]));
+    }
+  };
+
+  if constexpr (kPar) {
+    dd.offsets(oK, a.k.st);
+    dd.offsets(oV, a.v.st);
+    dd.offsets(ogK, a.gk.st);
+    dd.offsets(ogV, a.gv.st);
+    auto dma_set = [&](int nb, T* k, T* v, T* gk, T* gv) __attribute__((always_inline)) {
+      const int n0 = nb * kBlk;
+      if (n0 + kBlk <= T_) {  // uniform: one test per tile for all four tiles and P
+        dd.load_full(k, Kn, oK);
+        dd.load_full(v, Vn, oV);
+        dd.load_full(gk, gKn, ogK);
+        dd.load_full(gv, gVn, ogV);
+        if constexpr (LOADP) {
+          pn[0] = load_frag_g<T>(Pn);
+          pn[1] = load_frag_g<T>(Pn + 32);
+        }
+      } else {
+        dd.load_ragged(k, Kn, a.k.st, T_ - n0, D);
+        dd.load_ragged(v, Vn, a.v.st, T_ - n0, D);
+        dd.load_ragged(gk, gKn, a.gk.st, T_ - n0, D);
+        dd.load_ragged(gv, gVn, a.gv.st, T_ - n0, D);
+        if constexpr (LOADP) load_p_frags<T>(pn, Pm, n0, T_);
+      }
+      advance();
+    };
+    // Tile nb from set P while tile nb + 1 streams into set 1 - P.
+    auto step = [&](auto par, int nb) __attribute__((always_inline)) {
+      constexpr int P = decltype(par)::value;
+      dma_wait();       // this wave's loads of tile nb (LDS tiles and P fragments)
+      __syncthreads();  // everyone's, and everyone is done with the other set
+      Tile p;
+      p_from_frags(p);
+      // Keep the conversion ahead of the next tile's loads: sunk below them,
+      // it would wait for those loads (vmcnt) before the tile's work.
+      __builtin_amdgcn_sched_barrier(0);
+      if (nb + 1 < cr.t1) {
+        if constexpr (P == 0)
+          dma_set(nb + 1, pK1, pV1, pgK1, pgV1);
+        else
+          dma_set(nb + 1, pK0, pV0, pgK0, pgV0);
+      }
+      if constexpr (P == 0)
+        tile_body(nb, pK0, pV0, pgK0, pgV0, p);
+      else
+        tile_body(nb, pK1, pV1, pgK1, pgV1, p);
+    };
+    dma_set(cr.t0, pK0, pV0, pgK0, pgV0);
+    for (int nb = cr.t0; nb < cr.t1; nb += 2) {
+      step(Parity<0>{}, nb);
+      if (nb + 1 < cr.t1) step(Parity<1>{}, nb + 1);
+    }
+  } else {
+    if constexpr (kDma) {
+      dd.offsets(oK, a.k.st);
+      dd.offsets(oV, a.v.st);
+      dd.offsets(ogK, a.gk.st);
+      dd.offsets(ogV, a.gv.st);
+      dma_tile(cr.t0, 0);
+    } else {
+      load_tile(cr.t0);
+    }
+    for (int nb = cr.t0; nb < cr.t1; ++nb) {
+      const int cur = kDma ? ((nb - cr.t0) & 1) : 0;
+      if constexpr (kDma) {
+        dma_wait();  // this wave's loads of tile nb (LDS tiles and P fragments)
+        __syncthreads();  // everyone's, and everyone is done with the other buffer
+      } else {
+        __syncthreads();
+        stage_store_rows<T, D>(s0, sK[0]);
+        stage_store_rows<T, D>(s1, sV[0]);
+        stage_store_rows<T, D>(s2, sgK[0]);
+        stage_store_rows<T, D>(s3, sgV[0]);
+        __syncthreads();
+      }
+      Tile p;
+      p_from_frags(p);
+      if (nb + 1 < cr.t1) {
+        if constexpr (kDma)
+          dma_tile(nb + 1, cur ^ 1);
+        else
+          load_tile(nb + 1);
+      }
+      tile_body(nb, sK[cur], sV[cur], sgK[cur], sgV[cur], p);
     }
   }
   const float Ev = group_sum(e_acc);

@@ -98,6 +98,11 @@ static_assert(TTT_GG_HEAD_DIM == 64 || TTT_GG_HEAD_DIM == 128, "head dim of this
 #ifndef TTT_GG_ROW_DMA_WIDE
 #define TTT_GG_ROW_DMA_WIDE 1
 #endif
+// The row kernel at D = 64 uses the two-set form too (1) or run-time-picked
+// buffers of one array per operand (0).
+#ifndef TTT_GG_ROW_PAR64
+#define TTT_GG_ROW_PAR64 0
+#endif
 #ifndef TTT_GG_COL_DMA_WIDE
 #define TTT_GG_COL_DMA_WIDE 1
 #endif
@@ -131,8 +136,8 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
   // (kPar), so that the current tile's LDS reads need not wait for the next
   // tile's loads (with one workgroup per CU at D = 128 nothing else would hide
   // that wait).  The rest stage tiles through registers into one buffer.
-  constexpr bool kDma = L::kSwizzle && D == 64;
-  constexpr bool kPar = L::kSwizzle && D == 128 && TTT_GG_ROW_DMA_WIDE;
+  constexpr bool kPar = L::kSwizzle && ((D == 128 && TTT_GG_ROW_DMA_WIDE) || (D == 64 && TTT_GG_ROW_PAR64));
+  constexpr bool kDma = L::kSwizzle && D == 64 && !kPar;
   constexpr int kBuf = kDma ? 2 : 1;
   constexpr int kE = kPar ? 8 : L::kRowElems;  // the run-time-indexed arrays (unused with kPar)
   __shared__ __align__(16) T sK[kBuf][kE];

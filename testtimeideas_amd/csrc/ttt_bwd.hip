@@ -24,6 +24,11 @@
 #include "ttt_common.h"
 #include "ttt_launch.h"
 
+// The saved-P dQ kernel streams 16-bit D = 64 key tiles by direct loads (1)
+// or through registers (0).
+#ifndef TTT_DQ_DMA
+#define TTT_DQ_DMA 1
+#endif
 #ifndef TTT_DQ_FULLTILE
 #define TTT_DQ_FULLTILE 1
 #endif
@@ -87,8 +92,12 @@ __attribute__((amdgpu_waves_per_eu(DqWaves<T, D, LOADP>::value))) void k_bwd_dq(
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
-  __shared__ __align__(16) T sK[L::kRowElems];
-  __shared__ __align__(16) T sV[L::kRowElems];
+  // Saved-P 16-bit tiles stream straight into two LDS buffers per operand
+  // (TileDma, picked at run time; the other workgroups on a CU cover the wait
+  // for the next tile's loads that the compiler puts before LDS reads).
+  constexpr bool kDma = TTT_DQ_DMA && LOADP && L::kSwizzle && D == 64;  // D = 128: measured 4 % slower
+  __shared__ __align__(16) T sK[kDma ? 2 : 1][L::kRowElems];
+  __shared__ __align__(16) T sV[kDma ? 2 : 1][L::kRowElems];
 
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
@@ -166,23 +175,63 @@ __attribute__((amdgpu_waves_per_eu(DqWaves<T, D, LOADP>::value))) void k_bwd_dq(
     Vn += kBlk * a.v.st;
     if constexpr (LOADP) Pn += kBlk;
   };
-  fetch(cr.t0);
   // The last tile is peeled off the loop, so inside it the next tile's fetch
   // is unconditional and its registers need no copies across iterations.
+  // Direct loads of key tile nb into buffer `buf` (kDma).
+  const TileDma<T, D> dd;
+  int oK[TileDma<T, D>::kPerWave], oV[TileDma<T, D>::kPerWave];
+  if constexpr (kDma) {
+    dd.offsets(oK, a.k.st);
+    dd.offsets(oV, a.v.st);
+  }
+  auto fetch_dma = [&](int nb, int buf) __attribute__((always_inline)) {
+    const int n1 = nb * kBlk;
+    if (n1 + kBlk <= T_) {
+      dd.load_full(sK[buf], Kn, oK);
+      dd.load_full(sV[buf], Vn, oV);
+      pn[0] = load_frag_g<T>(Pn);
+      pn[1] = load_frag_g<T>(Pn + 32);
+    } else {
+      dd.load_ragged(sK[buf], Kn, a.k.st, T_ - n1, D);
+      dd.load_ragged(sV[buf], Vn, a.v.st, T_ - n1, D);
+      load_p_frags<T>(pn, Pm, n1, T_);
+    }
+    Kn += kBlk * a.k.st;
+    Vn += kBlk * a.v.st;
+    Pn += kBlk;
+  };
+  if constexpr (kDma)
+    fetch_dma(cr.t0, 0);
+  else
+    fetch(cr.t0);
   auto tile = [&](int nb, auto prefetch) __attribute__((always_inline)) {
     const int n0 = nb * kBlk;
-    __syncthreads();
-    stage_store_rows<T, D>(stK, sK);
-    stage_store_rows<T, D>(stV, sV);
-    __syncthreads();
+    const int cur = kDma ? ((nb - cr.t0) & 1) : 0;
+    if constexpr (kDma) {
+      dma_wait();       // this wave's loads of tile nb
+      __syncthreads();  // everyone's, and everyone is done with the other buffer
+    } else {
+      __syncthreads();
+      stage_store_rows<T, D>(stK, sK[0]);
+      stage_store_rows<T, D>(stV, sV[0]);
+      __syncthreads();
+    }
+    const T* cK = sK[cur];
+    const T* cV = sV[cur];
     Tile p;
     if constexpr (LOADP) frags_to_tile<T>(p, pn);
-    if constexpr (decltype(prefetch)::value == 1) fetch(nb + 1);
-    if constexpr (decltype(prefetch)::value == 2)
-      if (nb + 1 < cr.t1) fetch(nb + 1);
+    if constexpr (kDma) {
+      if constexpr (decltype(prefetch)::value == 1) fetch_dma(nb + 1, cur ^ 1);
+      if constexpr (decltype(prefetch)::value == 2)
+        if (nb + 1 < cr.t1) fetch_dma(nb + 1, cur ^ 1);
+    } else {
+      if constexpr (decltype(prefetch)::value == 1) fetch(nb + 1);
+      if constexpr (decltype(prefetch)::value == 2)
+        if (nb + 1 < cr.t1) fetch(nb + 1);
+    }
     if constexpr (!LOADP) {
       p.zero();
-      mm_d<T, D>(p, sK, qf);
+      mm_d<T, D>(p, cK, qf);
       recompute_p_row<T, XM>(p, a, brow, n0, lse2, a.scale_log2);
     }
     if (mk.tile(nb)) {
@@ -194,7 +243,7 @@ __attribute__((amdgpu_waves_per_eu(DqWaves<T, D, LOADP>::value))) void k_bwd_dq(
     }
     Tile dp;
     dp.zero();
-    mm_d<T, D>(dp, sV, dof);
+    mm_d<T, D>(dp, cV, dof);
     frag dsf[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -203,7 +252,7 @@ __attribute__((amdgpu_waves_per_eu(DqWaves<T, D, LOADP>::value))) void k_bwd_dq(
       for (int j = 0; j < 8; ++j) v[j] = p.at(kb, j) * (dp.at(kb, j) - Dm);
       dsf[kb] = vals_frag<T>(v);
     }
-    mm_s<T, D>(acc, sK, dsf);
+    mm_s<T, D>(acc, cK, dsf);
   };
   if constexpr (TTT_DQ_PEEL && LOADP) {
     for (int nb = cr.t0; nb + 1 < cr.t1; ++nb) tile(nb, Parity<1>{});

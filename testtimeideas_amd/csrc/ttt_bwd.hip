@@ -44,6 +44,11 @@
 #ifndef TTT_DKDV_FULLTILE
 #define TTT_DKDV_FULLTILE 0
 #endif
+// The saved-P dK/dV kernel streams 16-bit D = 64 tiles by direct loads (1) or
+// through registers (0).
+#ifndef TTT_DKDV_DMA
+#define TTT_DKDV_DMA 1
+#endif
 #ifndef TTT_DKDV_PEEL
 #define TTT_DKDV_PEEL 0
 #endif
@@ -275,14 +280,18 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_BWD_RECOMPUTE && !LOADP && 
   typedef Lds<T, D> L;
   typedef Lds<T, kBlk> LP;
   constexpr bool kNeedQ = !DV_ONLY || !LOADP;
-  __shared__ __align__(16) T sdO[L::kRowElems];
-  __shared__ __align__(16) T sQ[kNeedQ ? L::kRowElems : 8];
-  __shared__ __align__(16) T sP[LOADP ? LP::kRowElems : 8];
   // Staged row statistics of the streamed tile: D (unless DV_ONLY), then lse
   // (recompute only).
   constexpr int kNS = (DV_ONLY ? 0 : 1) + (LOADP ? 0 : 1);
   constexpr int kSD = 0, kSL = DV_ONLY ? 0 : 1;
-  __shared__ __align__(16) float sS[kNS > 0 ? kNS * kBlk : 4];
+  // Saved-P 16-bit D = 64 tiles (dO, Q, P and the rowsum slice) stream
+  // straight into two LDS buffers each (TileDma; buffer picked at run time).
+  constexpr bool kDma = TTT_DKDV_DMA && LOADP && !DV_ONLY && L::kSwizzle && D == 64;
+  constexpr int kB = kDma ? 2 : 1;
+  __shared__ __align__(16) T sdO[kB][L::kRowElems];
+  __shared__ __align__(16) T sQ[kB][kNeedQ ? L::kRowElems : 8];
+  __shared__ __align__(16) T sP[kB][LOADP ? LP::kRowElems : 8];
+  __shared__ __align__(16) float sS[kB][kNS > 0 ? kNS * kBlk : 4];
 
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
@@ -346,34 +355,77 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_BWD_RECOMPUTE && !LOADP && 
     if constexpr (kNeedQ) Qn += kBlk * a.q.st;
     if constexpr (LOADP) Pn += kBlk * a.p.st;
   };
-  load_tile(cr.t0);
+  // Direct loads of query tile mb into buffer `buf` (kDma), in order through
+  // the same running pointers.
+  const TileDma<T, D> dd;
+  const TileDma<T, kBlk> dpt;
+  int odO[TileDma<T, D>::kPerWave], oQ[TileDma<T, D>::kPerWave], oP[TileDma<T, kBlk>::kPerWave];
+  if constexpr (kDma) {
+    dd.offsets(odO, a.dout.st);
+    dd.offsets(oQ, a.q.st);
+    dpt.offsets(oP, a.p.st);
+  }
+  const StatDma<1> sdma(rs, nullptr, nullptr, nullptr);
+  auto dma_tile = [&](int mb, int buf) __attribute__((always_inline)) {
+    const int m0 = mb * kBlk;
+    if (m0 + kBlk <= T_ && cols_full) {
+      dd.load_full(sdO[buf], dOn, odO);
+      dd.load_full(sQ[buf], Qn, oQ);
+      dpt.load_full(sP[buf], Pn, oP);
+    } else {
+      dd.load_ragged(sdO[buf], dOn, a.dout.st, T_ - m0, D);
+      dd.load_ragged(sQ[buf], Qn, a.q.st, T_ - m0, D);
+      dpt.load_ragged(sP[buf], Pn, a.p.st, T_ - m0, T_ - n0);
+    }
+    sdma.load(sS[buf], m0, T_ - m0);
+    dOn += kBlk * a.dout.st;
+    Qn += kBlk * a.q.st;
+    Pn += kBlk * a.p.st;
+  };
+  if constexpr (kDma)
+    dma_tile(cr.t0, 0);
+  else
+    load_tile(cr.t0);
   // The last tile is peeled off the loop, so inside it the next tile's fetch
   // is unconditional.
   auto tile = [&](int mb, auto prefetch) __attribute__((always_inline)) {
     const int m0 = mb * kBlk;
-    __syncthreads();
-    stage_store_rows<T, D>(stdO, sdO);
-    if constexpr (kNeedQ) stage_store_rows<T, D>(stQ, sQ);
-    if constexpr (LOADP) stage_store_rows<T, kBlk>(stP, sP);
-    if constexpr (kNS > 0) stat_store<kNS>(stv, sS);
-    __syncthreads();
-    if constexpr (decltype(prefetch)::value == 1) load_tile(mb + 1);
-    if constexpr (decltype(prefetch)::value == 2)
-      if (mb + 1 < cr.t1) load_tile(mb + 1);
+    const int cur = kDma ? ((mb - cr.t0) & 1) : 0;
+    if constexpr (kDma) {
+      dma_wait();       // this wave's loads of tile mb
+      __syncthreads();  // everyone's; everyone is also done with the other buffer
+      if constexpr (decltype(prefetch)::value == 1) dma_tile(mb + 1, cur ^ 1);
+      if constexpr (decltype(prefetch)::value == 2)
+        if (mb + 1 < cr.t1) dma_tile(mb + 1, cur ^ 1);
+    } else {
+      __syncthreads();
+      stage_store_rows<T, D>(stdO, sdO[0]);
+      if constexpr (kNeedQ) stage_store_rows<T, D>(stQ, sQ[0]);
+      if constexpr (LOADP) stage_store_rows<T, kBlk>(stP, sP[0]);
+      if constexpr (kNS > 0) stat_store<kNS>(stv, sS[0]);
+      __syncthreads();
+      if constexpr (decltype(prefetch)::value == 1) load_tile(mb + 1);
+      if constexpr (decltype(prefetch)::value == 2)
+        if (mb + 1 < cr.t1) load_tile(mb + 1);
+    }
+    const T* cdO = sdO[cur];
+    const T* cQ = sQ[cur];
+    const T* cP = sP[cur];
+    const float* cS = sS[cur];
 
     // P(m, n) for streamed m = m0 + 32kb + 8g + j, stationary n.
     Tile p;
     if constexpr (LOADP) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const frag f = load_frag_tr<T, kBlk>(sP, 32 * kb, 16 * w);
+        const frag f = load_frag_tr<T, kBlk>(cP, 32 * kb, 16 * w);
 #pragma unroll
         for (int j = 0; j < 8; ++j) p.set(kb, j, E::f32(f[j]));
       }
     } else {
       p.zero();
-      mm_d<T, D>(p, sQ, kf);
-      recompute_p_col<T, XM>(p, a, bcol, m0, sS, kSL, a.scale_log2);
+      mm_d<T, D>(p, cQ, kf);
+      recompute_p_col<T, XM>(p, a, bcol, m0, cS, kSL, a.scale_log2);
     }
     if (mk.tile(mb)) {
 #pragma unroll
@@ -385,21 +437,21 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_BWD_RECOMPUTE && !LOADP && 
     frag pf[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) pf[kb] = tile_frag<T>(p, kb);
-    mm_s<T, D>(acc_dv, sdO, pf);
+    mm_s<T, D>(acc_dv, cdO, pf);
     if constexpr (!DV_ONLY) {
       Tile dp;
       dp.zero();
-      mm_d<T, D>(dp, sdO, vf);
+      mm_d<T, D>(dp, cdO, vf);
       frag dsf[2];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         float d8[8], v[8];
-        stat_read8(d8, sS, kSD, kb);
+        stat_read8(d8, cS, kSD, kb);
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = p.at(kb, j) * (dp.at(kb, j) - d8[j]);
         dsf[kb] = vals_frag<T>(v);
       }
-      mm_s<T, D>(acc_dk, sQ, dsf);
+      mm_s<T, D>(acc_dk, cQ, dsf);
     }
   };
 #if TTT_DKDV_PEEL

@@ -29,6 +29,11 @@
 #ifndef TTT_DQ_DMA
 #define TTT_DQ_DMA 1
 #endif
+// The saved-P dQ kernel's direct loads go to two buffer sets in distinct
+// arrays with compile-time roles (1) or to run-time-picked buffers (0).
+#ifndef TTT_DQ_PAR
+#define TTT_DQ_PAR 0
+#endif
 #ifndef TTT_DQ_FULLTILE
 #define TTT_DQ_FULLTILE 1
 #endif
@@ -87,7 +92,12 @@ __device__ __forceinline__ void frags_to_tile(Tile& p, const typename Elem<T>::f
 template <typename T, int D, bool LOADP>
 struct DqWaves {
   static constexpr bool kVacc = TTT_VACC_BWD_RECOMPUTE && !LOADP && D == 64;
-  static constexpr int value = kVacc ? (sizeof(T) == 2 ? 4 : AccWaves<true>::value) : AccWaves<false>::value;
+  // The saved-P 16-bit D = 64 kernel in the two-set form (two tiles per loop
+  // step): without a register cap the compiler keeps the accumulators in
+  // AGPRs and copies them every step.
+  static constexpr bool kPar = TTT_DQ_DMA && TTT_DQ_PAR && LOADP && sizeof(T) == 2 && D == 64;
+  static constexpr int value =
+      kVacc ? (sizeof(T) == 2 ? 4 : AccWaves<true>::value) : kPar ? 3 : AccWaves<false>::value;
 };
 
 // ---------------------------------------------------------------------------
@@ -98,11 +108,29 @@ __attribute__((amdgpu_waves_per_eu(DqWaves<T, D, LOADP>::value))) void k_bwd_dq(
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
   // Saved-P 16-bit tiles stream straight into two LDS buffers per operand
-  // (TileDma, picked at run time; the other workgroups on a CU cover the wait
-  // for the next tile's loads that the compiler puts before LDS reads).
+  // (TileDma): with kPar, two sets in distinct arrays with a compile-time role
+  // per loop step (so that the current tile's LDS reads need not wait for the
+  // next tile's loads), else two buffers of one array picked at run time.
   constexpr bool kDma = TTT_DQ_DMA && LOADP && L::kSwizzle && D == 64;  // D = 128: measured 4 % slower
-  __shared__ __align__(16) T sK[kDma ? 2 : 1][L::kRowElems];
-  __shared__ __align__(16) T sV[kDma ? 2 : 1][L::kRowElems];
+  constexpr bool kPar = kDma && TTT_DQ_PAR;
+  constexpr bool kRt = kDma && !kPar;
+  constexpr int kE1 = kPar ? L::kRowElems : 8, kER = kRt ? L::kRowElems : 8;
+  __shared__ __align__(16) T sK0[kRt ? 8 : L::kRowElems];
+  __shared__ __align__(16) T sV0[kRt ? 8 : L::kRowElems];
+  __shared__ __align__(16) T sK1[kE1];
+  __shared__ __align__(16) T sV1[kE1];
+  __shared__ __align__(16) T sKr[kRt ? 2 : 1][kER];
+  __shared__ __align__(16) T sVr[kRt ? 2 : 1][kER];
+  auto set_k = [&](auto par) __attribute__((always_inline)) -> T* {
+    if constexpr (std::is_same_v<decltype(par), RtBuf>) return sKr[par.cur];
+    else if constexpr (decltype(par)::value == 0) return sK0;
+    else return sK1;
+  };
+  auto set_v = [&](auto par) __attribute__((always_inline)) -> T* {
+    if constexpr (std::is_same_v<decltype(par), RtBuf>) return sVr[par.cur];
+    else if constexpr (decltype(par)::value == 0) return sV0;
+    else return sV1;
+  };
 
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
@@ -180,55 +208,57 @@ __attribute__((amdgpu_waves_per_eu(DqWaves<T, D, LOADP>::value))) void k_bwd_dq(
     Vn += kBlk * a.v.st;
     if constexpr (LOADP) Pn += kBlk;
   };
-  // The last tile is peeled off the loop, so inside it the next tile's fetch
-  // is unconditional and its registers need no copies across iterations.
-  // Direct loads of key tile nb into buffer `buf` (kDma).
+  // Direct loads of key tile nb into buffer set `par` (kDma).
   const TileDma<T, D> dd;
   int oK[TileDma<T, D>::kPerWave], oV[TileDma<T, D>::kPerWave];
   if constexpr (kDma) {
     dd.offsets(oK, a.k.st);
     dd.offsets(oV, a.v.st);
   }
-  auto fetch_dma = [&](int nb, int buf) __attribute__((always_inline)) {
+  auto fetch_dma = [&](int nb, auto par) __attribute__((always_inline)) {
     const int n1 = nb * kBlk;
     if (n1 + kBlk <= T_) {
-      dd.load_full(sK[buf], Kn, oK);
-      dd.load_full(sV[buf], Vn, oV);
+      dd.load_full(set_k(par), Kn, oK);
+      dd.load_full(set_v(par), Vn, oV);
       pn[0] = load_frag_g<T>(Pn);
       pn[1] = load_frag_g<T>(Pn + 32);
     } else {
-      dd.load_ragged(sK[buf], Kn, a.k.st, T_ - n1, D);
-      dd.load_ragged(sV[buf], Vn, a.v.st, T_ - n1, D);
+      dd.load_ragged(set_k(par), Kn, a.k.st, T_ - n1, D);
+      dd.load_ragged(set_v(par), Vn, a.v.st, T_ - n1, D);
       load_p_frags<T>(pn, Pm, n1, T_);
+      dma_wait();
     }
     Kn += kBlk * a.k.st;
     Vn += kBlk * a.v.st;
     Pn += kBlk;
   };
-  if constexpr (kDma)
-    fetch_dma(cr.t0, 0);
+  if constexpr (kPar)
+    fetch_dma(cr.t0, Parity<0>{});
+  else if constexpr (kRt)
+    fetch_dma(cr.t0, RtBuf{0});
   else
     fetch(cr.t0);
-  auto tile = [&](int nb, auto prefetch) __attribute__((always_inline)) {
+  // Tile nb from buffer set `par`; `prefetch`: 1 fetch tile nb + 1, 2 fetch it
+  // if it exists, 0 none.
+  auto tile = [&](int nb, auto prefetch, auto par) __attribute__((always_inline)) {
     const int n0 = nb * kBlk;
-    const int cur = kDma ? ((nb - cr.t0) & 1) : 0;
     if constexpr (kDma) {
       dma_wait();       // this wave's loads of tile nb
-      __syncthreads();  // everyone's, and everyone is done with the other buffer
+      __syncthreads();  // everyone's, and everyone is done with the other set
     } else {
       __syncthreads();
-      stage_store_rows<T, D>(stK, sK[0]);
-      stage_store_rows<T, D>(stV, sV[0]);
+      stage_store_rows<T, D>(stK, sK0);
+      stage_store_rows<T, D>(stV, sV0);
       __syncthreads();
     }
-    const T* cK = sK[cur];
-    const T* cV = sV[cur];
+    const T* cK = set_k(par);
+    const T* cV = set_v(par);
     Tile p;
     if constexpr (LOADP) frags_to_tile<T>(p, pn);
     if constexpr (kDma) {
-      if constexpr (decltype(prefetch)::value == 1) fetch_dma(nb + 1, cur ^ 1);
+      if constexpr (decltype(prefetch)::value == 1) fetch_dma(nb + 1, other_buf(par));
       if constexpr (decltype(prefetch)::value == 2)
-        if (nb + 1 < cr.t1) fetch_dma(nb + 1, cur ^ 1);
+        if (nb + 1 < cr.t1) fetch_dma(nb + 1, other_buf(par));
     } else {
       if constexpr (decltype(prefetch)::value == 1) fetch(nb + 1);
       if constexpr (decltype(prefetch)::value == 2)
@@ -259,11 +289,24 @@ __attribute__((amdgpu_waves_per_eu(DqWaves<T, D, LOADP>::value))) void k_bwd_dq(
     }
     mm_s<T, D>(acc, cK, dsf);
   };
-  if constexpr (TTT_DQ_PEEL && LOADP) {
-    for (int nb = cr.t0; nb + 1 < cr.t1; ++nb) tile(nb, Parity<1>{});
-    tile(cr.t1 - 1, Parity<0>{});
+  if constexpr (kPar) {
+    for (int nb = cr.t0; nb < cr.t1; nb += 2) {
+      tile(nb, Parity<2>{}, Parity<0>{});
+      if (nb + 1 < cr.t1) tile(nb + 1, Parity<2>{}, Parity<1>{});
+    }
+  } else if constexpr (kRt && TTT_DQ_PEEL) {
+    // The last tile is peeled off the loop, so inside it the next tile's
+    // fetch is unconditional and its registers need no copies across
+    // iterations.
+    for (int nb = cr.t0; nb + 1 < cr.t1; ++nb) tile(nb, Parity<1>{}, RtBuf{(nb - cr.t0) & 1});
+    tile(cr.t1 - 1, Parity<0>{}, RtBuf{(cr.t1 - 1 - cr.t0) & 1});
+  } else if constexpr (kRt) {
+    for (int nb = cr.t0; nb < cr.t1; ++nb) tile(nb, Parity<2>{}, RtBuf{(nb - cr.t0) & 1});
+  } else if constexpr (TTT_DQ_PEEL && LOADP) {
+    for (int nb = cr.t0; nb + 1 < cr.t1; ++nb) tile(nb, Parity<1>{}, Parity<0>{});
+    tile(cr.t1 - 1, Parity<0>{}, Parity<0>{});
   } else {
-    for (int nb = cr.t0; nb < cr.t1; ++nb) tile(nb, Parity<2>{});
+    for (int nb = cr.t0; nb < cr.t1; ++nb) tile(nb, Parity<2>{}, Parity<0>{});
   }
   if (cr.nch == 1)
     store_acc_rows<T, D>(at<T>(a.dq, b, h), a.dq.st, m, T_, acc, a.scale);
@@ -272,9 +315,22 @@ __attribute__((amdgpu_waves_per_eu(DqWaves<T, D, LOADP>::value))) void k_bwd_dq(
 }
 
 // ---------------------------------------------------------------------------
+// Waves per SIMD the dK/dV kernel is compiled for: recompute at D = 64 caps
+// registers for VGPR accumulators; the saved-P 16-bit D = 64 kernel (direct
+// loads) for TTT_DKDV_WAVES waves.
+#ifndef TTT_DKDV_WAVES
+#define TTT_DKDV_WAVES 3
+#endif
+template <typename T, int D, bool LOADP, bool DV_ONLY>
+struct DkdvWaves {
+  static constexpr bool kDma = TTT_DKDV_DMA && LOADP && !DV_ONLY && sizeof(T) == 2 && D == 64;
+  static constexpr int value =
+      kDma ? TTT_DKDV_WAVES : AccWaves<TTT_VACC_BWD_RECOMPUTE && !LOADP && D == 64>::value;
+};
+
 template <typename T, int D, bool LOADP, bool DV_ONLY, bool XM>
 __global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_BWD_RECOMPUTE && !LOADP && D == 64>::value))) void k_bwd_dkdv(Params a) {
+__attribute__((amdgpu_waves_per_eu(DkdvWaves<T, D, LOADP, DV_ONLY>::value))) void k_bwd_dkdv(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
@@ -285,13 +341,29 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_BWD_RECOMPUTE && !LOADP && 
   constexpr int kNS = (DV_ONLY ? 0 : 1) + (LOADP ? 0 : 1);
   constexpr int kSD = 0, kSL = DV_ONLY ? 0 : 1;
   // Saved-P 16-bit D = 64 tiles (dO, Q, P and the rowsum slice) stream
-  // straight into two LDS buffers each (TileDma; buffer picked at run time).
+  // straight into two LDS buffer sets (TileDma) in distinct arrays with a
+  // compile-time role per loop step, so that the current tile's LDS reads
+  // need not wait for the next tile's loads.
   constexpr bool kDma = TTT_DKDV_DMA && LOADP && !DV_ONLY && L::kSwizzle && D == 64;
-  constexpr int kB = kDma ? 2 : 1;
-  __shared__ __align__(16) T sdO[kB][L::kRowElems];
-  __shared__ __align__(16) T sQ[kB][kNeedQ ? L::kRowElems : 8];
-  __shared__ __align__(16) T sP[kB][LOADP ? LP::kRowElems : 8];
-  __shared__ __align__(16) float sS[kB][kNS > 0 ? kNS * kBlk : 4];
+  constexpr int kQE = kNeedQ ? L::kRowElems : 8, kPE = LOADP ? LP::kRowElems : 8, kSE = kNS > 0 ? kNS * kBlk : 4;
+  __shared__ __align__(16) T sdO0[L::kRowElems];
+  __shared__ __align__(16) T sQ0[kQE];
+  __shared__ __align__(16) T sP0[kPE];
+  __shared__ __align__(16) float sS0[kSE];
+  __shared__ __align__(16) T sdO1[kDma ? L::kRowElems : 8];
+  __shared__ __align__(16) T sQ1[kDma ? kQE : 8];
+  __shared__ __align__(16) T sP1[kDma ? kPE : 8];
+  __shared__ __align__(16) float sS1[kDma ? kSE : 4];
+  struct Bufs {
+    T *dout, *q, *p;
+    float* st;
+  };
+  auto bufs = [&](auto par) __attribute__((always_inline)) -> Bufs {
+    if constexpr (decltype(par)::value == 0)
+      return Bufs{sdO0, sQ0, sP0, sS0};
+    else
+      return Bufs{sdO1, sQ1, sP1, sS1};
+  };
 
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
@@ -355,8 +427,8 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_BWD_RECOMPUTE && !LOADP && 
     if constexpr (kNeedQ) Qn += kBlk * a.q.st;
     if constexpr (LOADP) Pn += kBlk * a.p.st;
   };
-  // Direct loads of query tile mb into buffer `buf` (kDma), in order through
-  // the same running pointers.
+  // Direct loads of query tile mb into buffer set `par` (kDma), in order
+  // through the same running pointers.
   const TileDma<T, D> dd;
   const TileDma<T, kBlk> dpt;
   int odO[TileDma<T, D>::kPerWave], oQ[TileDma<T, D>::kPerWave], oP[TileDma<T, kBlk>::kPerWave];
@@ -366,52 +438,55 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_BWD_RECOMPUTE && !LOADP && 
     dpt.offsets(oP, a.p.st);
   }
   const StatDma<1> sdma(rs, nullptr, nullptr, nullptr);
-  auto dma_tile = [&](int mb, int buf) __attribute__((always_inline)) {
+  auto dma_tile = [&](int mb, auto par) __attribute__((always_inline)) {
     const int m0 = mb * kBlk;
+    const Bufs bf = bufs(par);
     if (m0 + kBlk <= T_ && cols_full) {
-      dd.load_full(sdO[buf], dOn, odO);
-      dd.load_full(sQ[buf], Qn, oQ);
-      dpt.load_full(sP[buf], Pn, oP);
+      dd.load_full(bf.dout, dOn, odO);
+      dd.load_full(bf.q, Qn, oQ);
+      dpt.load_full(bf.p, Pn, oP);
     } else {
-      dd.load_ragged(sdO[buf], dOn, a.dout.st, T_ - m0, D);
-      dd.load_ragged(sQ[buf], Qn, a.q.st, T_ - m0, D);
-      dpt.load_ragged(sP[buf], Pn, a.p.st, T_ - m0, T_ - n0);
+      dd.load_ragged(bf.dout, dOn, a.dout.st, T_ - m0, D);
+      dd.load_ragged(bf.q, Qn, a.q.st, T_ - m0, D);
+      dpt.load_ragged(bf.p, Pn, a.p.st, T_ - m0, T_ - n0);
+      dma_wait();
     }
-    sdma.load(sS[buf], m0, T_ - m0);
+    sdma.load(bf.st, m0, T_ - m0);
     dOn += kBlk * a.dout.st;
     Qn += kBlk * a.q.st;
     Pn += kBlk * a.p.st;
   };
   if constexpr (kDma)
-    dma_tile(cr.t0, 0);
+    dma_tile(cr.t0, Parity<0>{});
   else
     load_tile(cr.t0);
-  // The last tile is peeled off the loop, so inside it the next tile's fetch
-  // is unconditional.
-  auto tile = [&](int mb, auto prefetch) __attribute__((always_inline)) {
+  // Tile mb from buffer set `par`; `prefetch`: 1 fetch tile mb + 1, 2 fetch it
+  // if it exists, 0 none.
+  auto tile = [&](int mb, auto prefetch, auto par) __attribute__((always_inline)) {
     const int m0 = mb * kBlk;
-    const int cur = kDma ? ((mb - cr.t0) & 1) : 0;
+    constexpr int P = decltype(par)::value;
     if constexpr (kDma) {
       dma_wait();       // this wave's loads of tile mb
-      __syncthreads();  // everyone's; everyone is also done with the other buffer
-      if constexpr (decltype(prefetch)::value == 1) dma_tile(mb + 1, cur ^ 1);
+      __syncthreads();  // everyone's; everyone is also done with the other set
+      if constexpr (decltype(prefetch)::value == 1) dma_tile(mb + 1, Parity<1 - P>{});
       if constexpr (decltype(prefetch)::value == 2)
-        if (mb + 1 < cr.t1) dma_tile(mb + 1, cur ^ 1);
+        if (mb + 1 < cr.t1) dma_tile(mb + 1, Parity<1 - P>{});
     } else {
       __syncthreads();
-      stage_store_rows<T, D>(stdO, sdO[0]);
-      if constexpr (kNeedQ) stage_store_rows<T, D>(stQ, sQ[0]);
-      if constexpr (LOADP) stage_store_rows<T, kBlk>(stP, sP[0]);
-      if constexpr (kNS > 0) stat_store<kNS>(stv, sS[0]);
+      stage_store_rows<T, D>(stdO, sdO0);
+      if constexpr (kNeedQ) stage_store_rows<T, D>(stQ, sQ0);
+      if constexpr (LOADP) stage_store_rows<T, kBlk>(stP, sP0);
+      if constexpr (kNS > 0) stat_store<kNS>(stv, sS0);
       __syncthreads();
       if constexpr (decltype(prefetch)::value == 1) load_tile(mb + 1);
       if constexpr (decltype(prefetch)::value == 2)
         if (mb + 1 < cr.t1) load_tile(mb + 1);
     }
-    const T* cdO = sdO[cur];
-    const T* cQ = sQ[cur];
-    const T* cP = sP[cur];
-    const float* cS = sS[cur];
+    const Bufs cb = bufs(par);
+    const T* cdO = cb.dout;
+    const T* cQ = cb.q;
+    const T* cP = cb.p;
+    const float* cS = cb.st;
 
     // P(m, n) for streamed m = m0 + 32kb + 8g + j, stationary n.
     Tile p;
@@ -454,12 +529,21 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_BWD_RECOMPUTE && !LOADP && 
       mm_s<T, D>(acc_dk, cQ, dsf);
     }
   };
+  if constexpr (kDma) {
+    for (int mb = cr.t0; mb < cr.t1; mb += 2) {
+      tile(mb, Parity<2>{}, Parity<0>{});
+      if (mb + 1 < cr.t1) tile(mb + 1, Parity<2>{}, Parity<1>{});
+    }
+  } else {
 #if TTT_DKDV_PEEL
-  for (int mb = cr.t0; mb + 1 < cr.t1; ++mb) tile(mb, Parity<1>{});
-  tile(cr.t1 - 1, Parity<0>{});
+    // The last tile is peeled off the loop, so inside it the next tile's
+    // fetch is unconditional.
+    for (int mb = cr.t0; mb + 1 < cr.t1; ++mb) tile(mb, Parity<1>{}, Parity<0>{});
+    tile(cr.t1 - 1, Parity<0>{}, Parity<0>{});
 #else
-  for (int mb = cr.t0; mb < cr.t1; ++mb) tile(mb, Parity<2>{});
+    for (int mb = cr.t0; mb < cr.t1; ++mb) tile(mb, Parity<2>{}, Parity<0>{});
 #endif
+  }
   if (cr.nch == 1) {
     store_acc_rows<T, D>(at<T>(a.dv, b, h), a.dv.st, n, T_, acc_dv, 1.f);
     if constexpr (!DV_ONLY) store_acc_rows<T, D>(at<T>(a.dk, b, h), a.dk.st, n, T_, acc_dk, a.scale);

@@ -35,6 +35,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 // Tile products read all their LDS fragments before the first MFMA (1), or
 // leave the order to the compiler (0), which tends to pair each read with its
 // MFMA and expose every LDS latency.
@@ -917,6 +919,10 @@ __device__ __forceinline__ void stat_read8(float* v, const float* lds, int st, i
 // ---------------------------------------------------------------------------
 typedef __attribute__((address_space(3))) void lds_void_t;
 
+// Word 3 of a raw buffer resource on gfx9-family parts (gfx950): 32-bit
+// data format, no swizzle, no index stride.
+constexpr int kBufWord3 = 0x00020000;
+
 template <typename T, int NCOL>
 struct TileDma {  // for the unpadded (chunk-permuted) layout only: Lds<T, NCOL>::kSwizzle
   typedef Lds<T, NCOL> L;
@@ -952,11 +958,27 @@ struct TileDma {  // for the unpadded (chunk-permuted) layout only: Lds<T, NCOL>
     else
       load_full(lds, g, off);
   }
-  // An interior tile (every row and column valid).
+  // An interior tile (every row and column valid), through the buffer form:
+  // a resource for the tile base (uniform) and the per-lane byte offsets as
+  // they are (32-bit voffset).  The global form would need the offsets' zero
+  // extension next to each load; hoisted out of a loop, it leaves a 64-bit
+  // per-lane address (two registers per load, a 64-bit add per issue, and a
+  // fresh register whose reuse soon after the load makes the compiler wait
+  // for the load to complete).  The resource does no range checking.
   __device__ __forceinline__ void load_full(T* lds, const T* g, const int* off) const {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(g), (short)0, (int)0xFFFFFFFF, kBufWord3);
 #pragma unroll
-    for (int q = 0; q < kPerWave; ++q) issue(lds, g, off[q], q);
+    for (int q = 0; q < kPerWave; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(reinterpret_cast<char*>(lds) + wslice + 4096 * q), 16,
+                                               off[q], 0, 0, 0);
+#endif
   }
+  // A ragged tile's clamped offsets live in temporaries: callers wait for
+  // these loads (dma_wait) before leaving the ragged branch, since with loads
+  // pending on those registers the compiler would wait at the registers' next
+  // use, which after the branches merge is on the full-tile path too.
   __device__ __forceinline__ void load_ragged(T* lds, const T* g, int64_t ld, int rows_valid, int cols_valid) const {
 #pragma unroll
     for (int q = 0; q < kPerWave; ++q) {
@@ -995,16 +1017,28 @@ template <int NS>
 struct StatDma {
   const float* src;  // this wave's statistic, or null (w >= NS)
   int w;
+  int loff;  // 4 * lane: the byte offset of this lane's row in a full tile
   __device__ __forceinline__ StatDma(const float* s0, const float* s1, const float* s2, const float* s3) {
     w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     src = w >= NS ? nullptr : w == 0 ? s0 : w == 1 ? s1 : w == 2 ? s2 : s3;
+    loff = 4 * (threadIdx.x & 63);
   }
+  // A full tile goes through the buffer form with the fixed per-lane offset
+  // (a per-tile offset register, reused soon after the load, would make the
+  // compiler wait for the load); a ragged one clamps its rows.
   __device__ __forceinline__ void load(float* lds, int m0, int rows_valid) const {
     if (w >= NS) return;
 #if defined(__HIP_DEVICE_COMPILE__)
-    const int lane = threadIdx.x & 63;
-    const char* p = reinterpret_cast<const char*>(src + m0) + (uint32_t)(lane < rows_valid ? lane : 0) * 4u;
-    __builtin_amdgcn_global_load_lds(p, (lds_void_t*)(lds + kBlk * w), 4, 0, 0);
+    if (rows_valid >= kBlk) {
+      const __amdgpu_buffer_rsrc_t r =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(src + m0), (short)0, (int)0xFFFFFFFF, kBufWord3);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(lds + kBlk * w), 4, loff, 0, 0, 0);
+    } else {
+      const int lane = threadIdx.x & 63;
+      const char* p = reinterpret_cast<const char*>(src + m0) + (uint32_t)(lane < rows_valid ? lane : 0) * 4u;
+      __builtin_amdgcn_global_load_lds(p, (lds_void_t*)(lds + kBlk * w), 4, 0, 0);
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // see TileDma::load_ragged
+    }
 #endif
   }
 };
@@ -1028,6 +1062,13 @@ template <int P>
 struct Parity {
   static constexpr int value = P;
 };
+// A buffer role picked at run time (buffer `cur` of a two-buffer array).
+struct RtBuf {
+  int cur;
+};
+template <int P>
+__device__ __forceinline__ Parity<1 - P> other_buf(Parity<P>) { return {}; }
+__device__ __forceinline__ RtBuf other_buf(RtBuf b) { return RtBuf{b.cur ^ 1}; }
 
 // Eight consecutive fp32 values v[0..7] = src[idx0 .. idx0+7], zero past n.
 // `fast` (uniform) asserts idx0 + 8 <= n and a 16-byte aligned src + idx0.

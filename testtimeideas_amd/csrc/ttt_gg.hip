@@ -98,10 +98,13 @@ static_assert(TTT_GG_HEAD_DIM == 64 || TTT_GG_HEAD_DIM == 128, "head dim of this
 #ifndef TTT_GG_ROW_DMA_WIDE
 #define TTT_GG_ROW_DMA_WIDE 1
 #endif
-// The row kernel at D = 64 uses the two-set form too (1) or run-time-picked
-// buffers of one array per operand (0).
+// The row kernel at D = 64 without GdO uses the two-set form too (1) or
+// run-time-picked buffers of one array per operand (0).  The compiler cannot
+// tell the two buffers of one array apart, so with run-time buffers it waits
+// for the next tile's direct loads before the current tile's first LDS read.
+// (The GdO variants keep run-time buffers: they spill in the two-set form.)
 #ifndef TTT_GG_ROW_PAR64
-#define TTT_GG_ROW_PAR64 0
+#define TTT_GG_ROW_PAR64 1
 #endif
 #ifndef TTT_GG_COL_DMA_WIDE
 #define TTT_GG_COL_DMA_WIDE 1
@@ -130,13 +133,12 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
   constexpr int NACC = GDO ? 7 : 4;
-  // 16-bit types stream tiles straight into LDS (TileDma): at D = 64 into two
-  // buffers of one array per operand, picked at run time; at D = 128 into two
-  // buffer sets in distinct arrays with a compile-time role per loop step
-  // (kPar), so that the current tile's LDS reads need not wait for the next
-  // tile's loads (with one workgroup per CU at D = 128 nothing else would hide
-  // that wait).  The rest stage tiles through registers into one buffer.
-  constexpr bool kPar = L::kSwizzle && ((D == 128 && TTT_GG_ROW_DMA_WIDE) || (D == 64 && TTT_GG_ROW_PAR64));
+  // 16-bit types stream tiles straight into LDS (TileDma), into two buffer
+  // sets in distinct arrays with a compile-time role per loop step (kPar), so
+  // that the current tile's LDS reads need not wait for the next tile's loads;
+  // the D = 64 GdO variants into two buffers of one array per operand, picked
+  // at run time.  The rest stage tiles through registers into one buffer.
+  constexpr bool kPar = L::kSwizzle && ((D == 128 && TTT_GG_ROW_DMA_WIDE) || (D == 64 && TTT_GG_ROW_PAR64 && !GDO));
   constexpr bool kDma = L::kSwizzle && D == 64 && !kPar;
   constexpr int kBuf = kDma ? 2 : 1;
   constexpr int kE = kPar ? 8 : L::kRowElems;  // the run-time-indexed arrays (unused with kPar)
@@ -262,6 +264,7 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
         dd.load_ragged(sgK[buf], gKn, a.gk.st, T_ - n0, D);
         dd.load_ragged(sgV[buf], gVn, a.gv.st, T_ - n0, D);
         if constexpr (LOADP) load_p_frags<T>(pn, Pm, n0, T_);
+        dma_wait();
       }
       advance();
     }
@@ -368,6 +371,7 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
         dd.load_ragged(gk, gKn, a.gk.st, T_ - n0, D);
         dd.load_ragged(gv, gVn, a.gv.st, T_ - n0, D);
         if constexpr (LOADP) load_p_frags<T>(pn, Pm, n0, T_);
+        dma_wait();
       }
       advance();
     };
@@ -645,6 +649,7 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_COL_WAVES_PER_EU, true>:
         dd.load_ragged(wb.gq, gQn, a.gq.st, T_ - m0, D);
         dd.load_ragged(wb.dout, dOn, a.dout.st, T_ - m0, D);
         if constexpr (LOADP) dpt.load_ragged(wb.p, Pn, a.p.st, T_ - m0, T_ - n0);
+        dma_wait();
       }
       sdma.load(wb.st, m0, T_ - m0);
       Qn += kBlk * a.q.st;

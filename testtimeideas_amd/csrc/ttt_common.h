@@ -919,6 +919,10 @@ __device__ __forceinline__ void stat_read8(float* v, const float* lds, int st, i
 // ---------------------------------------------------------------------------
 typedef __attribute__((address_space(3))) void lds_void_t;
 
+// Interior tiles through the buffer form (1) or the global form (0).
+#ifndef TTT_DMA_BUF
+#define TTT_DMA_BUF 1
+#endif
 // Word 3 of a raw buffer resource on gfx9-family parts (gfx950): 32-bit
 // data format, no swizzle, no index stride.
 constexpr int kBufWord3 = 0x00020000;
@@ -966,7 +970,10 @@ struct TileDma {  // for the unpadded (chunk-permuted) layout only: Lds<T, NCOL>
   // fresh register whose reuse soon after the load makes the compiler wait
   // for the load to complete).  The resource does no range checking.
   __device__ __forceinline__ void load_full(T* lds, const T* g, const int* off) const {
-#if defined(__HIP_DEVICE_COMPILE__)
+#if defined(__HIP_DEVICE_COMPILE__) && !TTT_DMA_BUF
+#pragma unroll
+    for (int q = 0; q < kPerWave; ++q) issue(lds, g, off[q], q);
+#elif defined(__HIP_DEVICE_COMPILE__)
     const __amdgpu_buffer_rsrc_t r =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(g), (short)0, (int)0xFFFFFFFF, kBufWord3);
 #pragma unroll

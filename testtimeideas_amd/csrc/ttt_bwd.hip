@@ -30,7 +30,11 @@
 #define TTT_DQ_DMA 1
 #endif
 // The saved-P dQ kernel's direct loads go to two buffer sets in distinct
-// arrays with compile-time roles (1) or to run-time-picked buffers (0).
+// arrays with compile-time roles (1) or to run-time-picked buffers (0) at
+// D = 64; at D = 128 (TTT_DQ_DMA_WIDE) always to two sets.
+#ifndef TTT_DQ_DMA_WIDE
+#define TTT_DQ_DMA_WIDE 1
+#endif
 #ifndef TTT_DQ_PAR
 #define TTT_DQ_PAR 0
 #endif
@@ -95,9 +99,10 @@ struct DqWaves {
   // The saved-P 16-bit D = 64 kernel in the two-set form (two tiles per loop
   // step): without a register cap the compiler keeps the accumulators in
   // AGPRs and copies them every step.
-  static constexpr bool kPar = TTT_DQ_DMA && TTT_DQ_PAR && LOADP && sizeof(T) == 2 && D == 64;
+  static constexpr bool kPar =
+      TTT_DQ_DMA && LOADP && sizeof(T) == 2 && ((D == 64 && TTT_DQ_PAR) || (D == 128 && TTT_DQ_DMA_WIDE));
   static constexpr int value =
-      kVacc ? (sizeof(T) == 2 ? 4 : AccWaves<true>::value) : kPar ? 3 : AccWaves<false>::value;
+      kVacc ? (sizeof(T) == 2 ? 4 : AccWaves<true>::value) : kPar ? (D == 64 ? 3 : 2) : AccWaves<false>::value;
 };
 
 // ---------------------------------------------------------------------------
@@ -111,8 +116,8 @@ __attribute__((amdgpu_waves_per_eu(DqWaves<T, D, LOADP>::value))) void k_bwd_dq(
   // (TileDma): with kPar, two sets in distinct arrays with a compile-time role
   // per loop step (so that the current tile's LDS reads need not wait for the
   // next tile's loads), else two buffers of one array picked at run time.
-  constexpr bool kDma = TTT_DQ_DMA && LOADP && L::kSwizzle && D == 64;  // D = 128: measured 4 % slower
-  constexpr bool kPar = kDma && TTT_DQ_PAR;
+  constexpr bool kDma = TTT_DQ_DMA && LOADP && L::kSwizzle && (D == 64 || TTT_DQ_DMA_WIDE);
+  constexpr bool kPar = kDma && (TTT_DQ_PAR || D == 128);
   constexpr bool kRt = kDma && !kPar;
   constexpr int kE1 = kPar ? L::kRowElems : 8, kER = kRt ? L::kRowElems : 8;
   __shared__ __align__(16) T sK0[kRt ? 8 : L::kRowElems];

@@ -45,6 +45,11 @@
 #ifndef TTT_FWD_P_FUSED
 #define TTT_FWD_P_FUSED 1
 #endif
+// The P pass streams 16-bit D = 64 key tiles by direct loads (1) or through
+// registers (0).
+#ifndef TTT_FWD_DMA
+#define TTT_FWD_DMA 1
+#endif
 #ifndef TTT_FWD_FULLTILE
 #define TTT_FWD_FULLTILE 1
 #endif
@@ -355,16 +360,32 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_FWD_WIDE && D == 128 && siz
 }
 
 // ---------------------------------------------------------------------------
+// Waves per SIMD the P pass is compiled for: the 16-bit D = 64 two-set form
+// (two tiles per loop step) without a register cap keeps its accumulators in
+// AGPRs and copies them every step.
+template <typename T, int D>
+struct FwdPWaves {
+  static constexpr bool kDma = TTT_FWD_DMA && sizeof(T) == 2 && D == 64;
+  static constexpr int value = kDma ? 3 : AccWaves<TTT_VACC_FWD_WIDE && D == 128 && sizeof(T) == 2>::value;
+};
+
 template <typename T, int D, bool XM>
 __global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_FWD_WIDE && D == 128 && sizeof(T) == 2>::value))) void k_fwd_p(Params a) {
+__attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_p(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
   // R key tiles per barrier round (as in k_fwd_stats).
   constexpr int R = TTT_FWD_P_TILES;
-  __shared__ __align__(16) T sK[R][L::kRowElems];
-  __shared__ __align__(16) T sV[R][L::kRowElems];
+  // 16-bit D = 64 tiles stream straight into two LDS buffer sets (TileDma) in
+  // distinct arrays with a compile-time role per loop step, one tile per
+  // barrier round; the rest stage R tiles per round through registers.
+  constexpr bool kDma = TTT_FWD_DMA && L::kSwizzle && sizeof(T) == 2 && D == 64;
+  constexpr int kR = kDma ? 1 : R;
+  __shared__ __align__(16) T sK[kR][L::kRowElems];
+  __shared__ __align__(16) T sV[kR][L::kRowElems];
+  __shared__ __align__(16) T sK1[kDma ? L::kRowElems : 8];
+  __shared__ __align__(16) T sV1[kDma ? L::kRowElems : 8];
 
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
@@ -409,7 +430,7 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_FWD_WIDE && D == 128 && siz
 #pragma unroll
   for (int i = 0; i < D / 16; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  Stage<T, D> stK[R], stV[R];
+  Stage<T, D> stK[kR], stV[kR];
   // Tiles past the chunk load its last tile again (unconditional loads); their
   // P is neither stored nor accumulated.
   const StageOff<T, D> soK = stage_offsets<T, D>(a.k.st), soV = stage_offsets<T, D>(a.v.st);
@@ -425,24 +446,9 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_FWD_WIDE && D == 128 && siz
       stage_load<T, D>(sv, vp, a.v.st, T_ - n1, D);
     }
   };
-#pragma unroll
-  for (int i = 0; i < R; ++i) load_kv(cr.t0 + i, stK[i], stV[i]);
-  for (int nb = cr.t0; nb < cr.t1; nb += R) {
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < R; ++i) {
-      stage_store_rows<T, D>(stK[i], sK[i]);
-      stage_store_rows<T, D>(stV[i], sV[i]);
-    }
-    __syncthreads();
-    if (nb + R < cr.t1) {
-#pragma unroll
-      for (int i = 0; i < R; ++i) load_kv(nb + R + i, stK[i], stV[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < R; ++i) {
-      const bool valid = i == 0 || nb + i < cr.t1;
-      const int n0 = (nb + i) * kBlk;
+  // Key tile `nt` from LDS tiles cK, cV (`valid`: inside the chunk).
+  auto body = [&](int nt, const T* cK, const T* cV, bool valid) __attribute__((always_inline)) {
+      const int n0 = nt * kBlk;
       frag pf[2];
       if constexpr (!XM && sizeof(T) == 2 && TTT_FWD_P_FUSED) {
         // Raw scores; P = exp2(raw * scale*log2e - lse) in one FMA, masked
@@ -450,8 +456,8 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_FWD_WIDE && D == 128 && siz
         // the MFMA fragment and the stored P.
         Tile s;
         s.zero();
-        mm_d<T, D>(s, sK[i], qf);
-        const bool need_mask = mk.tile(nb + i);
+        mm_d<T, D>(s, cK, qf);
+        const bool need_mask = mk.tile(nt);
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
           float pv[8];
@@ -483,7 +489,7 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_FWD_WIDE && D == 128 && siz
         }
       } else {
         Tile s;
-        fwd_scores<T, D, XM>(s, sK[i], qf, a, mk, brow, nb + i);
+        fwd_scores<T, D, XM>(s, cK, qf, a, mk, brow, nt);
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
           float pv[8];
@@ -502,7 +508,64 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_FWD_WIDE && D == 128 && siz
           }
         }
       }
-      mm_s<T, D>(acc, sV[i], pf);
+      mm_s<T, D>(acc, cV, pf);
+  };
+  if constexpr (kDma) {
+    const TileDma<T, D> dd;
+    int oK[TileDma<T, D>::kPerWave], oV[TileDma<T, D>::kPerWave];
+    dd.offsets(oK, a.k.st);
+    dd.offsets(oV, a.v.st);
+    auto fetch = [&](int nt, T* k, T* v) __attribute__((always_inline)) {
+      const int n1 = nt * kBlk;
+      const T* kp = K + (int64_t)n1 * a.k.st;
+      const T* vp = V + (int64_t)n1 * a.v.st;
+      if (n1 + kBlk <= T_) {
+        dd.load_full(k, kp, oK);
+        dd.load_full(v, vp, oV);
+      } else {
+        dd.load_ragged(k, kp, a.k.st, T_ - n1, D);
+        dd.load_ragged(v, vp, a.v.st, T_ - n1, D);
+        dma_wait();
+      }
+    };
+    // Tile nt from set P while tile nt + 1 streams into set 1 - P.
+    auto step = [&](auto par, int nt) __attribute__((always_inline)) {
+      constexpr int P = decltype(par)::value;
+      dma_wait();       // this wave's loads of tile nt
+      __syncthreads();  // everyone's, and everyone is done with the other set
+      if (nt + 1 < cr.t1) {
+        if constexpr (P == 0)
+          fetch(nt + 1, sK1, sV1);
+        else
+          fetch(nt + 1, sK[0], sV[0]);
+      }
+      if constexpr (P == 0)
+        body(nt, sK[0], sV[0], true);
+      else
+        body(nt, sK1, sV1, true);
+    };
+    fetch(cr.t0, sK[0], sV[0]);
+    for (int nb = cr.t0; nb < cr.t1; nb += 2) {
+      step(Parity<0>{}, nb);
+      if (nb + 1 < cr.t1) step(Parity<1>{}, nb + 1);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kR; ++i) load_kv(cr.t0 + i, stK[i], stV[i]);
+    for (int nb = cr.t0; nb < cr.t1; nb += kR) {
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < kR; ++i) {
+        stage_store_rows<T, D>(stK[i], sK[i]);
+        stage_store_rows<T, D>(stV[i], sV[i]);
+      }
+      __syncthreads();
+      if (nb + kR < cr.t1) {
+#pragma unroll
+        for (int i = 0; i < kR; ++i) load_kv(nb + kR + i, stK[i], stV[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < kR; ++i) body(nb + i, sK[i], sV[i], i == 0 || nb + i < cr.t1);
     }
   }
   if (cr.nch == 1) {

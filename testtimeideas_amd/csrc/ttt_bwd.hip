@@ -58,6 +58,14 @@
 #ifndef TTT_DKDV_DMA
 #define TTT_DKDV_DMA 1
 #endif
+// The same at D = 128 for dO, Q and the rowsum slice, with P staged (1), or
+// all through registers (0).
+#ifndef TTT_DKDV_DMA_WIDE
+#define TTT_DKDV_DMA_WIDE 1
+#endif
+#ifndef TTT_DKDV_LATE_FETCH
+#define TTT_DKDV_LATE_FETCH 1
+#endif
 #ifndef TTT_DKDV_PEEL
 #define TTT_DKDV_PEEL 0
 #endif
@@ -294,7 +302,20 @@ __attribute__((amdgpu_waves_per_eu(DqWaves<T, D, LOADP>::value))) void k_bwd_dq(
     }
     mm_s<T, D>(acc, cK, dsf);
   };
-  if constexpr (kPar) {
+  if constexpr (kPar && TTT_DQ_PEEL && D == 64) {
+    // Pairs of tiles with unconditional prefetch; the last one or two peeled.
+    int nb = cr.t0;
+    for (; nb + 2 < cr.t1; nb += 2) {
+      tile(nb, Parity<1>{}, Parity<0>{});
+      tile(nb + 1, Parity<1>{}, Parity<1>{});
+    }
+    if (nb + 1 < cr.t1) {
+      tile(nb, Parity<1>{}, Parity<0>{});
+      tile(nb + 1, Parity<0>{}, Parity<1>{});
+    } else {
+      tile(nb, Parity<0>{}, Parity<0>{});
+    }
+  } else if constexpr (kPar) {
     for (int nb = cr.t0; nb < cr.t1; nb += 2) {
       tile(nb, Parity<2>{}, Parity<0>{});
       if (nb + 1 < cr.t1) tile(nb + 1, Parity<2>{}, Parity<1>{});
@@ -328,9 +349,10 @@ __attribute__((amdgpu_waves_per_eu(DqWaves<T, D, LOADP>::value))) void k_bwd_dq(
 #endif
 template <typename T, int D, bool LOADP, bool DV_ONLY>
 struct DkdvWaves {
-  static constexpr bool kDma = TTT_DKDV_DMA && LOADP && !DV_ONLY && sizeof(T) == 2 && D == 64;
+  static constexpr bool kDma =
+      TTT_DKDV_DMA && LOADP && !DV_ONLY && sizeof(T) == 2 && (D == 64 || (D == 128 && TTT_DKDV_DMA_WIDE));
   static constexpr int value =
-      kDma ? TTT_DKDV_WAVES : AccWaves<TTT_VACC_BWD_RECOMPUTE && !LOADP && D == 64>::value;
+      kDma ? (D == 64 ? TTT_DKDV_WAVES : 2) : AccWaves<TTT_VACC_BWD_RECOMPUTE && !LOADP && D == 64>::value;
 };
 
 template <typename T, int D, bool LOADP, bool DV_ONLY, bool XM>
@@ -349,7 +371,14 @@ __attribute__((amdgpu_waves_per_eu(DkdvWaves<T, D, LOADP, DV_ONLY>::value))) voi
   // straight into two LDS buffer sets (TileDma) in distinct arrays with a
   // compile-time role per loop step, so that the current tile's LDS reads
   // need not wait for the next tile's loads.
-  constexpr bool kDma = TTT_DKDV_DMA && LOADP && !DV_ONLY && L::kSwizzle && D == 64;
+  // At D = 128 (kMix) P stays staged through registers into one buffer: two
+  // sets of all three tiles would need 80 KB of LDS, one workgroup per CU.
+  constexpr bool kDma = TTT_DKDV_DMA && LOADP && !DV_ONLY && L::kSwizzle && (D == 64 || TTT_DKDV_DMA_WIDE);
+  constexpr bool kMix = kDma && D == 128;
+  // The next tile's loads are issued after this tile's P reads (1) or before
+  // them (0): the compiler waits for outstanding direct loads before one of
+  // those transposed reads.
+  constexpr bool kLateFetch = kDma && TTT_DKDV_LATE_FETCH;
   constexpr int kQE = kNeedQ ? L::kRowElems : 8, kPE = LOADP ? LP::kRowElems : 8, kSE = kNS > 0 ? kNS * kBlk : 4;
   __shared__ __align__(16) T sdO0[L::kRowElems];
   __shared__ __align__(16) T sQ0[kQE];
@@ -357,7 +386,7 @@ __attribute__((amdgpu_waves_per_eu(DkdvWaves<T, D, LOADP, DV_ONLY>::value))) voi
   __shared__ __align__(16) float sS0[kSE];
   __shared__ __align__(16) T sdO1[kDma ? L::kRowElems : 8];
   __shared__ __align__(16) T sQ1[kDma ? kQE : 8];
-  __shared__ __align__(16) T sP1[kDma ? kPE : 8];
+  __shared__ __align__(16) T sP1[kDma && !kMix ? kPE : 8];
   __shared__ __align__(16) float sS1[kDma ? kSE : 4];
   struct Bufs {
     T *dout, *q, *p;
@@ -367,7 +396,7 @@ __attribute__((amdgpu_waves_per_eu(DkdvWaves<T, D, LOADP, DV_ONLY>::value))) voi
     if constexpr (decltype(par)::value == 0)
       return Bufs{sdO0, sQ0, sP0, sS0};
     else
-      return Bufs{sdO1, sQ1, sP1, sS1};
+      return Bufs{sdO1, sQ1, kMix ? sP0 : sP1, sS1};
   };
 
   const int T_ = a.T;
@@ -449,14 +478,15 @@ __attribute__((amdgpu_waves_per_eu(DkdvWaves<T, D, LOADP, DV_ONLY>::value))) voi
     if (m0 + kBlk <= T_ && cols_full) {
       dd.load_full(bf.dout, dOn, odO);
       dd.load_full(bf.q, Qn, oQ);
-      dpt.load_full(bf.p, Pn, oP);
+      if constexpr (!kMix) dpt.load_full(bf.p, Pn, oP);
     } else {
       dd.load_ragged(bf.dout, dOn, a.dout.st, T_ - m0, D);
       dd.load_ragged(bf.q, Qn, a.q.st, T_ - m0, D);
-      dpt.load_ragged(bf.p, Pn, a.p.st, T_ - m0, T_ - n0);
+      if constexpr (!kMix) dpt.load_ragged(bf.p, Pn, a.p.st, T_ - m0, T_ - n0);
       dma_wait();
     }
     sdma.load(bf.st, m0, T_ - m0);
+    if constexpr (kMix) stage_load<T, kBlk>(stP, Pn, a.p.st, T_ - m0, T_ - n0);
     dOn += kBlk * a.dout.st;
     Qn += kBlk * a.q.st;
     Pn += kBlk * a.p.st;
@@ -473,9 +503,15 @@ __attribute__((amdgpu_waves_per_eu(DkdvWaves<T, D, LOADP, DV_ONLY>::value))) voi
     if constexpr (kDma) {
       dma_wait();       // this wave's loads of tile mb
       __syncthreads();  // everyone's; everyone is also done with the other set
-      if constexpr (decltype(prefetch)::value == 1) dma_tile(mb + 1, Parity<1 - P>{});
-      if constexpr (decltype(prefetch)::value == 2)
-        if (mb + 1 < cr.t1) dma_tile(mb + 1, Parity<1 - P>{});
+      if constexpr (kMix) {
+        stage_store_rows<T, kBlk>(stP, sP0);
+        __syncthreads();
+      }
+      if constexpr (!kLateFetch) {
+        if constexpr (decltype(prefetch)::value == 1) dma_tile(mb + 1, Parity<1 - P>{});
+        if constexpr (decltype(prefetch)::value == 2)
+          if (mb + 1 < cr.t1) dma_tile(mb + 1, Parity<1 - P>{});
+      }
     } else {
       __syncthreads();
       stage_store_rows<T, D>(stdO, sdO0);
@@ -501,6 +537,11 @@ __attribute__((amdgpu_waves_per_eu(DkdvWaves<T, D, LOADP, DV_ONLY>::value))) voi
         const frag f = load_frag_tr<T, kBlk>(cP, 32 * kb, 16 * w);
 #pragma unroll
         for (int j = 0; j < 8; ++j) p.set(kb, j, E::f32(f[j]));
+      }
+      if constexpr (kLateFetch) {
+        if constexpr (decltype(prefetch)::value == 1) dma_tile(mb + 1, Parity<1 - P>{});
+        if constexpr (decltype(prefetch)::value == 2)
+          if (mb + 1 < cr.t1) dma_tile(mb + 1, Parity<1 - P>{});
       }
     } else {
       p.zero();

@@ -89,6 +89,21 @@ def test_ragged_lengths(t, causal, save_p):
     _compare(out, _ref(xs, causal, scale), dt, causal, t)
 
 
+@pytest.mark.parametrize("t", [37, 191, 257])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("save_p", [True, False])
+def test_ragged_lengths_d128(t, causal, save_p):
+    """Head dim 128 (16-bit direct-load kernels: two buffer sets, P staged in
+    dK/dV) over ragged lengths, unsplit: paired steps, an odd last step and a
+    ragged last tile."""
+    dt = torch.bfloat16
+    xs = _inputs(1, 2, t, 128, dt, seed=t + 1)
+    scale = 1.0 / math.sqrt(128)
+    print(f"[case] ragged d128 t={t} causal={causal} save_p={save_p}", flush=True)
+    out = _run(xs, causal, scale, save_p)
+    _compare(out, _ref(xs, causal, scale), dt, causal, t)
+
+
 @pytest.mark.parametrize("scale", [-0.125, 0.0, 0.37])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("save_p", [True, False])

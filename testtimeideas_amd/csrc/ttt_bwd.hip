@@ -35,6 +35,11 @@
 #ifndef TTT_DQ_DMA_WIDE
 #define TTT_DQ_DMA_WIDE 1
 #endif
+// The recompute dQ kernel (16-bit, D = 64) streams K and V by direct loads into
+// two buffer sets (1) or through registers (0).
+#ifndef TTT_DQ_DMA_RECOMPUTE
+#define TTT_DQ_DMA_RECOMPUTE 1
+#endif
 #ifndef TTT_DQ_PAR
 #define TTT_DQ_PAR 0
 #endif
@@ -124,8 +129,8 @@ __attribute__((amdgpu_waves_per_eu(DqWaves<T, D, LOADP>::value))) void k_bwd_dq(
   // (TileDma): with kPar, two sets in distinct arrays with a compile-time role
   // per loop step (so that the current tile's LDS reads need not wait for the
   // next tile's loads), else two buffers of one array picked at run time.
-  constexpr bool kDma = TTT_DQ_DMA && LOADP && L::kSwizzle && (D == 64 || TTT_DQ_DMA_WIDE);
-  constexpr bool kPar = kDma && (TTT_DQ_PAR || D == 128);
+  constexpr bool kDma = TTT_DQ_DMA && L::kSwizzle && (LOADP ? (D == 64 || TTT_DQ_DMA_WIDE) : (D == 64 && TTT_DQ_DMA_RECOMPUTE));
+  constexpr bool kPar = kDma && (TTT_DQ_PAR || D == 128 || !LOADP);
   constexpr bool kRt = kDma && !kPar;
   constexpr int kE1 = kPar ? L::kRowElems : 8, kER = kRt ? L::kRowElems : 8;
   __shared__ __align__(16) T sK0[kRt ? 8 : L::kRowElems];
@@ -233,17 +238,19 @@ __attribute__((amdgpu_waves_per_eu(DqWaves<T, D, LOADP>::value))) void k_bwd_dq(
     if (n1 + kBlk <= T_) {
       dd.load_full(set_k(par), Kn, oK);
       dd.load_full(set_v(par), Vn, oV);
-      pn[0] = load_frag_g<T>(Pn);
-      pn[1] = load_frag_g<T>(Pn + 32);
+      if constexpr (LOADP) {
+        pn[0] = load_frag_g<T>(Pn);
+        pn[1] = load_frag_g<T>(Pn + 32);
+      }
     } else {
       dd.load_ragged(set_k(par), Kn, a.k.st, T_ - n1, D);
       dd.load_ragged(set_v(par), Vn, a.v.st, T_ - n1, D);
-      load_p_frags<T>(pn, Pm, n1, T_);
+      if constexpr (LOADP) load_p_frags<T>(pn, Pm, n1, T_);
       dma_wait();
     }
     Kn += kBlk * a.k.st;
     Vn += kBlk * a.v.st;
-    Pn += kBlk;
+    if constexpr (LOADP) Pn += kBlk;
   };
   if constexpr (kPar)
     fetch_dma(cr.t0, Parity<0>{});

@@ -68,6 +68,11 @@
 #ifndef TTT_DKDV_DMA_WIDE
 #define TTT_DKDV_DMA_WIDE 1
 #endif
+// The recompute dK/dV kernel (16-bit, D = 64) streams dO, Q and its two row
+// statistics by direct loads into two buffer sets (1) or through registers (0).
+#ifndef TTT_DKDV_DMA_RECOMPUTE
+#define TTT_DKDV_DMA_RECOMPUTE 1
+#endif
 #ifndef TTT_DKDV_LATE_FETCH
 #define TTT_DKDV_LATE_FETCH 1
 #endif
@@ -380,12 +385,13 @@ __attribute__((amdgpu_waves_per_eu(DkdvWaves<T, D, LOADP, DV_ONLY>::value))) voi
   // need not wait for the next tile's loads.
   // At D = 128 (kMix) P stays staged through registers into one buffer: two
   // sets of all three tiles would need 80 KB of LDS, one workgroup per CU.
-  constexpr bool kDma = TTT_DKDV_DMA && LOADP && !DV_ONLY && L::kSwizzle && (D == 64 || TTT_DKDV_DMA_WIDE);
+  constexpr bool kDma = TTT_DKDV_DMA && !DV_ONLY && L::kSwizzle &&
+                        (LOADP ? (D == 64 || TTT_DKDV_DMA_WIDE) : (D == 64 && TTT_DKDV_DMA_RECOMPUTE));
   constexpr bool kMix = kDma && D == 128;
   // The next tile's loads are issued after this tile's P reads (1) or before
   // them (0): the compiler waits for outstanding direct loads before one of
   // those transposed reads.
-  constexpr bool kLateFetch = kDma && TTT_DKDV_LATE_FETCH;
+  constexpr bool kLateFetch = kDma && LOADP && TTT_DKDV_LATE_FETCH;
   constexpr int kQE = kNeedQ ? L::kRowElems : 8, kPE = LOADP ? LP::kRowElems : 8, kSE = kNS > 0 ? kNS * kBlk : 4;
   __shared__ __align__(16) T sdO0[L::kRowElems];
   __shared__ __align__(16) T sQ0[kQE];
@@ -476,27 +482,27 @@ __attribute__((amdgpu_waves_per_eu(DkdvWaves<T, D, LOADP, DV_ONLY>::value))) voi
   if constexpr (kDma) {
     dd.offsets(odO, a.dout.st);
     dd.offsets(oQ, a.q.st);
-    dpt.offsets(oP, a.p.st);
+    if constexpr (LOADP) dpt.offsets(oP, a.p.st);
   }
-  const StatDma<1> sdma(rs, nullptr, nullptr, nullptr);
+  const StatDma<kNS> sdma(DV_ONLY ? lse : rs, lse, nullptr, nullptr);
   auto dma_tile = [&](int mb, auto par) __attribute__((always_inline)) {
     const int m0 = mb * kBlk;
     const Bufs bf = bufs(par);
     if (m0 + kBlk <= T_ && cols_full) {
       dd.load_full(bf.dout, dOn, odO);
       dd.load_full(bf.q, Qn, oQ);
-      if constexpr (!kMix) dpt.load_full(bf.p, Pn, oP);
+      if constexpr (LOADP && !kMix) dpt.load_full(bf.p, Pn, oP);
     } else {
       dd.load_ragged(bf.dout, dOn, a.dout.st, T_ - m0, D);
       dd.load_ragged(bf.q, Qn, a.q.st, T_ - m0, D);
-      if constexpr (!kMix) dpt.load_ragged(bf.p, Pn, a.p.st, T_ - m0, T_ - n0);
+      if constexpr (LOADP && !kMix) dpt.load_ragged(bf.p, Pn, a.p.st, T_ - m0, T_ - n0);
       dma_wait();
     }
     sdma.load(bf.st, m0, T_ - m0);
     if constexpr (kMix) stage_load<T, kBlk>(stP, Pn, a.p.st, T_ - m0, T_ - n0);
     dOn += kBlk * a.dout.st;
     Qn += kBlk * a.q.st;
-    Pn += kBlk * a.p.st;
+    if constexpr (LOADP) Pn += kBlk * a.p.st;
   };
   if constexpr (kDma)
     dma_tile(cr.t0, Parity<0>{});

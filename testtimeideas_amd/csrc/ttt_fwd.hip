@@ -45,8 +45,8 @@
 #ifndef TTT_FWD_P_FUSED
 #define TTT_FWD_P_FUSED 1
 #endif
-// The P pass streams 16-bit D = 64 key tiles by direct loads (1) or through
-// registers (0).
+// The P pass and the online forward stream 16-bit D = 64 key/value tiles by
+// direct loads (1) or through registers (0).
 #ifndef TTT_FWD_DMA
 #define TTT_FWD_DMA 1
 #endif
@@ -109,8 +109,14 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_ONLINE>::value))) void k_fw
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
+  // 16-bit D = 64 tiles stream straight into two LDS buffer sets (TileDma) in
+  // distinct arrays with a compile-time role per loop step; the rest stage
+  // them through registers.
+  constexpr bool kDma = TTT_FWD_DMA && L::kSwizzle && sizeof(T) == 2 && D == 64;
   __shared__ __align__(16) T sK[L::kRowElems];
   __shared__ __align__(16) T sV[L::kRowElems];
+  __shared__ __align__(16) T sK1[kDma ? L::kRowElems : 8];
+  __shared__ __align__(16) T sV1[kDma ? L::kRowElems : 8];
 
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
@@ -141,7 +147,7 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_ONLINE>::value))) void k_fw
 
   // Register stages for the next kPre tiles' K and V (loads issued kPre
   // tiles ahead of their use).
-  constexpr int kPre = TTT_FWD_PREFETCH;
+  constexpr int kPre = kDma ? 1 : TTT_FWD_PREFETCH;
   Stage<T, D> stK[kPre], stV[kPre];
   const StageOff<T, D> soK = stage_offsets<T, D>(a.k.st), soV = stage_offsets<T, D>(a.v.st);
   auto load_kv = [&](int nb, Stage<T, D>& sk, Stage<T, D>& sv) __attribute__((always_inline)) {
@@ -156,17 +162,10 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_ONLINE>::value))) void k_fw
       stage_load<T, D>(sv, vp, a.v.st, T_ - n1, D);
     }
   };
-#pragma unroll
-  for (int i = 0; i < kPre; ++i)
-    if (i == 0 || cr.t0 + i < cr.t1) load_kv(cr.t0 + i, stK[i], stV[i]);
-  auto tile = [&](int nb, Stage<T, D>& sk, Stage<T, D>& sv) __attribute__((always_inline)) {
-    __syncthreads();
-    stage_store_rows<T, D>(sk, sK);
-    stage_store_rows<T, D>(sv, sV);
-    __syncthreads();
-    if (nb + kPre < cr.t1) load_kv(nb + kPre, sk, sv);
+  // Key tile nb from LDS tiles cK, cV.
+  auto body = [&](int nb, const T* cK, const T* cV) __attribute__((always_inline)) {
     Tile s;
-    fwd_scores<T, D, XM>(s, sK, qf, a, mk, brow, nb);
+    fwd_scores<T, D, XM>(s, cK, qf, a, mk, brow, nb);
     const float mnew = fmaxf(mx, tile_max(s));
     // A window can mask a row's every key of a tile so far: shift by 0 then.
     const float msh = (XM && mnew == -INFINITY) ? 0.f : mnew;
@@ -187,12 +186,64 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_ONLINE>::value))) void k_fw
     mx = mnew;
 #pragma unroll
     for (int i = 0; i < D / 16; ++i) acc[i] *= alpha;
-    mm_s<T, D>(acc, sV, pf);
+    mm_s<T, D>(acc, cV, pf);
   };
-  for (int nb = cr.t0; nb < cr.t1; nb += kPre) {
+  if constexpr (kDma) {
+    const TileDma<T, D> dd;
+    int oK[TileDma<T, D>::kPerWave], oV[TileDma<T, D>::kPerWave];
+    dd.offsets(oK, a.k.st);
+    dd.offsets(oV, a.v.st);
+    auto fetch = [&](int nt, T* k, T* v) __attribute__((always_inline)) {
+      const int n1 = nt * kBlk;
+      const T* kp = K + (int64_t)n1 * a.k.st;
+      const T* vp = V + (int64_t)n1 * a.v.st;
+      if (n1 + kBlk <= T_) {
+        dd.load_full(k, kp, oK);
+        dd.load_full(v, vp, oV);
+      } else {
+        dd.load_ragged(k, kp, a.k.st, T_ - n1, D);
+        dd.load_ragged(v, vp, a.v.st, T_ - n1, D);
+        dma_wait();
+      }
+    };
+    // Tile nt from set P while tile nt + 1 streams into set 1 - P.
+    auto step = [&](auto par, int nt) __attribute__((always_inline)) {
+      constexpr int P = decltype(par)::value;
+      dma_wait();       // this wave's loads of tile nt
+      __syncthreads();  // everyone's, and everyone is done with the other set
+      if (nt + 1 < cr.t1) {
+        if constexpr (P == 0)
+          fetch(nt + 1, sK1, sV1);
+        else
+          fetch(nt + 1, sK, sV);
+      }
+      if constexpr (P == 0)
+        body(nt, sK, sV);
+      else
+        body(nt, sK1, sV1);
+    };
+    fetch(cr.t0, sK, sV);
+    for (int nb = cr.t0; nb < cr.t1; nb += 2) {
+      step(Parity<0>{}, nb);
+      if (nb + 1 < cr.t1) step(Parity<1>{}, nb + 1);
+    }
+  } else {
 #pragma unroll
     for (int i = 0; i < kPre; ++i)
-      if (i == 0 || nb + i < cr.t1) tile(nb + i, stK[i], stV[i]);
+      if (i == 0 || cr.t0 + i < cr.t1) load_kv(cr.t0 + i, stK[i], stV[i]);
+    auto tile = [&](int nb, Stage<T, D>& sk, Stage<T, D>& sv) __attribute__((always_inline)) {
+      __syncthreads();
+      stage_store_rows<T, D>(sk, sK);
+      stage_store_rows<T, D>(sv, sV);
+      __syncthreads();
+      if (nb + kPre < cr.t1) load_kv(nb + kPre, sk, sv);
+      body(nb, sK, sV);
+    };
+    for (int nb = cr.t0; nb < cr.t1; nb += kPre) {
+#pragma unroll
+      for (int i = 0; i < kPre; ++i)
+        if (i == 0 || nb + i < cr.t1) tile(nb + i, stK[i], stV[i]);
+    }
   }
 
   l = group_sum(l);

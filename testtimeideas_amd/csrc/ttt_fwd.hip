@@ -45,8 +45,8 @@
 #ifndef TTT_FWD_P_FUSED
 #define TTT_FWD_P_FUSED 1
 #endif
-// The P pass and the online forward stream 16-bit D = 64 key/value tiles by
-// direct loads (1) or through registers (0).
+// The forward kernels (statistics pass, P pass, online) stream 16-bit D = 64
+// key/value tiles by direct loads (1) or through registers (0).
 #ifndef TTT_FWD_DMA
 #define TTT_FWD_DMA 1
 #endif
@@ -262,16 +262,29 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_ONLINE>::value))) void k_fw
 }
 
 // ---------------------------------------------------------------------------
+// Waves per SIMD the statistics and P passes are compiled for: their 16-bit
+// D = 64 two-set forms (two steps per loop iteration) without a register cap
+// keep their MFMA results in AGPRs and copy them every step.
+template <typename T, int D>
+struct FwdPWaves {
+  static constexpr bool kDma = TTT_FWD_DMA && sizeof(T) == 2 && D == 64;
+  static constexpr int value = kDma ? 3 : AccWaves<TTT_VACC_FWD_WIDE && D == 128 && sizeof(T) == 2>::value;
+};
+
 template <typename T, int D, bool XM>
 __global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_FWD_WIDE && D == 128 && sizeof(T) == 2>::value))) void k_fwd_stats(Params a) {
+__attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_stats(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
   // R key tiles per round: one pair of barriers and R independent score
   // products per round.
   constexpr int R = TTT_FWD_STATS_TILES;
+  // 16-bit D = 64: the R tiles of a round stream straight into LDS (TileDma),
+  // alternating between two sets in distinct arrays with compile-time roles.
+  constexpr bool kDma = TTT_FWD_DMA && L::kSwizzle && sizeof(T) == 2 && D == 64;
   __shared__ __align__(16) T sK[R][L::kRowElems];
+  __shared__ __align__(16) T sK1[R][kDma ? L::kRowElems : 8];
 
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
@@ -309,88 +322,126 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_FWD_WIDE && D == 128 && siz
     else
       stage_load<T, D>(sk, kp, a.k.st, T_ - n1, D);
   };
-#pragma unroll
-  for (int i = 0; i < R; ++i) load_k(cr.t0 + i, stK[i]);
-  for (int nb = cr.t0; nb < cr.t1; nb += R) {
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < R; ++i) stage_store_rows<T, D>(stK[i], sK[i]);
-    __syncthreads();
-    if (nb + R < cr.t1) {
-#pragma unroll
-      for (int i = 0; i < R; ++i) load_k(nb + R + i, stK[i]);
-    }
-    Tile s[R];
-    if constexpr (!XM && TTT_FWD_STATS_FUSED) {
-      if (raw_units) {
-        // Max and sum in raw-score units: exp2(raw * csl - max * csl) with the
-        // scale csl = scale*log2e > 0 folded into one FMA per element.
-#pragma unroll
-        for (int i = 0; i < R; ++i) {
-          s[i].zero();
-          mm_d<T, D>(s[i], sK[i], qf);
-          const int n0 = (nb + i) * kBlk;
-          if ((i > 0 && nb + i >= cr.t1) || mk.tile(nb + i)) {
-            const bool past = i > 0 && nb + i >= cr.t1;
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-              for (int j = 0; j < 8; ++j)
-                s[i].set(kb, j, (past || mk.masked(n0 + stream_index(kb, g, j))) ? -INFINITY : s[i].at(kb, j));
+  // One round: key tiles nb .. nb + R - 1 from the LDS tiles tile_k(i).
+  auto round = [&](int nb, auto tile_k) __attribute__((always_inline)) {
+      Tile s[R];
+      if constexpr (!XM && TTT_FWD_STATS_FUSED) {
+        if (raw_units) {
+          // Max and sum in raw-score units: exp2(raw * csl - max * csl) with the
+          // scale csl = scale*log2e > 0 folded into one FMA per element.
+  #pragma unroll
+          for (int i = 0; i < R; ++i) {
+            s[i].zero();
+            mm_d<T, D>(s[i], tile_k(i), qf);
+            const int n0 = (nb + i) * kBlk;
+            if ((i > 0 && nb + i >= cr.t1) || mk.tile(nb + i)) {
+              const bool past = i > 0 && nb + i >= cr.t1;
+  #pragma unroll
+              for (int kb = 0; kb < 2; ++kb)
+  #pragma unroll
+                for (int j = 0; j < 8; ++j)
+                  s[i].set(kb, j, (past || mk.masked(n0 + stream_index(kb, g, j))) ? -INFINITY : s[i].at(kb, j));
+            }
           }
+          float tmax = -INFINITY;
+  #pragma unroll
+          for (int i = 0; i < R; ++i)
+  #pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+  #pragma unroll
+              for (int j = 0; j < 8; ++j) tmax = fmaxf(tmax, s[i].at(kb, j));
+          const float mnew = fmaxf(mx, tmax);
+          const float shift = mnew == -INFINITY ? 0.f : mnew * csl;
+          float ts = 0.f;
+  #pragma unroll
+          for (int i = 0; i < R; ++i)
+  #pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+  #pragma unroll
+              for (int j = 0; j < 8; ++j) ts += fast_exp2(fmaf(s[i].at(kb, j), csl, -shift));
+          l = l * fast_exp2(mx * csl - shift) + ts;
+          mx = mnew;
+          return;
         }
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < R; ++i)
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) tmax = fmaxf(tmax, s[i].at(kb, j));
-        const float mnew = fmaxf(mx, tmax);
-        const float shift = mnew == -INFINITY ? 0.f : mnew * csl;
-        float ts = 0.f;
-#pragma unroll
-        for (int i = 0; i < R; ++i)
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) ts += fast_exp2(fmaf(s[i].at(kb, j), csl, -shift));
-        l = l * fast_exp2(mx * csl - shift) + ts;
-        mx = mnew;
-        continue;
       }
-    }
-#pragma unroll
-    for (int i = 0; i < R; ++i) {
-      fwd_scores<T, D, XM>(s[i], sK[i], qf, a, mk, brow, nb + i);
-      if (i > 0 && nb + i >= cr.t1) {
-#pragma unroll
+  #pragma unroll
+      for (int i = 0; i < R; ++i) {
+        fwd_scores<T, D, XM>(s[i], tile_k(i), qf, a, mk, brow, nb + i);
+        if (i > 0 && nb + i >= cr.t1) {
+  #pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+  #pragma unroll
+            for (int j = 0; j < 8; ++j) s[i].set(kb, j, -INFINITY);
+        }
+      }
+      // Per-lane running max and sum over this lane's columns; combined across
+      // the four lane groups after the loop.  A lane whose columns are all
+      // masked so far keeps max -inf and sum 0 (shift by 0 avoids -inf - -inf).
+      float tmax = -INFINITY;
+  #pragma unroll
+      for (int i = 0; i < R; ++i)
+  #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
+  #pragma unroll
+          for (int j = 0; j < 8; ++j) tmax = fmaxf(tmax, s[i].at(kb, j));
+      const float mnew = fmaxf(mx, tmax);
+      const float shift = mnew == -INFINITY ? 0.f : mnew;
+      float ts = 0.f;
+  #pragma unroll
+      for (int i = 0; i < R; ++i)
+  #pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+  #pragma unroll
+          for (int j = 0; j < 8; ++j) ts += fast_exp2(s[i].at(kb, j) - shift);
+      l = l * fast_exp2(mx - shift) + ts;
+      mx = mnew;
+  };
+  if constexpr (kDma) {
+    const TileDma<T, D> dd;
+    int oK[TileDma<T, D>::kPerWave];
+    dd.offsets(oK, a.k.st);
+    // Tiles past the chunk load its last tile again (the round masks them).
+    auto fetch_set = [&](int nb, auto par) __attribute__((always_inline)) {
 #pragma unroll
-          for (int j = 0; j < 8; ++j) s[i].set(kb, j, -INFINITY);
+      for (int i = 0; i < R; ++i) {
+        const int n1 = (nb + i < cr.t1 ? nb + i : cr.t1 - 1) * kBlk;
+        T* dst = decltype(par)::value == 0 ? sK[i] : sK1[i];
+        const T* kp = K + (int64_t)n1 * a.k.st;
+        if (n1 + kBlk <= T_) {
+          dd.load_full(dst, kp, oK);
+        } else {
+          dd.load_ragged(dst, kp, a.k.st, T_ - n1, D);
+          dma_wait();
+        }
       }
+    };
+    // Round nb from set P while round nb + R streams into set 1 - P.
+    auto step = [&](auto par, int nb) __attribute__((always_inline)) {
+      constexpr int P = decltype(par)::value;
+      dma_wait();       // this wave's loads of round nb
+      __syncthreads();  // everyone's, and everyone is done with the other set
+      if (nb + R < cr.t1) fetch_set(nb + R, Parity<1 - P>{});
+      round(nb, [&](int i) -> const T* { return P == 0 ? sK[i] : sK1[i]; });
+    };
+    fetch_set(cr.t0, Parity<0>{});
+    for (int nb = cr.t0; nb < cr.t1; nb += 2 * R) {
+      step(Parity<0>{}, nb);
+      if (nb + R < cr.t1) step(Parity<1>{}, nb + R);
     }
-    // Per-lane running max and sum over this lane's columns; combined across
-    // the four lane groups after the loop.  A lane whose columns are all
-    // masked so far keeps max -inf and sum 0 (shift by 0 avoids -inf - -inf).
-    float tmax = -INFINITY;
+  } else {
 #pragma unroll
-    for (int i = 0; i < R; ++i)
+    for (int i = 0; i < R; ++i) load_k(cr.t0 + i, stK[i]);
+    for (int nb = cr.t0; nb < cr.t1; nb += R) {
+      __syncthreads();
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int i = 0; i < R; ++i) stage_store_rows<T, D>(stK[i], sK[i]);
+      __syncthreads();
+      if (nb + R < cr.t1) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) tmax = fmaxf(tmax, s[i].at(kb, j));
-    const float mnew = fmaxf(mx, tmax);
-    const float shift = mnew == -INFINITY ? 0.f : mnew;
-    float ts = 0.f;
-#pragma unroll
-    for (int i = 0; i < R; ++i)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) ts += fast_exp2(s[i].at(kb, j) - shift);
-    l = l * fast_exp2(mx - shift) + ts;
-    mx = mnew;
+        for (int i = 0; i < R; ++i) load_k(nb + R + i, stK[i]);
+      }
+      round(nb, [&](int i) -> const T* { return sK[i]; });
+    }
   }
   if (!XM && TTT_FWD_STATS_FUSED && raw_units && mx != -INFINITY) mx *= csl;  // back to base-2 units
   {
@@ -411,14 +462,6 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_FWD_WIDE && D == 128 && siz
 }
 
 // ---------------------------------------------------------------------------
-// Waves per SIMD the P pass is compiled for: the 16-bit D = 64 two-set form
-// (two tiles per loop step) without a register cap keeps its accumulators in
-// AGPRs and copies them every step.
-template <typename T, int D>
-struct FwdPWaves {
-  static constexpr bool kDma = TTT_FWD_DMA && sizeof(T) == 2 && D == 64;
-  static constexpr int value = kDma ? 3 : AccWaves<TTT_VACC_FWD_WIDE && D == 128 && sizeof(T) == 2>::value;
-};
 
 template <typename T, int D, bool XM>
 __global__ __launch_bounds__(kThreads)

@@ -50,6 +50,10 @@
 #ifndef TTT_FWD_DMA
 #define TTT_FWD_DMA 1
 #endif
+// The statistics and P passes do the same at D = 128 (1) or not (0).
+#ifndef TTT_FWD_DMA_WIDE
+#define TTT_FWD_DMA_WIDE 1
+#endif
 #ifndef TTT_FWD_FULLTILE
 #define TTT_FWD_FULLTILE 1
 #endif
@@ -267,8 +271,9 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_ONLINE>::value))) void k_fw
 // keep their MFMA results in AGPRs and copy them every step.
 template <typename T, int D>
 struct FwdPWaves {
-  static constexpr bool kDma = TTT_FWD_DMA && sizeof(T) == 2 && D == 64;
-  static constexpr int value = kDma ? 3 : AccWaves<TTT_VACC_FWD_WIDE && D == 128 && sizeof(T) == 2>::value;
+  static constexpr bool kDma = TTT_FWD_DMA && sizeof(T) == 2 && (D == 64 || TTT_FWD_DMA_WIDE);
+  static constexpr int value =
+      kDma ? (D == 64 ? 3 : 2) : AccWaves<TTT_VACC_FWD_WIDE && D == 128 && sizeof(T) == 2>::value;
 };
 
 template <typename T, int D, bool XM>
@@ -282,7 +287,7 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_stats(Pa
   constexpr int R = TTT_FWD_STATS_TILES;
   // 16-bit D = 64: the R tiles of a round stream straight into LDS (TileDma),
   // alternating between two sets in distinct arrays with compile-time roles.
-  constexpr bool kDma = TTT_FWD_DMA && L::kSwizzle && sizeof(T) == 2 && D == 64;
+  constexpr bool kDma = TTT_FWD_DMA && L::kSwizzle && sizeof(T) == 2 && (D == 64 || TTT_FWD_DMA_WIDE);
   __shared__ __align__(16) T sK[R][L::kRowElems];
   __shared__ __align__(16) T sK1[R][kDma ? L::kRowElems : 8];
 
@@ -474,7 +479,7 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_p(Params
   // 16-bit D = 64 tiles stream straight into two LDS buffer sets (TileDma) in
   // distinct arrays with a compile-time role per loop step, one tile per
   // barrier round; the rest stage R tiles per round through registers.
-  constexpr bool kDma = TTT_FWD_DMA && L::kSwizzle && sizeof(T) == 2 && D == 64;
+  constexpr bool kDma = TTT_FWD_DMA && L::kSwizzle && sizeof(T) == 2 && (D == 64 || TTT_FWD_DMA_WIDE);
   constexpr int kR = kDma ? 1 : R;
   __shared__ __align__(16) T sK[kR][L::kRowElems];
   __shared__ __align__(16) T sV[kR][L::kRowElems];

@@ -25,10 +25,12 @@
  *   - P is a [B,H,T,T] matrix described by a ttt_view whose stride_t is the row
  *     stride; the column dimension must be contiguous and the row stride (in
  *     bytes) 16-byte aligned.  Rows are read in runs of 8 elements, so the
- *     storage must extend to column T rounded up to 8 of the last row.  With causal=1 only the lower block triangle of
- *     64x64 tiles (block column <= block row) is written or read; the other
- *     tiles are never touched.  A window narrows this to the tiles that hold
- *     a visible key of some row.
+ *     storage must extend to column T rounded up to 8 of the last row.  The
+ *     forward writes every element of P (masked entries as exact zeros, as
+ *     the softmax gives them).  With causal=1 the backward entry points read
+ *     only the lower block triangle of 64x64 tiles (block column <= block
+ *     row); a window narrows this to the tiles that hold a visible key of
+ *     some row.
  *   - Row statistics (lse, rowsum, E, F) are contiguous fp32 [B*H*T] arrays,
  *     index (b*H + h)*T + t.  lse is the natural-log log-sum-exp of the scaled
  *     scores of each row.

@@ -57,7 +57,10 @@ def _compare(out, ref, dtype, p_mask=None):
     check("lse", out["lse"], ref["lse"], torch.float32, abs_tol=2e-5 if dtype == torch.float32 else 2e-3)
     check("rowsum", out["rowsum"], ref["rowsum"], dtype)
     if out["p"] is not None and p_mask is not None:
-        check("p", out["p"].double().cpu().numpy()[..., p_mask], ref["p"][..., p_mask], dtype)
+        got = out["p"].double().cpu().numpy()
+        check("p", got[..., p_mask], ref["p"][..., p_mask], dtype)
+        # the forward writes all of P: tiles no row of their block sees hold zeros
+        assert not np.any(got[..., ~p_mask]), "P outside the visible tiles is not zero"
 
 
 def _window_case(dtype, d, t, w, kind, save_p, b=1, h=2, seed=0):

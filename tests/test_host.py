@@ -337,3 +337,14 @@ def test_golden_fixture_reproduces():
     now = golden.build()
     for key in ref.files:
         assert np.array_equal(ref[key], now[key]), key
+
+
+def test_expanded_operand_is_copied():
+    """An operand expanded along T (stride 0 there) is not what the C ABI
+    takes (it needs a positive T stride), so the binding copies it."""
+    x = torch.randn(2, 3, 1, 64).expand(2, 3, 5, 64)
+    assert x.stride(2) == 0
+    assert not _lib._kernel_ok(x)
+    y = _lib.prep(x, 64)
+    assert y.stride(2) > 0 and torch.equal(y, x)
+    assert _lib._kernel_ok(y)

@@ -231,7 +231,12 @@ def padded_head_dim(d: int) -> int:
 
 
 def _kernel_ok(t: torch.Tensor) -> bool:
+    """The C ABI takes `t` as it is: unit last stride, a positive T stride (an
+    operand expanded along T has stride 0 there and is copied), 16-byte
+    aligned base and strides."""
     if t.stride(-1) != 1 and t.size(-1) > 1:
+        return False
+    if t.stride(2) <= 0:
         return False
     eb = t.element_size()
     if t.data_ptr() % 16:

@@ -97,6 +97,52 @@ __device__ __forceinline__ void fwd_scores(Tile& s, const T* sK, const typename 
   }
 }
 
+// Zero the 64x64 tile (rb, cb) of one slice's P (rows and columns clipped to
+// T), with 16-byte stores spread over the workgroup.
+template <typename T>
+__device__ __forceinline__ void zero_p_tile(T* P, int64_t ld, int rb, int cb, int T_) {
+  constexpr int kEl = 16 / (int)sizeof(T);  // elements per store
+  constexpr int kPerRow = kBlk / kEl;
+  constexpr int kIters = kBlk * kPerRow / kThreads;
+  typedef __attribute__((address_space(1))) u32x4 gu32x4;
+#pragma unroll
+  for (int i = 0; i < kIters; ++i) {
+    const int idx = (int)threadIdx.x + i * kThreads;
+    const int r = rb * kBlk + idx / kPerRow;
+    const int c = cb * kBlk + (idx % kPerRow) * kEl;
+    if (r < T_) {
+      T* dst = P + (int64_t)r * ld + c;
+      if (c + kEl <= T_) {
+        *(gu32x4*)dst = u32x4{0u, 0u, 0u, 0u};
+      } else {
+        for (int j = 0; c + j < T_; ++j) __builtin_memset(dst + j, 0, sizeof(T));
+      }
+    }
+  }
+}
+
+// The tiles of P that no row of their block sees, zeroed by the statistics
+// pass so that P holds the softmax everywhere (the P pass writes the active
+// tiles, masked entries as exact zeros).  Workgroup (mb, ch) zeroes the
+// mirrors (t, mb) of its chunk's tiles below the diagonal (work in proportion
+// to its active tiles) and, with a window, every cr.nch-th tile t left of the
+// block's first visible key together with its mirror (t, mb).  Together these
+// cover each masked tile once.
+template <typename T, bool XM>
+__device__ __forceinline__ void zero_masked_tiles(const Params& a, int b, int h, int mb, const Range& rg,
+                                                  const Chunk& cr, int ch) {
+  if (!a.causal) return;
+  T* P = at<T>(a.p, b, h);
+  const int t_end = cr.t1 < mb ? cr.t1 : mb;
+  for (int t = cr.t0; t < t_end; ++t) zero_p_tile<T>(P, a.p.st, t, mb, a.T);
+  if constexpr (XM) {
+    for (int t = ch; t < rg.lo; t += cr.nch) {
+      zero_p_tile<T>(P, a.p.st, mb, t, a.T);
+      zero_p_tile<T>(P, a.p.st, t, mb, a.T);
+    }
+  }
+}
+
 __device__ __forceinline__ float tile_max(const Tile& s) {
   float t = -INFINITY;
 #pragma unroll
@@ -449,6 +495,7 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_stats(Pa
     }
   }
   if (!XM && TTT_FWD_STATS_FUSED && raw_units && mx != -INFINITY) mx *= csl;  // back to base-2 units
+  zero_masked_tiles<T, XM>(a, b, h, mb, rg, cr, ch);
   {
     // Finite without a window (every row sees a key of its first tile); with
     // one a chunk can miss all of a row's keys, and then max -inf, sum 0.

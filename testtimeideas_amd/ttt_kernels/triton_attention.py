@@ -14,8 +14,9 @@ reference's ``bwd_mode`` strings.  All modes run hand-written gfx950 kernels:
     ``dv_only``) and any unknown string (the reference's default branch,
     :416-420): the forward keeps only the row LSE and later passes recompute P
     tile by tile.
-  * ``custom``: first-order gradients from the recompute kernels, returned
-    without a graph (the reference routes this mode to its stubs, :345-349).
+  * ``custom``: the reference routes this mode to its not-implemented stubs
+    (:345-349).  Here it runs the recompute-mode kernels: the same
+    gradients, differentiable under ``create_graph=True`` like every mode.
 
 With ``create_graph=True`` the backward returns the outputs of a second
 autograd Function whose backward is the exact closed-form double backward
@@ -161,13 +162,9 @@ class TritonAttentionFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_out: torch.Tensor):
-        if ctx.bwd_mode == "custom":
-            q, k, v = ctx.saved_tensors[:3]
-            causal, scale = ctx.causal, ctx.scale
-            dq = backward_stubs.triton_attn_bwd_dq(q, k, v, grad_out, causal=causal, scale=scale)
-            dk = backward_stubs.triton_attn_bwd_dk(q, k, v, grad_out, causal=causal, scale=scale)
-            dv = backward_stubs.triton_attn_bwd_dv(q, k, v, grad_out, causal=causal, scale=scale)
-            return dq, dk, dv, None, None, None
+        # Every mode, `custom` included, takes the kernels' backward from the
+        # saved forward (O, LSE and, for save_p, P); under create_graph=True it
+        # stays differentiable.
         dq, dk, dv = attn_backward(ctx, grad_out)
         return dq, dk, dv, None, None, None
 

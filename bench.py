@@ -33,6 +33,16 @@ from ttt_kernels import triton_attention  # noqa: E402
 
 METRIC = "fwd+bwd+grad-grad ms at T=8k/16k d=64 fp16 causal; MFMA/HBM % of peak"
 REFERENCE_H100_MS = {"C3": 4.054, "C4_16k": 13.649}  # artifacts/gradgrad_sweep.csv (reduced grad-grad)
+# The reference's published sweep (artifacts/gradgrad_sweep.csv:2-13, triton_ms_mean; b1 h1 d64 fp16,
+# save_p_triton_full, its mean-loss harness, H100): (T, causal) -> ms.  Context only: its grad-grad
+# holds P constant.
+REFERENCE_SWEEP_H100_MS = {
+    (512, False): 1.901, (1024, False): 2.012, (2048, False): 1.981, (4096, False): 2.010,
+    (8192, False): 3.503, (16384, False): 11.466, (512, True): 1.994, (1024, True): 1.953,
+    (2048, True): 1.995, (4096, True): 2.083, (8192, True): 4.054, (16384, True): 13.649}
+# The reference's forward at C2 (artifacts/modal_bench_h100_latest.txt:3-5; triton_attention(q, k, v)
+# with the default mode, no grad): ms on H100.
+REFERENCE_C2_FWD_H100_MS = 0.137
 
 
 def _two_stage_sum(t: torch.Tensor) -> torch.Tensor:
@@ -178,6 +188,85 @@ def measured_traffic(entry: str, cfg: workloads.Config):
             total += rec["fetch_bytes"] + rec["write_bytes"]
             found = True
     return round(total) if found else None
+
+
+def fwd_mfma(cfg: workloads.Config, dev, reps: int = 20) -> dict:
+    """The O + LSE forward (recompute modes; the reference's default forward)
+    alone: mean duration from HIP events on the launch stream and its MFMA
+    utilisation by algorithmic FLOPs (QK^T and PV over the active tiles)."""
+    x = workloads.make_inputs(cfg, seed=0, device=dev)
+    q, k, v = x["q"], x["k"], x["v"]
+    with torch.no_grad():
+        for _ in range(3):
+            _lib.fwd(q, k, v, cfg.causal, cfg.scale, False)
+        with _lib.kernel_timing() as rec:
+            for _ in range(reps):
+                _lib.fwd(q, k, v, cfg.causal, cfg.scale, False)
+            torch.cuda.synchronize()
+            ms = _lib.mean_ms(rec)["ttt_attn_fwd"]
+    flops = 4.0 * cfg.b * cfg.h * cfg.d * workloads.cfg_area(cfg)
+    peak = workloads.PEAK_TFLOPS[workloads.DTYPE_TAG[cfg.torch_dtype]]
+    return {"us": round(ms * 1e3, 2), "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+            "mfma_frac": round(flops / (ms * 1e-3) / (peak * 1e12), 4)}
+
+
+def sweep_bench(dev, steps: int, warmup: int) -> list:
+    """The reference's published sweep (C4): b1 h1 d64 fp16, T = 512 ... 16384,
+    non-causal and causal, the full step per point."""
+    out = []
+    for causal in (False, True):
+        for t in (512, 1024, 2048, 4096, 8192, 16384):
+            cfg = workloads.sweep_config(t, causal)
+            x = workloads.make_inputs(cfg, seed=0, device=dev)
+            ms = time_steps(make_step(cfg, x), steps, warmup)
+            roof = workloads.roofline_us(cfg)
+            out.append({"t": t, "causal": causal, "ms": round(ms, 4),
+                        "tflops": round(roof["flops"] / (ms * 1e-3) / 1e12, 2),
+                        "step_roofline_frac": round(roof["roofline_us"] * 1e-3 / ms, 4),
+                        "reference_h100_ms": REFERENCE_SWEEP_H100_MS[(t, causal)]})
+            del x
+    return out
+
+
+def c2_bench(dev, steps: int, warmup: int) -> dict:
+    """C2 (b2 h4 T2048 d128 fp16 non-causal): the forward alone as the
+    reference's forward benchmark runs it (default mode, no grad), the save_p
+    forward (P written), and save_p forward + first backward."""
+    cfg = workloads.CONFIGS["C2"]
+    x = workloads.make_inputs(cfg, seed=0, device=dev)
+    q, k, v = x["q"], x["k"], x["v"]
+
+    def fwd(mode):
+        def run():
+            with torch.no_grad():
+                return triton_attention(q, k, v, causal=cfg.causal, bwd_mode=mode)
+        return run
+
+    fwd_ms = time_steps(fwd("recompute"), steps, warmup)
+    fwd_p_ms = time_steps(fwd("save_p"), steps, warmup)
+    step = make_step(cfg, x)
+    ms = time_steps(step, steps, warmup)
+    roof = workloads.roofline_us(cfg)
+    return {"fwd_ms": round(fwd_ms, 4), "fwd_save_p_ms": round(fwd_p_ms, 4), "fwd_bwd_ms": round(ms, 4),
+            "fwd_bwd_tflops": round(roof["flops"] / (ms * 1e-3) / 1e12, 2),
+            "fwd_bwd_roofline_frac": round(roof["roofline_us"] * 1e-3 / ms, 4),
+            "kernel_us": {k: round(v * 1e3, 2) for k, v in sorted(kernel_times(step, 5).items())},
+            "reference_h100_fwd_ms": REFERENCE_C2_FWD_H100_MS}
+
+
+def c5_bench(dev, steps: int, warmup: int) -> dict:
+    """C5 (b4 h16 T8192 d128 bf16 causal, q, k, v x 0.5): the full step."""
+    cfg = workloads.CONFIGS["C5"]
+    x = workloads.make_inputs(cfg, seed=0, device=dev)
+    step = make_step(cfg, x)
+    ms = time_steps(step, steps, warmup)
+    roof = workloads.roofline_us(cfg)
+    kt = kernel_times(step, 3)
+    return {"ms": round(ms, 3), "tflops": round(roof["flops"] / (ms * 1e-3) / 1e12, 1),
+            "step_roofline_us": round(roof["roofline_us"], 1),
+            "step_roofline_frac": round(roof["roofline_us"] * 1e-3 / ms, 4),
+            "kernel_us": {k: round(v * 1e3, 1) for k, v in sorted(kt.items())},
+            "roofline": roofline_entry(cfg, kt)}
 
 
 def _cpu_model() -> str:
@@ -371,16 +460,14 @@ def main():
         out["t16k_causal_ms"] = round(time_steps(make_step(cfg16, x16), max(5, args.steps // 2), 3), 4)
         del x16
         # forward-only, O + LSE (recompute mode): MFMA utilisation of the contraction kernel
-        q, k, v = (x[n].detach() for n in ("q", "k", "v"))
-        with torch.no_grad():
-            with _lib.kernel_timing() as rec:
-                for _ in range(20):
-                    _lib.fwd(q, k, v, True, cfg.scale, False)
-                torch.cuda.synchronize()
-                fwd_ms = _lib.mean_ms(rec)["ttt_attn_fwd"]
-        fwd_flops = 4.0 * cfg.b * cfg.h * cfg.d * workloads.active_area(cfg.t, cfg.causal)
-        out["fwd_lse_us"] = round(fwd_ms * 1e3, 2)
-        out["fwd_lse_mfma_frac"] = round(fwd_flops / (fwd_ms * 1e-3) / (workloads.PEAK_TFLOPS["f16"] * 1e12), 4)
+        fm = fwd_mfma(cfg, dev)
+        out["fwd_lse_us"] = fm["us"]
+        out["fwd_lse_mfma_frac"] = fm["mfma_frac"]
+        out["fwd_lse"] = {name: fwd_mfma(workloads.CONFIGS[name], dev) for name in ("C3", "C4_16k", "C2", "C5")}
+        # the reference's published points: the C4 sweep, the C2 forward and first backward, and C5
+        out["c4_sweep"] = sweep_bench(dev, max(10, args.steps // 5), 5)
+        out["c2"] = c2_bench(dev, max(10, args.steps // 5), 5)
+        out["c5"] = c5_bench(dev, 5, 2)
         # the reference TTT model's windowed attention (one launch per pass for its chunk loop)
         for name in ("TTT_W512", "TTT_W512_8K"):
             cw = workloads.CONFIGS[name]

@@ -25,12 +25,13 @@
  *   - P is a [B,H,T,T] matrix described by a ttt_view whose stride_t is the row
  *     stride; the column dimension must be contiguous and the row stride (in
  *     bytes) 16-byte aligned.  Rows are read in runs of 8 elements, so the
- *     storage must extend to column T rounded up to 8 of the last row.  The
- *     forward writes every element of P (masked entries as exact zeros, as
- *     the softmax gives them).  With causal=1 the backward entry points read
- *     only the lower block triangle of 64x64 tiles (block column <= block
- *     row); a window narrows this to the tiles that hold a visible key of
- *     some row.
+ *     storage must extend to column T rounded up to 8 of the last row.  With
+ *     causal=1 the forward writes, and the backward entry points read, only
+ *     the active 64x64 tiles: the lower block triangle (block column <= block
+ *     row), narrowed by a window to the tiles that hold a visible key of some
+ *     row.  Masked entries inside active tiles are written as exact zeros;
+ *     ttt_attn_fill_masked_p() zeroes the other tiles when the whole matrix
+ *     is wanted.
  *   - Row statistics (lse, rowsum, E, F) are contiguous fp32 [B*H*T] arrays,
  *     index (b*H + h)*T + t.  lse is the natural-log log-sum-exp of the scaled
  *     scores of each row.
@@ -165,6 +166,18 @@ int ttt_attn_fwd(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
                  const ttt_view* v, const ttt_view* o, float* lse,
                  const ttt_view* p, void* workspace,
                  int64_t workspace_bytes, void* stream);
+
+/*
+ * Zeros into the tiles of P that ttt_attn_fwd leaves unwritten (causal: the
+ * tiles past the diagonal and, with a window, before each row block's first
+ * visible key), so that P holds the softmax everywhere; nothing to do when
+ * causal=0.  The forward does not do this itself because the backward never
+ * reads those tiles (at b4 h16 T8192 causal they are 4 GiB of zeros).
+ * Replaces: the masked-tile stores of _attn_probs_kernel,
+ * ttt_kernels/triton_attention.py:208-256 (which writes every tile, masked
+ * entries as 0), for callers that read the whole of ctx.saved_probs.
+ */
+int ttt_attn_fill_masked_p(const ttt_problem* pr, const ttt_view* p, void* stream);
 
 /*
  * dQ (row-block kernel).  P is read from p when p != NULL, otherwise it is

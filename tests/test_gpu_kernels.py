@@ -35,6 +35,8 @@ def _run(xs, causal, scale, save_p, want_gdo=True):
     o, lse, p = _lib.fwd(q, k, v, causal, scale, save_p)
     dq, dk, dv, rowsum = _lib.bwd(q, k, v, o, do, lse, p, causal, scale)
     GQ, GK, GV, GdO = _lib.gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, causal, scale, want_gdo)
+    if p is not None:  # the tiles the forward leaves unwritten, zeroed for the comparison
+        _lib.fill_masked_p(p, causal)
     torch.cuda.synchronize()
     return dict(o=o, lse=lse, p=p, dq=dq, dk=dk, dv=dv, rowsum=rowsum, gq=GQ, gk=GK, gv=GV, gdo=GdO)
 
@@ -49,7 +51,8 @@ def _compare(out, ref, dtype, causal, t, names=("o", "dq", "dk", "dv", "gq", "gk
     errs["lse"] = check("lse", out["lse"], ref["lse"], torch.float32, abs_tol=2e-5 if dtype == torch.float32 else 2e-3)
     errs["rowsum"] = check("rowsum", out["rowsum"], ref["rowsum"], dtype)
     if out["p"] is not None:
-        # the forward writes all of P, masked entries as zeros
+        # masked entries are zeros (inside active tiles from the forward,
+        # elsewhere from fill_masked_p)
         got = out["p"].double().cpu().numpy()
         errs["p"] = check("p", got, ref["p"], dtype)
         if causal:

@@ -97,6 +97,7 @@ _SIGS = {
     "ttt_attn_bwd_dkdv": [_P(_Problem), _VP, _VP, _VP, _VP, _FP, _VP, _FP, _VP, _VP] + _WS + _ST,
     "ttt_attn_bwd": [_P(_Problem), _VP, _VP, _VP, _VP, _VP, _FP, _VP, _FP, _VP, _VP, _VP] + _WS + _ST,
     "ttt_attn_bwd_rowsum": [_P(_Problem), _VP, _VP, _VP, _FP] + _ST,
+    "ttt_attn_fill_masked_p": [_P(_Problem), _VP] + _ST,
     "ttt_attn_gg_row": [_P(_Problem), _VP, _VP, _VP, _VP, _FP, _VP, _FP, _VP, _VP, _VP, _VP, _VP, _FP, _FP]
                        + _WS + _ST,
     "ttt_attn_gg_col": [_P(_Problem), _VP, _VP, _VP, _VP, _FP, _VP, _FP, _FP, _FP, _VP, _VP, _VP, _VP, _VP]
@@ -487,6 +488,20 @@ def bwd_dkdv(q, k, v, do, p, lse, rowsum, mask, scale: float, want_dk: bool = Tr
     _timed("ttt_attn_bwd_dkdv", ctypes.byref(prob), _view(q), _view(k), _view(v), _view(do), _fptr(lse),
            _view(p), _fptr(rowsum), _view(dk), _view(dv), wp, wn, _stream())
     return dk, dv
+
+
+def fill_masked_p(p, mask) -> None:
+    """Zero the tiles of a forward's P that the forward leaves unwritten
+    (causal: past the diagonal; window: before the first visible key), so P
+    holds the softmax everywhere, as the reference's P kernel writes it
+    (ttt_kernels/triton_attention.py:208-256)."""
+    m = as_mask(mask)
+    if not m.causal or p.numel() == 0:
+        return
+    b, h, t, _ = p.shape
+    like = torch.empty((b, h, t, 64), dtype=p.dtype, device="meta")
+    pr = ctypes.byref(_problem(like, m, 1.0))
+    _timed("ttt_attn_fill_masked_p", pr, _view(p), _stream())
 
 
 def rowsum_from_p(p, do, v, mask):

@@ -412,6 +412,13 @@ int ttt_attn_fwd(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, co
   return launched(ttt::launch_fwd(pr->dtype, (int)pr->head_dim, a, wp, (hipStream_t)stream), "ttt_attn_fwd");
 }
 
+int ttt_attn_fill_masked_p(const ttt_problem* pr, const ttt_view* p, void* stream) {
+  TRY(check_problem(pr));
+  ttt::Params a = base_params(pr);
+  TRY(take_view(pr, p, "p", &a.p));
+  return launched(ttt::launch_fill_masked_p(pr->dtype, a, (hipStream_t)stream), "ttt_attn_fill_masked_p");
+}
+
 int ttt_attn_bwd_dq(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
                     const ttt_view* o, const ttt_view* dout, const float* lse, const ttt_view* p,
                     const float* rowsum_in, float* rowsum_out, const ttt_view* dq, void* workspace,

@@ -121,28 +121,6 @@ __device__ __forceinline__ void zero_p_tile(T* P, int64_t ld, int rb, int cb, in
   }
 }
 
-// The tiles of P that no row of their block sees, zeroed by the statistics
-// pass so that P holds the softmax everywhere (the P pass writes the active
-// tiles, masked entries as exact zeros).  Workgroup (mb, ch) zeroes the
-// mirrors (t, mb) of its chunk's tiles below the diagonal (work in proportion
-// to its active tiles) and, with a window, every cr.nch-th tile t left of the
-// block's first visible key together with its mirror (t, mb).  Together these
-// cover each masked tile once.
-template <typename T, bool XM>
-__device__ __forceinline__ void zero_masked_tiles(const Params& a, int b, int h, int mb, const Range& rg,
-                                                  const Chunk& cr, int ch) {
-  if (!a.causal) return;
-  T* P = at<T>(a.p, b, h);
-  const int t_end = cr.t1 < mb ? cr.t1 : mb;
-  for (int t = cr.t0; t < t_end; ++t) zero_p_tile<T>(P, a.p.st, t, mb, a.T);
-  if constexpr (XM) {
-    for (int t = ch; t < rg.lo; t += cr.nch) {
-      zero_p_tile<T>(P, a.p.st, mb, t, a.T);
-      zero_p_tile<T>(P, a.p.st, t, mb, a.T);
-    }
-  }
-}
-
 __device__ __forceinline__ float tile_max(const Tile& s) {
   float t = -INFINITY;
 #pragma unroll
@@ -495,7 +473,6 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_stats(Pa
     }
   }
   if (!XM && TTT_FWD_STATS_FUSED && raw_units && mx != -INFINITY) mx *= csl;  // back to base-2 units
-  zero_masked_tiles<T, XM>(a, b, h, mb, rg, cr, ch);
   {
     // Finite without a window (every row sees a key of its first tile); with
     // one a chunk can miss all of a row's keys, and then max -inf, sum 0.
@@ -719,6 +696,44 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_p(Params
   } else {
     store_acc_partial<D>(a.ws_acc + part_index(a, bh, nblk, mb, ch) * kBlk * D, rl, acc);
   }
+}
+
+// ---------------------------------------------------------------------------
+// The tiles of P that the P pass leaves unwritten (no row of their block sees
+// a key in them: past the diagonal, or before a window's first visible key),
+// filled with zeros so that P holds the softmax everywhere.  Workgroup
+// (x, y, z) takes row block x, column tiles 8y .. 8y+7 of slice z.
+constexpr int kFillTiles = 8;
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void k_fill_masked_p(Params a) {
+  const int T_ = a.T;
+  const int nblk = (T_ + kBlk - 1) / kBlk;
+  const int rb = blockIdx.x, bh = blockIdx.z, b = bh / a.H, h = bh % a.H;
+  const Range rg = row_block_range(rb, nblk, T_, a.causal, a.win, a.win_kind);
+  T* P = at<T>(a.p, b, h);
+  const int c0 = blockIdx.y * kFillTiles;
+  const int c1 = c0 + kFillTiles < nblk ? c0 + kFillTiles : nblk;
+  for (int cb = c0; cb < c1; ++cb)
+    if (cb < rg.lo || cb >= rg.hi) zero_p_tile<T>(P, a.p.st, rb, cb, T_);
+}
+
+template <typename T>
+static hipError_t launch_fill_masked_p_t(const Params& a, hipStream_t st) {
+  const int nblk = (a.T + kBlk - 1) / kBlk;
+  dim3 grid(nblk, (nblk + kFillTiles - 1) / kFillTiles, a.B * a.H);
+  hipLaunchKernelGGL((k_fill_masked_p<T>), grid, dim3(kThreads), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_masked_p(int dtype, const Params& a, hipStream_t st) {
+  if (!a.causal) return hipSuccess;  // every tile is active
+  switch (dtype) {
+    case kF16: return launch_fill_masked_p_t<_Float16>(a, st);
+    case kBF16: return launch_fill_masked_p_t<__bf16>(a, st);
+    case kF32: return launch_fill_masked_p_t<float>(a, st);
+  }
+  return hipErrorInvalidValue;
 }
 
 // ---------------------------------------------------------------------------

@@ -88,6 +88,8 @@ inline int occupancy_gg_col(int dtype, int D, bool load_p, bool xm) {
 }
 
 hipError_t launch_fwd(int dtype, int D, const Params& a, bool write_p, hipStream_t st);
+// Zeros into the tiles of P that the forward's P pass does not write.
+hipError_t launch_fill_masked_p(int dtype, const Params& a, hipStream_t st);
 hipError_t launch_combine_sum(int dtype, int D, const Params& a, int which, hipStream_t st);
 hipError_t launch_combine_fwd(int dtype, int D, const Params& a, hipStream_t st);
 hipError_t launch_combine_gg_row(int dtype, int D, const Params& a, bool gdo, hipStream_t st);

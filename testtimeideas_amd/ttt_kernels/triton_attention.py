@@ -115,6 +115,35 @@ class _AttnBwdFn(torch.autograd.Function):
                 None, None, None, None, None, None, None, None, None)
 
 
+class SavedProbs(tuple):
+    """``ctx.saved_probs``: the one-tuple ``(P,)`` of a save_p forward.  The
+    forward writes only the tiles of P that some row sees; the first time P
+    is taken out of this tuple, the other tiles are filled with zeros
+    (``_lib.fill_masked_p``) on the current stream, so a caller that reads
+    ``ctx.saved_probs[0]`` (as the reference's backward does,
+    triton_attention.py:354-378) gets the whole softmax matrix.  The kernels'
+    own backward reads P from the saved tensors and never pays for the fill."""
+
+    def __new__(cls, p: torch.Tensor, mask: "_lib.Mask"):
+        obj = super().__new__(cls, (p,))
+        obj._mask = mask
+        obj._filled = False
+        return obj
+
+    def _complete(self) -> None:
+        if not self._filled:
+            _lib.fill_masked_p(tuple.__getitem__(self, 0), self._mask)
+            self._filled = True
+
+    def __getitem__(self, i):
+        self._complete()
+        return tuple.__getitem__(self, i)
+
+    def __iter__(self):
+        self._complete()
+        return tuple.__iter__(self)
+
+
 def attn_forward(ctx, q, k, v, mask: "_lib.Mask", scale: float, bwd_mode: str, lay: Layout) -> torch.Tensor:
     """Forward of an attention Function: runs the kernels on the laid-out
     operands and keeps what the backward needs on ctx."""
@@ -127,7 +156,7 @@ def attn_forward(ctx, q, k, v, mask: "_lib.Mask", scale: float, bwd_mode: str, l
     kp, vp = lay.k(k), lay.k(v)
     op, lse, p = _lib.fwd(qp, kp, vp, mask, scale, want_p=(kind == "save_p"))
     ctx.save_for_backward(q, k, v, qp, kp, vp, op, lse, p)
-    ctx.saved_probs = () if p is None else (p,)
+    ctx.saved_probs = () if p is None else SavedProbs(p, mask)
     return lay.uq(op)
 
 

@@ -279,6 +279,28 @@ int ttt_attn_gg(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
                 const ttt_view* gdout, float* e_buf, float* f_buf,
                 void* workspace, int64_t workspace_bytes, void* stream);
 
+/*
+ * ttt_attn_gg without any allocation: the same double backward, with the
+ * row statistics E and F and the split's partial sums held in a static
+ * device scratch of 64 MiB that the library keeps on every GPU it runs on
+ * until the process ends (no workspace, no e/f buffers).  The caller passes
+ * inputs and outputs only.  E and F take at most 16 MiB of it, so
+ * B*H*T <= 2^21 (larger problems fail with TTT_ERR_INVALID_ARGUMENT); the
+ * split is the one ttt_attn_gg uses when its partials fit in the rest, and
+ * otherwise one with fewer chunks per block (results then agree with
+ * ttt_attn_gg to summation order).  Calls on one GPU share its scratch, so
+ * calls that overlap on one GPU (two streams or two threads) race.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc).
+ */
+int ttt_attn_gg_noalloc(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
+                        const ttt_view* v, const ttt_view* dout, const float* lse,
+                        const ttt_view* p, const float* rowsum, const ttt_view* gq,
+                        const ttt_view* gk, const ttt_view* gv, const ttt_view* gq_out,
+                        const ttt_view* gk_out, const ttt_view* gv_out,
+                        const ttt_view* gdout, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -348,3 +348,14 @@ def test_expanded_operand_is_copied():
     y = _lib.prep(x, 64)
     assert y.stride(2) > 0 and torch.equal(y, x)
     assert _lib._kernel_ok(y)
+
+
+def test_noalloc_rejects_too_many_rows_without_gpu():
+    """ttt_attn_gg_noalloc keeps E and F in its static scratch (B*H*T <= 2^21)
+    and says so before touching the device."""
+    lib = _lib.load()
+    pr = _prob(batch=64, seqlen=32769)
+    rc = lib.ttt_attn_gg_noalloc(ctypes.byref(pr), _v(), _v(), _v(), _v(), 0x20000, None, 0x20000, _v(), _v(), _v(),
+                                 _v(), _v(), _v(), None, None)
+    assert rc == 1
+    assert b"B*H*T" in lib.ttt_last_error()

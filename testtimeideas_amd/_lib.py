@@ -104,6 +104,8 @@ _SIGS = {
                        + _WS + _ST,
     "ttt_attn_gg": [_P(_Problem), _VP, _VP, _VP, _VP, _FP, _VP, _FP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _FP,
                     _FP] + _WS + _ST,
+    "ttt_attn_gg_noalloc": [_P(_Problem), _VP, _VP, _VP, _VP, _FP, _VP, _FP, _VP, _VP, _VP, _VP, _VP, _VP, _VP]
+                           + _ST,
 }
 
 # ttt_entry codes (include/ttt_attn.h)
@@ -547,6 +549,23 @@ def gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, mask, scale: float, want_gdo: bo
         _timed("ttt_attn_gg_col", pr, _view(q), _view(k), _view(v), _view(do), lse_p, _view(p),
                rowsum.data_ptr(), e.data_ptr(), f.data_ptr(), _view(gq), _view(gk), _view(gv), _view(gk_out),
                _view(gv_out), wp, wn, st)
+    return gq_out, gk_out, gv_out, gdo
+
+
+def gg_noalloc(q, k, v, do, lse, p, rowsum, gq, gk, gv, mask, scale: float, want_gdo: bool):
+    """``gg`` through ttt_attn_gg_noalloc: the library's static device scratch
+    instead of a workspace and E/F buffers (outputs are still allocated
+    here).  No counterpart in the reference."""
+    gq_out = _empty_like_out(q)
+    gk_out = _empty_like_out(k)
+    gv_out = _empty_like_out(v)
+    gdo = _empty_like_out(do) if want_gdo else None
+    if q.numel() == 0:
+        return gq_out, gk_out, gv_out, gdo
+    prob = _problem(q, mask, scale)
+    _timed("ttt_attn_gg_noalloc", ctypes.byref(prob), _view(q), _view(k), _view(v), _view(do), _fptr(lse),
+           _view(p), rowsum.data_ptr(), _view(gq), _view(gk), _view(gv), _view(gq_out), _view(gk_out),
+           _view(gv_out), _view(gdo), _stream())
     return gq_out, gk_out, gv_out, gdo
 
 

@@ -327,9 +327,27 @@ ttt::Params base_params(const ttt_problem* pr) {
   return a;
 }
 
-// Attach the split and the workspace for kernel family `fam`.
-int attach_split(const ttt_problem* pr, int fam, bool load_p, void* ws, int64_t ws_bytes, ttt::Params* a) {
-  const Split s = choose_split(pr, fam, load_p);
+// The split of choose_split, with fewer chunks per block if its partials
+// would need more than `cap` bytes (cap < 0: no limit).  One chunk per block
+// needs none, so some split always fits.
+Split capped_split(const ttt_problem* pr, int fam, bool load_p, int64_t cap) {
+  Split s = choose_split(pr, fam, load_p);
+  if (cap < 0 || family_bytes(pr, s, fam) <= cap) return s;
+  const std::vector<int64_t> len = block_tiles(pr, column_family(fam));
+  const int64_t lmax = *std::max_element(len.begin(), len.end());
+  for (int64_t nch = s.nchunk_max - 1; nch >= 1; --nch) {
+    s.chunk = (int)((lmax + nch - 1) / nch);
+    s.nchunk_max = (int)((lmax + s.chunk - 1) / s.chunk);
+    if (family_bytes(pr, s, fam) <= cap) break;
+  }
+  return s;
+}
+
+// Attach the split and the workspace for kernel family `fam`; the split's
+// partials must fit in `cap` bytes (cap < 0: no limit).
+int attach_split(const ttt_problem* pr, int fam, bool load_p, void* ws, int64_t ws_bytes, ttt::Params* a,
+                 int64_t cap = -1) {
+  const Split s = capped_split(pr, fam, load_p, cap);
   a->chunk = s.chunk;
   a->nchunk_max = s.nchunk_max;
   const int64_t need = family_bytes(pr, s, fam);
@@ -364,6 +382,46 @@ int launched(hipError_t e, const char* what) {
     const int rc_ = (x);           \
     if (rc_ != TTT_OK) return rc_; \
   } while (0)
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Scratch of the entry point that allocates nothing (ttt_attn_gg_noalloc):
+// its E and F row statistics, then the partial sums of its split.  A
+// file-scope device array, so every GPU the library runs on holds its own
+// copy from module load until the process ends.  Host code never uses the
+// array's name as an address (on the host it is only a stand-in): the first
+// call on a device looks up that device's copy with hipGetSymbolAddress and
+// keeps the pointer.  Calls on one GPU share its copy, so calls that overlap
+// on one GPU (different streams, or threads) race; nothing in it needs to
+// start at zero (every kernel writes what it later reads).
+constexpr int64_t kNoAllocScratchBytes = 64ll << 20;
+constexpr int64_t kNoAllocStatBytes = 16ll << 20;  // E and F: B*H*T <= 2^21
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+// This device's copy of `scratch` (looked up once per device).
+int scratch_on_device(void** out) {
+  static std::mutex mu;
+  static void* ptr[kMaxDevices] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(TTT_ERR_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(TTT_ERR_UNSUPPORTED, "device %d: at most %d devices", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(TTT_ERR_LAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    ptr[dev] = p;
+  }
+  *out = ptr[dev];
+  return TTT_OK;
+}
 
 }  // namespace
 
@@ -500,11 +558,13 @@ int ttt_attn_bwd_rowsum(const ttt_problem* pr, const ttt_view* p, const ttt_view
                   "ttt_attn_bwd_rowsum");
 }
 
-int ttt_attn_gg_row(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
-                    const ttt_view* dout, const float* lse, const ttt_view* p, const float* rowsum,
-                    const ttt_view* gq, const ttt_view* gk, const ttt_view* gv, const ttt_view* gq_out,
-                    const ttt_view* gdout, float* e_out, float* f_out, void* workspace, int64_t workspace_bytes,
-                    void* stream) {
+// ttt_attn_gg_row / ttt_attn_gg_col with the split's partials held to `cap`
+// bytes (cap < 0: no limit).
+static int gg_row_impl(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
+                       const ttt_view* dout, const float* lse, const ttt_view* p, const float* rowsum,
+                       const ttt_view* gq, const ttt_view* gk, const ttt_view* gv, const ttt_view* gq_out,
+                       const ttt_view* gdout, float* e_out, float* f_out, void* workspace, int64_t workspace_bytes,
+                       void* stream, int64_t cap) {
   TRY(check_problem(pr));
   ttt::Params a = base_params(pr);
   TRY(take_view(pr, q, "q", &a.q));
@@ -526,16 +586,16 @@ int ttt_attn_gg_row(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
   a.rowsum_in = rowsum;
   a.e = e_out;
   a.f = f_out;
-  TRY(attach_split(pr, gdo ? ttt::kFamGgRowGdo : ttt::kFamGgRow, lp, workspace, workspace_bytes, &a));
+  TRY(attach_split(pr, gdo ? ttt::kFamGgRowGdo : ttt::kFamGgRow, lp, workspace, workspace_bytes, &a, cap));
   return launched(ttt::launch_gg_row(pr->dtype, (int)pr->head_dim, a, lp, gdo, (hipStream_t)stream),
                   "ttt_attn_gg_row");
 }
 
-int ttt_attn_gg_col(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
-                    const ttt_view* dout, const float* lse, const ttt_view* p, const float* rowsum,
-                    const float* e_in, const float* f_in, const ttt_view* gq, const ttt_view* gk,
-                    const ttt_view* gv, const ttt_view* gk_out, const ttt_view* gv_out, void* workspace,
-                    int64_t workspace_bytes, void* stream) {
+static int gg_col_impl(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
+                       const ttt_view* dout, const float* lse, const ttt_view* p, const float* rowsum,
+                       const float* e_in, const float* f_in, const ttt_view* gq, const ttt_view* gk,
+                       const ttt_view* gv, const ttt_view* gk_out, const ttt_view* gv_out, void* workspace,
+                       int64_t workspace_bytes, void* stream, int64_t cap) {
   TRY(check_problem(pr));
   ttt::Params a = base_params(pr);
   TRY(take_view(pr, q, "q", &a.q));
@@ -556,9 +616,27 @@ int ttt_attn_gg_col(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
   a.rowsum_in = rowsum;
   a.e = const_cast<float*>(e_in);
   a.f = const_cast<float*>(f_in);
-  TRY(attach_split(pr, ttt::kFamGgCol, lp, workspace, workspace_bytes, &a));
+  TRY(attach_split(pr, ttt::kFamGgCol, lp, workspace, workspace_bytes, &a, cap));
   return launched(ttt::launch_gg_col(pr->dtype, (int)pr->head_dim, a, lp, (hipStream_t)stream),
                   "ttt_attn_gg_col");
+}
+
+int ttt_attn_gg_row(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
+                    const ttt_view* dout, const float* lse, const ttt_view* p, const float* rowsum,
+                    const ttt_view* gq, const ttt_view* gk, const ttt_view* gv, const ttt_view* gq_out,
+                    const ttt_view* gdout, float* e_out, float* f_out, void* workspace, int64_t workspace_bytes,
+                    void* stream) {
+  return gg_row_impl(pr, q, k, v, dout, lse, p, rowsum, gq, gk, gv, gq_out, gdout, e_out, f_out, workspace,
+                     workspace_bytes, stream, -1);
+}
+
+int ttt_attn_gg_col(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
+                    const ttt_view* dout, const float* lse, const ttt_view* p, const float* rowsum,
+                    const float* e_in, const float* f_in, const ttt_view* gq, const ttt_view* gk,
+                    const ttt_view* gv, const ttt_view* gk_out, const ttt_view* gv_out, void* workspace,
+                    int64_t workspace_bytes, void* stream) {
+  return gg_col_impl(pr, q, k, v, dout, lse, p, rowsum, e_in, f_in, gq, gk, gv, gk_out, gv_out, workspace,
+                     workspace_bytes, stream, -1);
 }
 
 int ttt_attn_gg(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
@@ -570,6 +648,31 @@ int ttt_attn_gg(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, con
                       workspace_bytes, stream));
   return ttt_attn_gg_col(pr, q, k, v, dout, lse, p, rowsum, e_buf, f_buf, gq, gk, gv, gk_out, gv_out, workspace,
                          workspace_bytes, stream);
+}
+
+int ttt_attn_gg_noalloc(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
+                        const ttt_view* dout, const float* lse, const ttt_view* p, const float* rowsum,
+                        const ttt_view* gq, const ttt_view* gk, const ttt_view* gv, const ttt_view* gq_out,
+                        const ttt_view* gk_out, const ttt_view* gv_out, const ttt_view* gdout, void* stream) {
+  TRY(check_problem(pr));
+  const int64_t nstat = pr->batch * pr->heads * pr->seqlen;
+  const int64_t one = (nstat * (int64_t)sizeof(float) + 255) / 256 * 256;  // E, then F, 256-byte aligned
+  if (2 * one > kNoAllocStatBytes)
+    return fail(TTT_ERR_INVALID_ARGUMENT,
+                "ttt_attn_gg_noalloc: B*H*T = %lld needs %lld bytes of E/F statistics, more than the %lld its "
+                "scratch holds (B*H*T <= %lld); use ttt_attn_gg with caller buffers",
+                (long long)nstat, (long long)(2 * one), (long long)kNoAllocStatBytes,
+                (long long)(kNoAllocStatBytes / 8));
+  void* base = nullptr;
+  TRY(scratch_on_device(&base));
+  float* e = static_cast<float*>(base);
+  float* f = reinterpret_cast<float*>(static_cast<char*>(base) + one);
+  void* ws = static_cast<char*>(base) + 2 * one;
+  const int64_t ws_bytes = kNoAllocScratchBytes - 2 * one;
+  TRY(gg_row_impl(pr, q, k, v, dout, lse, p, rowsum, gq, gk, gv, gq_out, gdout, e, f, ws, ws_bytes, stream,
+                  ws_bytes));
+  return gg_col_impl(pr, q, k, v, dout, lse, p, rowsum, e, f, gq, gk, gv, gk_out, gv_out, ws, ws_bytes, stream,
+                     ws_bytes);
 }
 
 }  // extern "C"

@@ -325,8 +325,8 @@ def meta_bench(steps: int, warmup: int, dev) -> dict:
     meta_8k_v2 on this GPU, timed as the reference's loop is
     (scripts/train_meta.py:133-160): synthetic batch, meta_step, backward of
     the outer loss through every inner update, AdamW step."""
-    from testtimeideas_amd.ttt_e2e import data, meta
-    from testtimeideas_amd.ttt_e2e.model import ModelConfig, TTTModel
+    from ttt_e2e import data, meta
+    from ttt_e2e.model import ModelConfig, TTTModel
     c = META_8K
     torch.manual_seed(1337)
     model = TTTModel(ModelConfig(vocab_size=c["vocab_size"], max_seq_len=c["max_seq_len"],

@@ -5,8 +5,8 @@ parameter filter and chunking of the meta step (meta.py:9-41)."""
 import pytest
 import torch
 
-from testtimeideas_amd.ttt_e2e import data, meta
-from testtimeideas_amd.ttt_e2e.model import ModelConfig, TTTModel
+from ttt_e2e import data, meta
+from ttt_e2e.model import ModelConfig, TTTModel
 
 
 @pytest.mark.parametrize("far", [0.0, 0.5])
@@ -40,19 +40,24 @@ def test_param_filter_and_chunks():
     cfg = ModelConfig(vocab_size=32, max_seq_len=64, window_size=16, d_model=32, n_heads=2, n_layers=3, d_ff=64,
                       suffix_layers=1)
     m = TTTModel(cfg)
-    params, chosen = meta.split_params(m, "mlp_fast")
-    assert chosen and all("mlp_fast" in n for n in chosen) and len(params) == len(list(m.parameters()))
-    assert meta.split_params(m, None)[1] == list(params)
-    assert meta.split_params(m, "nothing_matches")[1] == list(params)
-    assert meta.split_params(m, ["mlp_fast", "ln_f"])[1] == [n for n in params if "mlp_fast" in n or "ln_f" in n]
-    assert [c.shape[1] for c in meta.chunks(torch.zeros(2, 48, 3), 16)] == [16, 16, 16]
+    names = [n for n, _ in m.named_parameters()]
+    chosen = meta.adapted_names(m, "mlp_fast")
+    assert chosen and all("mlp_fast" in n for n in chosen)
+    assert meta.adapted_names(m, None) == names
+    assert meta.adapted_names(m, "nothing_matches") == names
+    assert meta.adapted_names(m, " mlp_fast , ln_f ") == [n for n in names if "mlp_fast" in n or "ln_f" in n]
+    assert meta.adapted_names(m, ["mlp_fast", "ln_f"]) == [n for n in names if "mlp_fast" in n or "ln_f" in n]
+    assert meta._spans(48, 16) == [(0, 16), (16, 32), (32, 48)] and meta._spans(50, None) == [(0, 50)]
     with pytest.raises(ValueError):
-        meta.chunks(torch.zeros(2, 50), 16)
-    assert len(m.prefix_blocks) == 2 and len(m.suffix_blocks) == 1 and m.suffix_blocks[0].mlp_slow is not None
+        meta._spans(50, 16)
+    assert len(m.prefix_blocks) == 2 and len(m.suffix_blocks) == 1 and hasattr(m.suffix_blocks[0], "mlp_slow")
     # reference parameter names (model.py): embed, pos, prefix_blocks.i.{ln1,attn.*_proj,ln2,mlp}, suffix ...
-    names = set(params)
     for n in ("embed.weight", "pos.weight", "prefix_blocks.0.attn.q_proj.weight", "prefix_blocks.1.mlp.2.bias",
               "suffix_blocks.0.mlp_fast.0.weight", "suffix_blocks.0.mlp_slow.2.weight", "ln_f.weight",
               "head.weight"):
         assert n in names, n
     assert "head.bias" not in names
+    with pytest.raises(ValueError):
+        m(None, mode="full")
+    with pytest.raises(ValueError):
+        m(None, mode="suffix")

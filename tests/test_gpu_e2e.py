@@ -1,8 +1,10 @@
 """The TTT model's meta-learning step on the GPU (HIP attention, fp32)
 against the same model in float64 on the CPU with the reference's chunked
-attention restated in the oracle (oracle.math_path.window_chunks_attention):
-inner and outer losses, and the meta-gradient of every parameter, which runs
-the attention's double backward through the inner updates.
+attention restated in the oracle (oracle.math_path.window_chunks_attention),
+and against the reference's own meta step (the fixture written by
+tests/golden/make_meta_fixture.py): inner and outer losses, and the
+meta-gradient of every parameter, which runs the attention's double backward
+through the inner updates.
 
 Tolerances: losses relative 1e-5; meta-gradients relative Frobenius 1e-3 per
 parameter, against at least 1e-4 of the largest gradient norm (fp32 kernels
@@ -14,9 +16,11 @@ import pytest
 import torch
 
 from oracle import math_path
+from tests.golden.make_meta_fixture import CFG, STEP
+from tests.test_e2e_meta_fixture import load_fixture
 from testtimeideas_amd.ttt_e2e import attention as attn_mod
-from testtimeideas_amd.ttt_e2e import data, meta
-from testtimeideas_amd.ttt_e2e.model import ModelConfig, TTTModel
+from ttt_e2e import data, meta
+from ttt_e2e.model import ModelConfig, TTTModel
 
 pytestmark = pytest.mark.gpu
 
@@ -65,3 +69,24 @@ def test_meta_step_matches_float64_reference(t, window, chunk, monkeypatch):
         worst = max(worst, err)
         assert err <= 1e-3, f"{name}: relative error {err:.2e}"
     print(f"worst meta-gradient error {worst:.2e}", flush=True)
+
+
+def test_meta_step_on_gpu_matches_reference_fixture():
+    """The reference's meta step (fixture: its package run in float64 on the
+    CPU) against the harness model on the GPU, fp32, HIP attention."""
+    print("[case] meta_step reference fixture", flush=True)
+    params, grads, batch, inner_ref, outer_ref = load_fixture()
+    model = TTTModel(ModelConfig(**CFG))
+    model.load_state_dict({n: p.float() for n, p in params.items()}, strict=True)
+    model = model.cuda()
+    b = {n: (x.float() if x.is_floating_point() else x).cuda() for n, x in batch.items()}
+    inner, outer = meta.meta_step(model, b["input_ids"], b["targets"], b["inner_mask"], b["outer_mask"], **STEP)
+    outer.backward()
+    torch.cuda.synchronize()
+    assert abs(inner.item() - inner_ref) <= 1e-5 * abs(inner_ref)
+    assert abs(outer.item() - outer_ref) <= 1e-5 * abs(outer_ref)
+    top = max(float(g.norm()) for g in grads.values())
+    for name, p in model.named_parameters():
+        r = grads[name]
+        err = float((p.grad.double().cpu() - r).norm()) / max(float(r.norm()), 1e-4 * top)
+        assert err <= 1e-3, f"{name}: relative error {err:.2e}"

@@ -24,61 +24,24 @@
 #include "ttt_common.h"
 #include "ttt_launch.h"
 
-// The saved-P dQ kernel streams 16-bit D = 64 key tiles by direct loads (1)
-// or through registers (0).
-#ifndef TTT_DQ_DMA
-#define TTT_DQ_DMA 1
-#endif
-// The saved-P dQ kernel's direct loads go to two buffer sets in distinct
-// arrays with compile-time roles (1) or to run-time-picked buffers (0) at
-// D = 64; at D = 128 (TTT_DQ_DMA_WIDE) always to two sets.
-#ifndef TTT_DQ_DMA_WIDE
-#define TTT_DQ_DMA_WIDE 1
-#endif
-// The recompute dQ kernel (16-bit, D = 64) streams K and V by direct loads into
-// two buffer sets (1) or through registers (0).
-#ifndef TTT_DQ_DMA_RECOMPUTE
-#define TTT_DQ_DMA_RECOMPUTE 1
-#endif
-#ifndef TTT_DQ_PAR
-#define TTT_DQ_PAR 0
-#endif
-#ifndef TTT_DQ_FULLTILE
-#define TTT_DQ_FULLTILE 1
-#endif
-#ifndef TTT_DQ_PEEL
-#define TTT_DQ_PEEL 1
-#endif
-// Fetch forms, switchable for A/B timing.  FULLTILE: full tiles staged
-// through per-lane offsets computed once (else stage_load's clamped
-// addressing).  PEEL: the last tile peeled off the loop so the next tile's
-// fetch inside it is unconditional (its registers then need no copies across
-// iterations).  In dK/dV both cost registers (up to +24 VGPRs, past an
-// occupancy step at D = 128: C5 dK/dV +20 %), so they are off there.
-#ifndef TTT_DKDV_FULLTILE
-#define TTT_DKDV_FULLTILE 0
-#endif
-// The saved-P dK/dV kernel streams 16-bit D = 64 tiles by direct loads (1) or
-// through registers (0).
-#ifndef TTT_DKDV_DMA
-#define TTT_DKDV_DMA 1
-#endif
-// The same at D = 128 for dO, Q and the rowsum slice, with P staged (1), or
-// all through registers (0).
-#ifndef TTT_DKDV_DMA_WIDE
-#define TTT_DKDV_DMA_WIDE 1
-#endif
-// The recompute dK/dV kernel (16-bit, D = 64) streams dO, Q and its two row
-// statistics by direct loads into two buffer sets (1) or through registers (0).
-#ifndef TTT_DKDV_DMA_RECOMPUTE
-#define TTT_DKDV_DMA_RECOMPUTE 1
-#endif
-#ifndef TTT_DKDV_LATE_FETCH
-#define TTT_DKDV_LATE_FETCH 1
-#endif
-#ifndef TTT_DKDV_PEEL
-#define TTT_DKDV_PEEL 0
-#endif
+// Fetch forms, measured on MI355X and kept:
+//  * 16-bit tiles stream into LDS by direct loads: the saved-P dQ kernel's
+//    key tiles (D = 64: two buffers of one array picked at run time, which
+//    measured 3-12 % faster than two sets in distinct arrays; D = 128: two
+//    sets with compile-time roles), and the recompute dQ kernel's K and V
+//    (D = 64, two sets).
+//  * Register-staged dQ tiles: full tiles through per-lane offsets computed
+//    once (else stage_load's clamped addressing), and the last tile peeled
+//    off the loop so the next tile's fetch inside it is unconditional (its
+//    registers then need no copies across iterations).  In dK/dV both forms
+//    cost registers (up to +24 VGPRs, past an occupancy step at D = 128:
+//    b4 h16 T8192 dK/dV +20 %), so dK/dV stages with clamped addressing and
+//    no peeled tile.
+//  * The saved-P dK/dV kernel streams 16-bit tiles by direct loads into two
+//    buffer sets: dO, Q, P and the rowsum slice at D = 64; dO, Q and the
+//    rowsum slice at D = 128, with P staged through registers.  The
+//    recompute dK/dV kernel (16-bit, D = 64) streams dO, Q and its two row
+//    statistics the same way.
 
 namespace ttt {
 
@@ -110,15 +73,14 @@ __device__ __forceinline__ void frags_to_tile(Tile& p, const typename Elem<T>::f
 // for the D = 64 recompute variants, and for their 16-bit types a cap of 128
 // registers, which keeps four waves per SIMD (the window/bias variant sits
 // right at that boundary; at 132 registers it drops to three, measured
-// TTT_W512_8K dQ 101 -> 113 us).
+// b8 h6 T8192 d64 bf16 local window 512: dQ 101 -> 113 us).
 template <typename T, int D, bool LOADP>
 struct DqWaves {
-  static constexpr bool kVacc = TTT_VACC_BWD_RECOMPUTE && !LOADP && D == 64;
-  // The saved-P 16-bit D = 64 kernel in the two-set form (two tiles per loop
+  static constexpr bool kVacc = !LOADP && D == 64;
+  // The saved-P 16-bit D = 128 kernel in the two-set form (two tiles per loop
   // step): without a register cap the compiler keeps the accumulators in
   // AGPRs and copies them every step.
-  static constexpr bool kPar =
-      TTT_DQ_DMA && LOADP && sizeof(T) == 2 && ((D == 64 && TTT_DQ_PAR) || (D == 128 && TTT_DQ_DMA_WIDE));
+  static constexpr bool kPar = LOADP && sizeof(T) == 2 && D == 128;
   static constexpr int value =
       kVacc ? (sizeof(T) == 2 ? 4 : AccWaves<true>::value) : kPar ? (D == 64 ? 3 : 2) : AccWaves<false>::value;
 };
@@ -134,8 +96,8 @@ __attribute__((amdgpu_waves_per_eu(DqWaves<T, D, LOADP>::value))) void k_bwd_dq(
   // (TileDma): with kPar, two sets in distinct arrays with a compile-time role
   // per loop step (so that the current tile's LDS reads need not wait for the
   // next tile's loads), else two buffers of one array picked at run time.
-  constexpr bool kDma = TTT_DQ_DMA && L::kSwizzle && (LOADP ? (D == 64 || TTT_DQ_DMA_WIDE) : (D == 64 && TTT_DQ_DMA_RECOMPUTE));
-  constexpr bool kPar = kDma && (TTT_DQ_PAR || D == 128 || !LOADP);
+  constexpr bool kDma = L::kSwizzle && (LOADP || D == 64);
+  constexpr bool kPar = kDma && (D == 128 || !LOADP);
   constexpr bool kRt = kDma && !kPar;
   constexpr int kE1 = kPar ? L::kRowElems : 8, kER = kRt ? L::kRowElems : 8;
   __shared__ __align__(16) T sK0[kRt ? 8 : L::kRowElems];
@@ -215,7 +177,7 @@ __attribute__((amdgpu_waves_per_eu(DqWaves<T, D, LOADP>::value))) void k_bwd_dq(
       stage_load<T, D>(stV, V + (int64_t)n1 * a.v.st, a.v.st, T_ - n1, D);
       return;
     }
-    if (TTT_DQ_FULLTILE && n1 + kBlk <= T_) {
+    if (n1 + kBlk <= T_) {
       stage_load_full<T, D>(stK, Kn, soK);
       stage_load_full<T, D>(stV, Vn, soV);
       if constexpr (LOADP) {
@@ -314,7 +276,7 @@ __attribute__((amdgpu_waves_per_eu(DqWaves<T, D, LOADP>::value))) void k_bwd_dq(
     }
     mm_s<T, D>(acc, cK, dsf);
   };
-  if constexpr (kPar && TTT_DQ_PEEL && D == 64) {
+  if constexpr (kPar && D == 64) {
     // Pairs of tiles with unconditional prefetch; the last one or two peeled.
     int nb = cr.t0;
     for (; nb + 2 < cr.t1; nb += 2) {
@@ -332,15 +294,13 @@ __attribute__((amdgpu_waves_per_eu(DqWaves<T, D, LOADP>::value))) void k_bwd_dq(
       tile(nb, Parity<2>{}, Parity<0>{});
       if (nb + 1 < cr.t1) tile(nb + 1, Parity<2>{}, Parity<1>{});
     }
-  } else if constexpr (kRt && TTT_DQ_PEEL) {
+  } else if constexpr (kRt) {
     // The last tile is peeled off the loop, so inside it the next tile's
     // fetch is unconditional and its registers need no copies across
     // iterations.
     for (int nb = cr.t0; nb + 1 < cr.t1; ++nb) tile(nb, Parity<1>{}, RtBuf{(nb - cr.t0) & 1});
     tile(cr.t1 - 1, Parity<0>{}, RtBuf{(cr.t1 - 1 - cr.t0) & 1});
-  } else if constexpr (kRt) {
-    for (int nb = cr.t0; nb < cr.t1; ++nb) tile(nb, Parity<2>{}, RtBuf{(nb - cr.t0) & 1});
-  } else if constexpr (TTT_DQ_PEEL && LOADP) {
+  } else if constexpr (LOADP) {
     for (int nb = cr.t0; nb + 1 < cr.t1; ++nb) tile(nb, Parity<1>{}, Parity<0>{});
     tile(cr.t1 - 1, Parity<0>{}, Parity<0>{});
   } else {
@@ -354,17 +314,12 @@ __attribute__((amdgpu_waves_per_eu(DqWaves<T, D, LOADP>::value))) void k_bwd_dq(
 
 // ---------------------------------------------------------------------------
 // Waves per SIMD the dK/dV kernel is compiled for: recompute at D = 64 caps
-// registers for VGPR accumulators; the saved-P 16-bit D = 64 kernel (direct
-// loads) for TTT_DKDV_WAVES waves.
-#ifndef TTT_DKDV_WAVES
-#define TTT_DKDV_WAVES 3
-#endif
+// registers for VGPR accumulators; the saved-P 16-bit kernels (direct loads)
+// for three waves at D = 64 and two at D = 128.
 template <typename T, int D, bool LOADP, bool DV_ONLY>
 struct DkdvWaves {
-  static constexpr bool kDma =
-      TTT_DKDV_DMA && LOADP && !DV_ONLY && sizeof(T) == 2 && (D == 64 || (D == 128 && TTT_DKDV_DMA_WIDE));
-  static constexpr int value =
-      kDma ? (D == 64 ? TTT_DKDV_WAVES : 2) : AccWaves<TTT_VACC_BWD_RECOMPUTE && !LOADP && D == 64>::value;
+  static constexpr bool kDma = LOADP && !DV_ONLY && sizeof(T) == 2;
+  static constexpr int value = kDma ? (D == 64 ? 3 : 2) : AccWaves<!LOADP && D == 64>::value;
 };
 
 template <typename T, int D, bool LOADP, bool DV_ONLY, bool XM>
@@ -385,13 +340,12 @@ __attribute__((amdgpu_waves_per_eu(DkdvWaves<T, D, LOADP, DV_ONLY>::value))) voi
   // need not wait for the next tile's loads.
   // At D = 128 (kMix) P stays staged through registers into one buffer: two
   // sets of all three tiles would need 80 KB of LDS, one workgroup per CU.
-  constexpr bool kDma = TTT_DKDV_DMA && !DV_ONLY && L::kSwizzle &&
-                        (LOADP ? (D == 64 || TTT_DKDV_DMA_WIDE) : (D == 64 && TTT_DKDV_DMA_RECOMPUTE));
+  constexpr bool kDma = !DV_ONLY && L::kSwizzle && (LOADP || D == 64);
   constexpr bool kMix = kDma && D == 128;
-  // The next tile's loads are issued after this tile's P reads (1) or before
-  // them (0): the compiler waits for outstanding direct loads before one of
+  // The next tile's loads are issued after this tile's P reads: issued before
+  // them, the compiler waits for the outstanding direct loads before one of
   // those transposed reads.
-  constexpr bool kLateFetch = kDma && LOADP && TTT_DKDV_LATE_FETCH;
+  constexpr bool kLateFetch = kDma && LOADP;
   constexpr int kQE = kNeedQ ? L::kRowElems : 8, kPE = LOADP ? LP::kRowElems : 8, kSE = kNS > 0 ? kNS * kBlk : 4;
   __shared__ __align__(16) T sdO0[L::kRowElems];
   __shared__ __align__(16) T sQ0[kQE];
@@ -446,13 +400,11 @@ __attribute__((amdgpu_waves_per_eu(DkdvWaves<T, D, LOADP, DV_ONLY>::value))) voi
 #pragma unroll
   for (int i = 0; i < D / 16; ++i) acc_dv[i] = acc_dk[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Query tiles are fetched in order through running pointers; a full tile
-  // uses offsets computed once, a ragged one clamps (stage_load).
+  // Query tiles are fetched in order through running pointers with clamped
+  // addressing (stage_load).
   Stage<T, D> stdO, stQ;
   Stage<T, kBlk> stP;
   float stv = 0.f;
-  const StageOff<T, D> sodO = stage_offsets<T, D>(a.dout.st), soQ = stage_offsets<T, D>(a.q.st);
-  const StageOff<T, kBlk> soP = stage_offsets<T, kBlk>(LOADP ? a.p.st : 0);
   const int64_t t0r = (int64_t)cr.t0 * kBlk;
   const T* dOn = dO + t0r * a.dout.st;
   const T* Qn = Q + t0r * a.q.st;
@@ -460,15 +412,9 @@ __attribute__((amdgpu_waves_per_eu(DkdvWaves<T, D, LOADP, DV_ONLY>::value))) voi
   const bool cols_full = n0 + kBlk <= T_;
   auto load_tile = [&](int mb) __attribute__((always_inline)) {
     const int m0 = mb * kBlk;
-    if (TTT_DKDV_FULLTILE && m0 + kBlk <= T_ && cols_full) {
-      stage_load_full<T, D>(stdO, dOn, sodO);
-      if constexpr (kNeedQ) stage_load_full<T, D>(stQ, Qn, soQ);
-      if constexpr (LOADP) stage_load_full<T, kBlk>(stP, Pn, soP);
-    } else {
-      stage_load<T, D>(stdO, dOn, a.dout.st, T_ - m0, D);
-      if constexpr (kNeedQ) stage_load<T, D>(stQ, Qn, a.q.st, T_ - m0, D);
-      if constexpr (LOADP) stage_load<T, kBlk>(stP, Pn, a.p.st, T_ - m0, T_ - n0);
-    }
+    stage_load<T, D>(stdO, dOn, a.dout.st, T_ - m0, D);
+    if constexpr (kNeedQ) stage_load<T, D>(stQ, Qn, a.q.st, T_ - m0, D);
+    if constexpr (LOADP) stage_load<T, kBlk>(stP, Pn, a.p.st, T_ - m0, T_ - n0);
     if constexpr (kNS > 0) stv = stat_load<kNS>(DV_ONLY ? lse : rs, lse, nullptr, nullptr, m0, T_ - m0);
     dOn += kBlk * a.dout.st;
     if constexpr (kNeedQ) Qn += kBlk * a.q.st;
@@ -594,14 +540,7 @@ __attribute__((amdgpu_waves_per_eu(DkdvWaves<T, D, LOADP, DV_ONLY>::value))) voi
       if (mb + 1 < cr.t1) tile(mb + 1, Parity<2>{}, Parity<1>{});
     }
   } else {
-#if TTT_DKDV_PEEL
-    // The last tile is peeled off the loop, so inside it the next tile's
-    // fetch is unconditional.
-    for (int mb = cr.t0; mb + 1 < cr.t1; ++mb) tile(mb, Parity<1>{}, Parity<0>{});
-    tile(cr.t1 - 1, Parity<0>{}, Parity<0>{});
-#else
     for (int mb = cr.t0; mb < cr.t1; ++mb) tile(mb, Parity<2>{}, Parity<0>{});
-#endif
   }
   if (cr.nch == 1) {
     store_acc_rows<T, D>(at<T>(a.dv, b, h), a.dv.st, n, T_, acc_dv, 1.f);

@@ -37,15 +37,13 @@ int fail(int code, const char* fmt, ...) {
 // hardware would run the launch: workgroups go to the XCDs round-robin in
 // launch order and, within an XCD, to whichever of its slots frees first.
 // The simulated makespan plus a small per-workgroup cost (partials, combine)
-// is minimised over the chunk length.  TTT_SLOT_FILL is the share (percent)
+// is minimised over the chunk length.  kSlotFill is the share (percent)
 // of the nominal slots (CUs x workgroups per CU from the occupancy
 // calculator) the simulation assumes usable.  The constants were fitted to
 // MI355X sweeps of every kernel family at T = 8192 and 16384, where they pick
 // the measured fastest chunk length.  Without a device (workspace queries on
 // a host with no GPU) the slots default to kFallbackCus x kFallbackPerCu.
-#ifndef TTT_SLOT_FILL
-#define TTT_SLOT_FILL 90
-#endif
+constexpr int kSlotFill = 90;
 constexpr int kXcds = 8;
 constexpr double kWgOverheadTiles = 0.5;   // per workgroup, in tile times
 constexpr double kEmptyWgTiles = 0.05;     // a workgroup whose chunk is empty
@@ -145,7 +143,7 @@ int64_t family_slots(const ttt_problem* pr, int fam, bool load_p) {
   static std::atomic<int> per_cu[16][7][3][2][2][2];
   int dev = 0;
   const int cus = device_cus(&dev);
-  if (cus == 0) return (int64_t)kFallbackCus * kFallbackPerCu * TTT_SLOT_FILL / 100;
+  if (cus == 0) return (int64_t)kFallbackCus * kFallbackPerCu * kSlotFill / 100;
   const int dt = pr->dtype, ds = pr->head_dim == 128 ? 1 : 0, lp = load_p ? 1 : 0;
   const bool xm = has_xm(pr);
   int n = per_cu[dev][fam][dt][ds][lp][xm].load(std::memory_order_relaxed);
@@ -163,7 +161,7 @@ int64_t family_slots(const ttt_problem* pr, int fam, bool load_p) {
     if (n <= 0) n = kFallbackPerCu;
     per_cu[dev][fam][dt][ds][lp][xm].store(n, std::memory_order_relaxed);
   }
-  return std::max<int64_t>(1, (int64_t)cus * n * TTT_SLOT_FILL / 100);
+  return std::max<int64_t>(1, (int64_t)cus * n * kSlotFill / 100);
 }
 
 bool column_family(int fam) { return fam == ttt::kFamDkdv || fam == ttt::kFamGgCol; }
@@ -204,7 +202,7 @@ double simulate_launch(const std::vector<int64_t>& len, int64_t c, int64_t bh, i
   const int64_t nblk = (int64_t)len.size();
   const int64_t lmax = *std::max_element(len.begin(), len.end());
   const int64_t k = (lmax + c - 1) / c;
-  const bool by_slice = TTT_XCD_SLICES && bh % kXcds == 0;
+  const bool by_slice = bh % kXcds == 0;
   double end = 0.0;
   int64_t idx = 0, used = 0;
   for (int64_t y = 0; y < bh; ++y)

@@ -37,18 +37,6 @@
 
 #include <type_traits>
 
-// Tile products read all their LDS fragments before the first MFMA (1), or
-// leave the order to the compiler (0), which tends to pair each read with its
-// MFMA and expose every LDS latency.
-#ifndef TTT_MM_BATCH
-#define TTT_MM_BATCH 1
-#endif
-
-// Chunk-permuted (1) or padded (0) LDS rows for 16-bit types.
-#ifndef TTT_LDS_SWIZZLE
-#define TTT_LDS_SWIZZLE 1
-#endif
-
 namespace ttt {
 
 constexpr int kThreads = 256;  // four wave64s per workgroup
@@ -101,10 +89,7 @@ struct Params {
 // When the slices divide evenly by 8, slice y runs on XCD y % 8, so the tiles
 // the blocks of one slice share are fetched into one XCD's L2 instead of
 // eight; each XCD still takes its slices' blocks in launch order, and the
-// mapping is a bijection of the grid.  TTT_XCD_SLICES=0 keeps the launch order.
-#ifndef TTT_XCD_SLICES
-#define TTT_XCD_SLICES 1
-#endif
+// mapping is a bijection of the grid.
 
 // Where MFMA accumulators live.  A kernel whose register budget is capped at
 // 256 (at least two waves per EU) and whose inline asm names no AGPRs gets
@@ -112,21 +97,11 @@ struct Params {
 // the full 512-register budget the compiler keeps them in AGPRs and copies
 // each one out (v_accvgpr_read) before use.  AccWaves<true> asks for the
 // first, AccWaves<false> leaves the budget open.  Which is faster depends on
-// the kernel variant (measured), so each kernel chooses per variant; the
-// TTT_VACC_* switches below turn a choice off for A/B timing.
+// the kernel variant (measured), so each kernel chooses per variant.
 template <bool VGPR_ACC>
 struct AccWaves {
   static constexpr int value = VGPR_ACC ? 2 : 1;
 };
-#ifndef TTT_VACC_ONLINE
-#define TTT_VACC_ONLINE 1  // forward with online softmax (recompute modes)
-#endif
-#ifndef TTT_VACC_FWD_WIDE
-#define TTT_VACC_FWD_WIDE 1  // statistics and P passes at D = 128, 16-bit types
-#endif
-#ifndef TTT_VACC_BWD_RECOMPUTE
-#define TTT_VACC_BWD_RECOMPUTE 1  // dQ and dK/dV kernels that recompute P, D = 64
-#endif
 
 struct Slot {
   int x, y;
@@ -135,7 +110,7 @@ struct Slot {
 __device__ __forceinline__ Slot grid_slot() {
   Slot s;
   const int gx = gridDim.x, gy = gridDim.y;
-  if (!TTT_XCD_SLICES || (gy & 7) != 0) {
+  if ((gy & 7) != 0) {
     s.x = blockIdx.x;
     s.y = blockIdx.y;
     return s;
@@ -458,13 +433,12 @@ __device__ __forceinline__ typename Elem<T>::frag vals_frag(const float* v) {
 // (an unpadded, unswizzled tile costs 4x / 4x the conflict-free time, a
 // 16-byte row pad 2x / 2x).  swz(r) never depends on bit 2, so rows r and r+4
 // of a transposed read share it.
-// fp32 (and 16-bit types when TTT_LDS_SWIZZLE is 0): rows padded by one
-// 16-byte chunk, no permutation.
+// fp32: rows padded by one 16-byte chunk, no permutation.
 // ---------------------------------------------------------------------------
 template <typename T, int NCOL>
 struct Lds {
   static constexpr int kChunk = Elem<T>::kChunk;
-  static constexpr bool kSwizzle = TTT_LDS_SWIZZLE && sizeof(T) == 2;
+  static constexpr bool kSwizzle = sizeof(T) == 2;
   static constexpr int kChunksPerRow = NCOL / kChunk;
   static_assert(!kSwizzle || kChunksPerRow == 8 || kChunksPerRow == 16, "swizzled rows are 128 or 256 bytes");
   static constexpr int kRowPitch = kSwizzle ? NCOL : NCOL + kChunk;
@@ -694,7 +668,7 @@ __device__ __forceinline__ void mm_d(Tile& out, const T* rows, const typename El
   typedef typename Elem<T>::frag frag;
   const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
   constexpr int KS = D / 32;
-  constexpr int AB = (TTT_MM_BATCH && sizeof(T) == 2) ? (KS <= 2 ? 4 : 2) : 1;  // subtiles per batch
+  constexpr int AB = (sizeof(T) == 2) ? (KS <= 2 ? 4 : 2) : 1;  // subtiles per batch
 #pragma unroll
   for (int a0 = 0; a0 < 4; a0 += AB) {
     frag x[AB][KS];
@@ -713,7 +687,7 @@ __device__ __forceinline__ void mm_d(Tile& out, const T* rows, const typename El
 template <typename T, int D>
 __device__ __forceinline__ void mm_s(f32x4* acc, const T* X, const typename Elem<T>::frag* y) {
   typedef typename Elem<T>::frag frag;
-  constexpr int NB = (TTT_MM_BATCH && sizeof(T) == 2) ? 8 : 1;  // fragments per batch
+  constexpr int NB = (sizeof(T) == 2) ? 8 : 1;  // fragments per batch
   constexpr int DSN = D / 16;
 #pragma unroll
   for (int i0 = 0; i0 < 2 * DSN; i0 += NB) {
@@ -735,7 +709,7 @@ template <typename T, int D>
 __device__ __forceinline__ void mm_s2(f32x4* acc0, const typename Elem<T>::frag* y0, f32x4* acc1,
                                       const typename Elem<T>::frag* y1, const T* X) {
   typedef typename Elem<T>::frag frag;
-  constexpr int NB = (TTT_MM_BATCH && sizeof(T) == 2) ? 8 : 1;
+  constexpr int NB = (sizeof(T) == 2) ? 8 : 1;
   constexpr int DSN = D / 16;
 #pragma unroll
   for (int i0 = 0; i0 < 2 * DSN; i0 += NB) {
@@ -757,7 +731,7 @@ __device__ __forceinline__ void mm_s3(f32x4* acc0, const typename Elem<T>::frag*
                                       const typename Elem<T>::frag* y1, f32x4* acc2,
                                       const typename Elem<T>::frag* y2, const T* X) {
   typedef typename Elem<T>::frag frag;
-  constexpr int NB = (TTT_MM_BATCH && sizeof(T) == 2) ? 8 : 1;
+  constexpr int NB = (sizeof(T) == 2) ? 8 : 1;
   constexpr int DSN = D / 16;
 #pragma unroll
   for (int i0 = 0; i0 < 2 * DSN; i0 += NB) {
@@ -791,7 +765,7 @@ __device__ __forceinline__ void mm_d_half(Tile& out, int kb, const T* rows, cons
   for (int a = 0; a < 2; ++a)
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) x[a][ks] = load_frag<T>(rows + L::off(sigma(2 * kb + a, c), 32 * ks + 8 * g));
-  if constexpr (TTT_MM_BATCH && sizeof(T) == 2) __builtin_amdgcn_sched_barrier(0);
+  if constexpr (sizeof(T) == 2) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int a = 0; a < 2; ++a)
 #pragma unroll
@@ -812,7 +786,7 @@ __device__ __forceinline__ void mm_d2_half(Tile& out0, Tile& out1, int kb, const
   for (int a = 0; a < 2; ++a)
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) x[a][ks] = load_frag<T>(rows + L::off(sigma(2 * kb + a, c), 32 * ks + 8 * g));
-  if constexpr (TTT_MM_BATCH && sizeof(T) == 2) __builtin_amdgcn_sched_barrier(0);
+  if constexpr (sizeof(T) == 2) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int a = 0; a < 2; ++a)
 #pragma unroll
@@ -829,7 +803,7 @@ __device__ __forceinline__ void mm_s_half(f32x4* acc, int kb, const T* X, typena
   frag x[DSN];
 #pragma unroll
   for (int ds = 0; ds < DSN; ++ds) x[ds] = load_frag_tr<T, D>(X, 32 * kb, 16 * ds);
-  if constexpr (TTT_MM_BATCH && sizeof(T) == 2) __builtin_amdgcn_sched_barrier(0);
+  if constexpr (sizeof(T) == 2) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int ds = 0; ds < DSN; ++ds) acc[ds] = Elem<T>::mma(acc[ds], x[ds], y);
 }
@@ -919,10 +893,6 @@ __device__ __forceinline__ void stat_read8(float* v, const float* lds, int st, i
 // ---------------------------------------------------------------------------
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-// Interior tiles through the buffer form (1) or the global form (0).
-#ifndef TTT_DMA_BUF
-#define TTT_DMA_BUF 1
-#endif
 // Word 3 of a raw buffer resource on gfx9-family parts (gfx950): 32-bit
 // data format, no swizzle, no index stride.
 constexpr int kBufWord3 = 0x00020000;
@@ -970,10 +940,7 @@ struct TileDma {  // for the unpadded (chunk-permuted) layout only: Lds<T, NCOL>
   // fresh register whose reuse soon after the load makes the compiler wait
   // for the load to complete).  The resource does no range checking.
   __device__ __forceinline__ void load_full(T* lds, const T* g, const int* off) const {
-#if defined(__HIP_DEVICE_COMPILE__) && !TTT_DMA_BUF
-#pragma unroll
-    for (int q = 0; q < kPerWave; ++q) issue(lds, g, off[q], q);
-#elif defined(__HIP_DEVICE_COMPILE__)
+#if defined(__HIP_DEVICE_COMPILE__)
     const __amdgpu_buffer_rsrc_t r =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(g), (short)0, (int)0xFFFFFFFF, kBufWord3);
 #pragma unroll

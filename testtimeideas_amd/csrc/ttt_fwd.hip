@@ -29,46 +29,20 @@
 #include "ttt_common.h"
 #include "ttt_launch.h"
 
-// Tiles of K and V a forward kernel loads ahead of the one it computes
-// (measured on MI355X: 2 and 3 were no faster than 1).
-// Full key tiles are staged through per-lane offsets computed once (1) or
-// through stage_load's clamped addressing like ragged tiles (0).
-// The P pass without a window or bias computes P from raw scores with the
-// scale folded into the exponent's FMA and packs it to T once (1), or goes
-// through the scaled, masked score tile (0).
-// The statistics pass without a window or bias keeps its running max and sum
-// in raw-score units, the scale folded into the exponent's FMA (1), or
-// scales every score first (0).
-#ifndef TTT_FWD_STATS_FUSED
-#define TTT_FWD_STATS_FUSED 1
-#endif
-#ifndef TTT_FWD_P_FUSED
-#define TTT_FWD_P_FUSED 1
-#endif
-// The forward kernels (statistics pass, P pass, online) stream 16-bit D = 64
-// key/value tiles by direct loads (1) or through registers (0).
-#ifndef TTT_FWD_DMA
-#define TTT_FWD_DMA 1
-#endif
-// The statistics and P passes do the same at D = 128 (1) or not (0).
-#ifndef TTT_FWD_DMA_WIDE
-#define TTT_FWD_DMA_WIDE 1
-#endif
-#ifndef TTT_FWD_FULLTILE
-#define TTT_FWD_FULLTILE 1
-#endif
-#ifndef TTT_FWD_PREFETCH
-#define TTT_FWD_PREFETCH 1
-#endif
-// Key tiles per barrier round of the statistics pass and of the P pass
-// (measured on MI355X: two make the statistics pass 3 us faster at C3 and
-// leave C5 unchanged; the P pass is slower with two).
-#ifndef TTT_FWD_STATS_TILES
-#define TTT_FWD_STATS_TILES 2
-#endif
-#ifndef TTT_FWD_P_TILES
-#define TTT_FWD_P_TILES 1
-#endif
+// Measured on MI355X and kept:
+//  * 16-bit tiles stream into LDS by direct loads, into two buffer sets with
+//    a compile-time role per loop step (the online pass at D = 64; the
+//    statistics and P passes at D = 64 and 128); fp32 tiles are staged
+//    through registers, one tile ahead (deeper prefetch was no faster).
+//  * Full D = 64 key tiles staged through registers use per-lane offsets
+//    computed once; ragged tiles clamp their rows.
+//  * Without a window or bias, the statistics pass keeps its running max and
+//    sum in raw-score units and the P pass computes P = exp2(raw*c - lse)
+//    with the scale c = s*log2(e) folded into one FMA per element, packing P
+//    to T once for both the MFMA fragment and the store.
+//  * The statistics pass takes two key tiles per barrier round (3 us faster
+//    at b1 h1 T8192 d64, no change at b4 h16 T8192 d128); the P pass takes
+//    one (two were slower).
 
 namespace ttt {
 
@@ -133,14 +107,14 @@ __device__ __forceinline__ float tile_max(const Tile& s) {
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool XM>
 __global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_ONLINE>::value))) void k_fwd_online(Params a) {
+__attribute__((amdgpu_waves_per_eu(AccWaves<true>::value))) void k_fwd_online(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
   // 16-bit D = 64 tiles stream straight into two LDS buffer sets (TileDma) in
   // distinct arrays with a compile-time role per loop step; the rest stage
   // them through registers.
-  constexpr bool kDma = TTT_FWD_DMA && L::kSwizzle && sizeof(T) == 2 && D == 64;
+  constexpr bool kDma = L::kSwizzle && D == 64;
   __shared__ __align__(16) T sK[L::kRowElems];
   __shared__ __align__(16) T sV[L::kRowElems];
   __shared__ __align__(16) T sK1[kDma ? L::kRowElems : 8];
@@ -173,21 +147,20 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_ONLINE>::value))) void k_fw
   for (int i = 0; i < D / 16; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   float mx = -INFINITY, l = 0.f;
 
-  // Register stages for the next kPre tiles' K and V (loads issued kPre
-  // tiles ahead of their use).
-  constexpr int kPre = kDma ? 1 : TTT_FWD_PREFETCH;
-  Stage<T, D> stK[kPre], stV[kPre];
+  // Register stage of the next tile's K and V (loads issued one tile ahead
+  // of their use).
+  Stage<T, D> stK, stV;
   const StageOff<T, D> soK = stage_offsets<T, D>(a.k.st), soV = stage_offsets<T, D>(a.v.st);
-  auto load_kv = [&](int nb, Stage<T, D>& sk, Stage<T, D>& sv) __attribute__((always_inline)) {
+  auto load_kv = [&](int nb) __attribute__((always_inline)) {
     const int n1 = nb * kBlk;
     const T* kp = K + (int64_t)n1 * a.k.st;
     const T* vp = V + (int64_t)n1 * a.v.st;
-    if (TTT_FWD_FULLTILE && D == 64 && n1 + kBlk <= T_) {  // full tile: offsets computed once
-      stage_load_full<T, D>(sk, kp, soK);
-      stage_load_full<T, D>(sv, vp, soV);
+    if (D == 64 && n1 + kBlk <= T_) {  // full tile: offsets computed once
+      stage_load_full<T, D>(stK, kp, soK);
+      stage_load_full<T, D>(stV, vp, soV);
     } else {
-      stage_load<T, D>(sk, kp, a.k.st, T_ - n1, D);
-      stage_load<T, D>(sv, vp, a.v.st, T_ - n1, D);
+      stage_load<T, D>(stK, kp, a.k.st, T_ - n1, D);
+      stage_load<T, D>(stV, vp, a.v.st, T_ - n1, D);
     }
   };
   // Key tile nb from LDS tiles cK, cV.
@@ -256,21 +229,14 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_ONLINE>::value))) void k_fw
       if (nb + 1 < cr.t1) step(Parity<1>{}, nb + 1);
     }
   } else {
-#pragma unroll
-    for (int i = 0; i < kPre; ++i)
-      if (i == 0 || cr.t0 + i < cr.t1) load_kv(cr.t0 + i, stK[i], stV[i]);
-    auto tile = [&](int nb, Stage<T, D>& sk, Stage<T, D>& sv) __attribute__((always_inline)) {
+    load_kv(cr.t0);
+    for (int nb = cr.t0; nb < cr.t1; ++nb) {
       __syncthreads();
-      stage_store_rows<T, D>(sk, sK);
-      stage_store_rows<T, D>(sv, sV);
+      stage_store_rows<T, D>(stK, sK);
+      stage_store_rows<T, D>(stV, sV);
       __syncthreads();
-      if (nb + kPre < cr.t1) load_kv(nb + kPre, sk, sv);
+      if (nb + 1 < cr.t1) load_kv(nb + 1);
       body(nb, sK, sV);
-    };
-    for (int nb = cr.t0; nb < cr.t1; nb += kPre) {
-#pragma unroll
-      for (int i = 0; i < kPre; ++i)
-        if (i == 0 || nb + i < cr.t1) tile(nb + i, stK[i], stV[i]);
     }
   }
 
@@ -295,9 +261,7 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<TTT_VACC_ONLINE>::value))) void k_fw
 // keep their MFMA results in AGPRs and copy them every step.
 template <typename T, int D>
 struct FwdPWaves {
-  static constexpr bool kDma = TTT_FWD_DMA && sizeof(T) == 2 && (D == 64 || TTT_FWD_DMA_WIDE);
-  static constexpr int value =
-      kDma ? (D == 64 ? 3 : 2) : AccWaves<TTT_VACC_FWD_WIDE && D == 128 && sizeof(T) == 2>::value;
+  static constexpr int value = sizeof(T) == 2 ? (D == 64 ? 3 : 2) : AccWaves<false>::value;
 };
 
 template <typename T, int D, bool XM>
@@ -308,10 +272,10 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_stats(Pa
   typedef Lds<T, D> L;
   // R key tiles per round: one pair of barriers and R independent score
   // products per round.
-  constexpr int R = TTT_FWD_STATS_TILES;
-  // 16-bit D = 64: the R tiles of a round stream straight into LDS (TileDma),
+  constexpr int R = 2;
+  // 16-bit types: the R tiles of a round stream straight into LDS (TileDma),
   // alternating between two sets in distinct arrays with compile-time roles.
-  constexpr bool kDma = TTT_FWD_DMA && L::kSwizzle && sizeof(T) == 2 && (D == 64 || TTT_FWD_DMA_WIDE);
+  constexpr bool kDma = L::kSwizzle;
   __shared__ __align__(16) T sK[R][L::kRowElems];
   __shared__ __align__(16) T sK1[R][kDma ? L::kRowElems : 8];
 
@@ -346,7 +310,7 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_stats(Pa
   auto load_k = [&](int nb, Stage<T, D>& sk) __attribute__((always_inline)) {
     const int n1 = (nb < cr.t1 ? nb : cr.t1 - 1) * kBlk;
     const T* kp = K + (int64_t)n1 * a.k.st;
-    if (TTT_FWD_FULLTILE && D == 64 && n1 + kBlk <= T_)  // full tile: offsets computed once
+    if (D == 64 && n1 + kBlk <= T_)  // full tile: offsets computed once
       stage_load_full<T, D>(sk, kp, soK);
     else
       stage_load<T, D>(sk, kp, a.k.st, T_ - n1, D);
@@ -354,7 +318,7 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_stats(Pa
   // One round: key tiles nb .. nb + R - 1 from the LDS tiles tile_k(i).
   auto round = [&](int nb, auto tile_k) __attribute__((always_inline)) {
       Tile s[R];
-      if constexpr (!XM && TTT_FWD_STATS_FUSED) {
+      if constexpr (!XM) {
         if (raw_units) {
           // Max and sum in raw-score units: exp2(raw * csl - max * csl) with the
           // scale csl = scale*log2e > 0 folded into one FMA per element.
@@ -472,7 +436,7 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_stats(Pa
       round(nb, [&](int i) -> const T* { return sK[i]; });
     }
   }
-  if (!XM && TTT_FWD_STATS_FUSED && raw_units && mx != -INFINITY) mx *= csl;  // back to base-2 units
+  if (!XM && raw_units && mx != -INFINITY) mx *= csl;  // back to base-2 units
   {
     // Finite without a window (every row sees a key of its first tile); with
     // one a chunk can miss all of a row's keys, and then max -inf, sum 0.
@@ -498,15 +462,12 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_p(Params
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
-  // R key tiles per barrier round (as in k_fwd_stats).
-  constexpr int R = TTT_FWD_P_TILES;
-  // 16-bit D = 64 tiles stream straight into two LDS buffer sets (TileDma) in
+  // 16-bit tiles stream straight into two LDS buffer sets (TileDma) in
   // distinct arrays with a compile-time role per loop step, one tile per
-  // barrier round; the rest stage R tiles per round through registers.
-  constexpr bool kDma = TTT_FWD_DMA && L::kSwizzle && sizeof(T) == 2 && (D == 64 || TTT_FWD_DMA_WIDE);
-  constexpr int kR = kDma ? 1 : R;
-  __shared__ __align__(16) T sK[kR][L::kRowElems];
-  __shared__ __align__(16) T sV[kR][L::kRowElems];
+  // barrier round; fp32 tiles are staged through registers.
+  constexpr bool kDma = L::kSwizzle;
+  __shared__ __align__(16) T sK[L::kRowElems];
+  __shared__ __align__(16) T sV[L::kRowElems];
   __shared__ __align__(16) T sK1[kDma ? L::kRowElems : 8];
   __shared__ __align__(16) T sV1[kDma ? L::kRowElems : 8];
 
@@ -553,27 +514,25 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_p(Params
 #pragma unroll
   for (int i = 0; i < D / 16; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  Stage<T, D> stK[kR], stV[kR];
-  // Tiles past the chunk load its last tile again (unconditional loads); their
-  // P is neither stored nor accumulated.
+  Stage<T, D> stK, stV;
   const StageOff<T, D> soK = stage_offsets<T, D>(a.k.st), soV = stage_offsets<T, D>(a.v.st);
-  auto load_kv = [&](int nb, Stage<T, D>& sk, Stage<T, D>& sv) __attribute__((always_inline)) {
-    const int n1 = (nb < cr.t1 ? nb : cr.t1 - 1) * kBlk;
+  auto load_kv = [&](int nb) __attribute__((always_inline)) {
+    const int n1 = nb * kBlk;
     const T* kp = K + (int64_t)n1 * a.k.st;
     const T* vp = V + (int64_t)n1 * a.v.st;
-    if (TTT_FWD_FULLTILE && D == 64 && n1 + kBlk <= T_) {  // full tile: offsets computed once
-      stage_load_full<T, D>(sk, kp, soK);
-      stage_load_full<T, D>(sv, vp, soV);
+    if (D == 64 && n1 + kBlk <= T_) {  // full tile: offsets computed once
+      stage_load_full<T, D>(stK, kp, soK);
+      stage_load_full<T, D>(stV, vp, soV);
     } else {
-      stage_load<T, D>(sk, kp, a.k.st, T_ - n1, D);
-      stage_load<T, D>(sv, vp, a.v.st, T_ - n1, D);
+      stage_load<T, D>(stK, kp, a.k.st, T_ - n1, D);
+      stage_load<T, D>(stV, vp, a.v.st, T_ - n1, D);
     }
   };
-  // Key tile `nt` from LDS tiles cK, cV (`valid`: inside the chunk).
-  auto body = [&](int nt, const T* cK, const T* cV, bool valid) __attribute__((always_inline)) {
+  // Key tile `nt` from LDS tiles cK, cV.
+  auto body = [&](int nt, const T* cK, const T* cV) __attribute__((always_inline)) {
       const int n0 = nt * kBlk;
       frag pf[2];
-      if constexpr (!XM && sizeof(T) == 2 && TTT_FWD_P_FUSED) {
+      if constexpr (!XM && sizeof(T) == 2) {
         // Raw scores; P = exp2(raw * scale*log2e - lse) in one FMA, masked
         // entries selected to 0 afterwards, and one rounding to T gives both
         // the MFMA fragment and the stored P.
@@ -585,13 +544,13 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_p(Params
         for (int kb = 0; kb < 2; ++kb) {
           float pv[8];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) pv[j] = valid ? fast_exp2(fmaf(s.at(kb, j), a.scale_log2, -lse2)) : 0.f;
+          for (int j = 0; j < 8; ++j) pv[j] = fast_exp2(fmaf(s.at(kb, j), a.scale_log2, -lse2));
           if (need_mask) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) pv[j] = mk.masked(n0 + stream_index(kb, g, j)) ? 0.f : pv[j];
           }
           pf[kb] = vals_frag<T>(pv);
-          if (valid && m < T_) {
+          if (m < T_) {
             const int n = n0 + stream_index(kb, g, 0);
             if (n + 8 <= T_) {
               store_frag_g<T>(Pm + n, pf[kb]);
@@ -617,9 +576,9 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_p(Params
         for (int kb = 0; kb < 2; ++kb) {
           float pv[8];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) pv[j] = valid ? E::f32(E::cvt(fast_exp2(s.at(kb, j) - lse2))) : 0.f;
+          for (int j = 0; j < 8; ++j) pv[j] = E::f32(E::cvt(fast_exp2(s.at(kb, j) - lse2)));
           pf[kb] = vals_frag<T>(pv);
-          if (valid && m < T_) {
+          if (m < T_) {
             const int n = n0 + stream_index(kb, g, 0);
             if (n + 8 <= T_) {
               store8<T>(Pm + n, pv);
@@ -660,35 +619,27 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_p(Params
         if constexpr (P == 0)
           fetch(nt + 1, sK1, sV1);
         else
-          fetch(nt + 1, sK[0], sV[0]);
+          fetch(nt + 1, sK, sV);
       }
       if constexpr (P == 0)
-        body(nt, sK[0], sV[0], true);
+        body(nt, sK, sV);
       else
-        body(nt, sK1, sV1, true);
+        body(nt, sK1, sV1);
     };
-    fetch(cr.t0, sK[0], sV[0]);
+    fetch(cr.t0, sK, sV);
     for (int nb = cr.t0; nb < cr.t1; nb += 2) {
       step(Parity<0>{}, nb);
       if (nb + 1 < cr.t1) step(Parity<1>{}, nb + 1);
     }
   } else {
-#pragma unroll
-    for (int i = 0; i < kR; ++i) load_kv(cr.t0 + i, stK[i], stV[i]);
-    for (int nb = cr.t0; nb < cr.t1; nb += kR) {
+    load_kv(cr.t0);
+    for (int nb = cr.t0; nb < cr.t1; ++nb) {
       __syncthreads();
-#pragma unroll
-      for (int i = 0; i < kR; ++i) {
-        stage_store_rows<T, D>(stK[i], sK[i]);
-        stage_store_rows<T, D>(stV[i], sV[i]);
-      }
+      stage_store_rows<T, D>(stK, sK);
+      stage_store_rows<T, D>(stV, sV);
       __syncthreads();
-      if (nb + kR < cr.t1) {
-#pragma unroll
-        for (int i = 0; i < kR; ++i) load_kv(nb + kR + i, stK[i], stV[i]);
-      }
-#pragma unroll
-      for (int i = 0; i < kR; ++i) body(nb + i, sK[i], sV[i], i == 0 || nb + i < cr.t1);
+      if (nb + 1 < cr.t1) load_kv(nb + 1);
+      body(nb, sK, sV);
     }
   }
   if (cr.nch == 1) {

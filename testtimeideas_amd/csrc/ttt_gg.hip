@@ -70,65 +70,38 @@ static_assert(TTT_GG_HEAD_DIM == 64 || TTT_GG_HEAD_DIM == 128, "head dim of this
 // limited to 512 / this per lane): two at D = 64 (16-bit types; and fp32 in
 // the column kernel, whose few spills cost less than half the waves), one
 // otherwise, where two spill heavily (fp32 fragments take twice the
-// registers, D = 128 twice the accumulators).  Measured on MI355X: C5 (bf16,
-// D = 128) grad-grad 43.8 -> 14.9 ms, fp32 D = 64 row pass 352 -> 268 us.
-#ifndef TTT_GG_WAVES_PER_EU
-#define TTT_GG_WAVES_PER_EU 2
-#endif
-#ifndef TTT_GG_COL_WAVES_PER_EU
-#define TTT_GG_COL_WAVES_PER_EU TTT_GG_WAVES_PER_EU
-#endif
-// The stationary Q, gQ (row pass) and K, gK (column pass) fragments are
-// scaled by s once (1), so the score products come out in units of s and the
-// per-element multiplications by s drop out, or not (0).
-#ifndef TTT_GG_PRESCALE
-#define TTT_GG_PRESCALE 1
-#endif
-// Row sums X = rowsum(Z1) and D = rowsum(Z2) in the row kernel for 16-bit
-// types: by MFMA against a ones fragment from the Z1, Z2 fragments the
-// products already use (1), or by VALU adds of the fp32 values (0).  The
-// MFMA form takes four MFMAs per tile for 32 adds, and sums the same rounded
-// values that the products with K consume.
-#ifndef TTT_GG_MFMA_ROWSUM
-#define TTT_GG_MFMA_ROWSUM 1
-#endif
-// The row kernel (TTT_GG_ROW_DMA_WIDE) and the column kernel
-// (TTT_GG_COL_DMA_WIDE) stream 16-bit D = 128 tiles by direct loads too (1),
-// or through registers (0).
-#ifndef TTT_GG_ROW_DMA_WIDE
-#define TTT_GG_ROW_DMA_WIDE 1
-#endif
-// The row kernel at D = 64 without GdO uses the two-set form too (1) or
-// run-time-picked buffers of one array per operand (0).  The compiler cannot
-// tell the two buffers of one array apart, so with run-time buffers it waits
-// for the next tile's direct loads before the current tile's first LDS read.
-// (The GdO variants keep run-time buffers: they spill in the two-set form.)
-#ifndef TTT_GG_ROW_PAR64
-#define TTT_GG_ROW_PAR64 1
-#endif
-#ifndef TTT_GG_COL_DMA_WIDE
-#define TTT_GG_COL_DMA_WIDE 1
-#endif
-// Products that stream the same LDS tile read each fragment once (1) or
-// once per product (0).
-#ifndef TTT_GG_SHARED_READS
-#define TTT_GG_SHARED_READS 1
-#endif
-#ifndef TTT_GG_WIDE_WAVES_PER_EU
-#define TTT_GG_WIDE_WAVES_PER_EU 1
-#endif
+// registers, D = 128 twice the accumulators).  Measured on MI355X: b4 h16
+// T8192 d128 bf16 grad-grad 43.8 -> 14.9 ms, fp32 D = 64 row pass
+// 352 -> 268 us.
+//
+// Also measured and kept:
+//  * The stationary Q, gQ (row pass) and K, gK (column pass) fragments are
+//    scaled by s once, so the score products come out in units of s and the
+//    per-element multiplications by s drop out.
+//  * Row sums X = rowsum(Z1) and D = rowsum(Z2) in the row kernel for 16-bit
+//    types without GdO by MFMA against a ones fragment, from the Z1, Z2
+//    fragments the products already use: four MFMAs per tile for 32 adds,
+//    summing the same rounded values that the products with K consume (the
+//    GdO variants spill with it and add on the VALU).
+//  * 16-bit tiles stream into LDS by direct loads (at D = 64 and 128), into
+//    two buffer sets in distinct arrays with compile-time roles (the compiler
+//    cannot tell two buffers of one array apart, and waits for the next
+//    tile's loads before the current tile's first LDS read); the row kernel's
+//    GdO variants at D = 64 keep run-time-picked buffers, since they spill in
+//    the two-set form.
+//  * Products that stream the same LDS tile read each fragment once.
 
 namespace ttt {
 
-template <typename T, int D, int NARROW, bool COL>
+template <typename T, int D, bool COL>
 struct GgWaves {
-  static constexpr int value = ((sizeof(T) == 2 || COL) && D == 64) ? NARROW : TTT_GG_WIDE_WAVES_PER_EU;
+  static constexpr int value = ((sizeof(T) == 2 || COL) && D == 64) ? 2 : 1;
 };
 
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool LOADP, bool GDO, bool XM>
 __global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::value))) void k_gg_row(Params a) {
+__attribute__((amdgpu_waves_per_eu(GgWaves<T, D, false>::value))) void k_gg_row(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
@@ -138,7 +111,7 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
   // that the current tile's LDS reads need not wait for the next tile's loads;
   // the D = 64 GdO variants into two buffers of one array per operand, picked
   // at run time.  The rest stage tiles through registers into one buffer.
-  constexpr bool kPar = L::kSwizzle && ((D == 128 && TTT_GG_ROW_DMA_WIDE) || (D == 64 && TTT_GG_ROW_PAR64 && !GDO));
+  constexpr bool kPar = L::kSwizzle && (D == 128 || !GDO);
   constexpr bool kDma = L::kSwizzle && D == 64 && !kPar;
   constexpr int kBuf = kDma ? 2 : 1;
   constexpr int kE = kPar ? 8 : L::kRowElems;  // the run-time-indexed arrays (unused with kPar)
@@ -186,7 +159,7 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
   for (int ks = 0; ks < D / 32; ++ks) {
     qf[ks] = load_frag_row<T>(Q, a.q.st, m, T_, 32 * ks + 8 * g);
     gqf[ks] = load_frag_row<T>(gQ, a.gq.st, m, T_, 32 * ks + 8 * g);
-    if constexpr (TTT_GG_PRESCALE) {
+    {
       qf[ks] = scale_frag<T>(qf[ks], a.scale);
       gqf[ks] = scale_frag<T>(gqf[ks], a.scale);
     }
@@ -197,7 +170,7 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
   const float lse2 = (!LOADP && row_ok) ? a.lse[ridx] * kLog2e : 0.f;
   const T* Pm = LOADP ? at<const T>(a.p, b, h) + (int64_t)(row_ok ? m : 0) * a.p.st : nullptr;
   const float s = a.scale;
-  const float kSl2 = TTT_GG_PRESCALE ? kLog2e : a.scale_log2;  // raw score -> base 2
+  const float kSl2 = kLog2e;  // raw score (in units of s) -> base 2
 
   f32x4 a1[D / 16], a2[D / 16], a3[D / 16], a4[D / 16];
   f32x4 b1[GDO ? D / 16 : 1], b2[GDO ? D / 16 : 1], b3[GDO ? D / 16 : 1];
@@ -209,7 +182,7 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
   float e_acc = 0.f, x_acc = 0.f, d_acc = 0.f;
   // MFMA row sums: lane (c, g) of ones x Z holds rowsum(Z) of stationary row
   // c in all four accumulator slots.
-  constexpr bool kMfmaSums = TTT_GG_MFMA_ROWSUM && sizeof(T) == 2 && !GDO;  // GdO variants spill with it
+  constexpr bool kMfmaSums = sizeof(T) == 2 && !GDO;  // GdO variants spill with it
   f32x4 xs4 = f32x4{0.f, 0.f, 0.f, 0.f}, ds4 = f32x4{0.f, 0.f, 0.f, 0.f};
   frag ones;
   {
@@ -302,7 +275,7 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float P = p.at(kb, j);
-        const float gd = TTT_GG_PRESCALE ? gds.at(kb, j) : s * gds.at(kb, j);
+        const float gd = gds.at(kb, j);
         const float dpv = dp.at(kb, j);
         const float z2 = P * dpv;
         const float ds = z2 - P * Dm;  // P o (dP - D)
@@ -328,13 +301,7 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
       if constexpr (GDO) z4f[kb] = vals_frag<T>(vz4);
     }
     mm_s<T, D>(a1, cgK, dsf);
-#if TTT_GG_SHARED_READS
     mm_s3<T, D>(a2, z1f, a3, z2f, a4, pf, cK);
-#else
-    mm_s<T, D>(a2, cK, z1f);
-    mm_s<T, D>(a3, cK, z2f);
-    mm_s<T, D>(a4, cK, pf);
-#endif
     if constexpr (GDO) {
       mm_s<T, D>(b1, cgV, pf);
       mm_s2<T, D>(b2, z4f, b3, pf, cV);
@@ -478,7 +445,7 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_WAVES_PER_EU, false>::va
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool LOADP, bool XM>
 __global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_COL_WAVES_PER_EU, true>::value))) void k_gg_col(Params a) {
+__attribute__((amdgpu_waves_per_eu(GgWaves<T, D, true>::value))) void k_gg_col(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
@@ -486,7 +453,7 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_COL_WAVES_PER_EU, true>:
   // 16-bit types at D = 64 stream tiles straight into two LDS buffers
   // (TileDma), set 0 and set 1, in distinct arrays with a compile-time role per
   // loop step; the rest stage them through registers into set 0.
-  constexpr bool kDma = L::kSwizzle && (D == 64 || TTT_GG_COL_DMA_WIDE);
+  constexpr bool kDma = L::kSwizzle;
   constexpr int kNS = LOADP ? 3 : 4;  // staged row statistics: D, E, F, then lse (recompute)
   constexpr int kE1 = kDma ? L::kRowElems : 8;
   constexpr int kP0 = LOADP ? LP::kRowElems : 8, kP1 = (LOADP && kDma) ? LP::kRowElems : 8;
@@ -539,14 +506,14 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_COL_WAVES_PER_EU, true>:
   const float* fv = a.f + (int64_t)bh * T_;
   const float* lse = LOADP ? nullptr : a.lse + (int64_t)bh * T_;
   const float s = a.scale;
-  const float kSl2 = TTT_GG_PRESCALE ? kLog2e : a.scale_log2;  // raw score -> base 2
+  const float kSl2 = kLog2e;  // raw score (in units of s) -> base 2
 
   frag kf[D / 32], gkf[D / 32], vf[D / 32], gvf[D / 32];
 #pragma unroll
   for (int ks = 0; ks < D / 32; ++ks) {
     kf[ks] = load_frag_row<T>(K, a.k.st, n, T_, 32 * ks + 8 * g);
     gkf[ks] = load_frag_row<T>(gK, a.gk.st, n, T_, 32 * ks + 8 * g);
-    if constexpr (TTT_GG_PRESCALE) {
+    {
       kf[ks] = scale_frag<T>(kf[ks], a.scale);
       gkf[ks] = scale_frag<T>(gkf[ks], a.scale);
     }
@@ -588,12 +555,7 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_COL_WAVES_PER_EU, true>:
     // elementwise terms, then its contributions to GK and GV.
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-#if TTT_GG_SHARED_READS
       mm_d2_half<T, D>(dp, gp1, kb, cb.dout, vf, gvf);
-#else
-      mm_d_half<T, D>(dp, kb, cb.dout, vf);
-      mm_d_half<T, D>(gp1, kb, cb.dout, gvf);
-#endif
       mm_d_half<T, D>(gds, kb, cb.gq, kf);
       mm_d_half<T, D>(gds, kb, cb.q, gkf);
       float d8[8], e8[8], f8[8];
@@ -605,7 +567,7 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, TTT_GG_COL_WAVES_PER_EU, true>:
       for (int j = 0; j < 8; ++j) {
         const float P = p.at(kb, j);
         const float dpv = dp.at(kb, j);
-        const float gd = TTT_GG_PRESCALE ? gds.at(kb, j) : s * gds.at(kb, j);
+        const float gd = gds.at(kb, j);
         const float dmd = dpv - d8[j];
         const float gp = gp1.at(kb, j) + gd * dmd - e8[j] * dpv;
         vds[j] = P * dmd;

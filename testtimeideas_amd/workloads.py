@@ -58,6 +58,8 @@ CONFIGS: Dict[str, Config] = {
     "C1": Config("C1", 1, 1, 64, 64, "fp32", False),
     "C2": Config("C2", 2, 4, 2048, 128, "fp16", False, gradgrad=False, bwd_mode="save_p"),
     "C3": Config("C3", 1, 1, 8192, 64, "fp16", True),
+    # C3 with P recomputed from the LSE (the reference's default mode): the online forward
+    "C3_recompute": Config("C3_recompute", 1, 1, 8192, 64, "fp16", True, bwd_mode="recompute"),
     "C4_16k": Config("C4_16k", 1, 1, 16384, 64, "fp16", True),
     "C5": Config("C5", 4, 16, 8192, 128, "bf16", True, qkv_scale=0.5),
     # The reference TTT model's attention (cloud_ttt_e2e/configs/meta_8k_v2.yaml: batch 8, d_model 384,

@@ -162,29 +162,19 @@ def roofline_entry(cfg, ktimes, with_p=None):
             "algorithmic_bytes": model["bytes"]}
 
 
-# Kernels behind each entry point, as named in the rocprof summaries.
-_ENTRY_KERNELS = {
-    "ttt_attn_fwd": ("k_fwd_stats", "k_fwd_p"),
-    "ttt_attn_bwd_dq": ("k_bwd_dq",),
-    "ttt_attn_bwd_dkdv": ("k_bwd_dkdv",),
-    "ttt_attn_gg_row": ("k_gg_row", "k_combine_gg_row"),
-    "ttt_attn_gg_col": ("k_gg_col",),
-}
-
-
 def measured_traffic(entry: str, cfg: workloads.Config):
     """HBM bytes per launch of `entry` from the committed rocprof PMC summary
-    (FETCH_SIZE + WRITE_SIZE scaled by a plain-copy calibration), or None."""
+    (FETCH_SIZE + WRITE_SIZE scaled by a plain-copy calibration, summed over
+    the kernels the summary attributes to the entry point, its combine
+    kernels included), or None."""
     path = os.path.join(ROOT, "profiles", f"pmc_traffic_{cfg.name}.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
         data = json.load(f)["kernels"]
-    tag = {"fp16": "DF16_", "bf16": "DF16b", "fp32": "f"}[cfg.dtype]
     total, found = 0.0, False
-    for kname, rec in data.items():
-        base, _, args = kname.partition("<")
-        if base in _ENTRY_KERNELS.get(entry, ()) and args.startswith(f"{tag},{cfg.d}".replace("_,", ",")):
+    for rec in data.values():
+        if rec.get("entry") == entry:
             total += rec["fetch_bytes"] + rec["write_bytes"]
             found = True
     return round(total) if found else None

@@ -105,9 +105,11 @@ def test_ragged_lengths_d128(t, causal, save_p):
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("save_p", [True, False])
 def test_scale_signs(scale, causal, save_p):
-    """Negative and zero scales take the forward's scaled-score path (the
-    fused raw-score statistics need a positive scale); a positive non-power
-    of two takes the fused one.  Ragged T covers the clamped tiles."""
+    """Negative and zero scales take the statistics pass's scaled-score path
+    (its fused raw-score form needs a positive scale), and in the online pass
+    a negated q (negative scale) and masked entries selected after the
+    exponential (zero scale, where -inf * 0 is NaN); a positive non-power of
+    two takes the fused forms.  Ragged T covers the clamped tiles."""
     dt = torch.float16
     t = 100
     xs = _inputs(1, 2, t, 64, dt, seed=11)

@@ -48,6 +48,7 @@ constexpr int kXcds = 8;
 constexpr double kWgOverheadTiles = 0.5;   // per workgroup, in tile times
 constexpr double kEmptyWgTiles = 0.05;     // a workgroup whose chunk is empty
 constexpr double kWgCostTiles = 0.015;     // per workgroup, added to the makespan
+constexpr int64_t kDeferRounds = 4;        // P pass: rounds of workgroups from which stores are deferred
 constexpr int64_t kMaxSimWorkgroups = 16;  // x slots: larger grids are not considered
 constexpr int kFallbackCus = 256;
 constexpr int kFallbackPerCu = 2;
@@ -465,6 +466,13 @@ int ttt_attn_fwd(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, co
   const bool wp = has_p(p);
   if (wp) TRY(take_view(pr, p, "p", &a.p));
   TRY(attach_split(pr, wp ? ttt::kFamFwdP : ttt::kFamFwdOnline, wp, workspace, workspace_bytes, &a));
+  // Deferred P stores pay off where the P writes run at bandwidth: several
+  // rounds of workgroups per slot (b4 h16 T8192 d128: P pass -11 %); with one
+  // round they cost about 1 % (b2 h4 T2048 d128).
+  if (wp) {
+    const int64_t blocks = pr->batch * pr->heads * ((pr->seqlen + ttt::kBlk - 1) / ttt::kBlk);
+    a.defer_p = blocks >= kDeferRounds * family_slots(pr, ttt::kFamFwdP, true) ? 1 : 0;
+  }
   return launched(ttt::launch_fwd(pr->dtype, (int)pr->head_dim, a, wp, (hipStream_t)stream), "ttt_attn_fwd");
 }
 

@@ -82,6 +82,9 @@ struct Params {
   // masks beyond causality (last, so the fields above keep their offsets)
   int win, win_kind;  // key window (0: none; else 0 < win < T, with causal), kWin*
   View bias;          // additive score bias [B,H,T,T] (p == nullptr: none); strides may be 0
+  // P pass: issue a full tile's P stores after the next tile's barrier
+  // rather than right away (set for launches of many workgroup rounds).
+  int defer_p;
 };
 
 // Logical grid position (x, slice y) of this workgroup.  The hardware hands

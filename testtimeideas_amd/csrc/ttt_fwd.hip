@@ -43,6 +43,13 @@
 //  * The statistics pass takes two key tiles per barrier round (3 us faster
 //    at b1 h1 T8192 d64, no change at b4 h16 T8192 d128); the P pass takes
 //    one (two were slower).
+//  * The online pass without a window or bias folds the scale into one FMA
+//    and rescales O only when a row's max grows by more than 2^8 (b1 h1
+//    T16384 d64 -9 %, b4 h16 T8192 d128 -2.6 %).  Row sums by MFMA (ones x P)
+//    were no faster there and moved the LSE by up to 8e-4.
+//  * Deferred P stores in the P pass (b4 h16 T8192 d128 -13 %; host-gated to
+//    launches of several workgroup rounds, since with one round they cost
+//    about 1 %).
 
 namespace ttt {
 
@@ -164,7 +171,65 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<true>::value))) void k_fwd_online(Pa
     }
   };
   // Key tile nb from LDS tiles cK, cV.
+  // Without a window or bias the scores stay raw (q.k): c = |s|*log2(e) is
+  // folded into one FMA per element (q negated for a negative scale), and the
+  // running shift sh (base 2) moves only when a row's max exceeds it by more
+  // than kSlack, so most tiles skip rescaling O and l (then P <= 2^kSlack,
+  // well inside T's range).  Other problems take the scaled form below.
+  constexpr float kSlack = 8.f;
+  float csl = a.scale_log2;
+  if constexpr (!XM) {
+    if (csl < 0.f) {
+      csl = -csl;
+#pragma unroll
+      for (int ks = 0; ks < D / 32; ++ks) qf[ks] = scale_frag<T>(qf[ks], -1.f);
+    }
+  }
+  float sh = -INFINITY;
+  auto body_raw = [&](int nb, const T* cK, const T* cV) __attribute__((always_inline)) {
+    Tile s;
+    s.zero();
+    mm_d<T, D>(s, cK, qf);
+    const bool need_mask = mk.tile(nb);
+    if (need_mask) {
+      const int n0 = nb * kBlk;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          s.set(kb, j, mk.masked(n0 + stream_index(kb, g, j)) ? -INFINITY : s.at(kb, j));
+    }
+    // Every row sees a key of every tile of its walk here, so tm is finite.
+    const float tm = tile_max(s) * csl;
+    if (__builtin_amdgcn_ballot_w64(tm > sh + kSlack) != 0) {  // uniform
+      const float sn = fmaxf(sh, tm);
+      const float alpha = fast_exp2(sh - sn);
+      l *= alpha;
+#pragma unroll
+      for (int i = 0; i < D / 16; ++i) acc[i] *= alpha;
+      sh = sn;
+    }
+    frag pf[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      float pv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pv[j] = fast_exp2(fmaf(s.at(kb, j), csl, -sh));
+      if (need_mask) {  // selected after the exponential: -inf * 0 is NaN at scale 0
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pv[j] = s.at(kb, j) == -INFINITY ? 0.f : pv[j];
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) l += pv[j];
+      pf[kb] = vals_frag<T>(pv);
+    }
+    mm_s<T, D>(acc, cV, pf);
+  };
   auto body = [&](int nb, const T* cK, const T* cV) __attribute__((always_inline)) {
+    if constexpr (!XM) {
+      body_raw(nb, cK, cV);
+      return;
+    }
     Tile s;
     fwd_scores<T, D, XM>(s, cK, qf, a, mk, brow, nb);
     const float mnew = fmaxf(mx, tile_max(s));
@@ -241,6 +306,7 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<true>::value))) void k_fwd_online(Pa
   }
 
   l = group_sum(l);
+  if constexpr (!XM) mx = sh;
   const int64_t ridx = (int64_t)bh * T_ + m;
   if (cr.nch == 1) {
     if (m < T_ && g == 0) a.lse[ridx] = (mx + __log2f(l)) * kLn2;
@@ -528,6 +594,22 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_p(Params
       stage_load<T, D>(stV, vp, a.v.st, T_ - n1, D);
     }
   };
+  // With a.defer_p, the P stores of a full tile wait in registers until the
+  // next tile's barrier: every step starts by waiting for all of the wave's
+  // memory operations, stores included (vmcnt counts both), so stores issued
+  // just before that wait would hold it; issued after it they drain during
+  // the next tile's work.
+  frag pend[2];
+  T* pend_ptr = nullptr;
+  auto flush = [&]() __attribute__((always_inline)) {
+    if constexpr (kDma) {
+      if (pend_ptr) {
+        store_frag_g<T>(pend_ptr, pend[0]);
+        store_frag_g<T>(pend_ptr + 32, pend[1]);
+        pend_ptr = nullptr;
+      }
+    }
+  };
   // Key tile `nt` from LDS tiles cK, cV.
   auto body = [&](int nt, const T* cK, const T* cV) __attribute__((always_inline)) {
       const int n0 = nt * kBlk;
@@ -550,7 +632,10 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_p(Params
             for (int j = 0; j < 8; ++j) pv[j] = mk.masked(n0 + stream_index(kb, g, j)) ? 0.f : pv[j];
           }
           pf[kb] = vals_frag<T>(pv);
-          if (m < T_) {
+          if (kDma && a.defer_p && n0 + kBlk <= T_) {
+            pend[kb] = pf[kb];
+            if (kb == 1 && m < T_) pend_ptr = Pm + n0 + stream_index(0, g, 0);
+          } else if (m < T_) {
             const int n = n0 + stream_index(kb, g, 0);
             if (n + 8 <= T_) {
               store_frag_g<T>(Pm + n, pf[kb]);
@@ -578,7 +663,10 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_p(Params
 #pragma unroll
           for (int j = 0; j < 8; ++j) pv[j] = E::f32(E::cvt(fast_exp2(s.at(kb, j) - lse2)));
           pf[kb] = vals_frag<T>(pv);
-          if (m < T_) {
+          if (kDma && a.defer_p && n0 + kBlk <= T_) {
+            pend[kb] = pf[kb];
+            if (kb == 1 && m < T_) pend_ptr = Pm + n0 + stream_index(0, g, 0);
+          } else if (m < T_) {
             const int n = n0 + stream_index(kb, g, 0);
             if (n + 8 <= T_) {
               store8<T>(Pm + n, pv);
@@ -615,6 +703,7 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_p(Params
       constexpr int P = decltype(par)::value;
       dma_wait();       // this wave's loads of tile nt
       __syncthreads();  // everyone's, and everyone is done with the other set
+      flush();          // the previous tile's P, if deferred
       if (nt + 1 < cr.t1) {
         if constexpr (P == 0)
           fetch(nt + 1, sK1, sV1);
@@ -631,6 +720,7 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_p(Params
       step(Parity<0>{}, nb);
       if (nb + 1 < cr.t1) step(Parity<1>{}, nb + 1);
     }
+    flush();
   } else {
     load_kv(cr.t0);
     for (int nb = cr.t0; nb < cr.t1; ++nb) {

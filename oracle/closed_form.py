@@ -39,11 +39,14 @@ def _mask(t: int) -> np.ndarray:
     return np.triu(np.ones((t, t), dtype=bool), 1)
 
 
-def forward(q, k, v, causal: bool, scale: float, bias=None) -> Dict[str, np.ndarray]:
+def forward(q, k, v, causal: bool, scale: float, bias=None, p_store=None) -> Dict[str, np.ndarray]:
     """bias: an additive score bias broadcastable to [..., Tq, Tk] (entries
     may be -inf), added before the causal mask and the softmax, as the
     reference TTT model's ``_attention`` does
-    (cloud_ttt_e2e/ttt_e2e/attention.py:9-18)."""
+    (cloud_ttt_e2e/ttt_e2e/attention.py:9-18).  p_store: None, or a map of P
+    to P as stored (a rounding to a storage format); O and every later use
+    of P then see the stored values, as in the save_p modes, whose forward
+    returns O from the cached probabilities (triton_attention.py:51-59)."""
     q, k, v = (np.asarray(x, dtype=np.float64) for x in (q, k, v))
     s = scale * (q @ _t(k))
     if bias is not None:
@@ -54,12 +57,14 @@ def forward(q, k, v, causal: bool, scale: float, bias=None) -> Dict[str, np.ndar
     e = np.exp(s - mx)
     l = e.sum(axis=-1, keepdims=True)
     p = e / l
+    if p_store is not None:
+        p = np.asarray(p_store(p), dtype=np.float64)
     return {"o": p @ v, "p": p, "lse": (mx + np.log(l))[..., 0]}
 
 
-def backward(q, k, v, do, causal: bool, scale: float, bias=None) -> Dict[str, np.ndarray]:
+def backward(q, k, v, do, causal: bool, scale: float, bias=None, p_store=None) -> Dict[str, np.ndarray]:
     q, k, v, do = (np.asarray(x, dtype=np.float64) for x in (q, k, v, do))
-    f = forward(q, k, v, causal, scale, bias)
+    f = forward(q, k, v, causal, scale, bias, p_store)
     p, o = f["p"], f["o"]
     dp = do @ _t(v)
     dd = (p * dp).sum(axis=-1, keepdims=True)
@@ -68,9 +73,10 @@ def backward(q, k, v, do, causal: bool, scale: float, bias=None) -> Dict[str, np
             "dv": _t(p) @ do, "rowsum": dd[..., 0], "ds": ds, "dp": dp}
 
 
-def double_backward(q, k, v, do, gq, gk, gv, causal: bool, scale: float, bias=None) -> Dict[str, np.ndarray]:
+def double_backward(q, k, v, do, gq, gk, gv, causal: bool, scale: float, bias=None,
+                    p_store=None) -> Dict[str, np.ndarray]:
     q, k, v, do, gq, gk, gv = (np.asarray(x, dtype=np.float64) for x in (q, k, v, do, gq, gk, gv))
-    b = backward(q, k, v, do, causal, scale, bias)
+    b = backward(q, k, v, do, causal, scale, bias, p_store)
     p, dp, ds = b["p"], b["dp"], b["ds"]
     dd = b["rowsum"][..., None]
     gds = scale * (gq @ _t(k) + q @ _t(gk))

@@ -27,7 +27,7 @@ if ROOT not in sys.path:
 
 import torch  # noqa: E402
 
-from testtimeideas_amd import _lib, workloads  # noqa: E402
+from testtimeideas_amd import _lib, autotune, workloads  # noqa: E402
 from testtimeideas_amd.ttt_e2e import windowed_attention  # noqa: E402
 from ttt_kernels import triton_attention  # noqa: E402
 
@@ -373,6 +373,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the T=16k point and forward-only metrics")
     ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay of the step")
+    ap.add_argument("--autotune", action="store_true",
+                    help="measured split per kernel family and shape (testtimeideas_amd.autotune), tuned in warmup")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="also run a plain device copy of this many MiB (counter calibration for rocprof)")
     args = ap.parse_args()
@@ -387,6 +389,7 @@ def main():
         sys.exit(2)
 
     dev = torch.device("cuda", 0)
+    autotune.enable(args.autotune)
     if args.copy_mb:
         copy_calibration(args.copy_mb)
     if args.config == "META_8K":
@@ -432,7 +435,8 @@ def main():
                                f"{cfg.bwd_mode} fwd+bwd{'+grad-grad' if cfg.gradgrad else ''}",
                    "batch": cfg.b, "heads": cfg.h, "seq_len": cfg.t, "head_dim": cfg.d,
                    "window": cfg.window or None, "bwd_mode": cfg.bwd_mode,
-                   "autograd": "eager, backward on the calling thread"},
+                   "autograd": "eager, backward on the calling thread",
+                   "splits": "autotuned" if args.autotune else "library choice"},
         "tflops": round(roof["flops"] / (ms * 1e-3) / 1e12, 3),
         "step_roofline_us": round(roof["roofline_us"], 2),
         "step_roofline_frac": round(roof["roofline_us"] * 1e-3 / ms, 5),

@@ -22,6 +22,8 @@ from typing import Dict, List, Optional, Tuple
 
 import torch
 
+from . import autotune
+
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libttt_attn.so")
 # torch binding of the three fused entry points (csrc/ttt_torch.cpp): the same
@@ -304,15 +306,33 @@ def split_chunk(n: int):
         _split_chunk = prev
 
 
-def _problem(x: torch.Tensor, mask, scale: float) -> _Problem:
+def _problem(x: torch.Tensor, mask, scale: float, split: Optional[int] = None) -> _Problem:
     b, h, t, d = x.shape
     m = as_mask(mask)
     bv = _View(None, 0, 0, 0)
     if m.bias is not None:
         s = m.bias.stride()
         bv = _View(m.bias.data_ptr(), s[0], s[1], s[2])
-    return _Problem(_DTYPE_CODE[x.dtype], 1 if m.causal else 0, b, h, t, d, float(scale), _split_chunk,
-                    int(m.window), int(m.window_kind), bv)
+    return _Problem(_DTYPE_CODE[x.dtype], 1 if m.causal else 0, b, h, t, d, float(scale),
+                    _split_chunk if split is None else int(split), int(m.window), int(m.window_kind), bv)
+
+
+def _split_for(entry: int, x: torch.Tensor, m, scale: float, load_p: bool, gdo: bool, run) -> int:
+    """The split to launch kernel family `entry` with: a split forced by
+    ``split_chunk``, else the autotuned one (``autotune``; `run(c)` launches
+    the call with split c), else 0, the library's choice."""
+    if _split_chunk or not autotune.enabled():
+        return _split_chunk
+    key = (entry, x.dtype, m.causal, tuple(x.shape), int(m.window), int(m.window_kind), m.bias is not None,
+           bool(load_p), bool(gdo))
+
+    def pick():
+        pr = _problem(x, m, scale, 0)
+        c0 = split_info(pr, entry, load_p, gdo)[0]
+        pr.split_chunk = 1 << 30  # clipped to the longest walk
+        return c0, split_info(pr, entry, load_p, gdo)[0]
+
+    return autotune.chunk(key, pick, run)
 
 
 def prep_bias(bias: torch.Tensor, b: int, h: int, t: int, dtype: torch.dtype, device) -> torch.Tensor:
@@ -418,17 +438,21 @@ def _empty_like_out(x: torch.Tensor) -> torch.Tensor:
 def fwd(q, k, v, mask, scale: float, want_p: bool):
     """Forward: O, LSE and (save_p) P.  Reference: TritonAttentionFn.forward,
     ttt_kernels/triton_attention.py:261-337 (P path :51-59, :270-273)."""
-    if q.numel() and _timing is None:
-        m = as_mask(mask)
-        o, lse, p = ext().fwd(q, k, v, m.causal, float(scale), bool(want_p), _split_chunk, int(m.window),
-                              int(m.window_kind), m.bias)
-        return o, lse, p
+    if q.numel() == 0:
+        return _empty_like_out(q), _stats(q), alloc_p(q) if want_p else None
+    m = as_mask(mask)
+    ent = ENTRY_FWD_P if want_p else ENTRY_FWD
+
+    def run(c):
+        return ext().fwd(q, k, v, m.causal, float(scale), bool(want_p), c, int(m.window), int(m.window_kind), m.bias)
+
+    c = _split_for(ent, q, m, scale, want_p, False, run)
+    if _timing is None:
+        return tuple(run(c))
     o = _empty_like_out(q)
     lse = _stats(q)
     p = alloc_p(q) if want_p else None
-    if q.numel() == 0:
-        return o, lse, p
-    pr = _problem(q, mask, scale)
+    pr = _problem(q, mask, scale, c)
     wp, wn, _wbuf = _workspace(pr, ENTRY_FWD_P if want_p else ENTRY_FWD, q.device)
     _timed("ttt_attn_fwd", ctypes.byref(pr), _view(q), _view(k), _view(v), _view(o), lse.data_ptr(),
            _view(p), wp, wn, _stream())
@@ -439,30 +463,33 @@ def bwd(q, k, v, o, do, lse, p, mask, scale: float):
     """First backward: dQ, dK, dV and the row statistic D = rowsum(dO o O).
     Reference: TritonAttentionFn.backward, triton_attention.py:351-379 and
     :416-420; launchers backward_stubs.py:154-181, 224-255, 362-425."""
-    if q.numel() and _timing is None:
-        m = as_mask(mask)
-        dq, dk, dv, rowsum = ext().bwd(q, k, v, o, do, lse, p, m.causal, float(scale), _split_chunk, int(m.window),
-                                       int(m.window_kind), m.bias)
-        return dq, dk, dv, rowsum
+    if q.numel() == 0:
+        return _empty_like_out(q), _empty_like_out(k), _empty_like_out(v), _stats(q)
+    m = as_mask(mask)
+    lp = p is not None
+
+    def run(cq, ck):
+        return ext().bwd(q, k, v, o, do, lse, p, m.causal, float(scale), cq, ck, int(m.window), int(m.window_kind),
+                         m.bias)
+
+    cq = _split_for(ENTRY_BWD_DQ, q, m, scale, lp, False, lambda c: run(c, 0))
+    ck = _split_for(ENTRY_BWD_DKDV, q, m, scale, lp, False, lambda c: run(cq, c))
+    if _timing is None:
+        return tuple(run(cq, ck))
     dq = _empty_like_out(q)
     dk = _empty_like_out(k)
     dv = _empty_like_out(v)
     rowsum = _stats(q)
-    if q.numel() == 0:
-        return dq, dk, dv, rowsum
-    prob = _problem(q, mask, scale)
-    pr = ctypes.byref(prob)
     st = _stream()
     lse_p = _fptr(lse)
-    wp, wn, _wbuf = _workspace(prob, ENTRY_BWD, q.device)
-    if _timing is None:
-        _call("ttt_attn_bwd", pr, _view(q), _view(k), _view(v), _view(o), _view(do), lse_p, _view(p),
-              rowsum.data_ptr(), _view(dq), _view(dk), _view(dv), wp, wn, st)
-    else:
-        _timed("ttt_attn_bwd_dq", pr, _view(q), _view(k), _view(v), _view(o), _view(do), lse_p, _view(p),
-               None, rowsum.data_ptr(), _view(dq), wp, wn, st)
-        _timed("ttt_attn_bwd_dkdv", pr, _view(q), _view(k), _view(v), _view(do), lse_p, _view(p),
-               rowsum.data_ptr(), _view(dk), _view(dv), wp, wn, st)
+    pq = _problem(q, mask, scale, cq)
+    pk = _problem(q, mask, scale, ck)
+    wp, wn, _wbuf = _workspace(pq, ENTRY_BWD_DQ, q.device)
+    _timed("ttt_attn_bwd_dq", ctypes.byref(pq), _view(q), _view(k), _view(v), _view(o), _view(do), lse_p, _view(p),
+           None, rowsum.data_ptr(), _view(dq), wp, wn, st)
+    wp, wn, _wbuf2 = _workspace(pk, ENTRY_BWD_DKDV, q.device)
+    _timed("ttt_attn_bwd_dkdv", ctypes.byref(pk), _view(q), _view(k), _view(v), _view(do), lse_p, _view(p),
+           rowsum.data_ptr(), _view(dk), _view(dv), wp, wn, st)
     return dq, dk, dv, rowsum
 
 
@@ -519,36 +546,38 @@ def rowsum_from_p(p, do, v, mask):
 def gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, mask, scale: float, want_gdo: bool):
     """Double backward: (GQ, GK, GV, GdO or None).  Reference stubs
     backward_stubs.py:539-548; torch version :434-514 (corrected)."""
-    if q.numel() and _timing is None:
-        m = as_mask(mask)
-        gq_out, gk_out, gv_out, gdo = ext().gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, m.causal, float(scale),
-                                               bool(want_gdo), _split_chunk, int(m.window), int(m.window_kind),
-                                               m.bias)
-        return gq_out, gk_out, gv_out, gdo
+    if q.numel() == 0:
+        return (_empty_like_out(q), _empty_like_out(k), _empty_like_out(v),
+                _empty_like_out(do) if want_gdo else None)
+    m = as_mask(mask)
+    lp = p is not None
+
+    def run(cr, cc):
+        return ext().gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, m.causal, float(scale), bool(want_gdo), cr, cc,
+                        int(m.window), int(m.window_kind), m.bias)
+
+    cr = _split_for(ENTRY_GG_ROW, q, m, scale, lp, want_gdo, lambda c: run(c, 0))
+    cc = _split_for(ENTRY_GG_COL, q, m, scale, lp, False, lambda c: run(cr, c))
+    if _timing is None:
+        return tuple(run(cr, cc))
     gq_out = _empty_like_out(q)
     gk_out = _empty_like_out(k)
     gv_out = _empty_like_out(v)
     gdo = _empty_like_out(do) if want_gdo else None
     e = _stats(q)
     f = _stats(q)
-    if q.numel() == 0:
-        return gq_out, gk_out, gv_out, gdo
-    prob = _problem(q, mask, scale)
-    pr = ctypes.byref(prob)
     st = _stream()
     lse_p = _fptr(lse)
-    wp, wn, _wbuf = _workspace(prob, ENTRY_GG, q.device, want_gdo)
-    if _timing is None:
-        _call("ttt_attn_gg", pr, _view(q), _view(k), _view(v), _view(do), lse_p, _view(p), rowsum.data_ptr(),
-              _view(gq), _view(gk), _view(gv), _view(gq_out), _view(gk_out), _view(gv_out), _view(gdo),
-              e.data_ptr(), f.data_ptr(), wp, wn, st)
-    else:
-        _timed("ttt_attn_gg_row", pr, _view(q), _view(k), _view(v), _view(do), lse_p, _view(p),
-               rowsum.data_ptr(), _view(gq), _view(gk), _view(gv), _view(gq_out), _view(gdo), e.data_ptr(),
-               f.data_ptr(), wp, wn, st)
-        _timed("ttt_attn_gg_col", pr, _view(q), _view(k), _view(v), _view(do), lse_p, _view(p),
-               rowsum.data_ptr(), e.data_ptr(), f.data_ptr(), _view(gq), _view(gk), _view(gv), _view(gk_out),
-               _view(gv_out), wp, wn, st)
+    prr = _problem(q, mask, scale, cr)
+    prc = _problem(q, mask, scale, cc)
+    wp, wn, _wbuf = _workspace(prr, ENTRY_GG_ROW, q.device, want_gdo)
+    _timed("ttt_attn_gg_row", ctypes.byref(prr), _view(q), _view(k), _view(v), _view(do), lse_p, _view(p),
+           rowsum.data_ptr(), _view(gq), _view(gk), _view(gv), _view(gq_out), _view(gdo), e.data_ptr(),
+           f.data_ptr(), wp, wn, st)
+    wp, wn, _wbuf2 = _workspace(prc, ENTRY_GG_COL, q.device)
+    _timed("ttt_attn_gg_col", ctypes.byref(prc), _view(q), _view(k), _view(v), _view(do), lse_p, _view(p),
+           rowsum.data_ptr(), e.data_ptr(), f.data_ptr(), _view(gq), _view(gk), _view(gv), _view(gk_out),
+           _view(gv_out), wp, wn, st)
     return gq_out, gk_out, gv_out, gdo
 
 

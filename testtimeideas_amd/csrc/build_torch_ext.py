@@ -1,5 +1,5 @@
-"""Build testtimeideas_amd/_ttt_torch.so, the torch binding of the fused C
-entry points (ttt_torch.cpp), against the in-tree libttt_attn.so (found next
+"""Build testtimeideas_amd/_ttt_torch.so, the torch binding of the C entry
+points (ttt_torch.cpp), against the in-tree libttt_attn.so (found next
 to the module through an $ORIGIN run path).  The object goes to _build/ext.
 Run after the library is built (``make -C testtimeideas_amd/csrc``)."""
 import os

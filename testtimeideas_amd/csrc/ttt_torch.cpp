@@ -1,5 +1,8 @@
-// ttt_torch.cpp — torch binding of the three fused entry points of the C ABI
-// (include/ttt_attn.h): ttt_attn_fwd, ttt_attn_bwd and ttt_attn_gg.
+// ttt_torch.cpp — torch binding of the forward, backward and double backward
+// of the C ABI (include/ttt_attn.h): ttt_attn_fwd, then ttt_attn_bwd_dq +
+// ttt_attn_bwd_dkdv (what ttt_attn_bwd does) and ttt_attn_gg_row +
+// ttt_attn_gg_col (what ttt_attn_gg does), each kernel family with its own
+// split (tiles per workgroup; 0 lets the library choose).
 //
 // The ctypes binding (testtimeideas_amd/_lib.py) spends tens of microseconds
 // of Python per call building views, problems and outputs; the autograd path
@@ -13,6 +16,7 @@
 #include <torch/extension.h>
 #include <c10/hip/HIPStream.h>
 
+#include <algorithm>
 #include <string>
 #include <vector>
 
@@ -79,9 +83,23 @@ at::Tensor alloc_p(const at::Tensor& x) {
   return tp == t ? buf : buf.narrow(3, 0, t);
 }
 
-at::Tensor workspace(const ttt_problem& pr, int32_t entry, bool gdo, const at::Tensor& like, int64_t* bytes) {
+int64_t workspace_size(const ttt_problem& pr, int32_t entry, bool gdo) {
   const int64_t n = ttt_attn_workspace_size(&pr, entry, gdo ? 1 : 0);
   TORCH_CHECK(n >= 0, "ttt_attn_workspace_size failed: ", ttt_last_error());
+  return n;
+}
+
+at::Tensor workspace(const ttt_problem& pr, int32_t entry, bool gdo, const at::Tensor& like, int64_t* bytes) {
+  const int64_t n = workspace_size(pr, entry, gdo);
+  *bytes = n;
+  return n > 0 ? at::empty({n}, like.options().dtype(at::kByte)) : at::Tensor();
+}
+
+// One workspace for two launches in stream order (the second starts after
+// the first, its combine included, has finished with it).
+at::Tensor workspace2(const ttt_problem& pr0, int32_t e0, const ttt_problem& pr1, int32_t e1, bool gdo,
+                      const at::Tensor& like, int64_t* bytes) {
+  const int64_t n = std::max(workspace_size(pr0, e0, gdo), workspace_size(pr1, e1, gdo));
   *bytes = n;
   return n > 0 ? at::empty({n}, like.options().dtype(at::kByte)) : at::Tensor();
 }
@@ -110,25 +128,31 @@ std::vector<at::Tensor> fwd(const at::Tensor& q, const at::Tensor& k, const at::
   return {o, lse, p};
 }
 
-// First backward: (dQ, dK, dV, D).
+// First backward: (dQ, dK, dV, D).  split_dq, split_dkdv: each family's split.
 std::vector<at::Tensor> bwd(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const at::Tensor& o,
                             const at::Tensor& dout, const at::Tensor& lse, const c10::optional<at::Tensor>& p,
-                            bool causal, double scale, int64_t split_chunk, int64_t window, int64_t window_kind,
-                            const c10::optional<at::Tensor>& bias) {
-  const ttt_problem pr = problem_of(q, causal, scale, split_chunk, window, window_kind, bias);
+                            bool causal, double scale, int64_t split_dq, int64_t split_dkdv, int64_t window,
+                            int64_t window_kind, const c10::optional<at::Tensor>& bias) {
+  const ttt_problem pq = problem_of(q, causal, scale, split_dq, window, window_kind, bias);
+  const ttt_problem pk = problem_of(q, causal, scale, split_dkdv, window, window_kind, bias);
   at::Tensor dq = at::empty(q.sizes(), q.options());
   at::Tensor dk = at::empty(k.sizes(), k.options());
   at::Tensor dv = at::empty(v.sizes(), v.options());
   at::Tensor rowsum = stats_of(q);
   int64_t wsb = 0;
-  at::Tensor ws = workspace(pr, TTT_ENTRY_BWD, false, q, &wsb);
+  at::Tensor ws = workspace2(pq, TTT_ENTRY_BWD_DQ, pk, TTT_ENTRY_BWD_DKDV, false, q, &wsb);
   const bool lp = p && p->defined();
   const ttt_view vq = view_of(q), vk = view_of(k), vv = view_of(v), vo = view_of(o), vdo = view_of(dout);
   const ttt_view vp = lp ? view_of(*p) : none_view();
   const ttt_view vdq = view_of(dq), vdk = view_of(dk), vdv = view_of(dv);
-  check(ttt_attn_bwd(&pr, &vq, &vk, &vv, &vo, &vdo, lse.data_ptr<float>(), lp ? &vp : nullptr,
-                     rowsum.data_ptr<float>(), &vdq, &vdk, &vdv, ptr_or_null(ws), wsb, stream_of(q)),
-        "ttt_attn_bwd");
+  void* st = stream_of(q);
+  float* rs = rowsum.data_ptr<float>();
+  check(ttt_attn_bwd_dq(&pq, &vq, &vk, &vv, &vo, &vdo, lse.data_ptr<float>(), lp ? &vp : nullptr, nullptr, rs, &vdq,
+                        ptr_or_null(ws), wsb, st),
+        "ttt_attn_bwd_dq");
+  check(ttt_attn_bwd_dkdv(&pk, &vq, &vk, &vv, &vdo, lse.data_ptr<float>(), lp ? &vp : nullptr, rs, &vdk, &vdv,
+                          ptr_or_null(ws), wsb, st),
+        "ttt_attn_bwd_dkdv");
   return {dq, dk, dv, rowsum};
 }
 
@@ -136,33 +160,40 @@ std::vector<at::Tensor> bwd(const at::Tensor& q, const at::Tensor& k, const at::
 std::vector<at::Tensor> gg(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const at::Tensor& dout,
                            const at::Tensor& lse, const c10::optional<at::Tensor>& p, const at::Tensor& rowsum,
                            const at::Tensor& gq, const at::Tensor& gk, const at::Tensor& gv, bool causal, double scale,
-                           bool want_gdo, int64_t split_chunk, int64_t window, int64_t window_kind,
+                           bool want_gdo, int64_t split_row, int64_t split_col, int64_t window, int64_t window_kind,
                            const c10::optional<at::Tensor>& bias) {
-  const ttt_problem pr = problem_of(q, causal, scale, split_chunk, window, window_kind, bias);
+  const ttt_problem pr = problem_of(q, causal, scale, split_row, window, window_kind, bias);
+  const ttt_problem pc = problem_of(q, causal, scale, split_col, window, window_kind, bias);
   at::Tensor gq_out = at::empty(q.sizes(), q.options());
   at::Tensor gk_out = at::empty(k.sizes(), k.options());
   at::Tensor gv_out = at::empty(v.sizes(), v.options());
   at::Tensor gdo = want_gdo ? at::empty(dout.sizes(), dout.options()) : at::Tensor();
   at::Tensor e = stats_of(q), f = stats_of(q);
   int64_t wsb = 0;
-  at::Tensor ws = workspace(pr, TTT_ENTRY_GG, want_gdo, q, &wsb);
+  at::Tensor ws = workspace2(pr, TTT_ENTRY_GG_ROW, pc, TTT_ENTRY_GG_COL, want_gdo, q, &wsb);
   const bool lp = p && p->defined();
   const ttt_view vq = view_of(q), vk = view_of(k), vv = view_of(v), vdo = view_of(dout);
   const ttt_view vp = lp ? view_of(*p) : none_view();
   const ttt_view vgq = view_of(gq), vgk = view_of(gk), vgv = view_of(gv);
   const ttt_view ogq = view_of(gq_out), ogk = view_of(gk_out), ogv = view_of(gv_out);
   const ttt_view ogdo = want_gdo ? view_of(gdo) : none_view();
-  check(ttt_attn_gg(&pr, &vq, &vk, &vv, &vdo, lse.data_ptr<float>(), lp ? &vp : nullptr, rowsum.data_ptr<float>(),
-                    &vgq, &vgk, &vgv, &ogq, &ogk, &ogv, want_gdo ? &ogdo : nullptr, e.data_ptr<float>(),
-                    f.data_ptr<float>(), ptr_or_null(ws), wsb, stream_of(q)),
-        "ttt_attn_gg");
+  void* st = stream_of(q);
+  const float* rs = rowsum.data_ptr<float>();
+  check(ttt_attn_gg_row(&pr, &vq, &vk, &vv, &vdo, lse.data_ptr<float>(), lp ? &vp : nullptr, rs, &vgq, &vgk, &vgv,
+                        &ogq, want_gdo ? &ogdo : nullptr, e.data_ptr<float>(), f.data_ptr<float>(), ptr_or_null(ws),
+                        wsb, st),
+        "ttt_attn_gg_row");
+  check(ttt_attn_gg_col(&pc, &vq, &vk, &vv, &vdo, lse.data_ptr<float>(), lp ? &vp : nullptr, rs,
+                        e.data_ptr<float>(), f.data_ptr<float>(), &vgq, &vgk, &vgv, &ogk, &ogv, ptr_or_null(ws), wsb,
+                        st),
+        "ttt_attn_gg_col");
   return {gq_out, gk_out, gv_out, gdo};
 }
 
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
-  m.doc() = "torch binding of ttt_attn_fwd / ttt_attn_bwd / ttt_attn_gg (libttt_attn.so)";
+  m.doc() = "torch binding of the forward, backward and double backward of libttt_attn.so";
   m.def("fwd", &fwd, "forward: (O, LSE, P or None)");
   m.def("bwd", &bwd, "first backward: (dQ, dK, dV, D)");
   m.def("gg", &gg, "double backward: (GQ, GK, GV, GdO or None)");

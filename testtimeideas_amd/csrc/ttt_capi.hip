@@ -48,6 +48,17 @@ constexpr int kXcds = 8;
 constexpr double kWgOverheadTiles = 0.5;   // per workgroup, in tile times
 constexpr double kEmptyWgTiles = 0.05;     // a workgroup whose chunk is empty
 constexpr double kWgCostTiles = 0.015;     // per workgroup, added to the makespan
+constexpr double kSplitTiles = 8.0;        // any split: the combine launch and the partials' traffic
+                                           // (b2 h4 T2048 d128: dQ, dK/dV -6 % unsplit)
+// Causal splits are considered while the blocks fill fewer than kSimBlocks
+// times the slots: up to twice the slots, a causal launch's longest blocks can
+// hold the makespan well above the average (b1 h4 T8192: the launch ends with
+// a 128-tile block sharing its CU); beyond that, heaviest-first order
+// balances it.  Measured on MI355X (b1 hH T8192 d64 fp16 causal, fwd + bwd +
+// grad-grad): H = 4 -5.5 %, H = 6 -6 %, H = 8 -1 %, other H unchanged.
+// Equal-length blocks (no causal mask) gain nothing from it and lose the
+// combine (b2 h4 T2048 d128 grad-grad +35 % when split).
+constexpr int64_t kSimBlocks = 2;
 constexpr int64_t kDeferRounds = 4;        // P pass: rounds of workgroups from which stores are deferred
 constexpr int64_t kMaxSimWorkgroups = 16;  // x slots: larger grids are not considered
 constexpr int kFallbackCus = 256;
@@ -221,8 +232,8 @@ double simulate_launch(const std::vector<int64_t>& len, int64_t c, int64_t bh, i
   return end;
 }
 
-// Tiles per workgroup (see above).  No split when the blocks alone fill the
-// slots; chunks are at least kMinChunk tiles.  Cached per shape.
+// Tiles per workgroup (see above).  Chunks are at least kMinChunk tiles, and a
+// split must beat no split by kSplitTiles.  Cached per shape.
 int64_t best_chunk(const ttt_problem* pr, const std::vector<int64_t>& len, bool col, int64_t bh, int64_t slots) {
   static std::mutex mu;
   static std::map<std::tuple<int64_t, int, int, int, int, int64_t, int64_t>, int64_t> cache;
@@ -244,7 +255,7 @@ int64_t best_chunk(const ttt_problem* pr, const std::vector<int64_t>& len, bool 
   for (int64_t c = std::min<int64_t>(kMinChunk, lmax); c < lmax; c = c < 64 ? c + 1 : c + std::max<int64_t>(1, c / 32)) {
     if (bh * slice_workgroups(len, c) > kMaxSimWorkgroups * slots) continue;
     int64_t used = 0;
-    const double cost = simulate_launch(len, c, bh, slots, &used) + kWgCostTiles * used;
+    const double cost = simulate_launch(len, c, bh, slots, &used) + kWgCostTiles * used + kSplitTiles;
     if (cost < best) {
       best = cost;
       best_c = c;
@@ -267,7 +278,10 @@ Split choose_split(const ttt_problem* pr, int fam, bool load_p) {
     c = pr->split_chunk;
   } else {
     const int64_t slots = family_slots(pr, fam, load_p);
-    c = bh * s.nblk >= slots ? lmax : best_chunk(pr, len, col, bh, slots);
+    // Blocks of unequal length (causal or windowed) are simulated up to
+    // kSimBlocks times the slots; equal blocks stop splitting at the slots.
+    const int64_t fill = (pr->causal ? kSimBlocks : 1) * slots;
+    c = bh * s.nblk >= fill ? lmax : best_chunk(pr, len, col, bh, slots);
   }
   s.chunk = (int)std::min<int64_t>(c, lmax);
   s.nchunk_max = (int)((lmax + s.chunk - 1) / s.chunk);

@@ -123,7 +123,8 @@ def _simulated_chunk(nblk, causal, bh, slots, min_chunk=4, lengths=None):
     slots spread round-robin over 8 XCDs (slice y to XCD y % 8 when b*h is a
     multiple of 8), cost = makespan + 0.015 per
     non-empty workgroup, each non-empty workgroup taking its tiles + 0.5 and
-    an empty one 0.05."""
+    an empty one 0.05, plus 8 for any split.  Blocks are split only while
+    they fill fewer than the slots (twice the slots when causal)."""
     import heapq
 
     lens = lengths or ([nblk - b for b in range(nblk)] if causal else [nblk] * nblk)
@@ -144,13 +145,13 @@ def _simulated_chunk(nblk, causal, bh, slots, min_chunk=4, lengths=None):
                     end, used, idx = max(end, f), used + (t > 0), idx + 1
         return end + 0.015 * used
 
-    if bh * nblk >= slots:
+    if bh * nblk >= (2 if causal else 1) * slots:
         return lmax
     best_c, best = lmax, cost(lmax)
     c = min(min_chunk, lmax)
     while c < lmax:
         if bh * sum(-(-ln // c) for ln in lens) <= 16 * slots:
-            v = cost(c)
+            v = cost(c) + 8.0
             if v < best:
                 best_c, best = c, v
         c = c + 1 if c < 64 else c + max(1, c // 32)

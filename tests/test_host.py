@@ -181,7 +181,7 @@ def test_split_info_matches_workspace():
     GPU here: 256 CUs x 2 workgroups, 90 % usable)."""
     pr = _prob(seqlen=8192)
     assert _lib.split_info(pr, _lib.ENTRY_GG_ROW, True) == (21, 7, 460)
-    assert _lib.workspace_bytes(pr, _lib.ENTRY_GG_ROW) == 128 * 7 * 64 * (4 * 64 + 3) * 4
+    assert _lib.workspace_bytes(pr, _lib.ENTRY_GG_ROW) == 128 * 7 * 64 * (3 * 64 + 3) * 4
     with pytest.raises(RuntimeError, match="single kernel family"):
         _lib.split_info(pr, _lib.ENTRY_GG, True)
 
@@ -225,7 +225,7 @@ def test_prep_bias_layouts():
 def test_workspace_sizes():
     # Without a GPU the split assumes 256 CUs x 2 workgroups, 90% usable = 460
     # slots.  Partial accumulators per chunk: nacc x 64 x D fp32 + nsc scalars
-    # per row (forward 1 acc + 2, dQ 1, dK/dV 2, GQ 4 + 3, GQ+GdO 7 + 3).
+    # per row (forward 1 acc + 2, dQ 1, dK/dV 2, GQ 3 + 3, GQ+GdO 5 + 3).
     slots = 460
     for (t, causal, bh) in [(8192, 1, 1), (16384, 1, 1), (8192, 0, 1), (4096, 1, 2), (2048, 1, 1)]:
         nblk = t // 64
@@ -234,8 +234,8 @@ def test_workspace_sizes():
         pr = _prob(seqlen=t, causal=causal, heads=bh)
         parts = bh * nblk * k if k > 1 else 0
         assert _lib.workspace_bytes(pr, _lib.ENTRY_FWD) == parts * 64 * (64 + 2) * 4, (t, causal, bh, c)
-        assert _lib.workspace_bytes(pr, _lib.ENTRY_GG_ROW) == parts * 64 * (4 * 64 + 3) * 4
-        assert _lib.workspace_bytes(pr, _lib.ENTRY_GG, True) == parts * 64 * (7 * 64 + 3) * 4
+        assert _lib.workspace_bytes(pr, _lib.ENTRY_GG_ROW) == parts * 64 * (3 * 64 + 3) * 4
+        assert _lib.workspace_bytes(pr, _lib.ENTRY_GG, True) == parts * 64 * (5 * 64 + 3) * 4
         assert _lib.workspace_bytes(pr, _lib.ENTRY_BWD) == parts * 64 * (2 * 64) * 4
     # C3: one round of 21-tile chunks (455 workgroups in the 460 slots; 20
     # tiles would need 476 and spill into a second round)

@@ -178,11 +178,11 @@ __global__ __launch_bounds__(kThreads) void k_combine_fwd(Params a) {
 
 // ---------------------------------------------------------------------------
 // Grad-grad row pass: E, F from chunk sums, then GQ (and GdO).
-// Accumulators: 0..3 = dS*gK, Z1*K, Z2*K, P*K; 4..6 = P*gV, (P o gdS)*V, P*V.
+// Accumulators: 0..2 = dS*gK + Z1*K, Z2*K, P*K; 3..4 = P*gV + (P o gdS)*V, P*V.
 // Scalars: 0 = E, 1 = rowsum(Z1), 2 = rowsum(Z2).
 template <typename T, int D, bool GDO>
 __global__ __launch_bounds__(kThreads) void k_combine_gg_row(Params a) {
-  constexpr int NACC = GDO ? 7 : 4;
+  constexpr int NACC = GDO ? 5 : 3;
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
   const CombineSlot<D> cs;
@@ -197,17 +197,17 @@ __global__ __launch_bounds__(kThreads) void k_combine_gg_row(Params a) {
   sum_scalars<3>(sc, a.ws_sc, p0, nch, r);
   const float ev = sc[0], xv = sc[1], dv = sc[2];
   const float fv = xv - ev * dv;
-  f32x4 t[4];
-  sum_parts<D, 4>(t, a.ws_acc, p0, nch, NACC, 0, r, cs.d0);
-  f32x4 acc = t[0] + t[1];
-  acc -= ev * t[2];
-  acc = a.scale * (acc - fv * t[3]);
+  f32x4 t[3];
+  sum_parts<D, 3>(t, a.ws_acc, p0, nch, NACC, 0, r, cs.d0);
+  f32x4 acc = t[0];
+  acc -= ev * t[1];
+  acc = a.scale * (acc - fv * t[2]);
   store_slot<T>(a.gq_out, b, h, row, cs.d0, acc);
   if constexpr (GDO) {
-    f32x4 u[3];
-    sum_parts<D, 3>(u, a.ws_acc, p0, nch, NACC, 4, r, cs.d0);
-    f32x4 go = u[0] + u[1];
-    go -= ev * u[2];
+    f32x4 u[2];
+    sum_parts<D, 2>(u, a.ws_acc, p0, nch, NACC, 3, r, cs.d0);
+    f32x4 go = u[0];
+    go -= ev * u[1];
     store_slot<T>(a.gdout, b, h, row, cs.d0, go);
   }
   if (cs.d0 == 0) {

@@ -17,7 +17,8 @@
 // and F = rowsum(Z1) - E * rowsum(Z2).  Likewise
 //   gdP*V = (P o gdS)*V - E o (P*V).
 // It writes GQ, optionally GdO, and E and F for the column pass.  When the
-// key loop is split, chunks write the four (seven) accumulators and the three
+// key loop is split, chunks write dS*gK + Z1*K, Z2*K and P*K (and, for GdO,
+// P*gV + (P o gdS)*V and P*V) and the three
 // row sums, and k_combine_gg_row applies the same formulas to the totals.
 //
 // k_gg_col (stationary key rows, streamed query tiles) reads D, E, F per
@@ -105,7 +106,7 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, false>::value))) void k_gg_row(
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
-  constexpr int NACC = GDO ? 7 : 4;
+  constexpr int NACC = GDO ? 5 : 3;  // split partials: dS*gK + Z1*K, Z2*K, P*K (+ P*gV + (P o gdS)*V, P*V)
   // 16-bit types stream tiles straight into LDS (TileDma), into two buffer
   // sets in distinct arrays with a compile-time role per loop step (kPar), so
   // that the current tile's LDS reads need not wait for the next tile's loads;
@@ -422,16 +423,20 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, false>::value))) void k_gg_row(
       a.f[ridx] = Fv;
     }
   } else {
+    // The combine needs only the sums a1 + a2 and b1 + b2: formed here, they
+    // cut the partials by a quarter (two sevenths with GdO).
     const int64_t part = part_index(a, bh, nblk, mb, ch);
     float* base = a.ws_acc + part * NACC * kBlk * D;
+#pragma unroll
+    for (int i = 0; i < D / 16; ++i) a1[i] += a2[i];
     store_acc_partial<D>(base, rl, a1);
-    store_acc_partial<D>(base + kBlk * D, rl, a2);
-    store_acc_partial<D>(base + 2 * kBlk * D, rl, a3);
-    store_acc_partial<D>(base + 3 * kBlk * D, rl, a4);
+    store_acc_partial<D>(base + kBlk * D, rl, a3);
+    store_acc_partial<D>(base + 2 * kBlk * D, rl, a4);
     if constexpr (GDO) {
-      store_acc_partial<D>(base + 4 * kBlk * D, rl, b1);
-      store_acc_partial<D>(base + 5 * kBlk * D, rl, b2);
-      store_acc_partial<D>(base + 6 * kBlk * D, rl, b3);
+#pragma unroll
+      for (int i = 0; i < D / 16; ++i) b1[i] += b2[i];
+      store_acc_partial<D>(base + 3 * kBlk * D, rl, b1);
+      store_acc_partial<D>(base + 4 * kBlk * D, rl, b3);
     }
     if (g == 0) {
       float* sc = a.ws_sc + part * 3 * kBlk;

@@ -35,7 +35,7 @@ enum : int { kOutO = 0, kOutDQ = 1, kOutDKDV = 2, kOutDV = 3, kOutGKGV = 4 };
 // Partial accumulators and row scalars per chunk, by kernel family.
 enum : int { kFamFwdOnline = 0, kFamFwdP = 1, kFamDq = 2, kFamDkdv = 3, kFamGgRow = 4, kFamGgRowGdo = 5,
              kFamGgCol = 6 };
-constexpr int kFamNacc[] = {1, 1, 1, 2, 4, 7, 2};
+constexpr int kFamNacc[] = {1, 1, 1, 2, 3, 5, 2};
 constexpr int kFamNsc[] = {2, 2, 0, 0, 3, 3, 0};
 
 // Workgroups of a kernel that one CU holds at once (HIP occupancy calculator

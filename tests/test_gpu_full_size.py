@@ -5,7 +5,9 @@ choosing its own split of every streamed loop:
   C4  b1 h1 d64 fp16, T in {512, ..., 16384} x {non-causal, causal}, both
       save_p_triton_full and recompute (C3 is the T = 8192 causal point);
   C2  b2 h4 T2048 d128 fp16 non-causal, save_p forward + first backward;
-  C5  b4 h16 T8192 d128 bf16 causal (q, k, v scaled by 0.5), full grad-grad.
+  C5  b4 h16 T8192 d128 bf16 causal (q, k, v scaled by 0.5), full grad-grad;
+  and beyond the reference's sweep, b1 h1 d64 fp16 causal at T = 32768 and
+  65536 in recompute mode (the LSE-only mode such lengths need).
 
 Reference values: float64 closed forms on the CPU, one block of query rows at
 a time (oracle/blocked.py), on the same dtype-rounded inputs.  C5 compares two
@@ -180,3 +182,22 @@ def test_c5_full_launch():
             for k, v in errs.items():
                 worst[k] = max(worst.get(k, 0.0), v)
     _log("  float32, worst over 64 slices: " + ", ".join(f"{k} {v:.2e}" for k, v in worst.items()))
+
+
+@pytest.mark.parametrize("t", [32768, 65536])
+def test_long_sequence_recompute(t):
+    """T = 32768 and 65536, b1 h1 d64 fp16 causal, recompute mode: every
+    output against the row-block closed forms in float32 on the GPU (the
+    float64 CPU oracle would take minutes at these lengths)."""
+    cfg = workloads.sweep_config(t, True)
+    xs = list(workloads.make_inputs(cfg, seed=0).values())
+    _log(f"[case] long T={t} recompute: {_split_note(cfg, xs)}")
+    t0 = time.time()
+    got = _gpu_step(xs, True, cfg.scale, "recompute")
+    _log(f"  gpu step done ({time.time() - t0:.1f} s)")
+    for n in GG_NAMES + ("lse",):
+        assert bool(torch.isfinite(got[n]).all()), f"T={t} {n}: non-finite values"
+    xg = [x.cuda() for x in xs]
+    ref, _ = _oracle_slice(xg, 0, 0, True, cfg.scale, True, device="cuda", dtype=torch.float32, block=2048)
+    errs = _compare_slice(f"long T={t}", got, ref, None, 0, 0, torch.float16, GG_NAMES)
+    _log("  " + ", ".join(f"{k} {v:.2e}" for k, v in errs.items()))

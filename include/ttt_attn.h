@@ -212,8 +212,12 @@ int ttt_attn_bwd_dkdv(const ttt_problem* pr, const ttt_view* q,
                       int64_t workspace_bytes, void* stream);
 
 /*
- * Full first backward in one call: ttt_attn_bwd_dq (computing D from O into
- * rowsum_out) followed by ttt_attn_bwd_dkdv on the same stream.
+ * Full first backward in one call: the work of ttt_attn_bwd_dq (computing D
+ * from O into rowsum_out) followed by ttt_attn_bwd_dkdv on the same stream,
+ * with bitwise the same results.  When dQ's loop is split, the dK/dV launch
+ * also sums dQ's partials (in workgroups appended to its grid) instead of a
+ * launch of their own, so the workspace (TTT_ENTRY_BWD) holds both families'
+ * partials at once.
  * Replaces: the save_p backward of TritonAttentionFn.backward,
  * triton_attention.py:351-379, and the default recompute backward :416-420.
  */

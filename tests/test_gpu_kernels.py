@@ -142,6 +142,37 @@ def test_per_kernel_entry_points_match_fused():
                         "ttt_attn_gg_col"}
 
 
+@pytest.mark.parametrize("b,h,t,d,dtype,save_p,chunk", [
+    (1, 2, 192, 64, "fp16", True, 1),
+    (1, 1, 300, 64, "bf16", True, 2),
+    (2, 4, 200, 64, "fp16", True, 2),
+    (2, 4, 200, 64, "fp16", False, 3),
+    (1, 3, 257, 128, "bf16", True, 2),
+    (1, 2, 130, 64, "fp32", True, 2),
+    (1, 1, 1024, 64, "fp16", True, 0),
+])
+def test_fused_backward_entry(b, h, t, d, dtype, save_p, chunk):
+    """ttt_attn_bwd, whose dK/dV launch also finishes dQ's split blocks, gives
+    bitwise the results of ttt_attn_bwd_dq + ttt_attn_bwd_dkdv."""
+    import ctypes
+    dt = DT[dtype]
+    q, k, v, do = (x.cuda() for x in _inputs(b, h, t, d, dt, seed=t + d)[:4])
+    print(f"[case] fused bwd b={b} h={h} t={t} d={d} {dtype} save_p={save_p} chunk={chunk}", flush=True)
+    o, lse, p = _lib.fwd(q, k, v, True, 0.125, save_p)
+    with _lib.split_chunk(chunk), _lib.kernel_timing():  # timing: the two per-family entry points
+        dq0, dk0, dv0, rs0 = _lib.bwd(q, k, v, o, do, lse, p, True, 0.125)
+    pr = _lib._problem(q, True, 0.125, chunk)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    rs = torch.empty(b, h, t, dtype=torch.float32, device=q.device)
+    wp, wn, _buf = _lib._workspace(pr, _lib.ENTRY_BWD, q.device)
+    _lib._call("ttt_attn_bwd", ctypes.byref(pr), _lib._view(q), _lib._view(k), _lib._view(v), _lib._view(o),
+               _lib._view(do), _lib._fptr(lse), _lib._view(p), rs.data_ptr(), _lib._view(dq), _lib._view(dk),
+               _lib._view(dv), wp, wn, _lib._stream())
+    torch.cuda.synchronize()
+    for n, x, y in (("dq", dq, dq0), ("dk", dk, dk0), ("dv", dv, dv0), ("rowsum", rs, rs0)):
+        assert torch.equal(x, y), n
+
+
 def test_deterministic():
     """Two runs give bitwise identical outputs (no atomics anywhere)."""
     xs = _inputs(1, 1, 320, 64, torch.bfloat16, seed=4)

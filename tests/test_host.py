@@ -236,7 +236,8 @@ def test_workspace_sizes():
         assert _lib.workspace_bytes(pr, _lib.ENTRY_FWD) == parts * 64 * (64 + 2) * 4, (t, causal, bh, c)
         assert _lib.workspace_bytes(pr, _lib.ENTRY_GG_ROW) == parts * 64 * (3 * 64 + 3) * 4
         assert _lib.workspace_bytes(pr, _lib.ENTRY_GG, True) == parts * 64 * (5 * 64 + 3) * 4
-        assert _lib.workspace_bytes(pr, _lib.ENTRY_BWD) == parts * 64 * (2 * 64) * 4
+        # the fused backward holds dQ's partials (one accumulator) and dK/dV's (two) at once
+        assert _lib.workspace_bytes(pr, _lib.ENTRY_BWD) == parts * 64 * (3 * 64) * 4
     # C3: one round of 21-tile chunks (455 workgroups in the 460 slots; 20
     # tiles would need 476 and spill into a second round)
     assert _simulated_chunk(128, True, 1, slots) == 21 and _slice_workgroups(128, 21, True) == 455

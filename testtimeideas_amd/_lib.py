@@ -475,6 +475,9 @@ def bwd(q, k, v, o, do, lse, p, mask, scale: float):
     cq = _split_for(ENTRY_BWD_DQ, q, m, scale, lp, False, lambda c: run(c, 0))
     ck = _split_for(ENTRY_BWD_DKDV, q, m, scale, lp, False, lambda c: run(cq, c))
     if _timing is None:
+        if cq == 0 and ck == 0:
+            return tuple(ext().bwd_fused(q, k, v, o, do, lse, p, m.causal, float(scale), int(m.window),
+                                         int(m.window_kind), m.bias))
         return tuple(run(cq, ck))
     dq = _empty_like_out(q)
     dk = _empty_like_out(k)

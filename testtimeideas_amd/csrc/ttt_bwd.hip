@@ -21,8 +21,7 @@
 //
 // Reference semantics: ttt_kernels/triton_attention.py:364-378 (save_p torch
 // backward), :416-420 (recompute); ttt_kernels/backward_stubs.py:124-425.
-#include "ttt_common.h"
-#include "ttt_launch.h"
+#include "ttt_combine.h"
 
 // Fetch forms, measured on MI355X and kept:
 //  * 16-bit tiles stream into LDS by direct loads: the saved-P dQ kernel's
@@ -324,7 +323,8 @@ struct DkdvWaves {
 
 template <typename T, int D, bool LOADP, bool DV_ONLY, bool XM>
 __global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(DkdvWaves<T, D, LOADP, DV_ONLY>::value))) void k_bwd_dkdv(Params a) {
+__attribute__((amdgpu_waves_per_eu(DkdvWaves<T, D, LOADP, DV_ONLY>::value))) void k_bwd_dkdv(Params a, Params dqc,
+                                                                                              int nx) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
@@ -369,6 +369,13 @@ __attribute__((amdgpu_waves_per_eu(DkdvWaves<T, D, LOADP, DV_ONLY>::value))) voi
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
   const Slot sl = grid_slot();
+  // Workgroups past the first nx columns of the grid finish the preceding dQ
+  // launch's split blocks (its partials are complete in stream order), in the
+  // tail of this launch rather than in a launch of their own.
+  if (sl.x >= nx) {
+    combine_sum_block<T, D>(dqc, kOutDQ, sl.x - nx, sl.y);
+    return;
+  }
   const int nb = sl.x % nblk, ch = sl.x / nblk;  // causal: column 0 has the most tiles
   const int bh = sl.y, b = bh / a.H, h = bh % a.H;
   const Range rg = col_block_range(nb, nblk, T_, a.causal, XM ? a.win : 0, a.win_kind);
@@ -621,40 +628,45 @@ static void launch_dq_x(const Params& a, bool load_p, dim3 grid, hipStream_t st)
 }
 
 template <typename T, int D>
-static hipError_t launch_dq_t(int dtype, const Params& a, bool load_p, hipStream_t st) {
+static hipError_t launch_dq_t(int dtype, const Params& a, bool load_p, hipStream_t st, bool combine) {
   const int nblk = (a.T + kBlk - 1) / kBlk;
   dim3 grid(nblk * a.nchunk_max, a.B * a.H);
   if (extended_mask(a))
     launch_dq_x<T, D, true>(a, load_p, grid, st);
   else
     launch_dq_x<T, D, false>(a, load_p, grid, st);
-  if (a.nchunk_max > 1) return launch_combine_sum(dtype, D, a, kOutDQ, st);
+  if (combine && a.nchunk_max > 1) return launch_combine_sum(dtype, D, a, kOutDQ, st);
   return hipGetLastError();
 }
 
 template <typename T, int D, bool XM>
-static void launch_dkdv_x(const Params& a, bool load_p, bool dv_only, dim3 grid, hipStream_t st) {
+static void launch_dkdv_x(const Params& a, bool load_p, bool dv_only, dim3 grid, hipStream_t st, const Params& c,
+                          int nx) {
   if (load_p) {
     if (dv_only)
-      hipLaunchKernelGGL((k_bwd_dkdv<T, D, true, true, XM>), grid, dim3(kThreads), 0, st, a);
+      hipLaunchKernelGGL((k_bwd_dkdv<T, D, true, true, XM>), grid, dim3(kThreads), 0, st, a, c, nx);
     else
-      hipLaunchKernelGGL((k_bwd_dkdv<T, D, true, false, XM>), grid, dim3(kThreads), 0, st, a);
+      hipLaunchKernelGGL((k_bwd_dkdv<T, D, true, false, XM>), grid, dim3(kThreads), 0, st, a, c, nx);
   } else {
     if (dv_only)
-      hipLaunchKernelGGL((k_bwd_dkdv<T, D, false, true, XM>), grid, dim3(kThreads), 0, st, a);
+      hipLaunchKernelGGL((k_bwd_dkdv<T, D, false, true, XM>), grid, dim3(kThreads), 0, st, a, c, nx);
     else
-      hipLaunchKernelGGL((k_bwd_dkdv<T, D, false, false, XM>), grid, dim3(kThreads), 0, st, a);
+      hipLaunchKernelGGL((k_bwd_dkdv<T, D, false, false, XM>), grid, dim3(kThreads), 0, st, a, c, nx);
   }
 }
 
 template <typename T, int D>
-static hipError_t launch_dkdv_t(int dtype, const Params& a, bool load_p, bool dv_only, hipStream_t st) {
+static hipError_t launch_dkdv_t(int dtype, const Params& a, bool load_p, bool dv_only, hipStream_t st,
+                                const Params* dqc) {
   const int nblk = (a.T + kBlk - 1) / kBlk;
-  dim3 grid(nblk * a.nchunk_max, a.B * a.H);
+  const int nx = nblk * a.nchunk_max;
+  const bool fold = dqc && dqc->nchunk_max > 1;
+  dim3 grid(nx + (fold ? nblk * CombineSlot<D>::kSub : 0), a.B * a.H);
+  const Params& c = fold ? *dqc : a;
   if (extended_mask(a))
-    launch_dkdv_x<T, D, true>(a, load_p, dv_only, grid, st);
+    launch_dkdv_x<T, D, true>(a, load_p, dv_only, grid, st, c, nx);
   else
-    launch_dkdv_x<T, D, false>(a, load_p, dv_only, grid, st);
+    launch_dkdv_x<T, D, false>(a, load_p, dv_only, grid, st, c, nx);
   if (a.nchunk_max > 1) return launch_combine_sum(dtype, D, a, dv_only ? kOutDV : kOutDKDV, st);
   return hipGetLastError();
 }
@@ -692,13 +704,14 @@ int occupancy_dkdv(int dtype, int D, bool load_p, bool xm) {
   return 0;
 }
 
-hipError_t launch_bwd_dq(int dtype, int D, const Params& a, bool load_p, hipStream_t st) {
-  DISPATCH_DTYPE_D(dtype, D, return launch_dq_t<ElemT, kD>(dtype, a, load_p, st));
+hipError_t launch_bwd_dq(int dtype, int D, const Params& a, bool load_p, hipStream_t st, bool combine) {
+  DISPATCH_DTYPE_D(dtype, D, return launch_dq_t<ElemT, kD>(dtype, a, load_p, st, combine));
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_bwd_dkdv(int dtype, int D, const Params& a, bool load_p, bool dv_only, hipStream_t st) {
-  DISPATCH_DTYPE_D(dtype, D, return launch_dkdv_t<ElemT, kD>(dtype, a, load_p, dv_only, st));
+hipError_t launch_bwd_dkdv(int dtype, int D, const Params& a, bool load_p, bool dv_only, hipStream_t st,
+                           const Params* dq_combine) {
+  DISPATCH_DTYPE_D(dtype, D, return launch_dkdv_t<ElemT, kD>(dtype, a, load_p, dv_only, st, dq_combine));
   return hipErrorInvalidValue;
 }
 

@@ -315,7 +315,8 @@ int64_t fam_bytes(const ttt_problem* pr, int fam) {
 }
 
 int64_t entry_bytes(const ttt_problem* pr, int entry, bool gdo) {
-  if (entry == TTT_ENTRY_BWD) return std::max(fam_bytes(pr, ttt::kFamDq), fam_bytes(pr, ttt::kFamDkdv));
+  // the fused backward keeps dQ's partials while dK/dV writes its own
+  if (entry == TTT_ENTRY_BWD) return fam_bytes(pr, ttt::kFamDq) + fam_bytes(pr, ttt::kFamDkdv);
   if (entry == TTT_ENTRY_GG)
     return std::max(fam_bytes(pr, family_of(TTT_ENTRY_GG_ROW, gdo)), fam_bytes(pr, ttt::kFamGgCol));
   const int fam = family_of(entry, gdo);
@@ -497,10 +498,12 @@ int ttt_attn_fill_masked_p(const ttt_problem* pr, const ttt_view* p, void* strea
   return launched(ttt::launch_fill_masked_p(pr->dtype, a, (hipStream_t)stream), "ttt_attn_fill_masked_p");
 }
 
-int ttt_attn_bwd_dq(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
-                    const ttt_view* o, const ttt_view* dout, const float* lse, const ttt_view* p,
-                    const float* rowsum_in, float* rowsum_out, const ttt_view* dq, void* workspace,
-                    int64_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+// Parameters of the dQ launch (ttt_attn_bwd_dq), its split and workspace.
+static int prep_dq(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
+                   const ttt_view* o, const ttt_view* dout, const float* lse, const ttt_view* p, const float* rowsum_in,
+                   float* rowsum_out, const ttt_view* dq, void* workspace, int64_t workspace_bytes, ttt::Params* out) {
   TRY(check_problem(pr));
   ttt::Params a = base_params(pr);
   TRY(take_view(pr, k, "k", &a.k));
@@ -520,14 +523,15 @@ int ttt_attn_bwd_dq(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
   a.rowsum_out = rowsum_out;
   if (!rowsum_in) TRY(take_view(pr, o, "o (needed to form D without rowsum_in)", &a.o));
   TRY(attach_split(pr, ttt::kFamDq, lp, workspace, workspace_bytes, &a));
-  return launched(ttt::launch_bwd_dq(pr->dtype, (int)pr->head_dim, a, lp, (hipStream_t)stream),
-                  "ttt_attn_bwd_dq");
+  *out = a;
+  return TTT_OK;
 }
 
-int ttt_attn_bwd_dkdv(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
-                      const ttt_view* dout, const float* lse, const ttt_view* p, const float* rowsum,
-                      const ttt_view* dk, const ttt_view* dv, void* workspace, int64_t workspace_bytes,
-                      void* stream) {
+// Parameters of the dK/dV launch (ttt_attn_bwd_dkdv), its split and workspace.
+static int prep_dkdv(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
+                     const ttt_view* dout, const float* lse, const ttt_view* p, const float* rowsum,
+                     const ttt_view* dk, const ttt_view* dv, void* workspace, int64_t workspace_bytes,
+                     ttt::Params* out) {
   TRY(check_problem(pr));
   ttt::Params a = base_params(pr);
   const bool lp = has_p(p);
@@ -549,19 +553,55 @@ int ttt_attn_bwd_dkdv(const ttt_problem* pr, const ttt_view* q, const ttt_view* 
   a.lse = const_cast<float*>(lse);
   a.rowsum_in = rowsum;
   TRY(attach_split(pr, ttt::kFamDkdv, lp, workspace, workspace_bytes, &a));
-  return launched(ttt::launch_bwd_dkdv(pr->dtype, (int)pr->head_dim, a, lp, dv_only, (hipStream_t)stream),
+  *out = a;
+  return TTT_OK;
+}
+
+extern "C" {
+
+int ttt_attn_bwd_dq(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
+                    const ttt_view* o, const ttt_view* dout, const float* lse, const ttt_view* p,
+                    const float* rowsum_in, float* rowsum_out, const ttt_view* dq, void* workspace,
+                    int64_t workspace_bytes, void* stream) {
+  ttt::Params a;
+  TRY(prep_dq(pr, q, k, v, o, dout, lse, p, rowsum_in, rowsum_out, dq, workspace, workspace_bytes, &a));
+  return launched(ttt::launch_bwd_dq(pr->dtype, (int)pr->head_dim, a, has_p(p), (hipStream_t)stream),
+                  "ttt_attn_bwd_dq");
+}
+
+int ttt_attn_bwd_dkdv(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
+                      const ttt_view* dout, const float* lse, const ttt_view* p, const float* rowsum,
+                      const ttt_view* dk, const ttt_view* dv, void* workspace, int64_t workspace_bytes,
+                      void* stream) {
+  ttt::Params a;
+  TRY(prep_dkdv(pr, q, k, v, dout, lse, p, rowsum, dk, dv, workspace, workspace_bytes, &a));
+  const bool dv_only = !(dk && dk->data);
+  return launched(ttt::launch_bwd_dkdv(pr->dtype, (int)pr->head_dim, a, has_p(p), dv_only, (hipStream_t)stream),
                   "ttt_attn_bwd_dkdv");
 }
 
+// dQ's partials go in the first part of the workspace and dK/dV's after them:
+// the dK/dV launch sums dQ's split blocks in workgroups appended to its grid
+// while its own blocks write their partials.
 int ttt_attn_bwd(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
                  const ttt_view* o, const ttt_view* dout, const float* lse, const ttt_view* p,
                  float* rowsum_out, const ttt_view* dq, const ttt_view* dk, const ttt_view* dv,
                  void* workspace, int64_t workspace_bytes, void* stream) {
   if (!rowsum_out) return fail(TTT_ERR_INVALID_ARGUMENT, "rowsum_out: null pointer");
   if (!dk || !dk->data) return fail(TTT_ERR_INVALID_ARGUMENT, "dk: null pointer");
-  TRY(ttt_attn_bwd_dq(pr, q, k, v, o, dout, lse, p, nullptr, rowsum_out, dq, workspace, workspace_bytes,
-                      stream));
-  return ttt_attn_bwd_dkdv(pr, q, k, v, dout, lse, p, rowsum_out, dk, dv, workspace, workspace_bytes, stream);
+  TRY(check_problem(pr));
+  const bool lp = has_p(p);
+  const int64_t dq_bytes = family_bytes(pr, choose_split(pr, ttt::kFamDq, lp), ttt::kFamDq);
+  const int64_t ws_bytes = workspace ? workspace_bytes : 0;
+  ttt::Params aq, ak;
+  TRY(prep_dq(pr, q, k, v, o, dout, lse, p, nullptr, rowsum_out, dq, workspace, ws_bytes, &aq));
+  if (ws_bytes < dq_bytes)  // prep_dq has checked this; kept for the pointer arithmetic below
+    return fail(TTT_ERR_WORKSPACE, "workspace of %lld bytes too small", (long long)ws_bytes);
+  void* ws_k = dq_bytes > 0 ? static_cast<void*>(static_cast<char*>(workspace) + dq_bytes) : workspace;
+  TRY(prep_dkdv(pr, q, k, v, dout, lse, p, rowsum_out, dk, dv, ws_k, ws_bytes - dq_bytes, &ak));
+  const hipStream_t st = (hipStream_t)stream;
+  TRY(launched(ttt::launch_bwd_dq(pr->dtype, (int)pr->head_dim, aq, lp, st, false), "ttt_attn_bwd"));
+  return launched(ttt::launch_bwd_dkdv(pr->dtype, (int)pr->head_dim, ak, lp, false, st, &aq), "ttt_attn_bwd");
 }
 
 int ttt_attn_bwd_rowsum(const ttt_problem* pr, const ttt_view* p, const ttt_view* dout, const ttt_view* v,

@@ -1,133 +1,19 @@
 // ttt_combine.hip — finish blocks whose streamed loop was split into chunks.
 //
-// Each main-kernel workgroup of a split block wrote fp32 partials to the
-// workspace: accumulators [part][nacc][64][D] and row scalars [part][nsc][64],
-// part = (bh*nblk + block)*nchunk_max + chunk.  The combine kernels read every
-// chunk of a block in chunk order (so results do not depend on scheduling) and
-// write the outputs.  Blocks with a single chunk were finished by the main
-// kernel and are skipped here.
-//
-// A block's 64 x D outputs are covered by D/16 workgroups; thread t of
-// workgroup `sub` owns one 4-wide slot: slot = 256*sub + t, row slot/(D/4),
-// columns 4*(slot % (D/4)) .. +3.  A thread issues the loads of all
-// accumulators of up to kBatch chunks together; the sums still run in chunk
-// order.
-#include "ttt_common.h"
-#include "ttt_launch.h"
+// The combine kernels read every chunk's fp32 partials of a block in chunk
+// order (layout and helpers in ttt_combine.h) and write the outputs.  Blocks
+// with a single chunk were finished by the main kernel and are skipped here.
+// A thread issues the loads of all accumulators of up to kBatch chunks
+// together; the sums still run in chunk order.
+#include "ttt_combine.h"
 
 namespace ttt {
-
-template <int D>
-struct CombineSlot {
-  static constexpr int kSub = kBlk * (D / 4) / kThreads;  // workgroups per block
-  int blk, r, d0;
-  __device__ __forceinline__ CombineSlot() {
-    blk = blockIdx.x / kSub;
-    const int slot = (blockIdx.x % kSub) * kThreads + threadIdx.x;
-    r = slot / (D / 4);
-    d0 = 4 * (slot % (D / 4));
-  }
-};
-
-__device__ __forceinline__ int block_nch(const Params& a, int blk, int nblk, bool col) {
-  const Range r = col ? col_block_range(blk, nblk, a.T, a.causal, a.win, a.win_kind)
-                      : row_block_range(blk, nblk, a.T, a.causal, a.win, a.win_kind);
-  return (r.hi - r.lo + a.chunk - 1) / a.chunk;
-}
-
-// Chunks whose loads a thread issues together before adding them.  The
-// loads of a batch are unconditional (chunk indices past nch-1 repeat the
-// last chunk) so that none waits for another; the adds still run in chunk
-// order 0, 1, ..., nch-1.
-constexpr int kBatch = 8;
-
-// out[i] = sum over chunks k (in order) of accumulator a0 + i at (r, d0..d0+3).
-template <int D, int NA>
-__device__ __forceinline__ void sum_parts(f32x4* out, const float* ws, int64_t p0, int nch, int nacc, int a0,
-                                          int r, int d0) {
-#pragma unroll
-  for (int i = 0; i < NA; ++i) out[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const float* base = ws + (p0 * nacc + a0) * kBlk * D + r * D + d0;
-  const int64_t step = (int64_t)nacc * kBlk * D;
-  for (int k0 = 0; k0 < nch; k0 += kBatch) {
-    f32x4 x[kBatch][NA];
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const int k = min(k0 + u, nch - 1);
-#pragma unroll
-      for (int i = 0; i < NA; ++i) x[u][i] = *reinterpret_cast<const f32x4*>(base + k * step + i * kBlk * D);
-    }
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u)
-      if (k0 + u < nch) {
-#pragma unroll
-        for (int i = 0; i < NA; ++i) out[i] += x[u][i];
-      }
-  }
-}
-
-// s[j] = sum over chunks k (in order) of row scalar j (of NS) at row r.
-template <int NS>
-__device__ __forceinline__ void sum_scalars(float* s, const float* ws_sc, int64_t p0, int nch, int r) {
-#pragma unroll
-  for (int j = 0; j < NS; ++j) s[j] = 0.f;
-  for (int k0 = 0; k0 < nch; k0 += kBatch) {
-    float x[kBatch][NS];
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const int k = min(k0 + u, nch - 1);
-#pragma unroll
-      for (int j = 0; j < NS; ++j) x[u][j] = ws_sc[(p0 + k) * NS * kBlk + j * kBlk + r];
-    }
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u)
-      if (k0 + u < nch) {
-#pragma unroll
-        for (int j = 0; j < NS; ++j) s[j] += x[u][j];
-      }
-  }
-}
-
-template <typename T>
-__device__ __forceinline__ void store_slot(const View& o, int b, int h, int row, int d0, f32x4 v) {
-  store4<T>(at<T>(o, b, h) + (int64_t)row * o.st + d0, v);
-}
 
 // ---------------------------------------------------------------------------
 // Plain sums: O (save_p forward), dQ, dK/dV, GK/GV.
 template <typename T, int D>
 __global__ __launch_bounds__(kThreads) void k_combine_sum(Params a, int which) {
-  const int T_ = a.T;
-  const int nblk = (T_ + kBlk - 1) / kBlk;
-  const CombineSlot<D> cs;
-  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
-  const bool col = which == kOutDKDV || which == kOutDV || which == kOutGKGV;
-  const int nch = block_nch(a, cs.blk, nblk, col);
-  if (nch <= 1) return;
-  const int row = cs.blk * kBlk + cs.r;
-  if (row >= T_) return;
-  const int64_t p0 = part_index(a, bh, nblk, cs.blk, 0);
-  if (which == kOutO || which == kOutDQ) {
-    f32x4 v;
-    sum_parts<D, 1>(&v, a.ws_acc, p0, nch, 1, 0, cs.r, cs.d0);
-    if (which == kOutO)
-      store_slot<T>(a.o, b, h, row, cs.d0, v);
-    else
-      store_slot<T>(a.dq, b, h, row, cs.d0, v * a.scale);
-    return;
-  }
-  // two-accumulator column kernels: index 0 = dV / GK, index 1 = dK / GV
-  const bool gg = which == kOutGKGV;
-  if (which == kOutDV) {
-    f32x4 v;
-    sum_parts<D, 1>(&v, a.ws_acc, p0, nch, 2, 0, cs.r, cs.d0);
-    store_slot<T>(a.dv, b, h, row, cs.d0, v);
-    return;
-  }
-  f32x4 v[2];
-  sum_parts<D, 2>(v, a.ws_acc, p0, nch, 2, 0, cs.r, cs.d0);
-  store_slot<T>(gg ? a.gk_out : a.dv, b, h, row, cs.d0, v[0] * (gg ? a.scale : 1.f));
-  store_slot<T>(gg ? a.gv_out : a.dk, b, h, row, cs.d0, v[1] * (gg ? 1.f : a.scale));
+  combine_sum_block<T, D>(a, which, blockIdx.x, blockIdx.y);
 }
 
 // ---------------------------------------------------------------------------
@@ -136,7 +22,7 @@ template <typename T, int D>
 __global__ __launch_bounds__(kThreads) void k_combine_fwd(Params a) {
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
-  const CombineSlot<D> cs;
+  const CombineSlot<D> cs(blockIdx.x);
   const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
   const int nch = block_nch(a, cs.blk, nblk, false);
   if (nch <= 1) return;
@@ -185,7 +71,7 @@ __global__ __launch_bounds__(kThreads) void k_combine_gg_row(Params a) {
   constexpr int NACC = GDO ? 5 : 3;
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
-  const CombineSlot<D> cs;
+  const CombineSlot<D> cs(blockIdx.x);
   const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
   const int nch = block_nch(a, cs.blk, nblk, false);
   if (nch <= 1) return;

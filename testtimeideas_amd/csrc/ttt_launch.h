@@ -93,8 +93,12 @@ hipError_t launch_fill_masked_p(int dtype, const Params& a, hipStream_t st);
 hipError_t launch_combine_sum(int dtype, int D, const Params& a, int which, hipStream_t st);
 hipError_t launch_combine_fwd(int dtype, int D, const Params& a, hipStream_t st);
 hipError_t launch_combine_gg_row(int dtype, int D, const Params& a, bool gdo, hipStream_t st);
-hipError_t launch_bwd_dq(int dtype, int D, const Params& a, bool load_p, hipStream_t st);
-hipError_t launch_bwd_dkdv(int dtype, int D, const Params& a, bool load_p, bool dv_only, hipStream_t st);
+// combine = false leaves a split dQ's partials for the dK/dV launch that
+// follows (launch_bwd_dkdv with dq_combine = that launch's parameters), which
+// finishes them in workgroups appended to its grid.
+hipError_t launch_bwd_dq(int dtype, int D, const Params& a, bool load_p, hipStream_t st, bool combine = true);
+hipError_t launch_bwd_dkdv(int dtype, int D, const Params& a, bool load_p, bool dv_only, hipStream_t st,
+                           const Params* dq_combine = nullptr);
 hipError_t launch_bwd_rowsum(int dtype, int D, const Params& a, hipStream_t st);
 hipError_t launch_gg_row64(int dtype, const Params& a, bool load_p, bool want_gdout, hipStream_t st);
 hipError_t launch_gg_row128h(int dtype, const Params& a, bool load_p, bool want_gdout, hipStream_t st);

@@ -1,6 +1,6 @@
 // ttt_torch.cpp — torch binding of the forward, backward and double backward
-// of the C ABI (include/ttt_attn.h): ttt_attn_fwd, then ttt_attn_bwd_dq +
-// ttt_attn_bwd_dkdv (what ttt_attn_bwd does) and ttt_attn_gg_row +
+// of the C ABI (include/ttt_attn.h): ttt_attn_fwd, then ttt_attn_bwd (or
+// ttt_attn_bwd_dq + ttt_attn_bwd_dkdv with splits of their own) and ttt_attn_gg_row +
 // ttt_attn_gg_col (what ttt_attn_gg does), each kernel family with its own
 // split (tiles per workgroup; 0 lets the library choose).
 //
@@ -156,6 +156,29 @@ std::vector<at::Tensor> bwd(const at::Tensor& q, const at::Tensor& k, const at::
   return {dq, dk, dv, rowsum};
 }
 
+// The same through ttt_attn_bwd when both families take the library's split:
+// the dK/dV launch then also finishes dQ's split blocks.
+std::vector<at::Tensor> bwd_fused(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                                  const at::Tensor& o, const at::Tensor& dout, const at::Tensor& lse,
+                                  const c10::optional<at::Tensor>& p, bool causal, double scale, int64_t window,
+                                  int64_t window_kind, const c10::optional<at::Tensor>& bias) {
+  const ttt_problem pr = problem_of(q, causal, scale, 0, window, window_kind, bias);
+  at::Tensor dq = at::empty(q.sizes(), q.options());
+  at::Tensor dk = at::empty(k.sizes(), k.options());
+  at::Tensor dv = at::empty(v.sizes(), v.options());
+  at::Tensor rowsum = stats_of(q);
+  int64_t wsb = 0;
+  at::Tensor ws = workspace(pr, TTT_ENTRY_BWD, false, q, &wsb);
+  const bool lp = p && p->defined();
+  const ttt_view vq = view_of(q), vk = view_of(k), vv = view_of(v), vo = view_of(o), vdo = view_of(dout);
+  const ttt_view vp = lp ? view_of(*p) : none_view();
+  const ttt_view vdq = view_of(dq), vdk = view_of(dk), vdv = view_of(dv);
+  check(ttt_attn_bwd(&pr, &vq, &vk, &vv, &vo, &vdo, lse.data_ptr<float>(), lp ? &vp : nullptr,
+                     rowsum.data_ptr<float>(), &vdq, &vdk, &vdv, ptr_or_null(ws), wsb, stream_of(q)),
+        "ttt_attn_bwd");
+  return {dq, dk, dv, rowsum};
+}
+
 // Double backward: (GQ, GK, GV, GdO or None).
 std::vector<at::Tensor> gg(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const at::Tensor& dout,
                            const at::Tensor& lse, const c10::optional<at::Tensor>& p, const at::Tensor& rowsum,
@@ -196,5 +219,6 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "torch binding of the forward, backward and double backward of libttt_attn.so";
   m.def("fwd", &fwd, "forward: (O, LSE, P or None)");
   m.def("bwd", &bwd, "first backward: (dQ, dK, dV, D)");
+  m.def("bwd_fused", &bwd_fused, "first backward in one entry call: (dQ, dK, dV, D)");
   m.def("gg", &gg, "double backward: (GQ, GK, GV, GdO or None)");
 }

@@ -269,8 +269,12 @@ int ttt_attn_gg_col(const ttt_problem* pr, const ttt_view* q,
                     int64_t workspace_bytes, void* stream);
 
 /*
- * Full double backward in one call: ttt_attn_gg_row then ttt_attn_gg_col on
- * the same stream.  e_buf and f_buf are caller-owned fp32 [B*H*T] buffers.
+ * Full double backward in one call: the work of ttt_attn_gg_row then
+ * ttt_attn_gg_col on the same stream, with bitwise the same results.  e_buf
+ * and f_buf are caller-owned fp32 [B*H*T] buffers.  When the row pass is
+ * split, a small launch forms E and F, and the column launch also sums GQ
+ * (and GdO) in workgroups appended to its grid, so the workspace
+ * (TTT_ENTRY_GG) holds both passes' partials at once.
  * Replaces: TritonDqDkFn.backward + TritonRowSumFn.backward +
  * TritonDvFn.backward, backward_stubs.py:434-514, as reached from
  * TritonAttentionFn.backward with create_graph=True, triton_attention.py:354-358.

@@ -173,6 +173,42 @@ def test_fused_backward_entry(b, h, t, d, dtype, save_p, chunk):
         assert torch.equal(x, y), n
 
 
+@pytest.mark.parametrize("b,h,t,d,dtype,save_p,gdo,chunk", [
+    (1, 2, 192, 64, "fp16", True, False, 1),
+    (1, 1, 300, 64, "bf16", True, True, 2),
+    (2, 4, 200, 64, "fp16", False, False, 2),
+    (2, 4, 200, 64, "bf16", True, True, 3),
+    (1, 3, 257, 128, "bf16", True, False, 2),
+    (1, 2, 190, 128, "fp16", True, True, 2),
+    (1, 2, 130, 128, "fp32", False, True, 2),
+    (1, 1, 1024, 64, "fp16", True, False, 0),
+])
+def test_fused_double_backward_entry(b, h, t, d, dtype, save_p, gdo, chunk):
+    """ttt_attn_gg, whose column launch also finishes the row pass's split
+    blocks, gives bitwise the results of ttt_attn_gg_row + ttt_attn_gg_col."""
+    import ctypes
+    dt = DT[dtype]
+    q, k, v, do, gq, gk, gv = (x.cuda() for x in _inputs(b, h, t, d, dt, seed=t + d + 1))
+    print(f"[case] fused gg b={b} h={h} t={t} d={d} {dtype} save_p={save_p} gdo={gdo} chunk={chunk}", flush=True)
+    o, lse, p = _lib.fwd(q, k, v, True, 0.125, save_p)
+    _, _, _, rs = _lib.bwd(q, k, v, o, do, lse, p, True, 0.125)
+    with _lib.split_chunk(chunk), _lib.kernel_timing():  # timing: the row and column entry points
+        ref = _lib.gg(q, k, v, do, lse, p, rs, gq, gk, gv, True, 0.125, gdo)
+    pr = _lib._problem(q, True, 0.125, chunk)
+    out = [torch.empty_like(x) for x in (q, k, v)] + [torch.empty_like(do) if gdo else None]
+    e = torch.empty(b, h, t, dtype=torch.float32, device=q.device)
+    f = torch.empty_like(e)
+    wp, wn, _buf = _lib._workspace(pr, _lib.ENTRY_GG, q.device, gdo)
+    _lib._call("ttt_attn_gg", ctypes.byref(pr), _lib._view(q), _lib._view(k), _lib._view(v), _lib._view(do),
+               _lib._fptr(lse), _lib._view(p), rs.data_ptr(), _lib._view(gq), _lib._view(gk), _lib._view(gv),
+               _lib._view(out[0]), _lib._view(out[1]), _lib._view(out[2]), _lib._view(out[3]), e.data_ptr(),
+               f.data_ptr(), wp, wn, _lib._stream())
+    torch.cuda.synchronize()
+    for n, x, y in zip(("gq", "gk", "gv", "gdo"), out, ref):
+        if y is not None:
+            assert torch.equal(x, y), n
+
+
 def test_deterministic():
     """Two runs give bitwise identical outputs (no atomics anywhere)."""
     xs = _inputs(1, 1, 320, 64, torch.bfloat16, seed=4)

@@ -235,7 +235,9 @@ def test_workspace_sizes():
         parts = bh * nblk * k if k > 1 else 0
         assert _lib.workspace_bytes(pr, _lib.ENTRY_FWD) == parts * 64 * (64 + 2) * 4, (t, causal, bh, c)
         assert _lib.workspace_bytes(pr, _lib.ENTRY_GG_ROW) == parts * 64 * (3 * 64 + 3) * 4
-        assert _lib.workspace_bytes(pr, _lib.ENTRY_GG, True) == parts * 64 * (5 * 64 + 3) * 4
+        # the fused double backward holds the row pass's partials (five accumulators, three row scalars)
+        # and the column pass's (two accumulators) at once
+        assert _lib.workspace_bytes(pr, _lib.ENTRY_GG, True) == parts * 64 * (5 * 64 + 3 + 2 * 64) * 4
         # the fused backward holds dQ's partials (one accumulator) and dK/dV's (two) at once
         assert _lib.workspace_bytes(pr, _lib.ENTRY_BWD) == parts * 64 * (3 * 64) * 4
     # C3: one round of 21-tile chunks (455 workgroups in the 460 slots; 20

@@ -562,6 +562,9 @@ def gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, mask, scale: float, want_gdo: bo
     cr = _split_for(ENTRY_GG_ROW, q, m, scale, lp, want_gdo, lambda c: run(c, 0))
     cc = _split_for(ENTRY_GG_COL, q, m, scale, lp, False, lambda c: run(cr, c))
     if _timing is None:
+        if cr == 0 and cc == 0:
+            return tuple(ext().gg_fused(q, k, v, do, lse, p, rowsum, gq, gk, gv, m.causal, float(scale),
+                                        bool(want_gdo), int(m.window), int(m.window_kind), m.bias))
         return tuple(run(cr, cc))
     gq_out = _empty_like_out(q)
     gk_out = _empty_like_out(k)

@@ -317,8 +317,9 @@ int64_t fam_bytes(const ttt_problem* pr, int fam) {
 int64_t entry_bytes(const ttt_problem* pr, int entry, bool gdo) {
   // the fused backward keeps dQ's partials while dK/dV writes its own
   if (entry == TTT_ENTRY_BWD) return fam_bytes(pr, ttt::kFamDq) + fam_bytes(pr, ttt::kFamDkdv);
-  if (entry == TTT_ENTRY_GG)
-    return std::max(fam_bytes(pr, family_of(TTT_ENTRY_GG_ROW, gdo)), fam_bytes(pr, ttt::kFamGgCol));
+  // the fused double backward keeps the row pass's partials while the column
+  // pass writes its own
+  if (entry == TTT_ENTRY_GG) return fam_bytes(pr, family_of(TTT_ENTRY_GG_ROW, gdo)) + fam_bytes(pr, ttt::kFamGgCol);
   const int fam = family_of(entry, gdo);
   return fam < 0 ? -1 : fam_bytes(pr, fam);
 }
@@ -620,11 +621,11 @@ int ttt_attn_bwd_rowsum(const ttt_problem* pr, const ttt_view* p, const ttt_view
 
 // ttt_attn_gg_row / ttt_attn_gg_col with the split's partials held to `cap`
 // bytes (cap < 0: no limit).
-static int gg_row_impl(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
+static int prep_gg_row(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
                        const ttt_view* dout, const float* lse, const ttt_view* p, const float* rowsum,
                        const ttt_view* gq, const ttt_view* gk, const ttt_view* gv, const ttt_view* gq_out,
                        const ttt_view* gdout, float* e_out, float* f_out, void* workspace, int64_t workspace_bytes,
-                       void* stream, int64_t cap) {
+                       int64_t cap, ttt::Params* out) {
   TRY(check_problem(pr));
   ttt::Params a = base_params(pr);
   TRY(take_view(pr, q, "q", &a.q));
@@ -647,15 +648,28 @@ static int gg_row_impl(const ttt_problem* pr, const ttt_view* q, const ttt_view*
   a.e = e_out;
   a.f = f_out;
   TRY(attach_split(pr, gdo ? ttt::kFamGgRowGdo : ttt::kFamGgRow, lp, workspace, workspace_bytes, &a, cap));
-  return launched(ttt::launch_gg_row(pr->dtype, (int)pr->head_dim, a, lp, gdo, (hipStream_t)stream),
+  *out = a;
+  return TTT_OK;
+}
+
+static int gg_row_impl(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
+                       const ttt_view* dout, const float* lse, const ttt_view* p, const float* rowsum,
+                       const ttt_view* gq, const ttt_view* gk, const ttt_view* gv, const ttt_view* gq_out,
+                       const ttt_view* gdout, float* e_out, float* f_out, void* workspace, int64_t workspace_bytes,
+                       void* stream, int64_t cap) {
+  ttt::Params a;
+  TRY(prep_gg_row(pr, q, k, v, dout, lse, p, rowsum, gq, gk, gv, gq_out, gdout, e_out, f_out, workspace,
+                  workspace_bytes, cap, &a));
+  return launched(ttt::launch_gg_row(pr->dtype, (int)pr->head_dim, a, has_p(p), a.gdout.p != nullptr,
+                                     (hipStream_t)stream),
                   "ttt_attn_gg_row");
 }
 
-static int gg_col_impl(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
+static int prep_gg_col(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
                        const ttt_view* dout, const float* lse, const ttt_view* p, const float* rowsum,
                        const float* e_in, const float* f_in, const ttt_view* gq, const ttt_view* gk,
                        const ttt_view* gv, const ttt_view* gk_out, const ttt_view* gv_out, void* workspace,
-                       int64_t workspace_bytes, void* stream, int64_t cap) {
+                       int64_t workspace_bytes, int64_t cap, ttt::Params* out) {
   TRY(check_problem(pr));
   ttt::Params a = base_params(pr);
   TRY(take_view(pr, q, "q", &a.q));
@@ -677,7 +691,19 @@ static int gg_col_impl(const ttt_problem* pr, const ttt_view* q, const ttt_view*
   a.e = const_cast<float*>(e_in);
   a.f = const_cast<float*>(f_in);
   TRY(attach_split(pr, ttt::kFamGgCol, lp, workspace, workspace_bytes, &a, cap));
-  return launched(ttt::launch_gg_col(pr->dtype, (int)pr->head_dim, a, lp, (hipStream_t)stream),
+  *out = a;
+  return TTT_OK;
+}
+
+static int gg_col_impl(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
+                       const ttt_view* dout, const float* lse, const ttt_view* p, const float* rowsum,
+                       const float* e_in, const float* f_in, const ttt_view* gq, const ttt_view* gk,
+                       const ttt_view* gv, const ttt_view* gk_out, const ttt_view* gv_out, void* workspace,
+                       int64_t workspace_bytes, void* stream, int64_t cap) {
+  ttt::Params a;
+  TRY(prep_gg_col(pr, q, k, v, dout, lse, p, rowsum, e_in, f_in, gq, gk, gv, gk_out, gv_out, workspace,
+                  workspace_bytes, cap, &a));
+  return launched(ttt::launch_gg_col(pr->dtype, (int)pr->head_dim, a, has_p(p), (hipStream_t)stream),
                   "ttt_attn_gg_col");
 }
 
@@ -704,10 +730,27 @@ int ttt_attn_gg(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, con
                 const ttt_view* gq, const ttt_view* gk, const ttt_view* gv, const ttt_view* gq_out,
                 const ttt_view* gk_out, const ttt_view* gv_out, const ttt_view* gdout, float* e_buf,
                 float* f_buf, void* workspace, int64_t workspace_bytes, void* stream) {
-  TRY(ttt_attn_gg_row(pr, q, k, v, dout, lse, p, rowsum, gq, gk, gv, gq_out, gdout, e_buf, f_buf, workspace,
-                      workspace_bytes, stream));
-  return ttt_attn_gg_col(pr, q, k, v, dout, lse, p, rowsum, e_buf, f_buf, gq, gk, gv, gk_out, gv_out, workspace,
-                         workspace_bytes, stream);
+  // The row pass's partials go in the first part of the workspace and the
+  // column pass's after them: the column launch sums the row pass's split
+  // blocks (GQ, GdO) in workgroups appended to its grid, after a small launch
+  // has formed E and F, which the column pass reads.
+  TRY(check_problem(pr));
+  const bool lp = has_p(p);
+  const bool gdo = gdout && gdout->data;
+  const int fam = gdo ? ttt::kFamGgRowGdo : ttt::kFamGgRow;
+  const int64_t row_bytes = family_bytes(pr, choose_split(pr, fam, lp), fam);
+  const int64_t ws_bytes = workspace ? workspace_bytes : 0;
+  ttt::Params ar, ac;
+  TRY(prep_gg_row(pr, q, k, v, dout, lse, p, rowsum, gq, gk, gv, gq_out, gdout, e_buf, f_buf, workspace, ws_bytes,
+                  -1, &ar));
+  if (ws_bytes < row_bytes)  // prep_gg_row has checked this; kept for the pointer arithmetic below
+    return fail(TTT_ERR_WORKSPACE, "workspace of %lld bytes too small", (long long)ws_bytes);
+  void* ws_c = row_bytes > 0 ? static_cast<void*>(static_cast<char*>(workspace) + row_bytes) : workspace;
+  TRY(prep_gg_col(pr, q, k, v, dout, lse, p, rowsum, e_buf, f_buf, gq, gk, gv, gk_out, gv_out, ws_c,
+                  ws_bytes - row_bytes, -1, &ac));
+  const hipStream_t st = (hipStream_t)stream;
+  TRY(launched(ttt::launch_gg_row(pr->dtype, (int)pr->head_dim, ar, lp, gdo, st, false), "ttt_attn_gg"));
+  return launched(ttt::launch_gg_col(pr->dtype, (int)pr->head_dim, ac, lp, st, &ar), "ttt_attn_gg");
 }
 
 int ttt_attn_gg_noalloc(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,

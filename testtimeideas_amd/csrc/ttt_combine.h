@@ -130,4 +130,45 @@ __device__ __forceinline__ void combine_sum_block(const Params& a, int which, in
   store_slot<T>(gg ? a.gv_out : a.dk, b, h, row, cs.d0, v[1] * (gg ? 1.f : a.scale));
 }
 
+// ---------------------------------------------------------------------------
+// Grad-grad row pass, combine workgroup (bx, by): E and F from the chunk
+// sums (written when write_ef), then GQ (and GdO).
+// Accumulators: 0..2 = dS*gK + Z1*K, Z2*K, P*K; 3..4 = P*gV + (P o gdS)*V, P*V.
+// Scalars: 0 = E, 1 = rowsum(Z1), 2 = rowsum(Z2).
+template <typename T, int D, bool GDO>
+__device__ __forceinline__ void combine_gg_row_block(const Params& a, int bx, int by, bool write_ef) {
+  constexpr int NACC = GDO ? 5 : 3;
+  const int T_ = a.T;
+  const int nblk = (T_ + kBlk - 1) / kBlk;
+  const CombineSlot<D> cs(bx);
+  const int bh = by, b = bh / a.H, h = bh % a.H;
+  const int nch = block_nch(a, cs.blk, nblk, false);
+  if (nch <= 1) return;
+  const int r = cs.r;
+  const int row = cs.blk * kBlk + r;
+  if (row >= T_) return;
+  const int64_t p0 = part_index(a, bh, nblk, cs.blk, 0);
+  float sc[3];
+  sum_scalars<3>(sc, a.ws_sc, p0, nch, r);
+  const float ev = sc[0], xv = sc[1], dv = sc[2];
+  const float fv = xv - ev * dv;
+  f32x4 t[3];
+  sum_parts<D, 3>(t, a.ws_acc, p0, nch, NACC, 0, r, cs.d0);
+  f32x4 acc = t[0];
+  acc -= ev * t[1];
+  acc = a.scale * (acc - fv * t[2]);
+  store_slot<T>(a.gq_out, b, h, row, cs.d0, acc);
+  if constexpr (GDO) {
+    f32x4 u[2];
+    sum_parts<D, 2>(u, a.ws_acc, p0, nch, NACC, 3, r, cs.d0);
+    f32x4 go = u[0];
+    go -= ev * u[1];
+    store_slot<T>(a.gdout, b, h, row, cs.d0, go);
+  }
+  if (write_ef && cs.d0 == 0) {
+    a.e[(int64_t)bh * T_ + row] = ev;
+    a.f[(int64_t)bh * T_ + row] = fv;
+  }
+}
+
 }  // namespace ttt

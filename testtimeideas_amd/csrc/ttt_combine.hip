@@ -63,43 +63,29 @@ __global__ __launch_bounds__(kThreads) void k_combine_fwd(Params a) {
 }
 
 // ---------------------------------------------------------------------------
-// Grad-grad row pass: E, F from chunk sums, then GQ (and GdO).
-// Accumulators: 0..2 = dS*gK + Z1*K, Z2*K, P*K; 3..4 = P*gV + (P o gdS)*V, P*V.
-// Scalars: 0 = E, 1 = rowsum(Z1), 2 = rowsum(Z2).
+// Grad-grad row pass: E, F, GQ (and GdO) of the split blocks.
 template <typename T, int D, bool GDO>
 __global__ __launch_bounds__(kThreads) void k_combine_gg_row(Params a) {
-  constexpr int NACC = GDO ? 5 : 3;
+  combine_gg_row_block<T, D, GDO>(a, blockIdx.x, blockIdx.y, true);
+}
+
+// E and F alone (one thread per row), for the fused double backward, whose
+// column launch sums GQ (and GdO) in workgroups appended to its grid.  The
+// same sums in the same order as combine_gg_row_block, so bitwise the same.
+__global__ __launch_bounds__(kThreads) void k_combine_gg_ef(Params a) {
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
-  const CombineSlot<D> cs(blockIdx.x);
-  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
-  const int nch = block_nch(a, cs.blk, nblk, false);
-  if (nch <= 1) return;
-  const int r = cs.r;
-  const int row = cs.blk * kBlk + r;
+  const int row = blockIdx.x * kThreads + threadIdx.x;
+  const int bh = blockIdx.y;
   if (row >= T_) return;
-  const int64_t p0 = part_index(a, bh, nblk, cs.blk, 0);
+  const int blk = row / kBlk, r = row % kBlk;
+  const int nch = block_nch(a, blk, nblk, false);
+  if (nch <= 1) return;
   float sc[3];
-  sum_scalars<3>(sc, a.ws_sc, p0, nch, r);
+  sum_scalars<3>(sc, a.ws_sc, part_index(a, bh, nblk, blk, 0), nch, r);
   const float ev = sc[0], xv = sc[1], dv = sc[2];
-  const float fv = xv - ev * dv;
-  f32x4 t[3];
-  sum_parts<D, 3>(t, a.ws_acc, p0, nch, NACC, 0, r, cs.d0);
-  f32x4 acc = t[0];
-  acc -= ev * t[1];
-  acc = a.scale * (acc - fv * t[2]);
-  store_slot<T>(a.gq_out, b, h, row, cs.d0, acc);
-  if constexpr (GDO) {
-    f32x4 u[2];
-    sum_parts<D, 2>(u, a.ws_acc, p0, nch, NACC, 3, r, cs.d0);
-    f32x4 go = u[0];
-    go -= ev * u[1];
-    store_slot<T>(a.gdout, b, h, row, cs.d0, go);
-  }
-  if (cs.d0 == 0) {
-    a.e[(int64_t)bh * T_ + row] = ev;
-    a.f[(int64_t)bh * T_ + row] = fv;
-  }
+  a.e[(int64_t)bh * T_ + row] = ev;
+  a.f[(int64_t)bh * T_ + row] = xv - ev * dv;
 }
 
 // ---------------------------------------------------------------------------
@@ -135,6 +121,12 @@ hipError_t launch_combine_sum(int dtype, int D, const Params& a, int which, hipS
 hipError_t launch_combine_fwd(int dtype, int D, const Params& a, hipStream_t st) {
   DISPATCH_DTYPE_D(dtype, D, return combine_fwd_t<ElemT, kD>(a, st));
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_combine_gg_ef(const Params& a, hipStream_t st) {
+  dim3 grid((a.T + kThreads - 1) / kThreads, a.B * a.H);
+  hipLaunchKernelGGL(k_combine_gg_ef, grid, dim3(kThreads), 0, st, a);
+  return hipGetLastError();
 }
 
 hipError_t launch_combine_gg_row(int dtype, int D, const Params& a, bool gdo, hipStream_t st) {

@@ -45,8 +45,7 @@
 // (C5 grad-grad -5 %).  The heaviest kernels (D = 128 with GdO, and fp32 at
 // D = 128) are built without it: ROCm 7.2's compiler crashes on some of them
 // with the flag.
-#include "ttt_common.h"
-#include "ttt_launch.h"
+#include "ttt_combine.h"
 
 #ifndef TTT_GG_HEAD_DIM
 #define TTT_GG_HEAD_DIM 64
@@ -450,7 +449,7 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, false>::value))) void k_gg_row(
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool LOADP, bool XM>
 __global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(GgWaves<T, D, true>::value))) void k_gg_col(Params a) {
+__attribute__((amdgpu_waves_per_eu(GgWaves<T, D, true>::value))) void k_gg_col(Params a, Params rowc, int nx) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
@@ -486,6 +485,16 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, true>::value))) void k_gg_col(P
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
   const Slot sl = grid_slot();
+  // Workgroups past the first nx columns of the grid finish the preceding row
+  // launch's split blocks (GQ, GdO; E and F are already written), in the tail
+  // of this launch rather than in a launch of their own.
+  if (sl.x >= nx) {
+    if (rowc.gdout.p)
+      combine_gg_row_block<T, D, true>(rowc, sl.x - nx, sl.y, false);
+    else
+      combine_gg_row_block<T, D, false>(rowc, sl.x - nx, sl.y, false);
+    return;
+  }
   const int nb = sl.x % nblk, ch = sl.x / nblk;
   const int bh = sl.y, b = bh / a.H, h = bh % a.H;
   const Range rg = col_block_range(nb, nblk, T_, a.causal, XM ? a.win : 0, a.win_kind);
@@ -698,31 +707,34 @@ static bool launch_gg_row_x(const Params& a, bool load_p, bool gdo, dim3 grid, h
 }
 
 template <typename T, int D>
-static hipError_t launch_gg_row_t(int dtype, const Params& a, bool load_p, bool gdo, hipStream_t st) {
+static hipError_t launch_gg_row_t(int dtype, const Params& a, bool load_p, bool gdo, hipStream_t st, bool combine) {
   const int nblk = (a.T + kBlk - 1) / kBlk;
   dim3 grid(nblk * a.nchunk_max, a.B * a.H);
   const bool ok = extended_mask(a) ? launch_gg_row_x<T, D, true>(a, load_p, gdo, grid, st)
                                     : launch_gg_row_x<T, D, false>(a, load_p, gdo, grid, st);
   if (!ok) return hipErrorInvalidDeviceFunction;
-  if (a.nchunk_max > 1) return launch_combine_gg_row(dtype, D, a, gdo, st);
+  if (a.nchunk_max > 1) return combine ? launch_combine_gg_row(dtype, D, a, gdo, st) : launch_combine_gg_ef(a, st);
   return hipGetLastError();
 }
 
 template <typename T, int D>
-static hipError_t launch_gg_col_t(int dtype, const Params& a, bool load_p, hipStream_t st) {
+static hipError_t launch_gg_col_t(int dtype, const Params& a, bool load_p, hipStream_t st, const Params* rowc) {
   const int nblk = (a.T + kBlk - 1) / kBlk;
-  dim3 grid(nblk * a.nchunk_max, a.B * a.H);
+  const int nx = nblk * a.nchunk_max;
+  const bool fold = rowc && rowc->nchunk_max > 1;
+  dim3 grid(nx + (fold ? nblk * CombineSlot<D>::kSub : 0), a.B * a.H);
+  const Params& c = fold ? *rowc : a;
   const bool xm = extended_mask(a);
   if (load_p) {
     if (xm)
-      hipLaunchKernelGGL((k_gg_col<T, D, true, true>), grid, dim3(kThreads), 0, st, a);
+      hipLaunchKernelGGL((k_gg_col<T, D, true, true>), grid, dim3(kThreads), 0, st, a, c, nx);
     else
-      hipLaunchKernelGGL((k_gg_col<T, D, true, false>), grid, dim3(kThreads), 0, st, a);
+      hipLaunchKernelGGL((k_gg_col<T, D, true, false>), grid, dim3(kThreads), 0, st, a, c, nx);
   } else {
     if (xm)
-      hipLaunchKernelGGL((k_gg_col<T, D, false, true>), grid, dim3(kThreads), 0, st, a);
+      hipLaunchKernelGGL((k_gg_col<T, D, false, true>), grid, dim3(kThreads), 0, st, a, c, nx);
     else
-      hipLaunchKernelGGL((k_gg_col<T, D, false, false>), grid, dim3(kThreads), 0, st, a);
+      hipLaunchKernelGGL((k_gg_col<T, D, false, false>), grid, dim3(kThreads), 0, st, a, c, nx);
   }
   if (a.nchunk_max > 1) return launch_combine_sum(dtype, D, a, kOutGKGV, st);
   return hipGetLastError();
@@ -773,8 +785,9 @@ int TTT_GG_NAME(occupancy_gg_row)(int dtype, bool load_p, bool gdo, bool xm) {
   return 0;
 }
 
-hipError_t TTT_GG_NAME(launch_gg_row)(int dtype, const Params& a, bool load_p, bool want_gdout, hipStream_t st) {
-  TTT_GG_DISPATCH(dtype, return launch_gg_row_t<ElemT, kD>(dtype, a, load_p, want_gdout, st));
+hipError_t TTT_GG_NAME(launch_gg_row)(int dtype, const Params& a, bool load_p, bool want_gdout, hipStream_t st,
+                                      bool combine) {
+  TTT_GG_DISPATCH(dtype, return launch_gg_row_t<ElemT, kD>(dtype, a, load_p, want_gdout, st, combine));
   return hipErrorInvalidValue;
 }
 
@@ -785,8 +798,8 @@ int TTT_GG_NAME(occupancy_gg_col)(int dtype, bool load_p, bool xm) {
   return 0;
 }
 
-hipError_t TTT_GG_NAME(launch_gg_col)(int dtype, const Params& a, bool load_p, hipStream_t st) {
-  TTT_GG_DISPATCH(dtype, return launch_gg_col_t<ElemT, kD>(dtype, a, load_p, st));
+hipError_t TTT_GG_NAME(launch_gg_col)(int dtype, const Params& a, bool load_p, hipStream_t st, const Params* rowc) {
+  TTT_GG_DISPATCH(dtype, return launch_gg_col_t<ElemT, kD>(dtype, a, load_p, st, rowc));
   return hipErrorInvalidValue;
 }
 #endif

@@ -100,24 +100,33 @@ hipError_t launch_bwd_dq(int dtype, int D, const Params& a, bool load_p, hipStre
 hipError_t launch_bwd_dkdv(int dtype, int D, const Params& a, bool load_p, bool dv_only, hipStream_t st,
                            const Params* dq_combine = nullptr);
 hipError_t launch_bwd_rowsum(int dtype, int D, const Params& a, hipStream_t st);
-hipError_t launch_gg_row64(int dtype, const Params& a, bool load_p, bool want_gdout, hipStream_t st);
-hipError_t launch_gg_row128h(int dtype, const Params& a, bool load_p, bool want_gdout, hipStream_t st);
-hipError_t launch_gg_row128hg(int dtype, const Params& a, bool load_p, bool want_gdout, hipStream_t st);
-hipError_t launch_gg_row128f(int dtype, const Params& a, bool load_p, bool want_gdout, hipStream_t st);
-hipError_t launch_gg_col64(int dtype, const Params& a, bool load_p, hipStream_t st);
-hipError_t launch_gg_col128h(int dtype, const Params& a, bool load_p, hipStream_t st);
-hipError_t launch_gg_col128f(int dtype, const Params& a, bool load_p, hipStream_t st);
-inline hipError_t launch_gg_row(int dtype, int D, const Params& a, bool load_p, bool want_gdout, hipStream_t st) {
-  if (D == 64) return launch_gg_row64(dtype, a, load_p, want_gdout, st);
+// The grad-grad row launch with combine = false finishes only E and F of its
+// split blocks (launch_combine_gg_ef); the column launch that follows, given
+// rowc = the row launch's parameters, sums GQ (and GdO) in workgroups
+// appended to its grid.
+hipError_t launch_combine_gg_ef(const Params& a, hipStream_t st);
+hipError_t launch_gg_row64(int dtype, const Params& a, bool load_p, bool want_gdout, hipStream_t st, bool combine);
+hipError_t launch_gg_row128h(int dtype, const Params& a, bool load_p, bool want_gdout, hipStream_t st, bool combine);
+hipError_t launch_gg_row128hg(int dtype, const Params& a, bool load_p, bool want_gdout, hipStream_t st,
+                              bool combine);
+hipError_t launch_gg_row128f(int dtype, const Params& a, bool load_p, bool want_gdout, hipStream_t st, bool combine);
+hipError_t launch_gg_col64(int dtype, const Params& a, bool load_p, hipStream_t st, const Params* rowc);
+hipError_t launch_gg_col128h(int dtype, const Params& a, bool load_p, hipStream_t st, const Params* rowc);
+hipError_t launch_gg_col128f(int dtype, const Params& a, bool load_p, hipStream_t st, const Params* rowc);
+inline hipError_t launch_gg_row(int dtype, int D, const Params& a, bool load_p, bool want_gdout, hipStream_t st,
+                                bool combine = true) {
+  if (D == 64) return launch_gg_row64(dtype, a, load_p, want_gdout, st, combine);
   if (D == 128)
-    return dtype == kF32 ? launch_gg_row128f(dtype, a, load_p, want_gdout, st)
-           : want_gdout  ? launch_gg_row128hg(dtype, a, load_p, want_gdout, st)
-                         : launch_gg_row128h(dtype, a, load_p, want_gdout, st);
+    return dtype == kF32 ? launch_gg_row128f(dtype, a, load_p, want_gdout, st, combine)
+           : want_gdout  ? launch_gg_row128hg(dtype, a, load_p, want_gdout, st, combine)
+                         : launch_gg_row128h(dtype, a, load_p, want_gdout, st, combine);
   return hipErrorInvalidValue;
 }
-inline hipError_t launch_gg_col(int dtype, int D, const Params& a, bool load_p, hipStream_t st) {
-  if (D == 64) return launch_gg_col64(dtype, a, load_p, st);
-  if (D == 128) return dtype == kF32 ? launch_gg_col128f(dtype, a, load_p, st) : launch_gg_col128h(dtype, a, load_p, st);
+inline hipError_t launch_gg_col(int dtype, int D, const Params& a, bool load_p, hipStream_t st,
+                                const Params* rowc = nullptr) {
+  if (D == 64) return launch_gg_col64(dtype, a, load_p, st, rowc);
+  if (D == 128)
+    return dtype == kF32 ? launch_gg_col128f(dtype, a, load_p, st, rowc) : launch_gg_col128h(dtype, a, load_p, st, rowc);
   return hipErrorInvalidValue;
 }
 

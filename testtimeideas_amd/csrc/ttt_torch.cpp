@@ -1,8 +1,8 @@
 // ttt_torch.cpp — torch binding of the forward, backward and double backward
-// of the C ABI (include/ttt_attn.h): ttt_attn_fwd, then ttt_attn_bwd (or
-// ttt_attn_bwd_dq + ttt_attn_bwd_dkdv with splits of their own) and ttt_attn_gg_row +
-// ttt_attn_gg_col (what ttt_attn_gg does), each kernel family with its own
-// split (tiles per workgroup; 0 lets the library choose).
+// of the C ABI (include/ttt_attn.h): ttt_attn_fwd, then ttt_attn_bwd and
+// ttt_attn_gg, or, with a split of each kernel family's own (tiles per
+// workgroup; 0 lets the library choose), ttt_attn_bwd_dq + ttt_attn_bwd_dkdv
+// and ttt_attn_gg_row + ttt_attn_gg_col.
 //
 // The ctypes binding (testtimeideas_amd/_lib.py) spends tens of microseconds
 // of Python per call building views, problems and outputs; the autograd path
@@ -213,6 +213,34 @@ std::vector<at::Tensor> gg(const at::Tensor& q, const at::Tensor& k, const at::T
   return {gq_out, gk_out, gv_out, gdo};
 }
 
+// The same through ttt_attn_gg when both passes take the library's split:
+// the column launch then also finishes the row pass's split blocks.
+std::vector<at::Tensor> gg_fused(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                                 const at::Tensor& dout, const at::Tensor& lse, const c10::optional<at::Tensor>& p,
+                                 const at::Tensor& rowsum, const at::Tensor& gq, const at::Tensor& gk,
+                                 const at::Tensor& gv, bool causal, double scale, bool want_gdo, int64_t window,
+                                 int64_t window_kind, const c10::optional<at::Tensor>& bias) {
+  const ttt_problem pr = problem_of(q, causal, scale, 0, window, window_kind, bias);
+  at::Tensor gq_out = at::empty(q.sizes(), q.options());
+  at::Tensor gk_out = at::empty(k.sizes(), k.options());
+  at::Tensor gv_out = at::empty(v.sizes(), v.options());
+  at::Tensor gdo = want_gdo ? at::empty(dout.sizes(), dout.options()) : at::Tensor();
+  at::Tensor e = stats_of(q), f = stats_of(q);
+  int64_t wsb = 0;
+  at::Tensor ws = workspace(pr, TTT_ENTRY_GG, want_gdo, q, &wsb);
+  const bool lp = p && p->defined();
+  const ttt_view vq = view_of(q), vk = view_of(k), vv = view_of(v), vdo = view_of(dout);
+  const ttt_view vp = lp ? view_of(*p) : none_view();
+  const ttt_view vgq = view_of(gq), vgk = view_of(gk), vgv = view_of(gv);
+  const ttt_view ogq = view_of(gq_out), ogk = view_of(gk_out), ogv = view_of(gv_out);
+  const ttt_view ogdo = want_gdo ? view_of(gdo) : none_view();
+  check(ttt_attn_gg(&pr, &vq, &vk, &vv, &vdo, lse.data_ptr<float>(), lp ? &vp : nullptr, rowsum.data_ptr<float>(),
+                    &vgq, &vgk, &vgv, &ogq, &ogk, &ogv, want_gdo ? &ogdo : nullptr, e.data_ptr<float>(),
+                    f.data_ptr<float>(), ptr_or_null(ws), wsb, stream_of(q)),
+        "ttt_attn_gg");
+  return {gq_out, gk_out, gv_out, gdo};
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -221,4 +249,5 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("bwd", &bwd, "first backward: (dQ, dK, dV, D)");
   m.def("bwd_fused", &bwd_fused, "first backward in one entry call: (dQ, dK, dV, D)");
   m.def("gg", &gg, "double backward: (GQ, GK, GV, GdO or None)");
+  m.def("gg_fused", &gg_fused, "double backward in one entry call: (GQ, GK, GV, GdO or None)");
 }

@@ -142,26 +142,36 @@ def test_per_kernel_entry_points_match_fused():
                         "ttt_attn_gg_col"}
 
 
-@pytest.mark.parametrize("b,h,t,d,dtype,save_p,chunk", [
-    (1, 2, 192, 64, "fp16", True, 1),
-    (1, 1, 300, 64, "bf16", True, 2),
-    (2, 4, 200, 64, "fp16", True, 2),
-    (2, 4, 200, 64, "fp16", False, 3),
-    (1, 3, 257, 128, "bf16", True, 2),
-    (1, 2, 130, 64, "fp32", True, 2),
-    (1, 1, 1024, 64, "fp16", True, 0),
+def _mask(win):
+    """Causal, or a (kind, W) key window."""
+    if win is None:
+        return True
+    return _lib.Mask(causal=True, window=win[1], window_kind=win[0])
+
+
+@pytest.mark.parametrize("b,h,t,d,dtype,save_p,chunk,win", [
+    (1, 2, 192, 64, "fp16", True, 1, None),
+    (1, 1, 300, 64, "bf16", True, 2, None),
+    (2, 4, 200, 64, "fp16", True, 2, None),
+    (2, 4, 200, 64, "fp16", False, 3, None),
+    (1, 3, 257, 128, "bf16", True, 2, None),
+    (1, 2, 130, 64, "fp32", True, 2, None),
+    (1, 1, 1024, 64, "fp16", True, 0, None),
+    (1, 2, 700, 64, "fp16", True, 2, (_lib.WINDOW_SLIDING, 200)),
+    (1, 1, 640, 64, "bf16", False, 3, (_lib.WINDOW_LOCAL, 128)),
 ])
-def test_fused_backward_entry(b, h, t, d, dtype, save_p, chunk):
+def test_fused_backward_entry(b, h, t, d, dtype, save_p, chunk, win):
     """ttt_attn_bwd, whose dK/dV launch also finishes dQ's split blocks, gives
     bitwise the results of ttt_attn_bwd_dq + ttt_attn_bwd_dkdv."""
     import ctypes
     dt = DT[dtype]
+    m = _mask(win)
     q, k, v, do = (x.cuda() for x in _inputs(b, h, t, d, dt, seed=t + d)[:4])
-    print(f"[case] fused bwd b={b} h={h} t={t} d={d} {dtype} save_p={save_p} chunk={chunk}", flush=True)
-    o, lse, p = _lib.fwd(q, k, v, True, 0.125, save_p)
+    print(f"[case] fused bwd b={b} h={h} t={t} d={d} {dtype} save_p={save_p} chunk={chunk} win={win}", flush=True)
+    o, lse, p = _lib.fwd(q, k, v, m, 0.125, save_p)
     with _lib.split_chunk(chunk), _lib.kernel_timing():  # timing: the two per-family entry points
-        dq0, dk0, dv0, rs0 = _lib.bwd(q, k, v, o, do, lse, p, True, 0.125)
-    pr = _lib._problem(q, True, 0.125, chunk)
+        dq0, dk0, dv0, rs0 = _lib.bwd(q, k, v, o, do, lse, p, m, 0.125)
+    pr = _lib._problem(q, m, 0.125, chunk)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     rs = torch.empty(b, h, t, dtype=torch.float32, device=q.device)
     wp, wn, _buf = _lib._workspace(pr, _lib.ENTRY_BWD, q.device)
@@ -173,28 +183,32 @@ def test_fused_backward_entry(b, h, t, d, dtype, save_p, chunk):
         assert torch.equal(x, y), n
 
 
-@pytest.mark.parametrize("b,h,t,d,dtype,save_p,gdo,chunk", [
-    (1, 2, 192, 64, "fp16", True, False, 1),
-    (1, 1, 300, 64, "bf16", True, True, 2),
-    (2, 4, 200, 64, "fp16", False, False, 2),
-    (2, 4, 200, 64, "bf16", True, True, 3),
-    (1, 3, 257, 128, "bf16", True, False, 2),
-    (1, 2, 190, 128, "fp16", True, True, 2),
-    (1, 2, 130, 128, "fp32", False, True, 2),
-    (1, 1, 1024, 64, "fp16", True, False, 0),
+@pytest.mark.parametrize("b,h,t,d,dtype,save_p,gdo,chunk,win", [
+    (1, 2, 192, 64, "fp16", True, False, 1, None),
+    (1, 1, 300, 64, "bf16", True, True, 2, None),
+    (2, 4, 200, 64, "fp16", False, False, 2, None),
+    (2, 4, 200, 64, "bf16", True, True, 3, None),
+    (1, 3, 257, 128, "bf16", True, False, 2, None),
+    (1, 2, 190, 128, "fp16", True, True, 2, None),
+    (1, 2, 130, 128, "fp32", False, True, 2, None),
+    (1, 1, 1024, 64, "fp16", True, False, 0, None),
+    (1, 2, 700, 64, "fp16", True, True, 2, (_lib.WINDOW_SLIDING, 200)),
+    (1, 1, 640, 64, "bf16", False, False, 3, (_lib.WINDOW_LOCAL, 128)),
 ])
-def test_fused_double_backward_entry(b, h, t, d, dtype, save_p, gdo, chunk):
+def test_fused_double_backward_entry(b, h, t, d, dtype, save_p, gdo, chunk, win):
     """ttt_attn_gg, whose column launch also finishes the row pass's split
     blocks, gives bitwise the results of ttt_attn_gg_row + ttt_attn_gg_col."""
     import ctypes
     dt = DT[dtype]
+    m = _mask(win)
     q, k, v, do, gq, gk, gv = (x.cuda() for x in _inputs(b, h, t, d, dt, seed=t + d + 1))
-    print(f"[case] fused gg b={b} h={h} t={t} d={d} {dtype} save_p={save_p} gdo={gdo} chunk={chunk}", flush=True)
-    o, lse, p = _lib.fwd(q, k, v, True, 0.125, save_p)
-    _, _, _, rs = _lib.bwd(q, k, v, o, do, lse, p, True, 0.125)
+    print(f"[case] fused gg b={b} h={h} t={t} d={d} {dtype} save_p={save_p} gdo={gdo} chunk={chunk} win={win}",
+          flush=True)
+    o, lse, p = _lib.fwd(q, k, v, m, 0.125, save_p)
+    _, _, _, rs = _lib.bwd(q, k, v, o, do, lse, p, m, 0.125)
     with _lib.split_chunk(chunk), _lib.kernel_timing():  # timing: the row and column entry points
-        ref = _lib.gg(q, k, v, do, lse, p, rs, gq, gk, gv, True, 0.125, gdo)
-    pr = _lib._problem(q, True, 0.125, chunk)
+        ref = _lib.gg(q, k, v, do, lse, p, rs, gq, gk, gv, m, 0.125, gdo)
+    pr = _lib._problem(q, m, 0.125, chunk)
     out = [torch.empty_like(x) for x in (q, k, v)] + [torch.empty_like(do) if gdo else None]
     e = torch.empty(b, h, t, dtype=torch.float32, device=q.device)
     f = torch.empty_like(e)

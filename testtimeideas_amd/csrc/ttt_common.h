@@ -974,22 +974,9 @@ struct TileDma {  // for the unpadded (chunk-permuted) layout only: Lds<T, NCOL>
   }
 };
 
-// Row statistics through the 4-byte form: wave w < NS fetches statistic w of
-// the tile's rows into lds[w][0..63] (rows at or beyond rows_valid read row 0).
-template <int NS>
-__device__ __forceinline__ void stat_dma(float* lds, const float* s0, const float* s1, const float* s2,
-                                         const float* s3, int m0, int rows_valid) {
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;  // w: uniform
-  if (w >= NS) return;
-  const float* src = w == 0 ? s0 : w == 1 ? s1 : w == 2 ? s2 : s3;
-#if defined(__HIP_DEVICE_COMPILE__)
-  const char* p = reinterpret_cast<const char*>(src + m0) + (uint32_t)(lane < rows_valid ? lane : 0) * 4u;
-  __builtin_amdgcn_global_load_lds(p, (lds_void_t*)(lds + kBlk * w), 4, 0, 0);
-#endif
-}
-
-// The same with the per-wave choices made once: wave w < NS fetches
-// statistic w (pointer and LDS slice fixed per wave, uniform).
+// Row statistics through the 4-byte direct-load form: wave w < NS fetches
+// statistic w of the tile's rows into lds[w][0..63] (pointer and LDS slice
+// fixed per wave, uniform; rows at or beyond rows_valid read row 0).
 template <int NS>
 struct StatDma {
   const float* src;  // this wave's statistic, or null (w >= NS)
@@ -1046,27 +1033,6 @@ struct RtBuf {
 template <int P>
 __device__ __forceinline__ Parity<1 - P> other_buf(Parity<P>) { return {}; }
 __device__ __forceinline__ RtBuf other_buf(RtBuf b) { return RtBuf{b.cur ^ 1}; }
-
-// Eight consecutive fp32 values v[0..7] = src[idx0 .. idx0+7], zero past n.
-// `fast` (uniform) asserts idx0 + 8 <= n and a 16-byte aligned src + idx0.
-__device__ __forceinline__ void load_vec8(float* v, const float* src, int idx0, int n, bool fast = false) {
-  if (fast) {
-    const f32x4 a = *reinterpret_cast<const f32x4*>(src + idx0);
-    const f32x4 b = *reinterpret_cast<const f32x4*>(src + idx0 + 4);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) { v[j] = a[j]; v[4 + j] = b[j]; }
-    return;
-  }
-  if (idx0 + 8 <= n && ((reinterpret_cast<uintptr_t>(src + idx0) & 15) == 0)) {
-    const f32x4 a = *reinterpret_cast<const f32x4*>(src + idx0);
-    const f32x4 b = *reinterpret_cast<const f32x4*>(src + idx0 + 4);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) { v[j] = a[j]; v[4 + j] = b[j]; }
-  } else {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = (idx0 + j < n) ? src[idx0 + j] : 0.f;
-  }
-}
 
 // ---------------------------------------------------------------------------
 // P = exp2(s*log2e*x [+ bias*log2e] - lse2) from raw scores x of a row-block

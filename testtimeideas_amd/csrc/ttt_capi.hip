@@ -60,6 +60,12 @@ constexpr double kSplitTiles = 8.0;        // any split: the combine launch and 
 // combine (b2 h4 T2048 d128 grad-grad +35 % when split).
 constexpr int64_t kSimBlocks = 2;
 constexpr int64_t kDeferRounds = 4;        // P pass: rounds of workgroups from which stores are deferred
+// P pass at d = 64: P written beyond this many bytes (half of MI355X's 256 MB
+// last-level cache) is stored with the non-temporal hint.  Its readers then
+// fetch it from HBM either way (b1 h1 T16384 d64 fp16 causal, 256 MB: forward
+// -7 %, dQ -6 %); below it they find it in that cache (b1 h1 T8192, 64 MB:
+// dQ +15 % with the hint).
+constexpr int64_t kPStreamBytes = 128ll << 20;
 constexpr int64_t kMaxSimWorkgroups = 16;  // x slots: larger grids are not considered
 constexpr int kFallbackCus = 256;
 constexpr int kFallbackPerCu = 2;
@@ -488,6 +494,9 @@ int ttt_attn_fwd(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, co
   if (wp) {
     const int64_t blocks = pr->batch * pr->heads * ((pr->seqlen + ttt::kBlk - 1) / ttt::kBlk);
     a.defer_p = blocks >= kDeferRounds * family_slots(pr, ttt::kFamFwdP, true) ? 1 : 0;
+    const int64_t written = pr->batch * pr->heads * pr->seqlen * pr->seqlen * (pr->dtype == TTT_F32 ? 4 : 2) /
+                            (pr->causal ? 2 : 1);
+    a.p_nt = written > kPStreamBytes ? 1 : 0;
   }
   return launched(ttt::launch_fwd(pr->dtype, (int)pr->head_dim, a, wp, (hipStream_t)stream), "ttt_attn_fwd");
 }

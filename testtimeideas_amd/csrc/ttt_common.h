@@ -85,6 +85,9 @@ struct Params {
   // P pass: issue a full tile's P stores after the next tile's barrier
   // rather than right away (set for launches of many workgroup rounds).
   int defer_p;
+  // P pass, d = 64: store P with the non-temporal hint (set when P is larger
+  // than the last-level cache, where its readers could not find it anyway).
+  int p_nt;
 };
 
 // Logical grid position (x, slice y) of this workgroup.  The hardware hands
@@ -309,6 +312,46 @@ __device__ __forceinline__ void store_frag_g(T* p, const typename Elem<T>::frag&
   typedef typename Elem<T>::frag F;
   typedef __attribute__((address_space(1))) F gF;
   *(gF*)p = f;
+}
+
+// Store a full 64-key tile of P from the row fragments of a row-block wave:
+// lane (c, g) holds row m = m16 + c of its wave's 16 rows, keys n0 + 8g .. +7
+// (f0) and n0 + 32 + 8g .. +7 (f1).  Stored as they are, each instruction
+// writes 16 half row segments (64 of 128 bytes), which measured about 2.7 TB/s
+// where whole 128-byte segments reach 4.1 TB/s.  So lanes c and c + 8 of each
+// 16-lane row trade one fragment (a DPP rotation of the row by 8): lane c < 8
+// keeps f0 and receives lane c + 8's f0, lane c >= 8 keeps f1 and receives
+// lane c - 8's f1.  The first store then writes rows m16 .. m16 + 7 whole (low
+// lanes their own f0, high lanes the received f1), the second rows m16 + 8 ..
+// m16 + 15.  Rows at or past T are skipped.  P: the slice, row stride ld.
+// nt (uniform): with the non-temporal hint.
+template <typename T>
+__device__ __forceinline__ void store_p_rows(T* P, int64_t ld, int m, int T_, int n0,
+                                             const typename Elem<T>::frag& f0,
+                                             const typename Elem<T>::frag& f1, bool nt) {
+  static_assert(sizeof(T) == 2, "16-bit fragments");
+  typedef typename Elem<T>::frag F;
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  const bool low = c < 8;
+  u32x4 send, recv;
+  {
+    const F& sf = low ? f1 : f0;
+    __builtin_memcpy(&send, &sf, 16);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) recv[i] = (unsigned)__builtin_amdgcn_mov_dpp((int)send[i], 0x128, 0xF, 0xF, false);
+  F r;
+  __builtin_memcpy(&r, &recv, 16);
+  const int col = n0 + (low ? 8 * g : 32 + 8 * g);
+  const int ra = low ? m : m - 8, rb = low ? m + 8 : m;
+  typedef __attribute__((address_space(1))) F gF;
+  if (nt) {
+    if (ra < T_) __builtin_nontemporal_store(low ? f0 : r, (gF*)(P + (int64_t)ra * ld + col));
+    if (rb < T_) __builtin_nontemporal_store(low ? r : f1, (gF*)(P + (int64_t)rb * ld + col));
+  } else {
+    if (ra < T_) store_frag_g<T>(P + (int64_t)ra * ld + col, low ? f0 : r);
+    if (rb < T_) store_frag_g<T>(P + (int64_t)rb * ld + col, low ? r : f1);
+  }
 }
 
 // The same from global memory, through an explicit global address space so

@@ -571,7 +571,11 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_p(Params
   const T* Q = at<const T>(a.q, b, h);
   const T* K = at<const T>(a.k, b, h);
   const T* V = at<const T>(a.v, b, h);
-  T* Pm = at<T>(a.p, b, h) + (int64_t)(m < T_ ? m : 0) * a.p.st;
+  T* Ps = at<T>(a.p, b, h);
+  T* Pm = Ps + (int64_t)(m < T_ ? m : 0) * a.p.st;
+  // 16-bit d = 64: full tiles of P stored in whole row segments (store_p_rows;
+  // at d = 128 the same stores measured slower steps).
+  constexpr bool kRowPair = sizeof(T) == 2 && D == 64;
   frag qf[D / 32];
 #pragma unroll
   for (int ks = 0; ks < D / 32; ++ks) qf[ks] = load_frag_row<T>(Q, a.q.st, m, T_, 32 * ks + 8 * g);
@@ -600,9 +604,15 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_p(Params
   // just before that wait would hold it; issued after it they drain during
   // the next tile's work.
   frag pend[2];
-  T* pend_ptr = nullptr;
+  T* pend_ptr = nullptr;  // this lane's row segment of the deferred tile (d = 128)
+  int pend_n0 = -1;       // key offset of the deferred tile (row-pair stores)
   auto flush = [&]() __attribute__((always_inline)) {
-    if constexpr (kDma) {
+    if constexpr (kDma && kRowPair) {
+      if (pend_n0 >= 0) {
+        store_p_rows<T>(Ps, a.p.st, m, T_, pend_n0, pend[0], pend[1], a.p_nt != 0);
+        pend_n0 = -1;
+      }
+    } else if constexpr (kDma) {
       if (pend_ptr) {
         store_frag_g<T>(pend_ptr, pend[0]);
         store_frag_g<T>(pend_ptr + 32, pend[1]);
@@ -632,7 +642,9 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_p(Params
             for (int j = 0; j < 8; ++j) pv[j] = mk.masked(n0 + stream_index(kb, g, j)) ? 0.f : pv[j];
           }
           pf[kb] = vals_frag<T>(pv);
-          if (kDma && a.defer_p && n0 + kBlk <= T_) {
+          if (kRowPair && n0 + kBlk <= T_) {
+            // stored whole below (or deferred)
+          } else if (kDma && a.defer_p && n0 + kBlk <= T_) {
             pend[kb] = pf[kb];
             if (kb == 1 && m < T_) pend_ptr = Pm + n0 + stream_index(0, g, 0);
           } else if (m < T_) {
@@ -654,6 +666,17 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_p(Params
             }
           }
         }
+        if constexpr (kRowPair) {
+          if (n0 + kBlk <= T_) {
+            if (kDma && a.defer_p) {
+              pend[0] = pf[0];
+              pend[1] = pf[1];
+              pend_n0 = n0;
+            } else {
+              store_p_rows<T>(Ps, a.p.st, m, T_, n0, pf[0], pf[1], a.p_nt != 0);
+            }
+          }
+        }
       } else {
         Tile s;
         fwd_scores<T, D, XM>(s, cK, qf, a, mk, brow, nt);
@@ -665,7 +688,12 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_p(Params
           pf[kb] = vals_frag<T>(pv);
           if (kDma && a.defer_p && n0 + kBlk <= T_) {
             pend[kb] = pf[kb];
-            if (kb == 1 && m < T_) pend_ptr = Pm + n0 + stream_index(0, g, 0);
+            if (kb == 1) {
+              if constexpr (kRowPair)
+                pend_n0 = n0;
+              else if (m < T_)
+                pend_ptr = Pm + n0 + stream_index(0, g, 0);
+            }
           } else if (m < T_) {
             const int n = n0 + stream_index(kb, g, 0);
             if (n + 8 <= T_) {

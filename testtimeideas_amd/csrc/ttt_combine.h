@@ -4,27 +4,31 @@
 // also runs inside the dK/dV launch for the dQ partials.
 //
 // Each main-kernel workgroup of a split block wrote fp32 partials to the
-// workspace: accumulators [part][nacc][64][D] and row scalars [part][nsc][64],
-// part = (bh*nblk + block)*nchunk_max + chunk.  The combine reads every chunk
-// of a block in chunk order (so results do not depend on scheduling).  A
-// block's 64 x D outputs are covered by D/16 workgroups; thread t of
-// workgroup `sub` owns one 4-wide slot: slot = 256*sub + t, row slot/(D/4),
-// columns 4*(slot % (D/4)) .. +3.
+// workspace: accumulators [part][nacc] as 64 x D blocks in part_off layout
+// (ttt_common.h) and row scalars [part][nsc][64], part = (bh*nblk + block)*
+// nchunk_max + chunk.  The combine reads every chunk of a block in chunk
+// order (so results do not depend on scheduling).  A block's 64 x D outputs
+// are covered by D/16 workgroups; thread t of workgroup `sub` owns the 4-wide
+// slot s = 256*sub + t (CombineSlot).
 #pragma once
 #include "ttt_common.h"
 #include "ttt_launch.h"
 
 namespace ttt {
 
+// Slot s of a block is the 16-byte run at 4*s floats of its part_off layout:
+// consecutive threads read consecutive runs, and each wave's 16 rows x 16
+// columns are written to the output together.
 template <int D>
 struct CombineSlot {
   static constexpr int kSub = kBlk * (D / 4) / kThreads;  // workgroups per block
   int blk, r, d0;
   __device__ __forceinline__ explicit CombineSlot(int bx) {
     blk = bx / kSub;
-    const int slot = (bx % kSub) * kThreads + threadIdx.x;
-    r = slot / (D / 4);
-    d0 = 4 * (slot % (D / 4));
+    const int s = (bx % kSub) * kThreads + threadIdx.x;
+    const int q = s % (4 * D);
+    r = 16 * (s / (4 * D)) + ((q >> 2) & 15);
+    d0 = 16 * (q >> 6) + 4 * (q & 3);
   }
 };
 
@@ -46,7 +50,7 @@ __device__ __forceinline__ void sum_parts(f32x4* out, const float* ws, int64_t p
                                           int r, int d0) {
 #pragma unroll
   for (int i = 0; i < NA; ++i) out[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const float* base = ws + (p0 * nacc + a0) * kBlk * D + r * D + d0;
+  const float* base = ws + (p0 * nacc + a0) * kBlk * D + part_off<D>(r, d0);
   const int64_t step = (int64_t)nacc * kBlk * D;
   for (int k0 = 0; k0 < nch; k0 += kBatch) {
     f32x4 x[kBatch][NA];

@@ -48,7 +48,7 @@ __global__ __launch_bounds__(kThreads) void k_combine_fwd(Params a) {
       const int64_t k = p0 + min(k0 + u, nch - 1);
       mk[u] = a.ws_sc[k * 2 * kBlk + r];
       lk[u] = a.ws_sc[k * 2 * kBlk + kBlk + r];
-      xk[u] = *reinterpret_cast<const f32x4*>(a.ws_acc + k * kBlk * D + r * D + cs.d0);
+      xk[u] = *reinterpret_cast<const f32x4*>(a.ws_acc + k * kBlk * D + part_off<D>(r, cs.d0));
     }
 #pragma unroll
     for (int u = 0; u < kBatch; ++u)

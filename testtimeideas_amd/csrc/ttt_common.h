@@ -77,7 +77,7 @@ struct Params {
   // split of the streamed loop
   int chunk;                 // tiles per workgroup
   int nchunk_max;            // chunks of the longest block
-  float* ws_acc;             // [BH][nblk][nchunk_max][nacc][64][D] partial accumulators
+  float* ws_acc;             // [BH][nblk][nchunk_max][nacc] blocks of 64 x D partials (part_off layout)
   float* ws_sc;              // [BH][nblk][nchunk_max][nsc][64] partial row scalars
   // masks beyond causality (last, so the fields above keep their offsets)
   int win, win_kind;  // key window (0: none; else 0 < win < T, with causal), kWin*
@@ -885,13 +885,25 @@ __device__ __forceinline__ void store_acc_rows(T* base, int64_t ld, int row, int
   for (int ds = 0; ds < D / 16; ++ds) store4<T>(rp + 16 * ds, acc[ds] * mul);
 }
 
-// Store a transposed accumulator as fp32 partial rows: dst[row_local][d].
+// Offset (floats) of element (row r, column d) in one 64 x D block of fp32
+// partials.  The block is laid out as [r / 16][d / 16][r % 16][d % 16]: one
+// wave's 16 rows of a 16-column slice are 1 KB contiguous, so each of
+// store_acc_partial's stores writes whole cache lines (a row-major block
+// would take four stores per 256-byte row, each writing 64 bytes of it), and
+// the combine kernels' threads read consecutive 16-byte slots.
+template <int D>
+__host__ __device__ __forceinline__ int part_off(int r, int d) {
+  return (r >> 4) * (16 * D) + (d >> 4) * 256 + (r & 15) * 16 + (d & 15);
+}
+
+// Store a transposed accumulator (this lane: row row_local, columns
+// 16*ds + 4g .. +3) as fp32 partials in part_off layout.
 template <int D>
 __device__ __forceinline__ void store_acc_partial(float* dst, int row_local, const f32x4* acc) {
   const int g = (threadIdx.x & 63) >> 4;
-  float* rp = dst + row_local * D + 4 * g;
 #pragma unroll
-  for (int ds = 0; ds < D / 16; ++ds) *reinterpret_cast<f32x4*>(rp + 16 * ds) = acc[ds];
+  for (int ds = 0; ds < D / 16; ++ds)
+    *reinterpret_cast<f32x4*>(dst + part_off<D>(row_local, 16 * ds + 4 * g)) = acc[ds];
 }
 
 // ---------------------------------------------------------------------------

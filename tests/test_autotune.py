@@ -45,13 +45,13 @@ def test_picks_fastest_and_caches(monkeypatch):
 def test_ties_keep_the_library_pick(monkeypatch):
     autotune.enable(True)
     monkeypatch.setattr(autotune, "_time", lambda run, c: 1.0)
-    assert autotune.chunk(("b",), lambda: (20, 128), lambda c: None) == 20
+    assert autotune.chunk(("b",), lambda: (20, 128), lambda c: None) == 0  # the library's own pick
 
 
 def test_single_candidate_is_not_timed(monkeypatch):
     autotune.enable(True)
     monkeypatch.setattr(autotune, "_time", lambda run, c: pytest.fail("timed a single candidate"))
-    assert autotune.chunk(("c",), lambda: (3, 3), lambda c: None) == 3
+    assert autotune.chunk(("c",), lambda: (3, 3), lambda c: None) == 0
 
 
 def test_graph_capture_keeps_library_choice(monkeypatch):

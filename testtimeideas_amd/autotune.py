@@ -44,7 +44,8 @@ def clear() -> None:
 
 
 def choices() -> Dict[tuple, int]:
-    """The splits chosen so far: {(family, shape key): tiles per workgroup}."""
+    """The splits chosen so far: {(family, shape key): tiles per workgroup},
+    0 where the library's own pick won."""
     return dict(_cache)
 
 
@@ -81,8 +82,10 @@ def chunk(key: tuple, pick: Callable[[], Tuple[int, int]], run: Callable[[int], 
     """The split to launch family/shape `key` with: 0 (the library's choice)
     when tuning is off or a graph is being captured; otherwise the cached
     choice, or the fastest of ``candidates`` timed with `run(c)` on the
-    current stream.  `pick()` gives (the library's split, the longest walk
-    in tiles)."""
+    current stream, with 0 again when that is the library's own pick (the
+    same launches, and the fused entry points, which take the library's
+    splits, stay usable).  `pick()` gives (the library's split, the longest
+    walk in tiles)."""
     if not _enabled:
         return 0
     c = _cache.get(key)
@@ -97,5 +100,7 @@ def chunk(key: tuple, pick: Callable[[], Tuple[int, int]], run: Callable[[int], 
     else:
         times = [(_time(run, c), i, c) for i, c in enumerate(cands)]
         best = min(times)[2]
+    if best == cands[0]:
+        best = 0
     _cache[key] = best
     return best

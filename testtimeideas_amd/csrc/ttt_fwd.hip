@@ -558,12 +558,32 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_p(Params
   if (cr.nch == 1) {
     lse2 = (m < T_) ? a.lse[ridx] * kLog2e : 0.f;
   } else {
-    const int64_t p0 = part_index(a, bh, nblk, mb, 0);
-    float mm = -INFINITY;
-    for (int k = 0; k < cr.nch; ++k) mm = fmaxf(mm, a.ws_sc[(p0 + k) * 2 * kBlk + rl]);
-    float ll = 0.f;
-    for (int k = 0; k < cr.nch; ++k)
-      ll += a.ws_sc[(p0 + k) * 2 * kBlk + kBlk + rl] * fast_exp2(a.ws_sc[(p0 + k) * 2 * kBlk + rl] - mm);
+    // The statistics of up to kBatch chunks are loaded together (chunk
+    // indices past the last repeat it), then merged in chunk order: loaded
+    // one at a time, each waited for the last, and the prologue of the
+    // longest blocks took several microseconds (b1 h1 T8192: 12 chunks).
+    constexpr int kBatch = 8;
+    const float* sc0 = a.ws_sc + part_index(a, bh, nblk, mb, 0) * 2 * kBlk + rl;
+    float mm = -INFINITY, ll = 0.f;
+    for (int k0 = 0; k0 < cr.nch; k0 += kBatch) {
+      float mk[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) mk[u] = sc0[(int64_t)min(k0 + u, cr.nch - 1) * 2 * kBlk];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) mm = fmaxf(mm, mk[u]);  // repeats of the last chunk leave the max
+    }
+    for (int k0 = 0; k0 < cr.nch; k0 += kBatch) {
+      float mk[kBatch], lk[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int64_t k = min(k0 + u, cr.nch - 1);
+        mk[u] = sc0[k * 2 * kBlk];
+        lk[u] = sc0[k * 2 * kBlk + kBlk];
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        if (k0 + u < cr.nch) ll += lk[u] * fast_exp2(mk[u] - mm);
+    }
     lse2 = mm + __log2f(ll);
     if (ch == 0 && g == 0 && m < T_) a.lse[ridx] = lse2 * kLn2;
   }

@@ -31,9 +31,9 @@
 
 // Measured on MI355X and kept:
 //  * 16-bit tiles stream into LDS by direct loads, into two buffer sets with
-//    a compile-time role per loop step (the online pass at D = 64; the
-//    statistics and P passes at D = 64 and 128); fp32 tiles are staged
-//    through registers, one tile ahead (deeper prefetch was no faster).
+//    a compile-time role per loop step (the online, statistics and P passes
+//    at D = 64 and 128); fp32 tiles are staged through registers, one tile
+//    ahead (deeper prefetch was no faster).
 //  * Full D = 64 key tiles staged through registers use per-lane offsets
 //    computed once; ragged tiles clamp their rows.
 //  * Without a window or bias, the statistics pass keeps its running max and
@@ -118,10 +118,12 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<true>::value))) void k_fwd_online(Pa
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
-  // 16-bit D = 64 tiles stream straight into two LDS buffer sets (TileDma) in
-  // distinct arrays with a compile-time role per loop step; the rest stage
-  // them through registers.
-  constexpr bool kDma = L::kSwizzle && D == 64;
+  // 16-bit tiles stream straight into two LDS buffer sets (TileDma) in
+  // distinct arrays with a compile-time role per loop step; fp32 tiles are
+  // staged through registers.  At D = 128 the two sets take 64 KB of LDS (two
+  // workgroups per CU instead of three) and still measured faster: b4 h16
+  // T8192 bf16 causal -9 %, b2 h4 T2048 fp16 -19 %.
+  constexpr bool kDma = L::kSwizzle;
   __shared__ __align__(16) T sK[L::kRowElems];
   __shared__ __align__(16) T sV[L::kRowElems];
   __shared__ __align__(16) T sK1[kDma ? L::kRowElems : 8];

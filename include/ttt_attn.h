@@ -153,6 +153,16 @@ int ttt_attn_split_info(const ttt_problem* pr, int32_t entry, int32_t load_p, in
                         int32_t* chunk, int32_t* nchunk_max, int64_t* slots);
 
 /*
+ * The chunk that grid column `column` (0 <= column < nblk * ceil(nblk /
+ * chunk)) of a split plain-causal slice runs: block (in launch order: block i
+ * streams nblk - i tiles) and chunk index, block -1 for a column with none.
+ * Full chunks come first, chunk index by chunk index, then the shorter last
+ * chunks, longest first.  Diagnostics; no reference counterpart (the
+ * reference's kernels are not split).
+ */
+int ttt_attn_launch_item(int32_t nblk, int32_t chunk, int32_t column, int32_t* block, int32_t* chunk_index);
+
+/*
  * Forward.  Writes O and lse; if p != NULL (and p->data != NULL) also writes
  * P = softmax(S) rounded to the input dtype, and computes O from that rounded
  * P (two passes over K: row statistics, then P and P*V).  With p == NULL it

@@ -116,6 +116,36 @@ def _block_tiles(t, causal, window=0, kind=0, col=False):
     return out
 
 
+def _grid_order(lens, c, longest_first):
+    """(block, chunk) run by each grid column of a slice, None where a column
+    runs nothing.  Chunk index by chunk index, blocks in launch order; with
+    `longest_first` (plain causal) every full chunk that way first, then the
+    blocks' shorter last chunks by length, longest first, ties in launch
+    order."""
+    k = -(-max(lens) // c)
+    cols = len(lens) * k
+    if not longest_first or k == 1:
+        return [(b, ch) if ch * c < lens[b] else None for ch in range(k) for b in range(len(lens))]
+    full = [(b, ch) for ch in range(k) for b in range(len(lens)) if lens[b] - ch * c >= c]
+    last = sorted(((b, lens[b] // c) for b in range(len(lens)) if lens[b] % c), key=lambda it: -(lens[it[0]] % c))
+    return full + last + [None] * (cols - len(full) - len(last))
+
+
+def test_launch_order_longest_first():
+    """ttt_attn_launch_item (the kernels' causal_item) against the order
+    written out directly, exhaustively for small slices: each chunk of each
+    block exactly once, full chunks first, then the last chunks longest
+    first, columns past them empty."""
+    for n in range(1, 70):
+        lens = [n - b for b in range(n)]
+        for c in range(1, n + 3):
+            want = _grid_order(lens, c, True)
+            got = [_lib.launch_item(n, c, x) for x in range(len(want))]
+            assert got == [(-1, 0) if w is None else w for w in want], (n, c)
+    with pytest.raises(RuntimeError):
+        _lib.launch_item(8, 3, 8 * 3)
+
+
 def _simulated_chunk(nblk, causal, bh, slots, min_chunk=4, lengths=None):
     """Independent restatement of the library's split chooser: list-schedule
     the grid (x = block + nblk*chunk, y = b*h; blocks in launch order with
@@ -129,20 +159,20 @@ def _simulated_chunk(nblk, causal, bh, slots, min_chunk=4, lengths=None):
 
     lens = lengths or ([nblk - b for b in range(nblk)] if causal else [nblk] * nblk)
     lmax = max(lens)
+    longest_first = causal and lengths is None
 
     def cost(c):
         per = max(1, slots // 8)
         heaps = [[0.0] * per for _ in range(8)]
         end, used, idx = 0.0, 0, 0
-        k = -(-lmax // c)
+        order = _grid_order(lens, c, longest_first)
         for y in range(bh):
-            for ch in range(k):
-                for ln in lens:
-                    t = max(0, min(c, ln - ch * c))
-                    h = heaps[y % 8 if bh % 8 == 0 else idx % 8]
-                    f = heapq.heappop(h) + (t + 0.5 if t else 0.05)
-                    heapq.heappush(h, f)
-                    end, used, idx = max(end, f), used + (t > 0), idx + 1
+            for item in order:
+                t = 0 if item is None else min(c, lens[item[0]] - item[1] * c)
+                h = heaps[y % 8 if bh % 8 == 0 else idx % 8]
+                f = heapq.heappop(h) + (t + 0.5 if t else 0.05)
+                heapq.heappush(h, f)
+                end, used, idx = max(end, f), used + (t > 0), idx + 1
         return end + 0.015 * used
 
     if bh * nblk >= (2 if causal else 1) * slots:
@@ -180,7 +210,7 @@ def test_split_info_matches_workspace():
     """ttt_attn_split_info reports the split the workspace is sized for (no
     GPU here: 256 CUs x 2 workgroups, 90 % usable)."""
     pr = _prob(seqlen=8192)
-    assert _lib.split_info(pr, _lib.ENTRY_GG_ROW, True) == (21, 7, 460)
+    assert _lib.split_info(pr, _lib.ENTRY_GG_ROW, True) == (19, 7, 460)
     assert _lib.workspace_bytes(pr, _lib.ENTRY_GG_ROW) == 128 * 7 * 64 * (3 * 64 + 3) * 4
     with pytest.raises(RuntimeError, match="single kernel family"):
         _lib.split_info(pr, _lib.ENTRY_GG, True)
@@ -240,10 +270,9 @@ def test_workspace_sizes():
         assert _lib.workspace_bytes(pr, _lib.ENTRY_GG, True) == parts * 64 * (5 * 64 + 3 + 2 * 64) * 4
         # the fused backward holds dQ's partials (one accumulator) and dK/dV's (two) at once
         assert _lib.workspace_bytes(pr, _lib.ENTRY_BWD) == parts * 64 * (3 * 64) * 4
-    # C3: one round of 21-tile chunks (455 workgroups in the 460 slots; 20
-    # tiles would need 476 and spill into a second round)
-    assert _simulated_chunk(128, True, 1, slots) == 21 and _slice_workgroups(128, 21, True) == 455
-    assert _slice_workgroups(128, 20, True) == 476
+    # C3: 19-tile chunks; of the 497 workgroups the 37 beyond the 460 slots
+    # are the shortest last chunks, which the longest-first order runs last
+    assert _simulated_chunk(128, True, 1, slots) == 19 and _slice_workgroups(128, 19, True) == 497
     # C5 fills the chip with blocks alone: no split, no workspace
     c5 = _prob(batch=4, heads=16, seqlen=8192, head_dim=128, dtype=1)
     assert all(_lib.workspace_bytes(c5, e) == 0 for e in range(8))

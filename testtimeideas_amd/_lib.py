@@ -139,6 +139,9 @@ def load() -> ctypes.CDLL:
     lib.ttt_attn_split_info.argtypes = [_P(_Problem), ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                         _P(ctypes.c_int32), _P(ctypes.c_int32), _P(ctypes.c_int64)]
     lib.ttt_attn_split_info.restype = ctypes.c_int
+    lib.ttt_attn_launch_item.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P(ctypes.c_int32),
+                                         _P(ctypes.c_int32)]
+    lib.ttt_attn_launch_item.restype = ctypes.c_int
     _lib = lib
     return lib
 
@@ -613,6 +616,15 @@ def split_info(pr: _Problem, entry: int, load_p: bool, gdo: bool = False) -> Tup
     return c.value, n.value, sl.value
 
 
+def launch_item(nblk: int, chunk: int, column: int) -> Tuple[int, int]:
+    """(block, chunk index) that grid column `column` of a split plain-causal
+    slice runs (block -1: none)."""
+    b, c = ctypes.c_int32(), ctypes.c_int32()
+    _call("ttt_attn_launch_item", nblk, chunk, column, ctypes.byref(b), ctypes.byref(c))
+    return b.value, c.value
+
+
 def exported_symbols() -> List[str]:
     """Names of the C entry points this binding uses (for ABI checks)."""
-    return list(_SIGS) + ["ttt_last_error", "ttt_version", "ttt_attn_workspace_size", "ttt_attn_split_info"]
+    return list(_SIGS) + ["ttt_last_error", "ttt_version", "ttt_attn_workspace_size", "ttt_attn_split_info",
+                          "ttt_attn_launch_item"]

@@ -207,12 +207,14 @@ int64_t slice_workgroups(const std::vector<int64_t>& len, int64_t c) {
   return n;
 }
 
-// Simulated makespan (tile times) of a launch: grid x = block + nblk*chunk,
-// y = (b,h); block i (launch order) has len[i] tiles; `slots` usable
-// workgroup slots spread over kXcds XCDs.  Workgroups go to the XCDs
-// round-robin in launch order, or slice y to XCD y % 8 when the slices divide
-// evenly (the kernels' grid_slot).
-double simulate_launch(const std::vector<int64_t>& len, int64_t c, int64_t bh, int64_t slots, int64_t* nonempty) {
+// Simulated makespan (tile times) of a launch: grid column x of slice y =
+// (b,h) runs the chunk the kernels' launch_item gives it (causal_item when
+// `longest_first`, else block x % nblk, chunk x / nblk); block i (launch
+// order) has len[i] tiles; `slots` usable workgroup slots spread over kXcds
+// XCDs.  Workgroups go to the XCDs round-robin in launch order, or slice y to
+// XCD y % 8 when the slices divide evenly (the kernels' grid_slot).
+double simulate_launch(const std::vector<int64_t>& len, int64_t c, int64_t bh, int64_t slots, bool longest_first,
+                       int64_t* nonempty) {
   const int64_t per = std::max<int64_t>(1, slots / kXcds);
   std::vector<std::priority_queue<double, std::vector<double>, std::greater<double>>> xcd(kXcds);
   for (auto& q : xcd)
@@ -224,16 +226,17 @@ double simulate_launch(const std::vector<int64_t>& len, int64_t c, int64_t bh, i
   double end = 0.0;
   int64_t idx = 0, used = 0;
   for (int64_t y = 0; y < bh; ++y)
-    for (int64_t ch = 0; ch < k; ++ch)
-      for (int64_t b = 0; b < nblk; ++b, ++idx) {
-        const int64_t t = std::max<int64_t>(0, std::min(c, len[b] - ch * c));
-        auto& q = xcd[by_slice ? y % kXcds : idx % kXcds];
-        const double f = q.top() + (t > 0 ? (double)t + kWgOverheadTiles : kEmptyWgTiles);
-        q.pop();
-        q.push(f);
-        end = std::max(end, f);
-        used += t > 0;
-      }
+    for (int64_t x = 0; x < nblk * k; ++x, ++idx) {
+      const ttt::Item it = (longest_first && k > 1) ? ttt::causal_item((int)x, (int)nblk, (int)c)
+                                                    : ttt::Item{(int)(x % nblk), (int)(x / nblk)};
+      const int64_t t = it.blk < 0 ? 0 : std::max<int64_t>(0, std::min(c, len[it.blk] - it.ch * c));
+      auto& q = xcd[by_slice ? y % kXcds : idx % kXcds];
+      const double f = q.top() + (t > 0 ? (double)t + kWgOverheadTiles : kEmptyWgTiles);
+      q.pop();
+      q.push(f);
+      end = std::max(end, f);
+      used += t > 0;
+    }
   *nonempty = used;
   return end;
 }
@@ -242,9 +245,11 @@ double simulate_launch(const std::vector<int64_t>& len, int64_t c, int64_t bh, i
 // split must beat no split by kSplitTiles.  Cached per shape.
 int64_t best_chunk(const ttt_problem* pr, const std::vector<int64_t>& len, bool col, int64_t bh, int64_t slots) {
   static std::mutex mu;
-  static std::map<std::tuple<int64_t, int, int, int, int, int64_t, int64_t>, int64_t> cache;
+  static std::map<std::tuple<int64_t, int, int, int, int, int64_t, int64_t, int>, int64_t> cache;
   const auto key = std::make_tuple((int64_t)pr->seqlen, pr->causal, eff_window(pr), pr->window_kind, col ? 1 : 0,
-                                   bh, slots);
+                                   bh, slots, pr->bias.data ? 1 : 0);
+  // plain causal launches run their chunks longest first (causal_item)
+  const bool longest_first = pr->causal && !has_xm(pr);
   {
     std::lock_guard<std::mutex> lock(mu);
     const auto it = cache.find(key);
@@ -255,13 +260,13 @@ int64_t best_chunk(const ttt_problem* pr, const std::vector<int64_t>& len, bool 
   double best = 0.0;
   {
     int64_t used = 0;
-    best = simulate_launch(len, lmax, bh, slots, &used) + kWgCostTiles * used;
+    best = simulate_launch(len, lmax, bh, slots, longest_first, &used) + kWgCostTiles * used;
   }
   // candidates: every length up to 64 tiles, then steps of ~3%
   for (int64_t c = std::min<int64_t>(kMinChunk, lmax); c < lmax; c = c < 64 ? c + 1 : c + std::max<int64_t>(1, c / 32)) {
     if (bh * slice_workgroups(len, c) > kMaxSimWorkgroups * slots) continue;
     int64_t used = 0;
-    const double cost = simulate_launch(len, c, bh, slots, &used) + kWgCostTiles * used + kSplitTiles;
+    const double cost = simulate_launch(len, c, bh, slots, longest_first, &used) + kWgCostTiles * used + kSplitTiles;
     if (cost < best) {
       best = cost;
       best_c = c;
@@ -470,6 +475,15 @@ int ttt_attn_split_info(const ttt_problem* pr, int32_t entry, int32_t load_p, in
   if (chunk) *chunk = s.chunk;
   if (nchunk_max) *nchunk_max = s.nchunk_max;
   if (slots) *slots = family_slots(pr, fam, load_p != 0);
+  return TTT_OK;
+}
+
+int ttt_attn_launch_item(int32_t nblk, int32_t chunk, int32_t column, int32_t* block, int32_t* chunk_index) {
+  if (nblk <= 0 || chunk <= 0 || column < 0 || (int64_t)column >= (int64_t)nblk * ((nblk + chunk - 1) / chunk))
+    return fail(TTT_ERR_INVALID_ARGUMENT, "launch_item: nblk %d, chunk %d, column %d", nblk, chunk, column);
+  const ttt::Item it = ttt::causal_item(column, nblk, chunk);
+  if (block) *block = it.blk;
+  if (chunk_index) *chunk_index = it.ch;
   return TTT_OK;
 }
 

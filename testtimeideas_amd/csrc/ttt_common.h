@@ -141,6 +141,72 @@ __device__ __forceinline__ Chunk chunk_of(int lo, int hi, int ch, int chunk) {
   return r;
 }
 
+// Which (block, chunk) grid column x of a split slice runs.  Blocks are
+// numbered in launch order; the grid is nblk * nchunk_max columns wide.
+struct Item {
+  int blk, ch;  // blk < 0: no chunk (the column's workgroup exits)
+};
+
+// Plain causal slices, whose block i (launch order) has n - i tiles, run
+// their chunks longest first: every full chunk of c tiles (chunk index by
+// chunk index, blocks in launch order), then the shorter last chunks by
+// length, longest first (the blocks of one length in launch order).  A
+// launch of more workgroups than slots then ends on its shortest chunks
+// instead of on the full last chunks of the longest blocks.  Closed forms
+// (every workgroup computes its own column):
+//   full chunks with index j: f(j) = n - (j+1)c + 1 of them, for j < n / c;
+//     before index j: S(j) = j(n+1) - c j(j+1)/2.
+//   last chunks of r = L mod c tiles (L = n - i; n = q c + s, 0 <= s < c):
+//     q + [r <= s] of them; lengths r > s come first, (c-1-s) q in all.
+__host__ __device__ inline Item causal_item(int x, int n, int c) {
+  Item it{-1, 0};
+  const int k1 = n / c;  // full-chunk indices
+  const long long full = (long long)k1 * (n + 1) - (long long)c * k1 * (k1 + 1) / 2;
+  if (x < full) {
+    // largest j with S(j) <= x (S increases on [0, k1]); a double estimate
+    // from the quadratic, then exact integer steps
+    const double b2 = 2.0 * n + 2.0 - c;
+    double disc = b2 * b2 - 8.0 * c * (double)x;
+    int j = (int)((b2 - sqrt(disc > 0.0 ? disc : 0.0)) / (2.0 * c));
+    if (j < 0) j = 0;
+    if (j > k1 - 1) j = k1 - 1;
+    auto S = [&](int jj) { return (long long)jj * (n + 1) - (long long)c * jj * (jj + 1) / 2; };
+    while (j > 0 && S(j) > x) --j;
+    while (j + 1 < k1 && S(j + 1) <= x) ++j;
+    it.blk = (int)(x - S(j));
+    it.ch = j;
+    return it;
+  }
+  const int q = n / c, s = n % c;
+  long long y = x - full;
+  int r, idx, m;
+  const long long a = (long long)(c - 1 - s) * q;  // last chunks longer than s tiles
+  if (y < a) {
+    r = c - 1 - (int)(y / q);
+    idx = (int)(y % q);
+    m = q;
+  } else {
+    y -= a;
+    if (y >= (long long)s * (q + 1)) return it;  // past the last chunk
+    r = s - (int)(y / (q + 1));
+    idx = (int)(y % (q + 1));
+    m = q + 1;
+  }
+  const int L = r + (m - 1 - idx) * c;  // blocks of this length in launch order (longest block first)
+  it.blk = n - L;
+  it.ch = L / c;
+  return it;
+}
+
+// The column's chunk: causal_item for plain causal split slices (XM false),
+// else x % nblk, x / nblk (chunk index by chunk index, blocks in launch
+// order; columns past a block's chunks exit on their chunk test).
+template <bool XM>
+__device__ __forceinline__ Item launch_item(const Params& a, int x, int nblk) {
+  if (!XM && a.causal && a.nchunk_max > 1) return causal_item(x, nblk, a.chunk);
+  return Item{x % nblk, x / nblk};
+}
+
 // ---------------------------------------------------------------------------
 // Masks.  Query row m sees key n iff n < T, n <= m (causal), n >= win_lo(m)
 // (window), and the additive bias, if any, leaves the score finite.  Window

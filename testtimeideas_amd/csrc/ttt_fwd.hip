@@ -19,7 +19,8 @@
 // block's first visible key and masks the tiles it cuts.  An additive bias is
 // added to the base-2 scores of every tile.  The window and bias code is a
 // separate instantiation (XM), so plain problems run the kernels without it.
-// Row blocks are issued heaviest first.  Blocks split into several chunks are
+// Row blocks are issued heaviest first, and the chunks of a split plain causal
+// launch longest first (launch_item).  Blocks split into several chunks are
 // finished by the combine kernels of ttt_combine.hip.
 //
 // Reference semantics: ttt_kernels/triton_attention.py:18-25 (math path),
@@ -132,7 +133,9 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<true>::value))) void k_fwd_online(Pa
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
   const Slot sl = grid_slot();
-  const int bi = sl.x % nblk, ch = sl.x / nblk;
+  const Item it = launch_item<XM>(a, sl.x, nblk);
+  if (it.blk < 0) return;
+  const int bi = it.blk, ch = it.ch;
   const int bh = sl.y, b = bh / a.H, h = bh % a.H;
   const int mb = a.causal ? (nblk - 1 - bi) : bi;
   const Range rg = row_block_range(mb, nblk, T_, a.causal, XM ? a.win : 0, a.win_kind);
@@ -350,7 +353,9 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_stats(Pa
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
   const Slot sl = grid_slot();
-  const int bi = sl.x % nblk, ch = sl.x / nblk;
+  const Item it = launch_item<XM>(a, sl.x, nblk);
+  if (it.blk < 0) return;
+  const int bi = it.blk, ch = it.ch;
   const int bh = sl.y, b = bh / a.H, h = bh % a.H;
   const int mb = a.causal ? (nblk - 1 - bi) : bi;
   const Range rg = row_block_range(mb, nblk, T_, a.causal, XM ? a.win : 0, a.win_kind);
@@ -542,7 +547,9 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_p(Params
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
   const Slot sl = grid_slot();
-  const int bi = sl.x % nblk, ch = sl.x / nblk;
+  const Item it = launch_item<XM>(a, sl.x, nblk);
+  if (it.blk < 0) return;
+  const int bi = it.blk, ch = it.ch;
   const int bh = sl.y, b = bh / a.H, h = bh % a.H;
   const int mb = a.causal ? (nblk - 1 - bi) : bi;
   const Range rg = row_block_range(mb, nblk, T_, a.causal, XM ? a.win : 0, a.win_kind);

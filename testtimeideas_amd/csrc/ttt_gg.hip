@@ -132,7 +132,9 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, false>::value))) void k_gg_row(
   const int T_ = a.T;
   const int nblk = (T_ + kBlk - 1) / kBlk;
   const Slot sl = grid_slot();
-  const int bi = sl.x % nblk, ch = sl.x / nblk;
+  const Item it = launch_item<XM>(a, sl.x, nblk);
+  if (it.blk < 0) return;
+  const int bi = it.blk, ch = it.ch;
   const int bh = sl.y, b = bh / a.H, h = bh % a.H;
   const int mb = a.causal ? (nblk - 1 - bi) : bi;
   const Range rg = row_block_range(mb, nblk, T_, a.causal, XM ? a.win : 0, a.win_kind);
@@ -495,7 +497,9 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, true>::value))) void k_gg_col(P
       combine_gg_row_block<T, D, false>(rowc, sl.x - nx, sl.y, false);
     return;
   }
-  const int nb = sl.x % nblk, ch = sl.x / nblk;
+  const Item it = launch_item<XM>(a, sl.x, nblk);
+  if (it.blk < 0) return;
+  const int nb = it.blk, ch = it.ch;
   const int bh = sl.y, b = bh / a.H, h = bh % a.H;
   const Range rg = col_block_range(nb, nblk, T_, a.causal, XM ? a.win : 0, a.win_kind);
   const Chunk cr = chunk_of(rg.lo, rg.hi, ch, a.chunk);

@@ -472,7 +472,7 @@ def main():
         out["fwd_lse_mfma_frac"] = fm["mfma_frac"]
         out["fwd_lse"] = {name: fwd_mfma(workloads.CONFIGS[name], dev) for name in ("C3", "C4_16k", "C2", "C5")}
         # the reference's published points: the C4 sweep, the C2 forward and first backward, and C5
-        out["c4_sweep"] = sweep_bench(dev, max(10, args.steps // 5), 5)
+        out["c4_sweep"] = sweep_bench(dev, max(30, args.steps // 3), 30)
         out["c2"] = c2_bench(dev, max(10, args.steps // 5), 5)
         out["c5"] = c5_bench(dev, 5, 2)
         # the reference TTT model's windowed attention (one launch per pass for its chunk loop)

@@ -193,7 +193,7 @@ def _simulated_chunk(nblk, causal, bh, slots, min_chunk=4, lengths=None):
 def test_window_workspace_matches_brute_force_ranges(t, window, kind):
     """The library's tile ranges under a window (seen through the workspace
     it asks for) equal the brute-force spans of visible pairs."""
-    slots = 460
+    slots = 512
     nblk = -(-t // 64)
     for col, entry, nacc_nsc in ((False, _lib.ENTRY_FWD, 64 + 2), (True, _lib.ENTRY_GG_COL, 2 * 64)):
         lens = _block_tiles(t, True, window, kind, col)
@@ -208,10 +208,10 @@ def test_window_workspace_matches_brute_force_ranges(t, window, kind):
 
 def test_split_info_matches_workspace():
     """ttt_attn_split_info reports the split the workspace is sized for (no
-    GPU here: 256 CUs x 2 workgroups, 90 % usable)."""
+    GPU here: 256 CUs x 2 workgroups, all usable)."""
     pr = _prob(seqlen=8192)
-    assert _lib.split_info(pr, _lib.ENTRY_GG_ROW, True) == (19, 7, 460)
-    assert _lib.workspace_bytes(pr, _lib.ENTRY_GG_ROW) == 128 * 7 * 64 * (3 * 64 + 3) * 4
+    assert _lib.split_info(pr, _lib.ENTRY_GG_ROW, True) == (17, 8, 512)
+    assert _lib.workspace_bytes(pr, _lib.ENTRY_GG_ROW) == 128 * 8 * 64 * (3 * 64 + 3) * 4
     with pytest.raises(RuntimeError, match="single kernel family"):
         _lib.split_info(pr, _lib.ENTRY_GG, True)
 
@@ -253,10 +253,10 @@ def test_prep_bias_layouts():
 
 
 def test_workspace_sizes():
-    # Without a GPU the split assumes 256 CUs x 2 workgroups, 90% usable = 460
+    # Without a GPU the split assumes 256 CUs x 2 workgroups, all usable = 512
     # slots.  Partial accumulators per chunk: nacc x 64 x D fp32 + nsc scalars
     # per row (forward 1 acc + 2, dQ 1, dK/dV 2, GQ 3 + 3, GQ+GdO 5 + 3).
-    slots = 460
+    slots = 512
     for (t, causal, bh) in [(8192, 1, 1), (16384, 1, 1), (8192, 0, 1), (4096, 1, 2), (2048, 1, 1)]:
         nblk = t // 64
         c = _simulated_chunk(nblk, bool(causal), bh, slots)
@@ -270,9 +270,9 @@ def test_workspace_sizes():
         assert _lib.workspace_bytes(pr, _lib.ENTRY_GG, True) == parts * 64 * (5 * 64 + 3 + 2 * 64) * 4
         # the fused backward holds dQ's partials (one accumulator) and dK/dV's (two) at once
         assert _lib.workspace_bytes(pr, _lib.ENTRY_BWD) == parts * 64 * (3 * 64) * 4
-    # C3: 19-tile chunks; of the 497 workgroups the 37 beyond the 460 slots
+    # C3: 17-tile chunks; of the 548 workgroups the 36 beyond the 512 slots
     # are the shortest last chunks, which the longest-first order runs last
-    assert _simulated_chunk(128, True, 1, slots) == 19 and _slice_workgroups(128, 19, True) == 497
+    assert _simulated_chunk(128, True, 1, slots) == 17 and _slice_workgroups(128, 17, True) == 548
     # C5 fills the chip with blocks alone: no split, no workspace
     c5 = _prob(batch=4, heads=16, seqlen=8192, head_dim=128, dtype=1)
     assert all(_lib.workspace_bytes(c5, e) == 0 for e in range(8))

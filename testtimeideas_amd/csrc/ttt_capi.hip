@@ -39,11 +39,14 @@ int fail(int code, const char* fmt, ...) {
 // The simulated makespan plus a small per-workgroup cost (partials, combine)
 // is minimised over the chunk length.  kSlotFill is the share (percent)
 // of the nominal slots (CUs x workgroups per CU from the occupancy
-// calculator) the simulation assumes usable.  The constants were fitted to
+// calculator) the simulation assumes usable: all of them.  Causal launches
+// run their shortest chunks last, so a few workgroups past the slots cost
+// little (90 % against 100 %, same box: b1 h1 T16384 d64 fp16 step 2 %
+// slower, b2 h4 T2048 d128 forward with P 10 % slower).  The constants were fitted to
 // MI355X sweeps of every kernel family at T = 8192 and 16384, where they pick
 // the measured fastest chunk length.  Without a device (workspace queries on
 // a host with no GPU) the slots default to kFallbackCus x kFallbackPerCu.
-constexpr int kSlotFill = 90;
+constexpr int kSlotFill = 100;
 constexpr int kXcds = 8;
 constexpr double kWgOverheadTiles = 0.5;   // per workgroup, in tile times
 constexpr double kEmptyWgTiles = 0.05;     // a workgroup whose chunk is empty

@@ -143,12 +143,34 @@ def kernel_times(step, reps: int = 10):
 SAVE_P = ("save_p", "save_p_triton", "save_p_triton_bwd", "save_p_triton_full")
 
 
-def roofline_entry(cfg, ktimes, with_p=None):
+def launch_times(step, steps: int) -> dict:
+    """Mean duration (ms) of each main kernel's launches while `steps` steps
+    run as in the timed region (fused entry points included), from the two HIP
+    events the library records on the launch stream around every main-kernel
+    launch while timing is on (ttt_kernel_timing)."""
+    with _lib.launch_timing(16 * steps + 64) as read:
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        return {k: v[0] for k, v in read().items()}
+
+
+# the main kernel of each entry point (the launch-timing names)
+ENTRY_KERNEL = {"ttt_attn_gg_row": "gg_row", "ttt_attn_gg_col": "gg_col", "ttt_attn_bwd_dq": "bwd_dq",
+                "ttt_attn_bwd_dkdv": "bwd_dkdv"}
+
+
+def roofline_entry(cfg, ktimes, launch_ms=None, with_p=None):
+    """Roofline of the dominant entry point (the longest in the per-entry
+    timing `ktimes`), priced on its main kernel's own launches in the step
+    (`launch_ms`) when they were timed, else on the entry's time."""
     if with_p is None:
         with_p = cfg.bwd_mode in SAVE_P
     name = max(ktimes, key=ktimes.get)
     model = workloads.kernel_model(name, cfg, with_p)
-    dur_s = ktimes[name] * 1e-3
+    kern = ENTRY_KERNEL.get(name)  # the forward entry runs two kernels with P: priced whole
+    kernel_ms = (launch_ms or {}).get(kern) if kern else None
+    dur_s = (kernel_ms if kernel_ms else ktimes[name]) * 1e-3
     tag = workloads.DTYPE_TAG[cfg.torch_dtype]
     if model["bound"] == "mfma":
         achieved = model["flops"] / dur_s / 1e12
@@ -156,22 +178,30 @@ def roofline_entry(cfg, ktimes, with_p=None):
     else:
         achieved = model["bytes"] / dur_s / 1e9
         peak, unit = workloads.PEAK_HBM_GBS, "GB/s"
-    return {"kernel": name, "bound": model["bound"], "achieved": round(achieved, 2), "peak": peak,
-            "unit": unit, "frac": round(achieved / peak, 4), "traffic": measured_traffic(name, cfg),
-            "avg_us": round(ktimes[name] * 1e3, 2), "algorithmic_flops": model["flops"],
-            "algorithmic_bytes": model["bytes"]}
+    return {"kernel": f"k_{kern}" if kernel_ms else name, "entry": name, "bound": model["bound"],
+            "achieved": round(achieved, 2), "peak": peak, "unit": unit, "frac": round(achieved / peak, 4),
+            "traffic": measured_traffic(name, cfg, kern if kernel_ms else None),
+            "avg_us": round(dur_s * 1e6, 2), "entry_us": round(ktimes[name] * 1e3, 2),
+            "algorithmic_flops": model["flops"], "algorithmic_bytes": model["bytes"]}
 
 
-def measured_traffic(entry: str, cfg: workloads.Config):
-    """HBM bytes per launch of `entry` from the committed rocprof PMC summary
-    (FETCH_SIZE + WRITE_SIZE scaled by a plain-copy calibration, summed over
-    the kernels the summary attributes to the entry point, its combine
-    kernels included), or None."""
+def measured_traffic(entry: str, cfg: workloads.Config, kernel=None):
+    """HBM bytes per launch from the committed rocprof PMC summary
+    (FETCH_SIZE + WRITE_SIZE scaled by a plain-copy calibration): of the main
+    kernel `kernel` alone as the step launches it (its fused form, with
+    combine workgroups appended, where there is one), or else summed over the
+    kernels the summary attributes to the entry point, its combine kernels
+    included; None without a summary."""
     path = os.path.join(ROOT, "profiles", f"pmc_traffic_{cfg.name}.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
         data = json.load(f)["kernels"]
+    if kernel is not None:
+        labels = [k for k in data if k.startswith(f"k_{kernel}<") and "@" not in k]
+        fused = [k for k in labels if "+" in k]
+        pick = (fused or labels)[:1]
+        return round(data[pick[0]]["fetch_bytes"] + data[pick[0]]["write_bytes"]) if pick else None
     total, found = 0.0, False
     for rec in data.values():
         if rec.get("entry") == entry:
@@ -265,11 +295,13 @@ def c5_bench(dev, steps: int, warmup: int) -> dict:
     ms = time_steps(step, steps, warmup)
     roof = workloads.roofline_us(cfg)
     kt = kernel_times(step, 3)
+    lt = launch_times(step, 3)
     return {"ms": round(ms, 3), "tflops": round(roof["flops"] / (ms * 1e-3) / 1e12, 1),
             "step_roofline_us": round(roof["roofline_us"], 1),
             "step_roofline_frac": round(roof["roofline_us"] * 1e-3 / ms, 4),
             "kernel_us": {k: round(v * 1e3, 1) for k, v in sorted(kt.items())},
-            "roofline": roofline_entry(cfg, kt)}
+            "launch_us": {k: round(v * 1e3, 1) for k, v in lt.items()},
+            "roofline": roofline_entry(cfg, kt, lt)}
 
 
 def _cpu_model() -> str:
@@ -426,6 +458,7 @@ def main():
     # the same step with the scalar sum(dQ*rq + dK*rk + dV*rv) formed and differentiated
     ms_scalar = time_steps(make_step(cfg, x, scalar_loss=True), args.steps, args.warmup) if cfg.gradgrad else None
     ktimes = kernel_times(step)
+    launch_ms = launch_times(step, args.steps)
     graph_ms = graph_steps(cfg, x, args.steps, args.warmup) if not args.no_graph else None
     roof = workloads.roofline_us(cfg)
 
@@ -457,7 +490,8 @@ def main():
         "scalar_loss_ms_per_step": None if ms_scalar is None else round(ms_scalar, 4),
         "kernel_us": {k: round(v * 1e3, 2) for k, v in sorted(ktimes.items())},
         "kernel_sum_us": round(sum(ktimes.values()) * 1e3, 2),
-        "roofline": roofline_entry(cfg, ktimes),
+        "launch_us": {k: round(v * 1e3, 2) for k, v in launch_ms.items()},
+        "roofline": roofline_entry(cfg, ktimes, launch_ms),
         "reference_h100_ms": REFERENCE_H100_MS.get(cfg.name),
     }
 

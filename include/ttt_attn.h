@@ -162,6 +162,29 @@ int ttt_attn_split_info(const ttt_problem* pr, int32_t entry, int32_t load_p, in
  */
 int ttt_attn_launch_item(int32_t nblk, int32_t chunk, int32_t column, int32_t* block, int32_t* chunk_index);
 
+/* Kernels that per-kernel timing tells apart (the main kernel of each family;
+ * a launch with combine workgroups appended to its grid is timed whole). */
+typedef enum {
+  TTT_KERNEL_FWD_ONLINE = 0,
+  TTT_KERNEL_FWD_STATS = 1,
+  TTT_KERNEL_FWD_P = 2,
+  TTT_KERNEL_BWD_DQ = 3,
+  TTT_KERNEL_BWD_DKDV = 4,
+  TTT_KERNEL_GG_ROW = 5,
+  TTT_KERNEL_GG_COL = 6
+} ttt_kernel;
+
+/*
+ * Per-kernel timing.  With capacity > 0, every later launch of a main kernel
+ * (up to `capacity` launches) is bracketed by two HIP events recorded on the
+ * launch's stream; capacity 0 turns it off.  Each call starts a new record.
+ * ttt_kernel_timing_read gives the mean duration (ms) and the number of timed
+ * launches of `kernel` since then (it waits for their events).  For one host
+ * thread at a time.  Diagnostics; no reference counterpart.
+ */
+int ttt_kernel_timing(int32_t capacity);
+int ttt_kernel_timing_read(int32_t kernel, float* mean_ms, int32_t* count);
+
 /*
  * Forward.  Writes O and lse; if p != NULL (and p->data != NULL) also writes
  * P = softmax(S) rounded to the input dtype, and computes O from that rounded

@@ -309,3 +309,32 @@ def test_slices_divisible_by_eight(b, h, save_p, chunk):
     with _lib.split_chunk(chunk):
         out = _run(xs, True, 0.125, save_p)
     _compare(out, _ref(xs, True, 0.125), dt, True, t)
+
+
+@pytest.mark.parametrize("save_p", [True, False])
+def test_launch_timing_counts_and_leaves_results_unchanged(save_p):
+    """Per-kernel timing (ttt_kernel_timing) brackets every main-kernel
+    launch of the fused step with events: one launch per family per step,
+    positive durations, each shorter than the steps' wall time, and results
+    bitwise those of an untimed step."""
+    import time
+    xs = _inputs(1, 2, 1100, 64, torch.float16, seed=5)
+    causal, scale = True, 0.125
+    ref = _run(xs, causal, scale, save_p)
+    steps = 3
+    with _lib.launch_timing() as read:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            out = _run(xs, causal, scale, save_p)
+        wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+        times = read()
+    fams = ("fwd_stats", "fwd_p") if save_p else ("fwd_online",)
+    for name in fams + ("bwd_dq", "bwd_dkdv", "gg_row", "gg_col"):
+        ms, n = times[name]
+        assert n == steps and 0.0 < ms < wall_ms, (name, ms, n, wall_ms)
+    assert set(times) == set(fams + ("bwd_dq", "bwd_dkdv", "gg_row", "gg_col"))
+    for key in ("o", "lse", "dq", "dk", "dv", "gq", "gk", "gv", "gdo"):
+        assert torch.equal(out[key], ref[key]), key
+    with _lib.launch_timing() as read:  # a new record each time, nothing timed yet
+        assert read() == {}

@@ -131,6 +131,18 @@ def _grid_order(lens, c, longest_first):
     return full + last + [None] * (cols - len(full) - len(last))
 
 
+def test_kernel_timing_validation():
+    """ttt_kernel_timing rejects a capacity past 65536 and
+    ttt_kernel_timing_read an unknown kernel; capacity 0 (off) always
+    succeeds, and with nothing timed a read reports no launches."""
+    lib = _lib.load()
+    assert lib.ttt_kernel_timing(70000) == 1 and b"capacity" in lib.ttt_last_error()
+    assert lib.ttt_kernel_timing(0) == 0
+    ms, n = ctypes.c_float(1.0), ctypes.c_int32(7)
+    assert lib.ttt_kernel_timing_read(len(_lib.KERNELS), ctypes.byref(ms), ctypes.byref(n)) == 1
+    assert lib.ttt_kernel_timing_read(5, ctypes.byref(ms), ctypes.byref(n)) == 0 and n.value == 0
+
+
 def test_launch_order_longest_first():
     """ttt_attn_launch_item (the kernels' causal_item) against the order
     written out directly, exhaustively for small slices: each chunk of each

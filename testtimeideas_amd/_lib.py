@@ -142,6 +142,10 @@ def load() -> ctypes.CDLL:
     lib.ttt_attn_launch_item.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P(ctypes.c_int32),
                                          _P(ctypes.c_int32)]
     lib.ttt_attn_launch_item.restype = ctypes.c_int
+    lib.ttt_kernel_timing.argtypes = [ctypes.c_int32]
+    lib.ttt_kernel_timing.restype = ctypes.c_int
+    lib.ttt_kernel_timing_read.argtypes = [ctypes.c_int32, _P(ctypes.c_float), _P(ctypes.c_int32)]
+    lib.ttt_kernel_timing_read.restype = ctypes.c_int
     _lib = lib
     return lib
 
@@ -624,7 +628,34 @@ def launch_item(nblk: int, chunk: int, column: int) -> Tuple[int, int]:
     return b.value, c.value
 
 
+# ttt_kernel codes (include/ttt_attn.h): the main kernels per-kernel timing tells apart
+KERNELS = ("fwd_online", "fwd_stats", "fwd_p", "bwd_dq", "bwd_dkdv", "gg_row", "gg_col")
+
+
+@contextlib.contextmanager
+def launch_timing(capacity: int = 4096):
+    """Time every main-kernel launch inside the block with HIP events on its
+    stream (ttt_kernel_timing), whichever entry point launches it, fused ones
+    included.  Yields a function returning {kernel: (mean ms, launches)};
+    call it after the work has been issued (it waits for the events)."""
+    _call("ttt_kernel_timing", capacity)
+
+    def read() -> Dict[str, Tuple[float, int]]:
+        out = {}
+        ms, n = ctypes.c_float(), ctypes.c_int32()
+        for i, name in enumerate(KERNELS):
+            _call("ttt_kernel_timing_read", i, ctypes.byref(ms), ctypes.byref(n))
+            if n.value:
+                out[name] = (ms.value, n.value)
+        return out
+
+    try:
+        yield read
+    finally:
+        _call("ttt_kernel_timing", 0)
+
+
 def exported_symbols() -> List[str]:
     """Names of the C entry points this binding uses (for ABI checks)."""
     return list(_SIGS) + ["ttt_last_error", "ttt_version", "ttt_attn_workspace_size", "ttt_attn_split_info",
-                          "ttt_attn_launch_item"]
+                          "ttt_attn_launch_item", "ttt_kernel_timing", "ttt_kernel_timing_read"]

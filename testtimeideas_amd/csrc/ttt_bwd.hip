@@ -625,6 +625,7 @@ __global__ __launch_bounds__(kThreads) void k_bwd_rowsum(Params a) {
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool XM>
 static void launch_dq_x(const Params& a, bool load_p, dim3 grid, hipStream_t st) {
+  const TimedLaunch tl(st, kTagDq);
   if (load_p)
     hipLaunchKernelGGL((k_bwd_dq<T, D, true, XM>), grid, dim3(kThreads), 0, st, a);
   else
@@ -646,6 +647,7 @@ static hipError_t launch_dq_t(int dtype, const Params& a, bool load_p, hipStream
 template <typename T, int D, bool XM>
 static void launch_dkdv_x(const Params& a, bool load_p, bool dv_only, dim3 grid, hipStream_t st, const Params& c,
                           int nx) {
+  const TimedLaunch tl(st, kTagDkdv);
   if (load_p) {
     if (dv_only)
       hipLaunchKernelGGL((k_bwd_dkdv<T, D, true, true, XM>), grid, dim3(kThreads), 0, st, a, c, nx);

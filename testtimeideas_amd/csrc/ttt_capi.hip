@@ -452,11 +452,82 @@ int scratch_on_device(void** out) {
   return TTT_OK;
 }
 
+// Per-kernel timing (ttt_kernel_timing): a pool of HIP events, two per timed
+// launch, recorded in launch order with their kernel tag.  Used from one host
+// thread at a time, as the ABI documents.
+struct TimingPool {
+  std::vector<hipEvent_t> ev;  // pairs: event 2i starts launch i, event 2i + 1 ends it
+  std::vector<int> tag;        // per event: the launch's kernel tag
+  int used = 0;
+  bool on = false;
+  bool open = false;  // a start is recorded and its end is not
+};
+TimingPool g_timing;
+
 }  // namespace
+
+namespace ttt {
+void timing_mark(hipStream_t st, int tag, bool end) {
+  TimingPool& t = g_timing;
+  if (!t.on || end != t.open) return;
+  if (end && t.tag[t.used - 1] != tag) return;
+  if (!end && t.used + 2 > (int)t.ev.size()) return;  // room for the pair
+  if (hipEventRecord(t.ev[t.used], st) != hipSuccess) {
+    (void)hipGetLastError();
+    if (end) {  // drop the unmatched start
+      --t.used;
+      t.open = false;
+    }
+    return;
+  }
+  t.tag[t.used++] = tag;
+  t.open = !end;
+}
+}  // namespace ttt
 
 extern "C" {
 
 int ttt_version(void) { return 200; }
+
+int ttt_kernel_timing(int32_t capacity) {
+  TimingPool& t = g_timing;
+  t.on = false;
+  t.open = false;
+  t.used = 0;
+  if (capacity <= 0) return TTT_OK;
+  if (capacity > (1 << 16)) return fail(TTT_ERR_INVALID_ARGUMENT, "kernel_timing: capacity %d > 65536", capacity);
+  while ((int)t.ev.size() < 2 * capacity) {
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) {
+      (void)hipGetLastError();
+      return fail(TTT_ERR_LAUNCH, "kernel_timing: hipEventCreate failed");
+    }
+    t.ev.push_back(e);
+    t.tag.push_back(-1);
+  }
+  t.on = true;
+  return TTT_OK;
+}
+
+int ttt_kernel_timing_read(int32_t kernel, float* mean_ms, int32_t* count) {
+  if (kernel < 0 || kernel >= ttt::kNumTags) return fail(TTT_ERR_INVALID_ARGUMENT, "kernel_timing_read: kernel %d", kernel);
+  TimingPool& t = g_timing;
+  double sum = 0.0;
+  int n = 0;
+  for (int i = 0; i + 1 < t.used; i += 2) {
+    if (t.tag[i] != kernel) continue;
+    float ms = 0.f;
+    if (hipEventSynchronize(t.ev[i + 1]) != hipSuccess || hipEventElapsedTime(&ms, t.ev[i], t.ev[i + 1]) != hipSuccess) {
+      (void)hipGetLastError();
+      return fail(TTT_ERR_LAUNCH, "kernel_timing_read: event %d", i);
+    }
+    sum += ms;
+    ++n;
+  }
+  if (mean_ms) *mean_ms = n ? (float)(sum / n) : 0.f;
+  if (count) *count = n;
+  return TTT_OK;
+}
 
 const char* ttt_last_error(void) { return g_err; }
 

@@ -838,9 +838,14 @@ hipError_t launch_fill_masked_p(int dtype, const Params& a, hipStream_t st) {
 template <typename T, int D, bool XM>
 static void launch_fwd_x(const Params& a, bool write_p, dim3 grid, hipStream_t st) {
   if (write_p) {
-    hipLaunchKernelGGL((k_fwd_stats<T, D, XM>), grid, dim3(kThreads), 0, st, a);
+    {
+      const TimedLaunch tl(st, kTagFwdStats);
+      hipLaunchKernelGGL((k_fwd_stats<T, D, XM>), grid, dim3(kThreads), 0, st, a);
+    }
+    const TimedLaunch tl(st, kTagFwdP);
     hipLaunchKernelGGL((k_fwd_p<T, D, XM>), grid, dim3(kThreads), 0, st, a);
   } else {
+    const TimedLaunch tl(st, kTagFwdOnline);
     hipLaunchKernelGGL((k_fwd_online<T, D, XM>), grid, dim3(kThreads), 0, st, a);
   }
 }

@@ -690,6 +690,7 @@ template <typename T, int D, bool XM>
 // False when the variant asked for is not in this object (ttt_launch.h
 // routes each variant to the object that has it).
 static bool launch_gg_row_x(const Params& a, bool load_p, bool gdo, dim3 grid, hipStream_t st) {
+  const TimedLaunch tl(st, kTagGgRow);
   if (gdo) {
     if constexpr ((TTT_GG_ROW_GDO & 2) != 0) {
       if (load_p)
@@ -729,16 +730,19 @@ static hipError_t launch_gg_col_t(int dtype, const Params& a, bool load_p, hipSt
   dim3 grid(nx + (fold ? nblk * CombineSlot<D>::kSub : 0), a.B * a.H);
   const Params& c = fold ? *rowc : a;
   const bool xm = extended_mask(a);
-  if (load_p) {
-    if (xm)
-      hipLaunchKernelGGL((k_gg_col<T, D, true, true>), grid, dim3(kThreads), 0, st, a, c, nx);
-    else
-      hipLaunchKernelGGL((k_gg_col<T, D, true, false>), grid, dim3(kThreads), 0, st, a, c, nx);
-  } else {
-    if (xm)
-      hipLaunchKernelGGL((k_gg_col<T, D, false, true>), grid, dim3(kThreads), 0, st, a, c, nx);
-    else
-      hipLaunchKernelGGL((k_gg_col<T, D, false, false>), grid, dim3(kThreads), 0, st, a, c, nx);
+  {
+    const TimedLaunch tl(st, kTagGgCol);
+    if (load_p) {
+      if (xm)
+        hipLaunchKernelGGL((k_gg_col<T, D, true, true>), grid, dim3(kThreads), 0, st, a, c, nx);
+      else
+        hipLaunchKernelGGL((k_gg_col<T, D, true, false>), grid, dim3(kThreads), 0, st, a, c, nx);
+    } else {
+      if (xm)
+        hipLaunchKernelGGL((k_gg_col<T, D, false, true>), grid, dim3(kThreads), 0, st, a, c, nx);
+      else
+        hipLaunchKernelGGL((k_gg_col<T, D, false, false>), grid, dim3(kThreads), 0, st, a, c, nx);
+    }
   }
   if (a.nchunk_max > 1) return launch_combine_sum(dtype, D, a, kOutGKGV, st);
   return hipGetLastError();

@@ -51,6 +51,21 @@ inline int occupancy_of(K kernel) {
   return n;
 }
 
+// Per-kernel timing (diagnostics, ttt_kernel_timing in include/ttt_attn.h):
+// while enabled, each launch of a main kernel is bracketed by two HIP events
+// recorded on its stream, tagged with its kind.  timing_mark does nothing
+// while disabled.  TimedLaunch records the start when constructed and the end
+// when it goes out of scope, around the launch statement.
+enum : int { kTagFwdOnline = 0, kTagFwdStats = 1, kTagFwdP = 2, kTagDq = 3, kTagDkdv = 4, kTagGgRow = 5,
+             kTagGgCol = 6, kNumTags = 7 };
+void timing_mark(hipStream_t st, int tag, bool end);
+struct TimedLaunch {
+  hipStream_t st;
+  int tag;
+  TimedLaunch(hipStream_t s, int t) : st(s), tag(t) { timing_mark(st, tag, false); }
+  ~TimedLaunch() { timing_mark(st, tag, true); }
+};
+
 // The problem has a key window or an additive bias: launches run the kernels'
 // XM instantiation.
 inline bool extended_mask(const Params& a) { return a.win > 0 || a.bias.p != nullptr; }

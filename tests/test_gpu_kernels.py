@@ -285,6 +285,20 @@ def test_split_chunks(dtype, d, causal, save_p, chunk):
     _compare(out, _ref(xs, causal, scale), dt, causal, t)
 
 
+@pytest.mark.parametrize("chunk", [5, 7])
+@pytest.mark.parametrize("save_p", [True, False])
+def test_longest_first_order_many_chunks(chunk, save_p):
+    """A split causal launch whose longest-first order has several full-chunk
+    indices and last chunks of every length below the chunk (24 blocks, three
+    slices, ragged T) gives the oracle's results in fp32 (max-abs 1e-5)."""
+    t = 1500
+    xs = _inputs(1, 3, t, 64, torch.float32, seed=23)
+    print(f"[case] longest-first chunk={chunk} save_p={save_p}", flush=True)
+    with _lib.split_chunk(chunk):
+        out = _run(xs, True, 0.125, save_p)
+    _compare(out, _ref(xs, True, 0.125), torch.float32, True, t)
+
+
 def test_split_matches_unsplit():
     """Split and unsplit runs agree to fp32 summation-order noise."""
     xs = _inputs(2, 1, 512, 64, torch.float32, seed=22)

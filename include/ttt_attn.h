@@ -157,8 +157,12 @@ int ttt_attn_split_info(const ttt_problem* pr, int32_t entry, int32_t load_p, in
  * chunk)) of a split plain-causal slice runs: block (in launch order: block i
  * streams nblk - i tiles) and chunk index, block -1 for a column with none.
  * Full chunks come first, chunk index by chunk index, then the shorter last
- * chunks, longest first.  Diagnostics; no reference counterpart (the
- * reference's kernels are not split).
+ * chunks, longest first.  When B*H is not a multiple of 8, the kernels permute
+ * the columns within each full group of 64 first, so that each XCD takes 8
+ * consecutive items (the XCD of a column is its index mod 8, the XCDs in
+ * reverse order in odd groups); `column` here is the position after that
+ * permutation.  Diagnostics; no reference counterpart (the reference's kernels
+ * are not split).
  */
 int ttt_attn_launch_item(int32_t nblk, int32_t chunk, int32_t column, int32_t* block, int32_t* chunk_index);
 

@@ -214,8 +214,9 @@ int64_t slice_workgroups(const std::vector<int64_t>& len, int64_t c) {
 // (b,h) runs the chunk the kernels' launch_item gives it (causal_item when
 // `longest_first`, else block x % nblk, chunk x / nblk); block i (launch
 // order) has len[i] tiles; `slots` usable workgroup slots spread over kXcds
-// XCDs.  Workgroups go to the XCDs round-robin in launch order, or slice y to
-// XCD y % 8 when the slices divide evenly (the kernels' grid_slot).
+// XCDs.  Workgroups go to the XCDs round-robin in grid-column order, each
+// column running the item xcd_local maps it to, or slice y to XCD y % 8 when
+// the slices divide evenly (the kernels' grid_slot).
 double simulate_launch(const std::vector<int64_t>& len, int64_t c, int64_t bh, int64_t slots, bool longest_first,
                        int64_t* nonempty) {
   const int64_t per = std::max<int64_t>(1, slots / kXcds);
@@ -230,8 +231,9 @@ double simulate_launch(const std::vector<int64_t>& len, int64_t c, int64_t bh, i
   int64_t idx = 0, used = 0;
   for (int64_t y = 0; y < bh; ++y)
     for (int64_t x = 0; x < nblk * k; ++x, ++idx) {
-      const ttt::Item it = (longest_first && k > 1) ? ttt::causal_item((int)x, (int)nblk, (int)c)
-                                                    : ttt::Item{(int)(x % nblk), (int)(x / nblk)};
+      const int xi = by_slice ? (int)x : ttt::xcd_local((int)x, (int)(nblk * k));  // as grid_slot
+      const ttt::Item it = (longest_first && k > 1) ? ttt::causal_item(xi, (int)nblk, (int)c)
+                                                    : ttt::Item{(int)(xi % nblk), (int)(xi / nblk)};
       const int64_t t = it.blk < 0 ? 0 : std::max<int64_t>(0, std::min(c, len[it.blk] - it.ch * c));
       auto& q = xcd[by_slice ? y % kXcds : idx % kXcds];
       const double f = q.top() + (t > 0 ? (double)t + kWgOverheadTiles : kEmptyWgTiles);

@@ -15,9 +15,11 @@ resident in HBM before timing starts.  Prints one JSON line (rank 0).
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import statistics
+import subprocess
 import sys
 import time
 
@@ -245,19 +247,41 @@ def fwd_mfma(cfg: workloads.Config, dev, reps: int = 50) -> dict:
 
 def sweep_bench(dev, steps: int, warmup: int) -> list:
     """The reference's published sweep (C4): b1 h1 d64 fp16, T = 512 ... 16384,
-    non-causal and causal, the full step per point."""
+    non-causal and causal, the full step per point: eager (`ms`) and replayed
+    from a HIP graph (`graph_ms`: the device time of the same launches
+    without the host's submission of each)."""
     out = []
     for causal in (False, True):
         for t in (512, 1024, 2048, 4096, 8192, 16384):
             cfg = workloads.sweep_config(t, causal)
             x = workloads.make_inputs(cfg, seed=0, device=dev)
             ms = time_steps(make_step(cfg, x), steps, warmup)
+            gms = graph_steps(cfg, x, steps, warmup)
             roof = workloads.roofline_us(cfg)
-            out.append({"t": t, "causal": causal, "ms": round(ms, 4),
+            out.append({"t": t, "causal": causal, "ms": round(ms, 4), "graph_ms": round(gms, 4),
                         "tflops": round(roof["flops"] / (ms * 1e-3) / 1e12, 2),
                         "step_roofline_frac": round(roof["roofline_us"] * 1e-3 / ms, 4),
                         "reference_h100_ms": REFERENCE_SWEEP_H100_MS[(t, causal)]})
             del x
+    return out
+
+
+# The reference's per-mode table at b1 h1 T8192 d64 fp16 non-causal
+# (artifacts/modal_bench_h100_latest.txt:79-93): ms on H100 for its Triton
+# path; its grad-grad in the save_p modes holds P constant.
+REFERENCE_MODES_T8192_H100_MS = {"recompute": 4.899, "save_p": 3.423, "save_p_triton_bwd": 3.511,
+                                 "save_p_triton_full": 3.591}
+
+
+def modes_bench(dev, steps: int, warmup: int) -> dict:
+    """The full step at b1 h1 T8192 d64 fp16 non-causal in each of the
+    reference's timed modes (all with the exact grad-grad here)."""
+    out = {}
+    base = workloads.sweep_config(8192, False)
+    x = workloads.make_inputs(base, seed=0, device=dev)
+    for mode, ref in REFERENCE_MODES_T8192_H100_MS.items():
+        cfg = dataclasses.replace(base, name=f"T8192_{mode}", bwd_mode=mode)
+        out[mode] = {"ms": round(time_steps(make_step(cfg, x), steps, warmup), 4), "reference_h100_ms": ref}
     return out
 
 
@@ -315,13 +339,38 @@ def _cpu_model() -> str:
     return "unknown"
 
 
+def _host_cpus() -> dict:
+    """The host's CPU as lscpu reports it (model, sockets x physical cores,
+    hardware threads) and the CPUs this process may use (its affinity and
+    cgroup quota)."""
+    info = {"model": _cpu_model(), "sockets": None, "physical_cores": None, "hw_threads": os.cpu_count()}
+    try:
+        out = subprocess.run(["lscpu", "-p=CORE,SOCKET"], capture_output=True, text=True, timeout=10).stdout
+        pairs = {tuple(line.split(",")[:2]) for line in out.splitlines() if line and not line.startswith("#")}
+        info["physical_cores"] = len(pairs)
+        info["sockets"] = len({s for _, s in pairs})
+    except (OSError, subprocess.SubprocessError):
+        pass
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if quota != "max":
+            usable = min(usable, max(1, int(int(quota) / int(period))))
+    except (OSError, ValueError):
+        pass
+    info["usable"] = usable
+    return info
+
+
 def cpu_baseline(cfg: workloads.Config, budget_s: float = 20.0):
     """The math path (oracle.math_path, the reference's _attention_math + autograd
-    restated) on the host CPU, on the same seeded inputs in the config dtype.
-    Bounded sample: one warmup step, then whole steps until ~budget_s of timed
-    CPU work (at least one)."""
+    restated) on the host CPU, on the same seeded inputs in the config dtype,
+    with one thread per physical core of the host, or as many as this process
+    may use if that is fewer.  Bounded sample: one warmup step, then whole
+    steps until ~budget_s of timed CPU work (at least one)."""
     from oracle import math_path
-    threads = min(os.cpu_count() or 1, 16)
+    cpus = _host_cpus()
+    threads = max(1, min(cpus["physical_cores"] or cpus["usable"], cpus["usable"]))
     torch.set_num_threads(threads)
     x = workloads.make_inputs(cfg, seed=0)
     args = [x[n] for n in ("q", "k", "v", "do", "rq", "rk", "rv")]
@@ -341,9 +390,12 @@ def cpu_baseline(cfg: workloads.Config, budget_s: float = 20.0):
         run()
         times.append((time.perf_counter() - t0) * 1e3)
     return {"value": round(statistics.median(times), 3), "unit": "ms", "cores": threads, "kind": "port",
+            "host": cpus,
             "sample": f"{len(times)} full {cfg.name} steps (b{cfg.b} h{cfg.h} T{cfg.t} d{cfg.d} {cfg.dtype} "
                       f"causal={cfg.causal}{f' window={cfg.window}' if cfg.window else ''}) after 1 warmup, "
-                      f"median; {what}; {threads} threads on {_cpu_model()}"}
+                      f"median; {what}; {threads} threads; host (lscpu): {cpus['model']}, "
+                      f"{cpus['sockets']} socket(s), {cpus['physical_cores']} physical cores, "
+                      f"{cpus['hw_threads']} hardware threads; this process may use {cpus['usable']}"}
 
 
 # The reference's meta-training configuration (cloud_ttt_e2e/configs/meta_8k_v2.yaml) and its H100 rate
@@ -496,17 +548,16 @@ def main():
     }
 
     if not args.no_extra and cfg.name == "C3":
-        cfg16 = workloads.CONFIGS["C4_16k"]
-        x16 = workloads.make_inputs(cfg16, seed=0, device=dev)
-        out["t16k_causal_ms"] = round(time_steps(make_step(cfg16, x16), max(5, args.steps // 2), 3), 4)
-        del x16
         # forward-only, O + LSE (recompute mode): MFMA utilisation of the contraction kernel
         fm = fwd_mfma(cfg, dev)
         out["fwd_lse_us"] = fm["us"]
         out["fwd_lse_mfma_frac"] = fm["mfma_frac"]
         out["fwd_lse"] = {name: fwd_mfma(workloads.CONFIGS[name], dev) for name in ("C3", "C4_16k", "C2", "C5")}
-        # the reference's published points: the C4 sweep, the C2 forward and first backward, and C5
+        # the reference's published points: the C4 sweep (its T=16384 causal point is the T16k figure),
+        # the per-mode table at T=8192 non-causal, the C2 forward and first backward, and C5
         out["c4_sweep"] = sweep_bench(dev, max(30, args.steps // 3), 30)
+        out["t16k_causal_ms"] = next(p["ms"] for p in out["c4_sweep"] if p["t"] == 16384 and p["causal"])
+        out["modes_t8192_noncausal"] = modes_bench(dev, max(30, args.steps // 3), 30)
         out["c2"] = c2_bench(dev, max(10, args.steps // 5), 5)
         out["c5"] = c5_bench(dev, 5, 2)
         # the reference TTT model's windowed attention (one launch per pass for its chunk loop)

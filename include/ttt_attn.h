@@ -157,12 +157,14 @@ int ttt_attn_split_info(const ttt_problem* pr, int32_t entry, int32_t load_p, in
  * chunk)) of a split plain-causal slice runs: block (in launch order: block i
  * streams nblk - i tiles) and chunk index, block -1 for a column with none.
  * Full chunks come first, chunk index by chunk index, then the shorter last
- * chunks, longest first.  When B*H is not a multiple of 8, the kernels permute
- * the columns within each full group of 64 first, so that each XCD takes 8
- * consecutive items (the XCD of a column is its index mod 8, the XCDs in
- * reverse order in odd groups); `column` here is the position after that
- * permutation.  Diagnostics; no reference counterpart (the reference's kernels
- * are not split).
+ * chunks, longest first.  Workgroups go to the 8 XCDs round-robin by linear
+ * workgroup id.  When B*H is not a multiple of 8 and column x of every slice
+ * runs on XCD x mod 8 (one slice, or a grid width that is a multiple of 8),
+ * the kernels permute the columns within each full group of 64 first, so
+ * that each XCD takes 8 consecutive items (the XCDs in reverse order in odd
+ * groups); `column` here is the position after that permutation.
+ * Diagnostics; no reference counterpart (the reference's kernels are not
+ * split).
  */
 int ttt_attn_launch_item(int32_t nblk, int32_t chunk, int32_t column, int32_t* block, int32_t* chunk_index);
 
@@ -325,16 +327,21 @@ int ttt_attn_gg(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
                 void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
- * ttt_attn_gg without any allocation: the same double backward, with the
- * row statistics E and F and the split's partial sums held in a static
- * device scratch of 64 MiB that the library keeps on every GPU it runs on
- * until the process ends (no workspace, no e/f buffers).  The caller passes
- * inputs and outputs only.  E and F take at most 16 MiB of it, so
+ * ttt_attn_gg with no device memory allocation: the same double backward,
+ * with the row statistics E and F and the split's partial sums held in a
+ * static device scratch of 64 MiB that the library keeps on every GPU it runs
+ * on until the process ends (no workspace, no e/f buffers).  The caller
+ * passes inputs and outputs only.  E and F take at most 16 MiB of it, so
  * B*H*T <= 2^21 (larger problems fail with TTT_ERR_INVALID_ARGUMENT); the
  * split is the one ttt_attn_gg uses when its partials fit in the rest, and
  * otherwise one with fewer chunks per block (results then agree with
  * ttt_attn_gg to summation order).  Calls on one GPU share its scratch, so
- * calls that overlap on one GPU (two streams or two threads) race.
+ * calls that overlap on one GPU (two streams or two threads) race.  It
+ * enqueues kernels only (no memset or copy), so it can be captured into a
+ * HIP graph; the first call on a device looks the scratch up
+ * (hipGetSymbolAddress) and queries kernel occupancy, so make one before
+ * capturing.  The host side still allocates host memory for its split
+ * bookkeeping.
  * No counterpart in the reference: for callers that cannot allocate device
  * memory (code under HIP graph capture, serving loops, harnesses that forbid
  * hipMalloc).

@@ -7,7 +7,10 @@ choosing its own split of every streamed loop:
   C2  b2 h4 T2048 d128 fp16 non-causal, save_p forward + first backward;
   C5  b4 h16 T8192 d128 bf16 causal (q, k, v scaled by 0.5), full grad-grad;
   and beyond the reference's sweep, b1 h1 d64 fp16 causal at T = 32768 and
-  65536 in recompute mode (the LSE-only mode such lengths need).
+  65536 in recompute mode (the LSE-only mode such lengths need);
+  TTT_W512 and TTT_W512_8K, the reference TTT model's windowed attention at
+  the sizes the benchmark runs (b8 h6 d64, local window of 512; T1024 fp32
+  and T8192 bf16), through ``windowed_attention``.
 
 Reference values: float64 closed forms on the CPU, one block of query rows at
 a time (oracle/blocked.py), on the same dtype-rounded inputs.  C5 compares two
@@ -28,6 +31,7 @@ import torch
 from oracle import blocked
 from tests._util import REL_FRO_16, check
 from testtimeideas_amd import _lib, workloads
+from testtimeideas_amd.ttt_e2e import windowed_attention
 from ttt_kernels import triton_attention
 
 pytestmark = pytest.mark.gpu
@@ -201,3 +205,50 @@ def test_long_sequence_recompute(t):
     ref, _ = _oracle_slice(xg, 0, 0, True, cfg.scale, True, device="cuda", dtype=torch.float32, block=2048)
     errs = _compare_slice(f"long T={t}", got, ref, None, 0, 0, torch.float16, GG_NAMES)
     _log("  " + ", ".join(f"{k} {v:.2e}" for k, v in errs.items()))
+
+
+def _gpu_window_step(xs, window, local, mode):
+    """O, (dQ, dK, dV) and the VJP of (dQ, dK, dV) with (rq, rk, rv) through
+    windowed_attention, as the TTT benchmark runs it."""
+    q, k, v, do, rq, rk, rv = (x.cuda() for x in xs)
+    q, k, v = (t.requires_grad_(True) for t in (q, k, v))
+    o = windowed_attention(q, k, v, window, local=local, bwd_mode=mode)
+    dq, dk, dv = torch.autograd.grad(o, (q, k, v), do, create_graph=True)
+    gq, gk, gv = torch.autograd.grad((dq, dk, dv), (q, k, v), (rq, rk, rv))
+    torch.cuda.synchronize()
+    return dict(o=o.detach(), dq=dq.detach(), dk=dk.detach(), dv=dv.detach(), gq=gq, gk=gk, gv=gv)
+
+
+@pytest.mark.parametrize("name", ["TTT_W512", "TTT_W512_8K"])
+def test_ttt_window_full(name):
+    """The benchmark's TTT workloads at full size (b8 h6 d64, local window
+    512): three (b, h) slices against the float64 row-block closed forms with
+    the same window (oracle/blocked.py, pinned to the dense closed forms with
+    the window as a bias); fp32 max-abs <= 1e-5, bf16 relative Frobenius <=
+    2e-2; bf16 also every one of the 48 slices against the same closed forms
+    in float32 on the GPU."""
+    cfg = workloads.CONFIGS[name]
+    local = cfg.window_kind == "local"
+    xs = list(workloads.make_inputs(cfg, seed=0).values())
+    _log(f"[case] {name}: b{cfg.b} h{cfg.h} T{cfg.t} {cfg.dtype} window {cfg.window} ({cfg.window_kind})")
+    got = _gpu_window_step(xs, cfg.window, local, cfg.bwd_mode)
+    for n in GG_NAMES:
+        assert bool(torch.isfinite(got[n]).all()), f"{name} {n}: non-finite values"
+    dt = cfg.torch_dtype
+    for bi, hi in ((0, 0), (3, 2), (cfg.b - 1, cfg.h - 1)):
+        args = [x[bi, hi].double() for x in xs]
+        ref = blocked.double_backward_blocked(*args, True, cfg.scale, block=512, window=cfg.window, local=local)
+        errs = {n: check(f"{name} ({bi},{hi}) {n}", got[n][bi, hi], ref[n], dt) for n in GG_NAMES}
+        _log(f"  float64 ({bi},{hi}): " + ", ".join(f"{k} {v:.2e}" for k, v in errs.items()))
+    if dt != torch.float32:
+        xg = [x.cuda() for x in xs]
+        worst = {}
+        for bi in range(cfg.b):
+            for hi in range(cfg.h):
+                args = [x[bi, hi].float() for x in xg]
+                ref = blocked.double_backward_blocked(*args, True, cfg.scale, block=1024, window=cfg.window,
+                                                      local=local)
+                for n in GG_NAMES:
+                    worst[n] = max(worst.get(n, 0.0), check(f"{name} f32 ({bi},{hi}) {n}", got[n][bi, hi],
+                                                            ref[n], dt))
+        _log("  float32, worst over 48 slices: " + ", ".join(f"{k} {v:.2e}" for k, v in worst.items()))

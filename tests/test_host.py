@@ -158,26 +158,45 @@ def test_launch_order_longest_first():
         _lib.launch_item(8, 3, 8 * 3)
 
 
-def _simulated_chunk(nblk, causal, bh, slots, min_chunk=4, lengths=None):
+def _xcd_local(x, gx):
+    """Column x's item in a grid of gx columns whose slices do not spread
+    evenly over the 8 XCDs: within each full group of 64 columns, the XCD of
+    column x (x mod 8) takes 8 consecutive items, the XCDs in reverse order
+    in odd groups; a last partial group keeps its order."""
+    grp = x // 64
+    if (grp + 1) * 64 > gx:
+        return x
+    r = x % 64
+    k = r % 8
+    return grp * 64 + 8 * (7 - k if grp % 2 else k) + r // 8
+
+
+def _simulated_chunk(nblk, causal, bh, slots, min_chunk=4, lengths=None, longest_first=None):
     """Independent restatement of the library's split chooser: list-schedule
     the grid (x = block + nblk*chunk, y = b*h; blocks in launch order with
     `lengths` tiles, by default nblk..1 when causal) onto `slots` workgroup
     slots spread round-robin over 8 XCDs (slice y to XCD y % 8 when b*h is a
-    multiple of 8), cost = makespan + 0.015 per
-    non-empty workgroup, each non-empty workgroup taking its tiles + 0.5 and
-    an empty one 0.05, plus 8 for any split.  Blocks are split only while
-    they fill fewer than the slots (twice the slots when causal)."""
+    multiple of 8; otherwise, when column x of every slice runs on XCD x % 8
+    (one slice, or a grid width that is a multiple of 8), column x runs the
+    item of _xcd_local(x)), cost =
+    makespan + 0.015 per non-empty workgroup, each non-empty workgroup taking
+    its tiles + 0.5 and an empty one 0.05, plus 8 for any split.  Blocks are
+    split only while they fill fewer than the slots (twice the slots when
+    causal)."""
     import heapq
 
     lens = lengths or ([nblk - b for b in range(nblk)] if causal else [nblk] * nblk)
     lmax = max(lens)
-    longest_first = causal and lengths is None
+    if longest_first is None:
+        longest_first = causal and lengths is None
 
     def cost(c):
         per = max(1, slots // 8)
         heaps = [[0.0] * per for _ in range(8)]
         end, used, idx = 0.0, 0, 0
         order = _grid_order(lens, c, longest_first)
+        if bh % 8 and (bh == 1 or len(order) % 8 == 0):
+            order = [order[_xcd_local(x, len(order))] for x in range(len(order))]
         for y in range(bh):
             for item in order:
                 t = 0 if item is None else min(c, lens[item[0]] - item[1] * c)
@@ -200,6 +219,21 @@ def _simulated_chunk(nblk, causal, bh, slots, min_chunk=4, lengths=None):
     return best_c
 
 
+def _simulated_pair_chunk(nblk, causal, bh, slots):
+    """The split of the O + LSE forward over row-block pairs (16-bit, d64, no
+    window or bias): the same chooser over npair = ceil(nblk/2) pairs of
+    2(npair - i) tiles in launch order when causal, simulated in units of two
+    tiles (longest-first order) with chunks of at least 8 units, else nblk
+    tiles each with chunks of at least 8 tiles; a causal chunk is even."""
+    npair = -(-nblk // 2)
+    if causal:
+        c = 2 * _simulated_chunk(npair, True, bh, slots, min_chunk=8, lengths=[npair - i for i in range(npair)],
+                                 longest_first=True)
+    else:
+        c = _simulated_chunk(npair, False, bh, slots, min_chunk=8, lengths=[nblk] * npair)
+    return min(c, nblk)
+
+
 @pytest.mark.parametrize("t,window,kind", [(8192, 512, 1), (8192, 512, 0), (1100, 512, 1), (1100, 300, 0),
                                            (4096, 64, 0), (4096, 100, 1), (2048, 4096, 0)])
 def test_window_workspace_matches_brute_force_ranges(t, window, kind):
@@ -209,7 +243,10 @@ def test_window_workspace_matches_brute_force_ranges(t, window, kind):
     nblk = -(-t // 64)
     for col, entry, nacc_nsc in ((False, _lib.ENTRY_FWD, 64 + 2), (True, _lib.ENTRY_GG_COL, 2 * 64)):
         lens = _block_tiles(t, True, window, kind, col)
-        c = _simulated_chunk(nblk, True, 1, slots, lengths=lens)
+        if entry == _lib.ENTRY_FWD and window >= t:  # no window: the row-pair forward
+            c = _simulated_pair_chunk(nblk, True, 1, slots)
+        else:
+            c = _simulated_chunk(nblk, True, 1, slots, lengths=lens)
         k = -(-max(lens) // min(c, max(lens)))
         pr = _prob(seqlen=t, window=window, window_kind=kind)
         parts = nblk * k if k > 1 else 0
@@ -226,6 +263,23 @@ def test_split_info_matches_workspace():
     assert _lib.workspace_bytes(pr, _lib.ENTRY_GG_ROW) == 128 * 8 * 64 * (3 * 64 + 3) * 4
     with pytest.raises(RuntimeError, match="single kernel family"):
         _lib.split_info(pr, _lib.ENTRY_GG, True)
+    # the chunk itself (not only the workspace it implies) against the restatement,
+    # XCD-local column order included (b*h not a multiple of 8)
+    for t in (8192, 16384, 3712, 5120, 8704):
+        for bh in (1, 2, 3):
+            nblk = t // 64
+            pr = _prob(seqlen=t, heads=bh)
+            assert _lib.split_info(pr, _lib.ENTRY_GG_ROW, True)[0] == _simulated_chunk(nblk, True, bh, 512), (t, bh)
+            assert _lib.split_info(pr, _lib.ENTRY_FWD, False)[0] == _simulated_pair_chunk(nblk, True, bh, 512), (t, bh)
+    assert _lib.split_info(_prob(seqlen=16384), _lib.ENTRY_GG_ROW, True)[0] == 64
+    # the row-pair forward at C3 and T16k: 16- and 34-tile chunks (even: whole pairs of tiles)
+    assert _lib.split_info(_prob(seqlen=8192), _lib.ENTRY_FWD, False)[:2] == (16, 8)
+    assert _lib.split_info(_prob(seqlen=16384), _lib.ENTRY_FWD, False)[:2] == (34, 8)
+    # a forced odd chunk of a causal row-pair launch is rounded up to whole pairs of tiles
+    assert _lib.split_info(_prob(seqlen=300, split_chunk=1), _lib.ENTRY_FWD, False)[:2] == (2, 3)
+    assert _lib.split_info(_prob(seqlen=300, split_chunk=1, causal=0), _lib.ENTRY_FWD, False)[:2] == (1, 5)
+    # fp32 and d128 keep the 64-row forward and its chooser
+    assert _lib.split_info(_prob(seqlen=300, split_chunk=1, dtype=2), _lib.ENTRY_FWD, False)[:2] == (1, 5)
 
 
 def test_window_and_bias_validation():
@@ -275,7 +329,13 @@ def test_workspace_sizes():
         k = -(-nblk // c)
         pr = _prob(seqlen=t, causal=causal, heads=bh)
         parts = bh * nblk * k if k > 1 else 0
-        assert _lib.workspace_bytes(pr, _lib.ENTRY_FWD) == parts * 64 * (64 + 2) * 4, (t, causal, bh, c)
+        # the O + LSE forward of 16-bit d64 problems runs over row-block pairs (its own split); fp32 does not
+        cp = _simulated_pair_chunk(nblk, bool(causal), bh, slots)
+        kp = -(-nblk // cp)
+        parts_p = bh * nblk * kp if kp > 1 else 0
+        assert _lib.workspace_bytes(pr, _lib.ENTRY_FWD) == parts_p * 64 * (64 + 2) * 4, (t, causal, bh, cp)
+        pr32 = _prob(seqlen=t, causal=causal, heads=bh, dtype=2)
+        assert _lib.workspace_bytes(pr32, _lib.ENTRY_FWD) == parts * 64 * (64 + 2) * 4, (t, causal, bh, c)
         assert _lib.workspace_bytes(pr, _lib.ENTRY_GG_ROW) == parts * 64 * (3 * 64 + 3) * 4
         # the fused double backward holds the row pass's partials (five accumulators, three row scalars)
         # and the column pass's (two accumulators) at once

@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import blocked, closed_form
+from oracle import blocked, closed_form, masks
 
 NAMES = ("o", "lse", "rowsum", "dq", "dk", "dv", "e", "f", "gq", "gk", "gv", "gdo")
 
@@ -52,3 +52,34 @@ def test_float32_agrees_with_float64():
         r = a[n].numpy()
         err = np.linalg.norm(b[n].double().numpy() - r) / np.linalg.norm(r)
         assert err < 1e-5, (n, err)
+
+
+@pytest.mark.parametrize("local", [True, False])
+@pytest.mark.parametrize("t,window,block", [(300, 64, 64), (300, 100, 64), (300, 37, 100), (257, 128, 300),
+                                            (300, 300, 64)])
+def test_blocked_window_matches_dense_bias(t, window, block, local):
+    """The key window of the row-block forms against the dense closed forms
+    with the window as an additive -inf bias (oracle.masks, pinned against
+    literal masks and the reference's chunk loop in tests/test_oracle_masks.py);
+    P is rebuilt from the blocks, zeros before each block's first key."""
+    xs = _inputs(t, 64, seed=t + window + block)
+    bias = masks.local_bias(t, window) if local else masks.window_bias(t, window)
+    ref = closed_form.double_backward(*(x.numpy() for x in xs), True, 0.125, bias=bias)
+    rows = {}
+    got = blocked.double_backward_blocked(*xs, True, 0.125, block=block, window=window, local=local,
+                                          on_p=lambda r0, r1, p: rows.__setitem__(r0, (r1, p.clone())))
+    for n in NAMES:
+        np.testing.assert_allclose(got[n].numpy(), ref[n], rtol=1e-10, atol=1e-12, err_msg=n)
+    p = np.zeros((t, t))
+    for r0, (r1, pb) in rows.items():
+        p[r0:r1, :pb.shape[1]] = pb.numpy()
+    np.testing.assert_allclose(p, ref["p"], rtol=1e-12, atol=1e-15)
+
+
+def test_blocked_window_planted_mistake_fails():
+    """A window one key too wide is caught by the dense reference."""
+    t, w = 200, 64
+    xs = _inputs(t, 64, seed=5)
+    ref = closed_form.double_backward(*(x.numpy() for x in xs), True, 0.125, bias=masks.window_bias(t, w))
+    wrong = blocked.double_backward_blocked(*xs, True, 0.125, block=64, window=w + 1, local=False)
+    assert not np.allclose(wrong["o"].numpy(), ref["o"], rtol=1e-6, atol=1e-8)

@@ -72,6 +72,36 @@ def test_noalloc_with_a_capped_split():
             check(f"t={t} {name} vs oracle", a[0, 0], o[name], torch.float16)
 
 
+def test_noalloc_captured_in_a_graph():
+    """One eager call first (the device's scratch lookup), then the entry
+    captured into a HIP graph and replayed three times, each replay followed
+    by an eager call of another size that overwrites the scratch: every
+    replay equals the eager result bitwise."""
+    print("[case] noalloc graph capture", flush=True)
+    xs = _inputs(1, 2, 1024, 64, torch.float16, seed=77)
+    q, k, v, do, rq, rk, rv = xs
+    o, lse, p = _lib.fwd(q, k, v, True, 0.125, True)
+    _, _, _, rowsum = _lib.bwd(q, k, v, o, do, lse, p, True, 0.125)
+    ref = _lib.gg_noalloc(q, k, v, do, lse, p, rowsum, rq, rk, rv, True, 0.125, True)
+    ref = [r.clone() for r in ref]
+    other = _inputs(1, 1, 300, 64, torch.float16, seed=78)
+    oq, ok, ov, odo, orq, ork, orv = other
+    oo, olse, op = _lib.fwd(oq, ok, ov, True, 0.125, True)
+    _, _, _, orow = _lib.bwd(oq, ok, ov, oo, odo, olse, op, True, 0.125)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = _lib.gg_noalloc(q, k, v, do, lse, p, rowsum, rq, rk, rv, True, 0.125, True)
+    for i in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, a, r in zip(("gq", "gk", "gv", "gdo"), out, ref):
+            assert torch.equal(a, r), f"replay {i}: {name} differs from the eager call"
+        _lib.gg_noalloc(oq, ok, ov, odo, olse, op, orow, orq, ork, orv, True, 0.125, True)
+        torch.cuda.synchronize()
+    del graph
+
+
 def test_noalloc_rejects_too_many_rows():
     """E and F must fit in their part of the scratch: B*H*T <= 2^21."""
     q = torch.empty(64, 1, 32769, 64, dtype=torch.float16, device="cuda")

@@ -74,6 +74,11 @@ constexpr int kFallbackCus = 256;
 constexpr int kFallbackPerCu = 2;
 // Chunks shorter than this are not worth a combine pass.
 constexpr int kMinChunk = 4;
+// The same for the row-pair forward, in units of two tiles: its workgroups
+// spend about four tile steps on their prologue (first loads and the shifts),
+// and b1 h1 T8192 d64 causal measured 25.3 us at 16-tile chunks against 28.1
+// at 12 (T16384: 34-tile chunks either way).
+constexpr int kMinPairChunk = 8;
 
 size_t elem_bytes(int dtype) { return dtype == TTT_F32 ? 4 : 2; }
 
@@ -214,9 +219,11 @@ int64_t slice_workgroups(const std::vector<int64_t>& len, int64_t c) {
 // (b,h) runs the chunk the kernels' launch_item gives it (causal_item when
 // `longest_first`, else block x % nblk, chunk x / nblk); block i (launch
 // order) has len[i] tiles; `slots` usable workgroup slots spread over kXcds
-// XCDs.  Workgroups go to the XCDs round-robin in grid-column order, each
-// column running the item xcd_local maps it to, or slice y to XCD y % 8 when
-// the slices divide evenly (the kernels' grid_slot).
+// XCDs.  Workgroups go to the XCDs round-robin in linear launch order; slice
+// y runs on XCD y % 8 when the slices divide evenly, else each column runs
+// the item xcd_local maps it to when xcd_columns holds (the kernels'
+// grid_slot).  The grid is taken as nblk * k columns wide (launches that
+// append combine workgroups to it are not modelled).
 double simulate_launch(const std::vector<int64_t>& len, int64_t c, int64_t bh, int64_t slots, bool longest_first,
                        int64_t* nonempty) {
   const int64_t per = std::max<int64_t>(1, slots / kXcds);
@@ -231,7 +238,9 @@ double simulate_launch(const std::vector<int64_t>& len, int64_t c, int64_t bh, i
   int64_t idx = 0, used = 0;
   for (int64_t y = 0; y < bh; ++y)
     for (int64_t x = 0; x < nblk * k; ++x, ++idx) {
-      const int xi = by_slice ? (int)x : ttt::xcd_local((int)x, (int)(nblk * k));  // as grid_slot
+      const int xi = (by_slice || !ttt::xcd_columns((int)(nblk * k), (int)bh))
+                         ? (int)x
+                         : ttt::xcd_local((int)x, (int)(nblk * k));  // as grid_slot
       const ttt::Item it = (longest_first && k > 1) ? ttt::causal_item(xi, (int)nblk, (int)c)
                                                     : ttt::Item{(int)(xi % nblk), (int)(xi / nblk)};
       const int64_t t = it.blk < 0 ? 0 : std::max<int64_t>(0, std::min(c, len[it.blk] - it.ch * c));
@@ -248,10 +257,11 @@ double simulate_launch(const std::vector<int64_t>& len, int64_t c, int64_t bh, i
 
 // Tiles per workgroup (see above).  Chunks are at least kMinChunk tiles, and a
 // split must beat no split by kSplitTiles.  Cached per shape.
-int64_t best_chunk(const ttt_problem* pr, const std::vector<int64_t>& len, bool col, int64_t bh, int64_t slots) {
+// kind: 0 row blocks, 1 column blocks, 2 row-block pairs (len in their units).
+int64_t best_chunk(const ttt_problem* pr, const std::vector<int64_t>& len, int kind, int64_t bh, int64_t slots) {
   static std::mutex mu;
   static std::map<std::tuple<int64_t, int, int, int, int, int64_t, int64_t, int>, int64_t> cache;
-  const auto key = std::make_tuple((int64_t)pr->seqlen, pr->causal, eff_window(pr), pr->window_kind, col ? 1 : 0,
+  const auto key = std::make_tuple((int64_t)pr->seqlen, pr->causal, eff_window(pr), pr->window_kind, kind,
                                    bh, slots, pr->bias.data ? 1 : 0);
   // plain causal launches run their chunks longest first (causal_item)
   const bool longest_first = pr->causal && !has_xm(pr);
@@ -268,7 +278,8 @@ int64_t best_chunk(const ttt_problem* pr, const std::vector<int64_t>& len, bool 
     best = simulate_launch(len, lmax, bh, slots, longest_first, &used) + kWgCostTiles * used;
   }
   // candidates: every length up to 64 tiles, then steps of ~3%
-  for (int64_t c = std::min<int64_t>(kMinChunk, lmax); c < lmax; c = c < 64 ? c + 1 : c + std::max<int64_t>(1, c / 32)) {
+  const int64_t cmin = kind == 2 ? kMinPairChunk : kMinChunk;
+  for (int64_t c = std::min<int64_t>(cmin, lmax); c < lmax; c = c < 64 ? c + 1 : c + std::max<int64_t>(1, c / 32)) {
     if (bh * slice_workgroups(len, c) > kMaxSimWorkgroups * slots) continue;
     int64_t used = 0;
     const double cost = simulate_launch(len, c, bh, slots, longest_first, &used) + kWgCostTiles * used + kSplitTiles;
@@ -282,7 +293,45 @@ int64_t best_chunk(const ttt_problem* pr, const std::vector<int64_t>& len, bool 
   return best_c;
 }
 
+// The O + LSE forward over row-block pairs (ttt::fwd_row_pairs): its
+// workgroups take two blocks' rows.  Causal pairs have 2(npair - i) tiles in
+// launch order (the last pair of an odd block count one fewer), so the
+// launch is simulated in units of two tiles, as causal_item orders it, and
+// the chunk is even; other pairs have nblk tiles each.  Partials stay per
+// 64-row block: nchunk_max = ceil(nblk / chunk).
+bool pair_family(const ttt_problem* pr, int fam) {
+  return fam == ttt::kFamFwdOnline && ttt::fwd_row_pairs(pr->dtype, (int)pr->head_dim, has_xm(pr));
+}
+
+Split choose_split_pairs(const ttt_problem* pr) {
+  Split s;
+  s.nblk = (int)((pr->seqlen + ttt::kBlk - 1) / ttt::kBlk);
+  const int64_t nblk = s.nblk, npair = (nblk + 1) / 2;
+  const int64_t bh = pr->batch * pr->heads;
+  int64_t c;
+  if (pr->split_chunk > 0) {
+    c = pr->split_chunk;
+  } else {
+    const int64_t slots = family_slots(pr, ttt::kFamFwdOnline, false);
+    const int64_t fill = (pr->causal ? kSimBlocks : 1) * slots;
+    if (bh * npair >= fill) {
+      c = nblk;
+    } else if (pr->causal) {
+      std::vector<int64_t> len(npair);
+      for (int64_t i = 0; i < npair; ++i) len[i] = npair - i;
+      c = 2 * best_chunk(pr, len, 2, bh, slots);
+    } else {
+      c = best_chunk(pr, std::vector<int64_t>(npair, nblk), 2, bh, slots);
+    }
+  }
+  if (pr->causal && (c & 1) && c < nblk) ++c;  // causal splits: whole pairs of tiles
+  s.chunk = (int)std::min<int64_t>(c, nblk);
+  s.nchunk_max = (int)((nblk + s.chunk - 1) / s.chunk);
+  return s;
+}
+
 Split choose_split(const ttt_problem* pr, int fam, bool load_p) {
+  if (pair_family(pr, fam)) return choose_split_pairs(pr);
   Split s;
   s.nblk = (int)((pr->seqlen + ttt::kBlk - 1) / ttt::kBlk);
   const int64_t bh = pr->batch * pr->heads;

@@ -31,6 +31,33 @@ __global__ __launch_bounds__(kThreads) void k_combine_fwd(Params a) {
   if (row >= T_) return;
   const int64_t p0 = part_index(a, bh, nblk, cs.blk, 0);
   float mm = -INFINITY;
+  if (nch <= kBatch) {
+    // One round of loads: every chunk's (m, l, acc), then the same max and
+    // the same in-order sum as the two-round form below.
+    float mk[kBatch], lk[kBatch];
+    f32x4 xk[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int64_t k = p0 + min(u, nch - 1);
+      mk[u] = a.ws_sc[k * 2 * kBlk + r];
+      lk[u] = a.ws_sc[k * 2 * kBlk + kBlk + r];
+      xk[u] = *reinterpret_cast<const f32x4*>(a.ws_acc + k * kBlk * D + part_off<D>(r, cs.d0));
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) mm = fmaxf(mm, mk[u]);
+    float ll = 0.f;
+    f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      if (u < nch) {
+        const float wk = fast_exp2(mk[u] - mm);
+        ll += lk[u] * wk;
+        v += wk * xk[u];
+      }
+    store_slot<T>(a.o, b, h, row, cs.d0, v * (1.f / ll));
+    if (cs.d0 == 0) a.lse[(int64_t)bh * T_ + row] = (mm + __log2f(ll)) * kLn2;
+    return;
+  }
   for (int k0 = 0; k0 < nch; k0 += kBatch) {
     float x[kBatch];
 #pragma unroll

@@ -129,11 +129,16 @@ __host__ __device__ inline int xcd_local(int x, int gx) {
   return grp * 64 + 8 * ((grp & 1) ? 7 - k : k) + (r >> 3);
 }
 
+// Whether column x of every slice runs on XCD x mod 8 (the condition under
+// which xcd_local keeps a column's items on one XCD): one slice, or a grid
+// width that is a multiple of 8 (linear id x + gx*y keeps x mod 8).
+__host__ __device__ inline bool xcd_columns(int gx, int gy) { return gy == 1 || (gx & 7) == 0; }
+
 __device__ __forceinline__ Slot grid_slot() {
   Slot s;
   const int gx = gridDim.x, gy = gridDim.y;
   if ((gy & 7) != 0) {
-    s.x = xcd_local(blockIdx.x, gx);
+    s.x = xcd_columns(gx, gy) ? xcd_local(blockIdx.x, gx) : (int)blockIdx.x;
     s.y = blockIdx.y;
     return s;
   }

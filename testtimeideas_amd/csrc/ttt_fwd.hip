@@ -327,6 +327,272 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<true>::value))) void k_fwd_online(Pa
 }
 
 // ---------------------------------------------------------------------------
+// O + LSE forward of 16-bit problems at D = 64 without a window or bias: the
+// forward of the recompute modes (TA:327-337, over the kernels of TA:87-206).
+//
+// A workgroup owns 128 query rows, row blocks 2j and 2j+1 of one slice (pair
+// j).  Wave w holds rows 16w + c of both blocks (row groups 0 and 1), so each
+// K and V fragment read from LDS feeds two MFMAs.  The walk is pipelined by
+// one key tile: the step of tile t issues tile t+1's score MFMAs, turns tile
+// t's scores into probabilities (work independent of those MFMAs, which the
+// compiler places among them), then issues tile t's P.V MFMAs.  K is staged
+// one tile ahead of V, both by direct loads into two LDS sets each.
+//
+// No row max is taken per tile.  Each row's shift is the exact max of its
+// walk's first tile, and a later tile keeps it unless a lane's 16
+// probabilities of one row sum past 2^15 (or to inf): then that tile is
+// redone for both groups with their exact maxima, and O and l are rescaled.
+// Probabilities stay below 2^15, inside f16's range; O and l are fp32.
+//
+// Measured on MI355X (b1 h1 d64 fp16 causal, O + LSE with its combine):
+// T16384 64 -> 52 us and T8192 27.7 -> 25.3 us against k_fwd_online.
+// Per-step cycle counts show each wave latency-bound (a 128-row step takes
+// about 2200 cycles with one or with two waves per SIMD), and neither a
+// forced interleave of MFMAs and probability work, MFMA row sums, nor the two
+// groups overlapped within a tile at three waves per SIMD was faster.
+//
+// Split walks: chunk ch of pair j covers key tiles [ch C, (ch+1) C) of both
+// blocks, and each block writes the partials of a 64-row block, as
+// k_fwd_online does (the same combine finishes them).  Causal launches run
+// the pairs' chunks longest first with causal_item over pairs in units of
+// two tiles, so C is even there (the host guarantees it).
+constexpr float kLseSumMax = 32768.f;  // 2^15
+
+
+template <typename T, int D>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_fwd_lse(Params a) {
+  static_assert(sizeof(T) == 2, "16-bit types");
+  typedef Elem<T> E;
+  typedef typename E::frag frag;
+  typedef Lds<T, D> L;
+  constexpr int KS = D / 32;
+  __shared__ __align__(16) T sK0[L::kRowElems];
+  __shared__ __align__(16) T sK1[L::kRowElems];
+  __shared__ __align__(16) T sV0[L::kRowElems];
+  __shared__ __align__(16) T sV1[L::kRowElems];
+
+  const int T_ = a.T;
+  const int nblk = (T_ + kBlk - 1) / kBlk;
+  const int npair = (nblk + 1) >> 1;
+  const int C = a.chunk;
+  const Slot sl = grid_slot();
+  const Item it =
+      (a.causal && a.nchunk_max > 1) ? causal_item(sl.x, npair, C >> 1) : Item{sl.x % npair, sl.x / npair};
+  if (it.blk < 0) return;
+  const int pj = a.causal ? npair - 1 - it.blk : it.blk;
+  const int ch = it.ch;
+  const int mb0 = 2 * pj, mb1 = mb0 + 1;
+  const int hi0 = a.causal ? mb0 + 1 : nblk, hi1 = a.causal ? mb1 + 1 : nblk;
+  const int t0 = ch * C;
+  const bool act0 = t0 < hi0;
+  const bool act1 = mb1 < nblk && t0 < hi1;
+  if (!act0 && !act1) return;
+  const int t1 = min(t0 + C, act1 ? hi1 : hi0);
+
+  const int bh = sl.y, b = bh / a.H, h = bh % a.H;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c = lane & 15, g = lane >> 4;
+  const int rl = 16 * w + c;
+  const int m0 = mb0 * kBlk + rl, m1 = mb1 * kBlk + rl;
+  const RowMask<false> mk0(a, mb0, m0), mk1(a, mb1, m1);
+  const T* Q = at<const T>(a.q, b, h);
+  const T* K = at<const T>(a.k, b, h);
+  const T* V = at<const T>(a.v, b, h);
+  frag qf[2][KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    qf[0][ks] = load_frag_row<T>(Q, a.q.st, m0, T_, 32 * ks + 8 * g);
+    qf[1][ks] = load_frag_row<T>(Q, a.q.st, m1, T_, 32 * ks + 8 * g);
+  }
+  // Raw scores q.k; c = |s| log2(e) is folded into one FMA per element (q
+  // negated for a negative scale).  Masks are applied after that FMA, so a
+  // zero scale (c = 0) gives every visible key the same probability.
+  float csl = a.scale_log2;
+  if (csl < 0.f) {
+    csl = -csl;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      qf[0][ks] = scale_frag<T>(qf[0][ks], -1.f);
+      qf[1][ks] = scale_frag<T>(qf[1][ks], -1.f);
+    }
+  }
+  f32x4 acc0[D / 16], acc1[D / 16];
+#pragma unroll
+  for (int i = 0; i < D / 16; ++i) acc0[i] = acc1[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float l0 = 0.f, l1 = 0.f, sh0, sh1;
+
+  const TileDma<T, D> dd;
+  int oK[TileDma<T, D>::kPerWave], oV[TileDma<T, D>::kPerWave];
+  dd.offsets(oK, a.k.st);
+  dd.offsets(oV, a.v.st);
+  auto fetch = [&](const T* base, int64_t ld, const int* off, int t, T* dst) __attribute__((always_inline)) {
+    const int n1 = t * kBlk;
+    const T* p = base + (int64_t)n1 * ld;
+    if (n1 + kBlk <= T_) {
+      dd.load_full(dst, p, off);
+    } else {
+      dd.load_ragged(dst, p, ld, T_ - n1, D);
+      dma_wait();
+    }
+  };
+  // Raw scores of both groups against the key tile in LDS (rows cK).
+  auto scores = [&](Tile* s, const T* cK) __attribute__((always_inline)) {
+    frag kf[4][KS];
+#pragma unroll
+    for (int a4 = 0; a4 < 4; ++a4)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kf[a4][ks] = load_frag<T>(cK + L::off(sigma(a4, c), 32 * ks + 8 * g));
+    s[0].zero();
+    s[1].zero();
+#pragma unroll
+    for (int a4 = 0; a4 < 4; ++a4)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        s[0].q[a4] = E::mma(s[0].q[a4], kf[a4][ks], qf[0][ks]);
+        s[1].q[a4] = E::mma(s[1].q[a4], kf[a4][ks], qf[1][ks]);
+      }
+  };
+  // Probabilities of one group's tile (keys from n0) under shift shv: the
+  // P.V fragments, and this lane's share of the row sum as returned.
+  auto probs = [&](auto maskc, const Tile& s, float shv, const RowMask<false>& mk, int n0, frag* pf)
+      __attribute__((always_inline)) {
+    constexpr bool MASK = decltype(maskc)::value;
+    float ts[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      float pv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float x = fmaf(s.at(kb, j), csl, -shv);
+        if constexpr (MASK) x = mk.masked(n0 + stream_index(kb, g, j)) ? -INFINITY : x;
+        pv[j] = fast_exp2(x);
+      }
+      ts[kb] = ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
+      pf[kb] = vals_frag<T>(pv);
+    }
+    return ts[0] + ts[1];
+  };
+  // Exact row max of one group's tile, base 2 (-inf where every key is masked).
+  auto exact_shift = [&](auto maskc, const Tile& s, const RowMask<false>& mk, int n0) __attribute__((always_inline)) {
+    constexpr bool MASK = decltype(maskc)::value;
+    float tm = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float x = s.at(kb, j) * csl;
+        if constexpr (MASK) x = mk.masked(n0 + stream_index(kb, g, j)) ? -INFINITY : x;
+        tm = fmaxf(tm, x);
+      }
+    return group_max(tm);
+  };
+  // The rare path: one group's tile with its exact max as the new shift.
+  auto redo = [&](auto maskc, const Tile& s, const RowMask<false>& mk, int n0, frag* pf, float& shv, float& lv,
+                  f32x4* ac) __attribute__((always_inline)) {
+    const float sn = fmaxf(shv, exact_shift(maskc, s, mk, n0));
+    const float alpha = fast_exp2(shv - sn);
+    lv *= alpha;
+#pragma unroll
+    for (int i = 0; i < D / 16; ++i) ac[i] *= alpha;
+    shv = sn;
+    return probs(maskc, s, sn, mk, n0, pf);
+  };
+  // Tiles at or past the pair's first diagonal, or ragged, take the masked step.
+  auto masked_tile = [&](int t) __attribute__((always_inline)) {
+    return (a.causal && t >= mb0) || (t * kBlk + kBlk > T_);
+  };
+
+  // Prologue: K and V of tile t0 and K of tile t0 + 1; tile t0's scores and
+  // the shifts.
+  fetch(K, a.k.st, oK, t0, sK0);
+  fetch(V, a.v.st, oV, t0, sV0);
+  if (t0 + 1 < t1) fetch(K, a.k.st, oK, t0 + 1, sK1);
+  dma_wait();
+  __syncthreads();
+  Tile s[2];
+  scores(s, sK0);
+  if (masked_tile(t0)) {
+    sh0 = exact_shift(std::true_type{}, s[0], mk0, t0 * kBlk);
+    sh1 = exact_shift(std::true_type{}, s[1], mk1, t0 * kBlk);
+  } else {
+    sh0 = exact_shift(std::false_type{}, s[0], mk0, t0 * kBlk);
+    sh1 = exact_shift(std::false_type{}, s[1], mk1, t0 * kBlk);
+  }
+  // -inf only for a group whose rows see no key of this chunk (a group with
+  // no work here; its results are not stored)
+  if (sh0 == -INFINITY) sh0 = 0.f;
+  if (sh1 == -INFINITY) sh1 = 0.f;
+
+  // The step of tile t, u = t - t0 of parity P: K of tile t + 1 is in set
+  // 1 - P and V of tile t in set P; s holds tile t's raw scores.
+  auto step = [&](auto par, auto maskc, int t) __attribute__((always_inline)) {
+    constexpr int P = decltype(par)::value;
+    dma_wait();       // this wave's loads of K(t + 1) and V(t)
+    __syncthreads();  // everyone's, and everyone is done with K(t) and V(t - 1)
+    if (t + 2 < t1) fetch(K, a.k.st, oK, t + 2, P == 0 ? sK0 : sK1);
+    if (t + 1 < t1) fetch(V, a.v.st, oV, t + 1, P == 0 ? sV1 : sV0);
+    const int n0 = t * kBlk;
+    frag pf0[2], pf1[2];
+    float ts0, ts1;
+    Tile sn[2];
+    if (t + 1 < t1) {
+      scores(sn, P == 0 ? sK1 : sK0);
+      ts0 = probs(maskc, s[0], sh0, mk0, n0, pf0);
+      ts1 = probs(maskc, s[1], sh1, mk1, n0, pf1);
+    } else {
+      ts0 = probs(maskc, s[0], sh0, mk0, n0, pf0);
+      ts1 = probs(maskc, s[1], sh1, mk1, n0, pf1);
+    }
+    // Both groups' probabilities are formed here, before the branch (left to
+    // itself the compiler sinks the work that only the common path uses below
+    // it, out of the MFMAs' reach).
+    asm volatile("" : "+v"(ts0), "+v"(ts1), "+v"(pf0[0]), "+v"(pf0[1]), "+v"(pf1[0]), "+v"(pf1[1]));
+    if (__builtin_amdgcn_ballot_w64(!(ts0 <= kLseSumMax) | !(ts1 <= kLseSumMax)) != 0) {
+      ts0 = redo(maskc, s[0], mk0, n0, pf0, sh0, l0, acc0);
+      ts1 = redo(maskc, s[1], mk1, n0, pf1, sh1, l1, acc1);
+    }
+    l0 += ts0;
+    l1 += ts1;
+    mm_s2<T, D>(acc0, pf0, acc1, pf1, P == 0 ? sV0 : sV1);
+    s[0] = sn[0];
+    s[1] = sn[1];
+  };
+  const int tq = min(t1, max(t0, min(a.causal ? mb0 : t1, (T_ % kBlk) ? nblk - 1 : t1)));  // first masked tile
+  int t = t0;
+  for (; t + 1 < tq; t += 2) {
+    step(Parity<0>{}, std::false_type{}, t);
+    step(Parity<1>{}, std::false_type{}, t + 1);
+  }
+  if (t < tq) {
+    step(Parity<0>{}, std::false_type{}, t);
+    ++t;
+  }
+  for (; t < t1; ++t) {
+    if ((t - t0) & 1)
+      step(Parity<1>{}, std::true_type{}, t);
+    else
+      step(Parity<0>{}, std::true_type{}, t);
+  }
+
+  const int64_t rbase = (int64_t)bh * T_;
+  auto finish = [&](int mb, int m, const f32x4* ac, float lv, float shv, int hi) __attribute__((always_inline)) {
+    const float lt = group_sum(lv);
+    if ((hi + C - 1) / C == 1) {
+      if (m < T_ && g == 0) a.lse[rbase + m] = (shv + __log2f(lt)) * kLn2;
+      store_acc_rows<T, D>(at<T>(a.o, b, h), a.o.st, m, T_, ac, 1.f / lt);
+    } else {
+      const int64_t part = part_index(a, bh, nblk, mb, ch);
+      store_acc_partial<D>(a.ws_acc + part * kBlk * D, rl, ac);
+      if (g == 0) {
+        a.ws_sc[part * 2 * kBlk + rl] = shv;
+        a.ws_sc[part * 2 * kBlk + kBlk + rl] = lt;
+      }
+    }
+  };
+  if (act0) finish(mb0, m0, acc0, l0, sh0, hi0);
+  if (act1) finish(mb1, m1, acc1, l1, sh1, hi1);
+}
+
+// ---------------------------------------------------------------------------
 // Waves per SIMD the statistics and P passes are compiled for: their 16-bit
 // D = 64 two-set forms (two steps per loop iteration) without a register cap
 // keep their MFMA results in AGPRs and copy them every step.
@@ -844,6 +1110,12 @@ static void launch_fwd_x(const Params& a, bool write_p, dim3 grid, hipStream_t s
     }
     const TimedLaunch tl(st, kTagFwdP);
     hipLaunchKernelGGL((k_fwd_p<T, D, XM>), grid, dim3(kThreads), 0, st, a);
+  } else if constexpr (!XM && sizeof(T) == 2 && D == 64) {  // fwd_row_pairs
+    const int npair = ((a.T + kBlk - 1) / kBlk + 1) >> 1;
+    const int c2 = a.chunk >> 1;
+    const int kp = (a.causal && a.nchunk_max > 1) ? (npair + c2 - 1) / c2 : a.nchunk_max;
+    const TimedLaunch tl(st, kTagFwdOnline);
+    hipLaunchKernelGGL((k_fwd_lse<T, D>), dim3(npair * kp, a.B * a.H), dim3(kThreads), 0, st, a);
   } else {
     const TimedLaunch tl(st, kTagFwdOnline);
     hipLaunchKernelGGL((k_fwd_online<T, D, XM>), grid, dim3(kThreads), 0, st, a);
@@ -854,6 +1126,9 @@ template <typename T, int D>
 static hipError_t launch_fwd_t(int dtype, const Params& a, bool write_p, hipStream_t st) {
   const int nblk = (a.T + kBlk - 1) / kBlk;
   dim3 grid(nblk * a.nchunk_max, a.B * a.H);
+  // row pairs of a split causal walk take chunks of an even number of tiles
+  if (!write_p && fwd_row_pairs(dtype, D, extended_mask(a)) && a.causal && a.nchunk_max > 1 && (a.chunk & 1))
+    return hipErrorInvalidValue;
   if (extended_mask(a))
     launch_fwd_x<T, D, true>(a, write_p, grid, st);
   else
@@ -865,6 +1140,8 @@ static hipError_t launch_fwd_t(int dtype, const Params& a, bool write_p, hipStre
 
 template <typename T, int D, bool XM>
 static int occupancy_fwd_t(bool write_p) {
+  if constexpr (!XM && sizeof(T) == 2 && D == 64)
+    if (!write_p) return occupancy_of(k_fwd_lse<T, D>);
   if (!write_p) return occupancy_of(k_fwd_online<T, D, XM>);
   return std::min(occupancy_of(k_fwd_stats<T, D, XM>), occupancy_of(k_fwd_p<T, D, XM>));
 }

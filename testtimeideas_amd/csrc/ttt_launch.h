@@ -70,6 +70,11 @@ struct TimedLaunch {
 // XM instantiation.
 inline bool extended_mask(const Params& a) { return a.win > 0 || a.bias.p != nullptr; }
 
+// The O + LSE forward of 16-bit problems at D = 64 without a window or bias
+// runs k_fwd_lse, whose workgroups take pairs of row blocks (split causal
+// walks in chunks of an even number of tiles); others run k_fwd_online.
+inline bool fwd_row_pairs(int dtype, int D, bool xm) { return dtype != kF32 && D == 64 && !xm; }
+
 // Occupancy of the kernels a launch of each family runs (the smaller one when
 // it runs two); xm selects the window/bias instantiation.
 int occupancy_fwd(int dtype, int D, bool write_p, bool xm);

@@ -320,7 +320,19 @@ def c5_bench(dev, steps: int, warmup: int) -> dict:
     roof = workloads.roofline_us(cfg)
     kt = kernel_times(step, 3)
     lt = launch_times(step, 3)
-    return {"ms": round(ms, 3), "tflops": round(roof["flops"] / (ms * 1e-3) / 1e12, 1),
+    # the same step with every kernel family's configuration measured per shape (the first step tunes)
+    was = autotune.enabled()
+    autotune.enable(True)
+    try:
+        step()
+        torch.cuda.synchronize()
+        tuned_ms = time_steps(step, steps, 1)
+        tuned = {str(k[0]): v for k, v in autotune.choices().items()}
+    finally:
+        autotune.enable(was)
+        autotune.clear()
+    return {"ms": round(ms, 3), "autotuned_ms": round(tuned_ms, 3), "autotuned_choices": tuned,
+            "tflops": round(roof["flops"] / (ms * 1e-3) / 1e12, 1),
             "step_roofline_us": round(roof["roofline_us"], 1),
             "step_roofline_frac": round(roof["roofline_us"] * 1e-3 / ms, 4),
             "kernel_us": {k: round(v * 1e3, 1) for k, v in sorted(kt.items())},

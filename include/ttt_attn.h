@@ -128,6 +128,15 @@ typedef struct ttt_problem {
                           like a mask, receives no gradient.  A row
                           left with no finite score gives NaN, as
                           softmax does.                           */
+  int32_t block_rows;  /* query rows per workgroup of the O + LSE
+                          forward (ttt_attn_fwd without p): 0 = the
+                          library's choice (128 for 16-bit types at
+                          D = 64 without a window or bias, else 64);
+                          64; or 128 (16-bit types without a window
+                          or bias).  Other entry points ignore it.
+                          A per-shape tuning knob, like split_chunk;
+                          the reference's kernels pick BLOCK_M per
+                          shape (triton_attention.py:78-85).      */
 } ttt_problem;
 
 /* Library version (major*10000 + minor*100 + patch). */

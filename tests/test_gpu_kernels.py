@@ -352,3 +352,43 @@ def test_launch_timing_counts_and_leaves_results_unchanged(save_p):
         assert torch.equal(out[key], ref[key]), key
     with _lib.launch_timing() as read:  # a new record each time, nothing timed yet
         assert read() == {}
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("rows", [64, 128])
+@pytest.mark.parametrize("chunk", [0, 2, 5])
+def test_fwd_block_rows(dtype, d, causal, rows, chunk):
+    """The O + LSE forward in 64-row blocks (k_fwd_online) and in 128-row
+    blocks (k_fwd_lse, pairs of row blocks), unsplit and split into chunks
+    (a causal row-pair launch rounds 5 up to 6 tiles), on a ragged sequence
+    of an odd block count (the last pair has one block): O and LSE against
+    the float64 oracle, and the first backward and grad-grad from that
+    forward."""
+    dt = DT[dtype]
+    t = 300
+    xs = _inputs(1, 3, t, d, dt, seed=60 + d + rows)
+    scale = 1.0 / math.sqrt(d)
+    print(f"[case] fwd block_rows={rows} dtype={dtype} d={d} causal={causal} chunk={chunk}", flush=True)
+    with _lib.block_rows(rows), _lib.split_chunk(chunk):
+        out = _run(xs, causal, scale, False)
+    _compare(out, _ref(xs, causal, scale), dt, causal, t)
+
+
+def test_fwd_block_rows_edge_cases():
+    """Rows past T in a pair's second block, T = 1, one pair whose second
+    block is absent, and a negative and a zero scale (q negated; every visible
+    key equally likely) in 128-row blocks."""
+    dt = torch.float16
+    for t, causal, scale in ((65, True, 0.125), (1, False, 0.125), (64, True, 0.125), (200, True, -0.125),
+                             (130, False, 0.0), (130, True, 0.0)):
+        xs = _inputs(2, 1, t, 64, dt, seed=t)
+        print(f"[case] fwd block_rows=128 t={t} causal={causal} scale={scale}", flush=True)
+        with _lib.block_rows(128):
+            q, k, v = (x.cuda() for x in xs[:3])
+            o, lse, _ = _lib.fwd(q, k, v, causal, scale, False)
+            torch.cuda.synchronize()
+        ref = cf.forward(*(x.double().numpy() for x in xs[:3]), causal, scale)
+        check(f"t={t} o", o, ref["o"], dt)
+        check(f"t={t} lse", lse, ref["lse"], torch.float32, abs_tol=2e-3)

@@ -43,10 +43,12 @@ def test_torch_binding_loads():
 
 def _prob(**kw):
     d = dict(dtype=0, causal=1, batch=1, heads=1, seqlen=128, head_dim=64, scale=0.125, split_chunk=0, window=0,
-             window_kind=0)
+             window_kind=0, block_rows=0)
     d.update(kw)
-    return _lib._Problem(d["dtype"], d["causal"], d["batch"], d["heads"], d["seqlen"], d["head_dim"],
-                         d["scale"], d["split_chunk"], d["window"], d["window_kind"])
+    pr = _lib._Problem(d["dtype"], d["causal"], d["batch"], d["heads"], d["seqlen"], d["head_dim"],
+                       d["scale"], d["split_chunk"], d["window"], d["window_kind"])
+    pr.block_rows = d["block_rows"]
+    return pr
 
 
 def _v(addr=0x10000, st=64):
@@ -464,3 +466,32 @@ def test_noalloc_rejects_too_many_rows_without_gpu():
                                  _v(), _v(), _v(), None, None)
     assert rc == 1
     assert b"B*H*T" in lib.ttt_last_error()
+
+
+def test_block_rows_choice():
+    """ttt_problem.block_rows: the library runs 128-row pairs for 16-bit d64
+    problems without a window or bias and 64-row blocks otherwise; 64 and
+    128 can be asked for (128 only where pairs run); the split follows the
+    kernel that runs."""
+    slots = 512
+    nblk = 8192 // 64
+    c64 = _simulated_chunk(nblk, True, 1, slots)
+    cp = _simulated_pair_chunk(nblk, True, 1, slots)
+    assert _lib.split_info(_prob(seqlen=8192), _lib.ENTRY_FWD, False)[0] == cp
+    assert _lib.split_info(_prob(seqlen=8192, block_rows=128), _lib.ENTRY_FWD, False)[0] == cp
+    assert _lib.split_info(_prob(seqlen=8192, block_rows=64), _lib.ENTRY_FWD, False)[0] == c64
+    # d128: 64-row blocks unless asked for, then pairs (the same pair chooser)
+    assert _lib.split_info(_prob(seqlen=8192, head_dim=128), _lib.ENTRY_FWD, False)[0] == c64
+    assert _lib.split_info(_prob(seqlen=8192, head_dim=128, block_rows=128), _lib.ENTRY_FWD, False)[0] == cp
+    # workspaces follow the same splits
+    k64, kp = -(-nblk // c64), -(-nblk // cp)
+    assert _lib.workspace_bytes(_prob(seqlen=8192, block_rows=64), _lib.ENTRY_FWD) == nblk * k64 * 64 * 66 * 4
+    assert _lib.workspace_bytes(_prob(seqlen=8192), _lib.ENTRY_FWD) == nblk * kp * 64 * 66 * 4
+    # the forward with P and the other entries ignore it
+    assert _lib.split_info(_prob(seqlen=8192, block_rows=64), _lib.ENTRY_FWD_P, True) == \
+        _lib.split_info(_prob(seqlen=8192), _lib.ENTRY_FWD_P, True)
+    lib = _lib.load()
+    assert _fwd_rc(_prob(block_rows=96)) == 1 and b"block_rows" in lib.ttt_last_error()
+    assert _fwd_rc(_prob(block_rows=128, dtype=2)) == 2 and b"block_rows" in lib.ttt_last_error()
+    assert _fwd_rc(_prob(block_rows=128, window=16)) == 2
+    assert lib.ttt_version() >= 300

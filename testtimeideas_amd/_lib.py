@@ -60,6 +60,7 @@ class _Problem(ctypes.Structure):
         ("window", ctypes.c_int32),
         ("window_kind", ctypes.c_int32),
         ("bias", _View),
+        ("block_rows", ctypes.c_int32),
     ]
 
 
@@ -313,7 +314,26 @@ def split_chunk(n: int):
         _split_chunk = prev
 
 
-def _problem(x: torch.Tensor, mask, scale: float, split: Optional[int] = None) -> _Problem:
+# Query rows per workgroup of the O + LSE forward (ttt_problem.block_rows);
+# 0 lets the library (or the autotuner) choose.
+_block_rows = 0
+
+
+@contextlib.contextmanager
+def block_rows(n: int):
+    """Force the block height of the O + LSE forward (64, or 128 for 16-bit
+    problems without a window or bias) inside the block; used by tests to
+    run either kernel."""
+    global _block_rows
+    prev = _block_rows
+    _block_rows = int(n)
+    try:
+        yield
+    finally:
+        _block_rows = prev
+
+
+def _problem(x: torch.Tensor, mask, scale: float, split: Optional[int] = None, rows: int = 0) -> _Problem:
     b, h, t, d = x.shape
     m = as_mask(mask)
     bv = _View(None, 0, 0, 0)
@@ -321,7 +341,7 @@ def _problem(x: torch.Tensor, mask, scale: float, split: Optional[int] = None) -
         s = m.bias.stride()
         bv = _View(m.bias.data_ptr(), s[0], s[1], s[2])
     return _Problem(_DTYPE_CODE[x.dtype], 1 if m.causal else 0, b, h, t, d, float(scale),
-                    _split_chunk if split is None else int(split), int(m.window), int(m.window_kind), bv)
+                    _split_chunk if split is None else int(split), int(m.window), int(m.window_kind), bv, int(rows))
 
 
 def _split_for(entry: int, x: torch.Tensor, m, scale: float, load_p: bool, gdo: bool, run) -> int:
@@ -340,6 +360,38 @@ def _split_for(entry: int, x: torch.Tensor, m, scale: float, load_p: bool, gdo: 
         return c0, split_info(pr, entry, load_p, gdo)[0]
 
     return autotune.chunk(key, pick, run)
+
+
+def _fwd_config(x: torch.Tensor, m, scale: float, run) -> Tuple[int, int]:
+    """(block_rows, split) of the O + LSE forward: (0, split_chunk) when a
+    split is forced, (0, 0) -- the library's choice -- with tuning off, else
+    the fastest of the library's choice and, for each block height the
+    problem allows (64 rows; 128 for 16-bit types without a window or bias),
+    the splits around that height's own pick, timed with `run((rows,
+    split))`; (0, 0) again when the library's choice wins."""
+    if _block_rows or _split_chunk or not autotune.enabled():
+        return _block_rows, _split_chunk
+    key = ("fwd_rows", x.dtype, m.causal, tuple(x.shape), int(m.window), int(m.window_kind), m.bias is not None)
+    t = x.shape[2]
+    pairs_ok = x.dtype != torch.float32 and m.bias is None and not (0 < int(m.window) < t)
+
+    def options():
+        opts = []
+        for rows in ((64, 128) if pairs_ok else (64,)):
+            pr = _problem(x, m, scale, 0, rows)
+            c0 = split_info(pr, ENTRY_FWD, False)[0]
+            pr.split_chunk = 1 << 30  # clipped to the longest walk
+            lmax = split_info(pr, ENTRY_FWD, False)[0]
+            for c in autotune.candidates(c0, lmax):
+                pr.split_chunk = c
+                ce = split_info(pr, ENTRY_FWD, False)[0]  # as launched (causal row pairs: even)
+                if (rows, ce) not in opts:
+                    opts.append((rows, ce))
+        pr = _problem(x, m, scale, 0, 0)
+        lib_rows = 128 if pairs_ok and x.shape[3] <= 64 else 64
+        return (lib_rows, split_info(pr, ENTRY_FWD, False)[0]), opts
+
+    return autotune.choose(key, options, run)
 
 
 def prep_bias(bias: torch.Tensor, b: int, h: int, t: int, dtype: torch.dtype, device) -> torch.Tensor:
@@ -450,16 +502,20 @@ def fwd(q, k, v, mask, scale: float, want_p: bool):
     m = as_mask(mask)
     ent = ENTRY_FWD_P if want_p else ENTRY_FWD
 
-    def run(c):
-        return ext().fwd(q, k, v, m.causal, float(scale), bool(want_p), c, int(m.window), int(m.window_kind), m.bias)
+    def run(c, rows=0):
+        return ext().fwd(q, k, v, m.causal, float(scale), bool(want_p), c, int(m.window), int(m.window_kind), m.bias,
+                         rows)
 
-    c = _split_for(ent, q, m, scale, want_p, False, run)
+    if want_p:
+        rows, c = 0, _split_for(ent, q, m, scale, want_p, False, run)
+    else:
+        rows, c = _fwd_config(q, m, scale, lambda rc: run(rc[1], rc[0]))
     if _timing is None:
-        return tuple(run(c))
+        return tuple(run(c, rows))
     o = _empty_like_out(q)
     lse = _stats(q)
     p = alloc_p(q) if want_p else None
-    pr = _problem(q, mask, scale, c)
+    pr = _problem(q, mask, scale, c, rows)
     wp, wn, _wbuf = _workspace(pr, ENTRY_FWD_P if want_p else ENTRY_FWD, q.device)
     _timed("ttt_attn_fwd", ctypes.byref(pr), _view(q), _view(k), _view(v), _view(o), lse.data_ptr(),
            _view(p), wp, wn, _stream())

@@ -1,4 +1,7 @@
-"""Measured choice of the split (tiles per workgroup) of each kernel family.
+"""Measured choice of the split (tiles per workgroup) of each kernel family,
+and of the block height (64 or 128 query rows per workgroup, which also sets
+the waves per SIMD and LDS buffer sets of the kernel that runs) of the O + LSE
+forward.
 
 The library picks a split by simulating the launch (csrc/ttt_capi.hip,
 ``choose_split``).  With autotuning on, the first call of a kernel family on a
@@ -23,7 +26,7 @@ from typing import Callable, Dict, List, Tuple
 import torch
 
 _enabled = os.environ.get("TTT_AUTOTUNE", "0") not in ("", "0")
-_cache: Dict[tuple, int] = {}
+_cache: Dict[tuple, object] = {}
 # Splits tried around the library's pick c0: c0 * these, and no split at all.
 _FACTORS = (0.5, 0.75, 1.25, 1.5, 2.0)
 _MIN_CHUNK = 4  # the library's smallest split (kMinChunk)
@@ -43,9 +46,10 @@ def clear() -> None:
     _cache.clear()
 
 
-def choices() -> Dict[tuple, int]:
-    """The splits chosen so far: {(family, shape key): tiles per workgroup},
-    0 where the library's own pick won."""
+def choices() -> Dict[tuple, object]:
+    """The choices so far: {(family, shape key): tiles per workgroup, or
+    (block rows, tiles) for the O + LSE forward}, 0 / (0, 0) where the
+    library's own pick won."""
     return dict(_cache)
 
 
@@ -76,6 +80,32 @@ def _time(run: Callable[[int], None], c: int) -> float:
     e.record()
     e.synchronize()
     return s.elapsed_time(e) / _REPS
+
+
+def choose(key: tuple, options: Callable[[], Tuple[tuple, List[tuple]]], run: Callable[[tuple], None]) -> tuple:
+    """A kernel configuration beyond the split (for the O + LSE forward:
+    (block rows, split)): the cached choice, or the fastest of the candidate
+    configurations timed with `run(cfg)` on the current stream.  `options()`
+    gives (the library's own configuration, the candidates, which include
+    it); (0, 0), meaning the library's choice, is returned when tuning is
+    off, a graph is being captured, or the library's own configuration
+    wins."""
+    if not _enabled or _capturing():
+        return (0, 0)
+    c = _cache.get(key)
+    if c is not None:
+        return c
+    lib, cands = options()
+    if lib not in cands:
+        cands = [lib] + cands
+    if len(cands) == 1:
+        best = cands[0]
+    else:
+        times = [(_time(run, cfg), i, cfg) for i, cfg in enumerate(cands)]
+        best = min(times)[2]
+    best = (0, 0) if best == lib else best
+    _cache[key] = best
+    return best
 
 
 def chunk(key: tuple, pick: Callable[[], Tuple[int, int]], run: Callable[[int], None]) -> int:

@@ -120,6 +120,8 @@ int check_problem(const ttt_problem* pr) {
   if (pr->window > 0 && pr->causal != 1) return fail(TTT_ERR_INVALID_ARGUMENT, "a window needs causal=1");
   if (pr->window_kind != TTT_WINDOW_SLIDING && pr->window_kind != TTT_WINDOW_LOCAL)
     return fail(TTT_ERR_INVALID_ARGUMENT, "window_kind %d is not sliding (0) or local (1)", pr->window_kind);
+  if (pr->block_rows != 0 && pr->block_rows != 64 && pr->block_rows != 128)
+    return fail(TTT_ERR_INVALID_ARGUMENT, "block_rows %d is not 0, 64 or 128", pr->block_rows);
   if (pr->bias.data) {
     const int64_t eb = (int64_t)elem_bytes(pr->dtype);
     if (!aligned16(pr->bias.data)) return fail(TTT_ERR_INVALID_ARGUMENT, "bias: base pointer not 16-byte aligned");
@@ -166,7 +168,7 @@ int device_cus(int* dev_out) {
 // Workgroup slots of family `fam`'s kernel (variant load_p) on the current
 // device; cached per (device, family, dtype, head dim, variant).
 int64_t family_slots(const ttt_problem* pr, int fam, bool load_p) {
-  static std::atomic<int> per_cu[16][7][3][2][2][2];
+  static std::atomic<int> per_cu[16][ttt::kNumFams][3][2][2][2];
   int dev = 0;
   const int cus = device_cus(&dev);
   if (cus == 0) return (int64_t)kFallbackCus * kFallbackPerCu * kSlotFill / 100;
@@ -177,6 +179,7 @@ int64_t family_slots(const ttt_problem* pr, int fam, bool load_p) {
     const int D = (int)pr->head_dim;
     switch (fam) {
       case ttt::kFamFwdOnline: n = ttt::occupancy_fwd(dt, D, false, xm); break;
+      case ttt::kFamFwdPairs: n = ttt::occupancy_fwd_pairs(dt, D); break;
       case ttt::kFamFwdP: n = ttt::occupancy_fwd(dt, D, true, xm); break;
       case ttt::kFamDq: n = ttt::occupancy_dq(dt, D, load_p, xm); break;
       case ttt::kFamDkdv: n = ttt::occupancy_dkdv(dt, D, load_p, xm); break;
@@ -293,15 +296,13 @@ int64_t best_chunk(const ttt_problem* pr, const std::vector<int64_t>& len, int k
   return best_c;
 }
 
-// The O + LSE forward over row-block pairs (ttt::fwd_row_pairs): its
+// The O + LSE forward over row-block pairs (kFamFwdPairs): its
 // workgroups take two blocks' rows.  Causal pairs have 2(npair - i) tiles in
 // launch order (the last pair of an odd block count one fewer), so the
 // launch is simulated in units of two tiles, as causal_item orders it, and
 // the chunk is even; other pairs have nblk tiles each.  Partials stay per
 // 64-row block: nchunk_max = ceil(nblk / chunk).
-bool pair_family(const ttt_problem* pr, int fam) {
-  return fam == ttt::kFamFwdOnline && ttt::fwd_row_pairs(pr->dtype, (int)pr->head_dim, has_xm(pr));
-}
+bool pair_family(int fam) { return fam == ttt::kFamFwdPairs; }
 
 Split choose_split_pairs(const ttt_problem* pr) {
   Split s;
@@ -312,7 +313,7 @@ Split choose_split_pairs(const ttt_problem* pr) {
   if (pr->split_chunk > 0) {
     c = pr->split_chunk;
   } else {
-    const int64_t slots = family_slots(pr, ttt::kFamFwdOnline, false);
+    const int64_t slots = family_slots(pr, ttt::kFamFwdPairs, false);
     const int64_t fill = (pr->causal ? kSimBlocks : 1) * slots;
     if (bh * npair >= fill) {
       c = nblk;
@@ -331,7 +332,7 @@ Split choose_split_pairs(const ttt_problem* pr) {
 }
 
 Split choose_split(const ttt_problem* pr, int fam, bool load_p) {
-  if (pair_family(pr, fam)) return choose_split_pairs(pr);
+  if (pair_family(fam)) return choose_split_pairs(pr);
   Split s;
   s.nblk = (int)((pr->seqlen + ttt::kBlk - 1) / ttt::kBlk);
   const int64_t bh = pr->batch * pr->heads;
@@ -353,9 +354,11 @@ Split choose_split(const ttt_problem* pr, int fam, bool load_p) {
   return s;
 }
 
-int family_of(int entry, bool gdo) {
+int family_of(const ttt_problem* pr, int entry, bool gdo) {
   switch (entry) {
-    case TTT_ENTRY_FWD: return ttt::kFamFwdOnline;
+    case TTT_ENTRY_FWD:
+      return ttt::fwd_row_pairs(pr->dtype, (int)pr->head_dim, has_xm(pr), pr->block_rows) ? ttt::kFamFwdPairs
+                                                                                          : ttt::kFamFwdOnline;
     case TTT_ENTRY_FWD_P: return ttt::kFamFwdP;
     case TTT_ENTRY_BWD_DQ: return ttt::kFamDq;
     case TTT_ENTRY_BWD_DKDV: return ttt::kFamDkdv;
@@ -384,8 +387,8 @@ int64_t entry_bytes(const ttt_problem* pr, int entry, bool gdo) {
   if (entry == TTT_ENTRY_BWD) return fam_bytes(pr, ttt::kFamDq) + fam_bytes(pr, ttt::kFamDkdv);
   // the fused double backward keeps the row pass's partials while the column
   // pass writes its own
-  if (entry == TTT_ENTRY_GG) return fam_bytes(pr, family_of(TTT_ENTRY_GG_ROW, gdo)) + fam_bytes(pr, ttt::kFamGgCol);
-  const int fam = family_of(entry, gdo);
+  if (entry == TTT_ENTRY_GG) return fam_bytes(pr, family_of(pr, TTT_ENTRY_GG_ROW, gdo)) + fam_bytes(pr, ttt::kFamGgCol);
+  const int fam = family_of(pr, entry, gdo);
   return fam < 0 ? -1 : fam_bytes(pr, fam);
 }
 
@@ -538,7 +541,7 @@ void timing_mark(hipStream_t st, int tag, bool end) {
 
 extern "C" {
 
-int ttt_version(void) { return 200; }
+int ttt_version(void) { return 300; }
 
 int ttt_kernel_timing(int32_t capacity) {
   TimingPool& t = g_timing;
@@ -594,7 +597,7 @@ int64_t ttt_attn_workspace_size(const ttt_problem* pr, int32_t entry, int32_t wa
 int ttt_attn_split_info(const ttt_problem* pr, int32_t entry, int32_t load_p, int32_t want_gdout, int32_t* chunk,
                         int32_t* nchunk_max, int64_t* slots) {
   TRY(check_problem(pr));
-  const int fam = family_of(entry, want_gdout != 0);
+  const int fam = family_of(pr, entry, want_gdout != 0);
   if (fam < 0) return fail(TTT_ERR_INVALID_ARGUMENT, "entry %d is not a single kernel family", entry);
   const Split s = choose_split(pr, fam, load_p != 0);
   if (chunk) *chunk = s.chunk;
@@ -626,7 +629,11 @@ int ttt_attn_fwd(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, co
   a.lse = lse;
   const bool wp = has_p(p);
   if (wp) TRY(take_view(pr, p, "p", &a.p));
-  TRY(attach_split(pr, wp ? ttt::kFamFwdP : ttt::kFamFwdOnline, wp, workspace, workspace_bytes, &a));
+  if (!wp && pr->block_rows == 128 && !ttt::fwd_pairs_allowed(pr->dtype, has_xm(pr)))
+    return fail(TTT_ERR_UNSUPPORTED, "block_rows 128: 16-bit types without a window or bias only");
+  const int fam = wp ? ttt::kFamFwdP : family_of(pr, TTT_ENTRY_FWD, false);
+  a.pairs = fam == ttt::kFamFwdPairs ? 1 : 0;
+  TRY(attach_split(pr, fam, wp, workspace, workspace_bytes, &a));
   // Deferred P stores pay off where the P writes run at bandwidth: several
   // rounds of workgroups per slot (b4 h16 T8192 d128: P pass -11 %); with one
   // round they cost about 1 % (b2 h4 T2048 d128).

@@ -88,6 +88,8 @@ struct Params {
   // P pass, d = 64: store P with the non-temporal hint (set when P is larger
   // than the last-level cache, where its readers could not find it anyway).
   int p_nt;
+  // O + LSE forward: run k_fwd_lse over pairs of row blocks.
+  int pairs;
 };
 
 // Logical grid position (x, slice y) of this workgroup.  The hardware hands

@@ -327,8 +327,11 @@ __attribute__((amdgpu_waves_per_eu(AccWaves<true>::value))) void k_fwd_online(Pa
 }
 
 // ---------------------------------------------------------------------------
-// O + LSE forward of 16-bit problems at D = 64 without a window or bias: the
-// forward of the recompute modes (TA:327-337, over the kernels of TA:87-206).
+// O + LSE forward of 16-bit problems without a window or bias, in 128-row
+// blocks: the forward of the recompute modes (TA:327-337, over the kernels
+// of TA:87-206).  The library runs it at D = 64 (two waves per SIMD); at
+// D = 128 it needs one wave per SIMD and runs when a problem asks for
+// 128-row blocks (ttt_problem.block_rows).
 //
 // A workgroup owns 128 query rows, row blocks 2j and 2j+1 of one slice (pair
 // j).  Wave w holds rows 16w + c of both blocks (row groups 0 and 1), so each
@@ -360,7 +363,7 @@ constexpr float kLseSumMax = 32768.f;  // 2^15
 
 
 template <typename T, int D>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_fwd_lse(Params a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 64 ? 2 : 1))) void k_fwd_lse(Params a) {
   static_assert(sizeof(T) == 2, "16-bit types");
   typedef Elem<T> E;
   typedef typename E::frag frag;
@@ -1110,13 +1113,17 @@ static void launch_fwd_x(const Params& a, bool write_p, dim3 grid, hipStream_t s
     }
     const TimedLaunch tl(st, kTagFwdP);
     hipLaunchKernelGGL((k_fwd_p<T, D, XM>), grid, dim3(kThreads), 0, st, a);
-  } else if constexpr (!XM && sizeof(T) == 2 && D == 64) {  // fwd_row_pairs
-    const int npair = ((a.T + kBlk - 1) / kBlk + 1) >> 1;
-    const int c2 = a.chunk >> 1;
-    const int kp = (a.causal && a.nchunk_max > 1) ? (npair + c2 - 1) / c2 : a.nchunk_max;
-    const TimedLaunch tl(st, kTagFwdOnline);
-    hipLaunchKernelGGL((k_fwd_lse<T, D>), dim3(npair * kp, a.B * a.H), dim3(kThreads), 0, st, a);
   } else {
+    if constexpr (!XM && sizeof(T) == 2) {
+      if (a.pairs) {
+        const int npair = ((a.T + kBlk - 1) / kBlk + 1) >> 1;
+        const int c2 = a.chunk >> 1;
+        const int kp = (a.causal && a.nchunk_max > 1) ? (npair + c2 - 1) / c2 : a.nchunk_max;
+        const TimedLaunch tl(st, kTagFwdOnline);
+        hipLaunchKernelGGL((k_fwd_lse<T, D>), dim3(npair * kp, a.B * a.H), dim3(kThreads), 0, st, a);
+        return;
+      }
+    }
     const TimedLaunch tl(st, kTagFwdOnline);
     hipLaunchKernelGGL((k_fwd_online<T, D, XM>), grid, dim3(kThreads), 0, st, a);
   }
@@ -1126,8 +1133,10 @@ template <typename T, int D>
 static hipError_t launch_fwd_t(int dtype, const Params& a, bool write_p, hipStream_t st) {
   const int nblk = (a.T + kBlk - 1) / kBlk;
   dim3 grid(nblk * a.nchunk_max, a.B * a.H);
-  // row pairs of a split causal walk take chunks of an even number of tiles
-  if (!write_p && fwd_row_pairs(dtype, D, extended_mask(a)) && a.causal && a.nchunk_max > 1 && (a.chunk & 1))
+  // row pairs: 16-bit types without a window or bias; a split causal walk
+  // takes chunks of an even number of tiles
+  if (!write_p && a.pairs &&
+      (!fwd_pairs_allowed(dtype, extended_mask(a)) || (a.causal && a.nchunk_max > 1 && (a.chunk & 1))))
     return hipErrorInvalidValue;
   if (extended_mask(a))
     launch_fwd_x<T, D, true>(a, write_p, grid, st);
@@ -1140,8 +1149,6 @@ static hipError_t launch_fwd_t(int dtype, const Params& a, bool write_p, hipStre
 
 template <typename T, int D, bool XM>
 static int occupancy_fwd_t(bool write_p) {
-  if constexpr (!XM && sizeof(T) == 2 && D == 64)
-    if (!write_p) return occupancy_of(k_fwd_lse<T, D>);
   if (!write_p) return occupancy_of(k_fwd_online<T, D, XM>);
   return std::min(occupancy_of(k_fwd_stats<T, D, XM>), occupancy_of(k_fwd_p<T, D, XM>));
 }
@@ -1149,6 +1156,12 @@ static int occupancy_fwd_t(bool write_p) {
 int occupancy_fwd(int dtype, int D, bool write_p, bool xm) {
   if (xm) DISPATCH_DTYPE_D(dtype, D, return occupancy_fwd_t<ElemT, kD, true>(write_p));
   else DISPATCH_DTYPE_D(dtype, D, return occupancy_fwd_t<ElemT, kD, false>(write_p));
+  return 0;
+}
+
+int occupancy_fwd_pairs(int dtype, int D) {
+  if (dtype == kF16) return D == 64 ? occupancy_of(k_fwd_lse<_Float16, 64>) : occupancy_of(k_fwd_lse<_Float16, 128>);
+  if (dtype == kBF16) return D == 64 ? occupancy_of(k_fwd_lse<__bf16, 64>) : occupancy_of(k_fwd_lse<__bf16, 128>);
   return 0;
 }
 

@@ -33,10 +33,11 @@ enum : int { kF16 = 0, kBF16 = 1, kF32 = 2 };
 enum : int { kOutO = 0, kOutDQ = 1, kOutDKDV = 2, kOutDV = 3, kOutGKGV = 4 };
 
 // Partial accumulators and row scalars per chunk, by kernel family.
+// kFamFwdPairs: the O + LSE forward over pairs of row blocks (k_fwd_lse).
 enum : int { kFamFwdOnline = 0, kFamFwdP = 1, kFamDq = 2, kFamDkdv = 3, kFamGgRow = 4, kFamGgRowGdo = 5,
-             kFamGgCol = 6 };
-constexpr int kFamNacc[] = {1, 1, 1, 2, 3, 5, 2};
-constexpr int kFamNsc[] = {2, 2, 0, 0, 3, 3, 0};
+             kFamGgCol = 6, kFamFwdPairs = 7, kNumFams = 8 };
+constexpr int kFamNacc[] = {1, 1, 1, 2, 3, 5, 2, 1};
+constexpr int kFamNsc[] = {2, 2, 0, 0, 3, 3, 0, 2};
 
 // Workgroups of a kernel that one CU holds at once (HIP occupancy calculator
 // on the current device); 0 when it cannot be queried.
@@ -70,14 +71,22 @@ struct TimedLaunch {
 // XM instantiation.
 inline bool extended_mask(const Params& a) { return a.win > 0 || a.bias.p != nullptr; }
 
-// The O + LSE forward of 16-bit problems at D = 64 without a window or bias
-// runs k_fwd_lse, whose workgroups take pairs of row blocks (split causal
-// walks in chunks of an even number of tiles); others run k_fwd_online.
-inline bool fwd_row_pairs(int dtype, int D, bool xm) { return dtype != kF32 && D == 64 && !xm; }
+// The O + LSE forward can run k_fwd_lse, whose workgroups take pairs of row
+// blocks (128 rows; split causal walks in chunks of an even number of
+// tiles), for 16-bit problems without a window or bias; k_fwd_online takes
+// 64-row blocks.  block_rows: the problem's choice (0 = the library's: row
+// pairs at D = 64, where they measured faster, and 64-row blocks at
+// D = 128, where the pair kernel runs one wave per SIMD and measured
+// slower: b4 h16 T8192 d128 bf16 causal 1.46 against 1.36 ms).
+inline bool fwd_pairs_allowed(int dtype, bool xm) { return dtype != kF32 && !xm; }
+inline bool fwd_row_pairs(int dtype, int D, bool xm, int block_rows) {
+  return fwd_pairs_allowed(dtype, xm) && (block_rows == 128 || (block_rows == 0 && D == 64));
+}
 
 // Occupancy of the kernels a launch of each family runs (the smaller one when
 // it runs two); xm selects the window/bias instantiation.
 int occupancy_fwd(int dtype, int D, bool write_p, bool xm);
+int occupancy_fwd_pairs(int dtype, int D);
 int occupancy_dq(int dtype, int D, bool load_p, bool xm);
 int occupancy_dkdv(int dtype, int D, bool load_p, bool xm);
 // Grad-grad entry points: ttt_gg.hip is built into one object per head dim

@@ -18,6 +18,7 @@
 
 #include <algorithm>
 #include <string>
+#include <cstring>
 #include <vector>
 
 #include "../../include/ttt_attn.h"
@@ -52,8 +53,9 @@ ttt_view none_view() {
 
 // The problem of [B,H,T,D] tensor x with the mask fields.
 ttt_problem problem_of(const at::Tensor& x, bool causal, double scale, int64_t split_chunk, int64_t window,
-                       int64_t window_kind, const c10::optional<at::Tensor>& bias) {
+                       int64_t window_kind, const c10::optional<at::Tensor>& bias, int64_t block_rows = 0) {
   ttt_problem pr;
+  std::memset(&pr, 0, sizeof(pr));
   pr.dtype = dtype_code(x);
   pr.causal = causal ? 1 : 0;
   pr.batch = x.size(0);
@@ -65,6 +67,7 @@ ttt_problem problem_of(const at::Tensor& x, bool causal, double scale, int64_t s
   pr.window = static_cast<int32_t>(window);
   pr.window_kind = static_cast<int32_t>(window_kind);
   pr.bias = (bias && bias->defined()) ? view_of(*bias) : none_view();
+  pr.block_rows = static_cast<int32_t>(block_rows);
   return pr;
 }
 
@@ -113,8 +116,8 @@ void* stream_of(const at::Tensor& x) {
 // Forward: (O, LSE, P or None).  Replaces TritonAttentionFn.forward's launches.
 std::vector<at::Tensor> fwd(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, bool causal, double scale,
                             bool want_p, int64_t split_chunk, int64_t window, int64_t window_kind,
-                            const c10::optional<at::Tensor>& bias) {
-  const ttt_problem pr = problem_of(q, causal, scale, split_chunk, window, window_kind, bias);
+                            const c10::optional<at::Tensor>& bias, int64_t block_rows) {
+  const ttt_problem pr = problem_of(q, causal, scale, split_chunk, window, window_kind, bias, block_rows);
   at::Tensor o = at::empty(q.sizes(), q.options());
   at::Tensor lse = stats_of(q);
   at::Tensor p = want_p ? alloc_p(q) : at::Tensor();

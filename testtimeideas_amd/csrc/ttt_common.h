@@ -943,6 +943,26 @@ __device__ __forceinline__ void mm_s_half(f32x4* acc, int kb, const T* X, typena
   for (int ds = 0; ds < DSN; ++ds) acc[ds] = Elem<T>::mma(acc[ds], x[ds], y);
 }
 
+// mm_s_half for three products over the same half tile (acc_n += y_n . X),
+// reading each fragment of X once.
+template <typename T, int D>
+__device__ __forceinline__ void mm_s3_half(f32x4* acc0, typename Elem<T>::frag y0, f32x4* acc1,
+                                           typename Elem<T>::frag y1, f32x4* acc2, typename Elem<T>::frag y2,
+                                           int kb, const T* X) {
+  typedef typename Elem<T>::frag frag;
+  constexpr int DSN = D / 16;
+  frag x[DSN];
+#pragma unroll
+  for (int ds = 0; ds < DSN; ++ds) x[ds] = load_frag_tr<T, D>(X, 32 * kb, 16 * ds);
+  if constexpr (sizeof(T) == 2) __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int ds = 0; ds < DSN; ++ds) {
+    acc0[ds] = Elem<T>::mma(acc0[ds], x[ds], y0);
+    acc1[ds] = Elem<T>::mma(acc1[ds], x[ds], y1);
+    acc2[ds] = Elem<T>::mma(acc2[ds], x[ds], y2);
+  }
+}
+
 // Reductions over the four lane groups (same c), with the gfx950 VALU lane
 // swaps: permlane16_swap(x, x) returns, in each lane, the pair {x[l], x[l^16]}
 // (order depending on the lane's 16-lane row); permlane32_swap does the same
@@ -1032,8 +1052,9 @@ __device__ __forceinline__ void stat_read8(float* v, const float* lds, int st, i
 // lane i's 16 bytes to LDS at (wave's base) + 16 i, so one wave instruction
 // fills 1 KiB of a tile linearly; pinned on the GPU with an in-bounds probe.
 // A lane therefore fetches the logical (row, chunk) stored at its LDS bytes:
-// row = byte / row_bytes, chunk = (byte % row_bytes) / 16 ^ swz(row).  Wave w
-// issues the tile's instructions w, w + 4, ...  The loads bypass registers and
+// row = byte / row_bytes, chunk = (byte % row_bytes) / 16 ^ swz(row).  With NW
+// waves per workgroup, wave w issues the tile's instructions w, w + NW, ...
+// The loads bypass registers and
 // complete on vmcnt; readers wait for them (dma_wait) and meet at a barrier.
 // As with stage_load, rows at or beyond rows_valid and chunks at or beyond
 // cols_valid read from row 0 / chunk 0 (finite data that consumers mask).
@@ -1044,13 +1065,13 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 // data format, no swizzle, no index stride.
 constexpr int kBufWord3 = 0x00020000;
 
-template <typename T, int NCOL>
+template <typename T, int NCOL, int NW = 4>
 struct TileDma {  // for the unpadded (chunk-permuted) layout only: Lds<T, NCOL>::kSwizzle
   typedef Lds<T, NCOL> L;
   static constexpr int kRowBytes = NCOL * (int)sizeof(T);
   static constexpr int kInstr = kBlk * kRowBytes / 1024;  // wave instructions per tile
-  static constexpr int kPerWave = kInstr / 4;
-  static_assert(kPerWave * 4 == kInstr, "tile shape");
+  static constexpr int kPerWave = kInstr / NW;
+  static_assert(kPerWave * NW == kInstr, "tile shape");
   int row[kPerWave], col[kPerWave];  // this lane's logical row and first column per instruction
   int wslice;                         // 1024 * wave index, uniform
   __device__ __forceinline__ TileDma() {
@@ -1058,7 +1079,7 @@ struct TileDma {  // for the unpadded (chunk-permuted) layout only: Lds<T, NCOL>
     wslice = 1024 * __builtin_amdgcn_readfirstlane(w);
 #pragma unroll
     for (int q = 0; q < kPerWave; ++q) {
-      const int byte = 1024 * (w + 4 * q) + 16 * lane;
+      const int byte = 1024 * (w + NW * q) + 16 * lane;
       const int r = byte / kRowBytes;
       row[q] = r;
       col[q] = (((byte % kRowBytes) / 16) ^ L::swz(r)) * L::kChunk;
@@ -1092,8 +1113,8 @@ struct TileDma {  // for the unpadded (chunk-permuted) layout only: Lds<T, NCOL>
         __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(g), (short)0, (int)0xFFFFFFFF, kBufWord3);
 #pragma unroll
     for (int q = 0; q < kPerWave; ++q)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(reinterpret_cast<char*>(lds) + wslice + 4096 * q), 16,
-                                               off[q], 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          r, (lds_void_t*)(reinterpret_cast<char*>(lds) + wslice + 1024 * NW * q), 16, off[q], 0, 0, 0);
 #endif
   }
   // A ragged tile's clamped offsets live in temporaries: callers wait for
@@ -1108,12 +1129,41 @@ struct TileDma {  // for the unpadded (chunk-permuted) layout only: Lds<T, NCOL>
       issue(lds, g, (int)(((int64_t)r * ld + c) * (int64_t)sizeof(T)), q);
     }
   }
-  // One 16-byte-per-lane load into the 1 KB slice (wave + 4q) of lds, in the
+  // The compact form (the eight-wave kernels): instruction q of a lane reads
+  // kRowStep rows below instruction 0 at the same column (the row step is a
+  // multiple of 16, so the chunk permutation is the same), so one per-lane
+  // offset per tensor suffices and the step goes into the uniform soffset.
+  static constexpr int kRowStep = 1024 * NW / kRowBytes;
+  __device__ __forceinline__ int offset0(int64_t ld) const {
+    static_assert(kRowStep % 16 == 0, "rows of one lane's instructions share the permutation");
+    return (int)(((int64_t)row[0] * ld + col[0]) * (int64_t)sizeof(T));
+  }
+  __device__ __forceinline__ void load_full0(T* lds, const T* g, int off0, int64_t ld) const {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(g), (short)0, (int)0xFFFFFFFF, kBufWord3);
+    const int step = (int)(kRowStep * ld * (int64_t)sizeof(T));
+#pragma unroll
+    for (int q = 0; q < kPerWave; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          r, (lds_void_t*)(reinterpret_cast<char*>(lds) + wslice + 1024 * NW * q), 16, off0, q * step, 0, 0);
+#endif
+  }
+  __device__ __forceinline__ void load_ragged0(T* lds, const T* g, int64_t ld, int rows_valid, int cols_valid) const {
+#pragma unroll
+    for (int q = 0; q < kPerWave; ++q) {
+      const int rq = row[0] + kRowStep * q;
+      const int r = rq < rows_valid ? rq : 0;
+      const int c = col[0] < cols_valid ? col[0] : 0;
+      issue(lds, g, (int)(((int64_t)r * ld + c) * (int64_t)sizeof(T)), q);
+    }
+  }
+  // One 16-byte-per-lane load into the 1 KB slice (wave + NW q) of lds, in the
   // saddr + voffset form: uniform base g, unsigned 32-bit byte offset.
   __device__ __forceinline__ void issue(T* lds, const T* g, int byte_off, int q) const {
 #if defined(__HIP_DEVICE_COMPILE__)  // the builtin exists only for the gfx950 target
     __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(g) + (uint32_t)byte_off,
-                                     (lds_void_t*)(reinterpret_cast<char*>(lds) + wslice + 4096 * q), 16, 0, 0);
+                                     (lds_void_t*)(reinterpret_cast<char*>(lds) + wslice + 1024 * NW * q), 16, 0, 0);
 #endif
   }
 };

@@ -65,14 +65,21 @@
 #define TTT_GG_COL 1
 #endif
 static_assert(TTT_GG_HEAD_DIM == 64 || TTT_GG_HEAD_DIM == 128, "head dim of this object");
+// The eight-wave column and row kernels (16-bit types at D = 128; the row
+// kernel without GdO) are in this object.
+#define TTT_GG_COL8 (TTT_GG_HEAD_DIM == 128 && (TTT_GG_TYPES & 1) && TTT_GG_COL)
+#define TTT_GG_ROW8 (TTT_GG_HEAD_DIM == 128 && (TTT_GG_TYPES & 1) && (TTT_GG_ROW_GDO & 1))
 
-// Waves per SIMD the grad-grad kernels are compiled for (registers are
-// limited to 512 / this per lane): two at D = 64 (16-bit types; and fp32 in
-// the column kernel, whose few spills cost less than half the waves), one
+// Waves per SIMD the four-wave grad-grad kernels are compiled for (registers
+// are limited to 512 / this per lane): two at D = 64 (16-bit types; and fp32
+// in the column kernel, whose few spills cost less than half the waves), one
 // otherwise, where two spill heavily (fp32 fragments take twice the
 // registers, D = 128 twice the accumulators).  Measured on MI355X: b4 h16
 // T8192 d128 bf16 grad-grad 43.8 -> 14.9 ms, fp32 D = 64 row pass
-// 352 -> 268 us.
+// 352 -> 268 us.  16-bit types at D = 128 (no window, bias or GdO) take the
+// eight-wave kernels k_gg_row8 / k_gg_col8 instead, which fit two waves per
+// SIMD by splitting each streamed tile between two waves (C5 grad-grad
+// 9.66 -> 9.04 ms with P loaded, 10.2 -> 9.3 ms with P recomputed).
 //
 // Also measured and kept:
 //  * The stationary Q, gQ (row pass) and K, gK (column pass) fragments are
@@ -92,6 +99,8 @@ static_assert(TTT_GG_HEAD_DIM == 64 || TTT_GG_HEAD_DIM == 128, "head dim of this
 //  * Products that stream the same LDS tile read each fragment once.
 
 namespace ttt {
+
+constexpr int kThreads8 = 2 * kThreads;  // the eight-wave kernels
 
 template <typename T, int D, bool COL>
 struct GgWaves {
@@ -685,6 +694,525 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, true>::value))) void k_gg_col(P
   }
 }
 
+#if TTT_GG_COL8
+// ---------------------------------------------------------------------------
+// k_gg_col at D = 128 for 16-bit types without a window or bias, in eight-wave
+// workgroups at two waves per SIMD.  The four-wave kernel keeps, per lane,
+// four stationary fragment sets (64 registers), the GK and GV accumulators
+// (64) and the score tiles of a 64-row streamed tile: more than the 256
+// registers of two waves per SIMD, so it runs one wave per SIMD.  Here waves
+// w and w + 4 (one SIMD) share the 16 key rows of key group w % 4:
+//  * each forms the score tiles (P, dP, gdS, gP1) and the three B operands
+//    (dS, gS, gdP) of its own 32-row half of every streamed tile;
+//  * the wave of half 0 owns the GK accumulator, the wave of half 1 GV.  Each
+//    first adds its own half's product, hands the operands its partner needs
+//    (dS and gS to half 0, gdP to half 1) over through LDS, and after a
+//    barrier adds the partner half's product from them.
+// No product is computed twice, the streamed tiles are fetched once per
+// workgroup, and each wave holds one accumulator.
+// ---------------------------------------------------------------------------
+template <typename T, bool LOADP>
+__global__ __launch_bounds__(kThreads8) void k_gg_col8(Params a, Params rowc, int nx) {
+  constexpr int D = 128;
+  typedef Elem<T> E;
+  typedef typename E::frag frag;
+  typedef Lds<T, D> L;
+  typedef Lds<T, kBlk> LP;
+  constexpr int kNS = LOADP ? 3 : 4;  // staged row statistics: D, E, F, then lse (recompute)
+  constexpr int kP = LOADP ? LP::kRowElems : 8;
+  __shared__ __align__(16) T sQ0[L::kRowElems];
+  __shared__ __align__(16) T sgQ0[L::kRowElems];
+  __shared__ __align__(16) T sdO0[L::kRowElems];
+  __shared__ __align__(16) T sP0[kP];
+  __shared__ __align__(16) float sS0[kNS * kBlk];
+  __shared__ __align__(16) T sQ1[L::kRowElems];
+  __shared__ __align__(16) T sgQ1[L::kRowElems];
+  __shared__ __align__(16) T sdO1[L::kRowElems];
+  __shared__ __align__(16) T sP1[kP];
+  __shared__ __align__(16) float sS1[kNS * kBlk];
+  // Operands handed between the two waves of a key group: [key group][dS, gS,
+  // gdP][lane], one 16-byte fragment each.
+  __shared__ __align__(16) frag sX[4 * 3 * 64];
+  struct Bufs {
+    T *q, *gq, *dout, *p;
+    float* st;
+  };
+  auto bufs = [&](auto par) __attribute__((always_inline)) -> Bufs {
+    if constexpr (decltype(par)::value == 0)
+      return Bufs{sQ0, sgQ0, sdO0, sP0, sS0};
+    else
+      return Bufs{sQ1, sgQ1, sdO1, sP1, sS1};
+  };
+
+  const int T_ = a.T;
+  const int nblk = (T_ + kBlk - 1) / kBlk;
+  const Slot sl = grid_slot();
+  if (sl.x >= nx) {  // the preceding row launch's split blocks, in the first four waves
+    if (threadIdx.x >= kThreads) return;
+    if (rowc.gdout.p)
+      combine_gg_row_block<T, D, true>(rowc, sl.x - nx, sl.y, false);
+    else
+      combine_gg_row_block<T, D, false>(rowc, sl.x - nx, sl.y, false);
+    return;
+  }
+  const Item it = launch_item<false>(a, sl.x, nblk);
+  if (it.blk < 0) return;
+  const int nb = it.blk, ch = it.ch;
+  const int bh = sl.y, b = bh / a.H, h = bh % a.H;
+  const Range rg = col_block_range(nb, nblk, T_, a.causal, 0, a.win_kind);
+  const Chunk cr = chunk_of(rg.lo, rg.hi, ch, a.chunk);
+  if (ch >= cr.nch) return;
+  const int n0 = nb * kBlk;
+  const int tid = threadIdx.x, lane = tid & 63, c = lane & 15, g = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kg = w & 3, half = w >> 2;
+  const int cl = 16 * kg + c;
+  const int n = n0 + cl;
+  const ColMask<false> mk(a, nb, n);
+  frag* const xk = sX + kg * 3 * 64 + lane;
+
+  const T* Q = at<const T>(a.q, b, h);
+  const T* K = at<const T>(a.k, b, h);
+  const T* V = at<const T>(a.v, b, h);
+  const T* dO = at<const T>(a.dout, b, h);
+  const T* gQ = at<const T>(a.gq, b, h);
+  const T* gK = at<const T>(a.gk, b, h);
+  const T* gV = at<const T>(a.gv, b, h);
+  const T* Pb = LOADP ? at<const T>(a.p, b, h) : nullptr;
+  const float* rs = a.rowsum_in + (int64_t)bh * T_;
+  const float* ev = a.e + (int64_t)bh * T_;
+  const float* fv = a.f + (int64_t)bh * T_;
+  const float* lse = LOADP ? nullptr : a.lse + (int64_t)bh * T_;
+  const float s = a.scale;
+  const float kSl2 = kLog2e;  // raw score (in units of s) -> base 2
+
+  frag kf[D / 32], gkf[D / 32], vf[D / 32], gvf[D / 32];
+#pragma unroll
+  for (int ks = 0; ks < D / 32; ++ks) {
+    kf[ks] = scale_frag<T>(load_frag_row<T>(K, a.k.st, n, T_, 32 * ks + 8 * g), s);
+    gkf[ks] = scale_frag<T>(load_frag_row<T>(gK, a.gk.st, n, T_, 32 * ks + 8 * g), s);
+    vf[ks] = load_frag_row<T>(V, a.v.st, n, T_, 32 * ks + 8 * g);
+    gvf[ks] = load_frag_row<T>(gV, a.gv.st, n, T_, 32 * ks + 8 * g);
+  }
+
+  f32x4 acc[D / 16];  // GK (half 0) or GV (half 1)
+#pragma unroll
+  for (int i = 0; i < D / 16; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Streamed tile mb from the staged buffers cb, in the wave of half HALF.
+  // The Tile containers use their first half only.  Rows 32 HALF .. +31 of a
+  // staged tile start at a fixed offset, since the LDS row permutation does
+  // not depend on bit 5 of the row; the half is a compile-time constant so
+  // that every LDS address is a lane base plus an immediate.
+  // pf: this wave's P fragment of the tile (read before the next tile's loads
+  // are issued, so that the read need not wait for them).
+  auto compute = [&](auto hf, int mb, const Bufs& cb, const frag& pf) __attribute__((always_inline)) {
+    constexpr int HALF = decltype(hf)::value;
+    constexpr int hq = 32 * HALF * L::kRowPitch, oq = 32 * (1 - HALF) * L::kRowPitch;
+    constexpr int hs = 32 * HALF;
+    const int m0 = mb * kBlk + hs;
+    const float* st = cb.st + hs;
+    Tile p, dp, gds, gp1;
+    if constexpr (LOADP) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) p.set(0, j, E::f32(pf[j]));
+    } else {
+      p.zero();
+      mm_d_half<T, D>(p, 0, cb.q + hq, kf);
+      float l2[8];
+      stat_read8(l2, st, 3, 0);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) p.set(0, j, fast_exp2(p.at(0, j) * kSl2 - l2[j] * kLog2e));
+    }
+    if (mk.tile(mb)) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) p.set(0, j, mk.masked(m0 + stream_index(0, g, j)) ? 0.f : p.at(0, j));
+    }
+    dp.zero();
+    gds.zero();
+    gp1.zero();
+    mm_d2_half<T, D>(dp, gp1, 0, cb.dout + hq, vf, gvf);
+    mm_d_half<T, D>(gds, 0, cb.gq + hq, kf);
+    mm_d_half<T, D>(gds, 0, cb.q + hq, gkf);
+    float d8[8], e8[8], f8[8];
+    stat_read8(d8, st, 0, 0);
+    stat_read8(e8, st, 1, 0);
+    stat_read8(f8, st, 2, 0);
+    float vds[8], vgs[8], vgdp[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float P = p.at(0, j);
+      const float dpv = dp.at(0, j);
+      const float gd = gds.at(0, j);
+      const float dmd = dpv - d8[j];
+      const float gp = gp1.at(0, j) + gd * dmd - e8[j] * dpv;
+      vds[j] = P * dmd;
+      vgdp[j] = P * (gd - e8[j]);
+      vgs[j] = P * (gp - f8[j]);
+    }
+    if constexpr (HALF == 0) {
+      xk[128] = vals_frag<T>(vgdp);
+      mm_s_half<T, D>(acc, 0, cb.gq + hq, vals_frag<T>(vds));
+      mm_s_half<T, D>(acc, 0, cb.q + hq, vals_frag<T>(vgs));
+    } else {
+      xk[0] = vals_frag<T>(vds);
+      xk[64] = vals_frag<T>(vgs);
+      mm_s_half<T, D>(acc, 0, cb.dout + hq, vals_frag<T>(vgdp));
+    }
+    __syncthreads();  // the partner's operands are in sX
+    if constexpr (HALF == 0) {
+      mm_s_half<T, D>(acc, 0, cb.gq + oq, xk[0]);
+      mm_s_half<T, D>(acc, 0, cb.q + oq, xk[64]);
+    } else {
+      mm_s_half<T, D>(acc, 0, cb.dout + oq, xk[128]);
+    }
+  };
+
+  {
+    const TileDma<T, D, 8> dd;
+    const int oQ = dd.offset0(a.q.st), ogQ = dd.offset0(a.gq.st), odO = dd.offset0(a.dout.st);
+    const TileDma<T, kBlk, 8> dpt;
+    const int oP = LOADP ? dpt.offset0(a.p.st) : 0;
+    const int64_t t0r = (int64_t)cr.t0 * kBlk;
+    const T* Qn = Q + t0r * a.q.st;
+    const T* gQn = gQ + t0r * a.gq.st;
+    const T* dOn = dO + t0r * a.dout.st;
+    const T* Pn = LOADP ? Pb + t0r * a.p.st + n0 : nullptr;
+    const bool cols_full = n0 + kBlk <= T_;
+    const StatDma<kNS> sdma(rs, ev, fv, lse);
+    auto dma_tile = [&](int mb, const Bufs& wb) __attribute__((always_inline)) {
+      const int m0 = mb * kBlk;
+      if (m0 + kBlk <= T_ && cols_full) {  // uniform: one test per tile
+        dd.load_full0(wb.q, Qn, oQ, a.q.st);
+        dd.load_full0(wb.gq, gQn, ogQ, a.gq.st);
+        dd.load_full0(wb.dout, dOn, odO, a.dout.st);
+        if constexpr (LOADP) dpt.load_full0(wb.p, Pn, oP, a.p.st);
+      } else {
+        dd.load_ragged0(wb.q, Qn, a.q.st, T_ - m0, D);
+        dd.load_ragged0(wb.gq, gQn, a.gq.st, T_ - m0, D);
+        dd.load_ragged0(wb.dout, dOn, a.dout.st, T_ - m0, D);
+        if constexpr (LOADP) dpt.load_ragged0(wb.p, Pn, a.p.st, T_ - m0, T_ - n0);
+        dma_wait();
+      }
+      sdma.load(wb.st, m0, T_ - m0);
+      Qn += kBlk * a.q.st;
+      gQn += kBlk * a.gq.st;
+      dOn += kBlk * a.dout.st;
+      if constexpr (LOADP) Pn += kBlk * a.p.st;
+    };
+    // Tile mb from buffer set P while the next tile streams into set 1 - P.
+    // The barrier at the top of a step also keeps a wave from overwriting sX
+    // before its partner has read the previous step's operands.
+    auto step = [&](auto hf, auto par, int mb) __attribute__((always_inline)) {
+      constexpr int P = decltype(par)::value;
+      constexpr int hp = 32 * decltype(hf)::value * LP::kRowPitch;
+      dma_wait();       // this wave's loads of tile mb
+      __syncthreads();  // everyone's, and everyone is done with the other set
+      frag pf;
+      if constexpr (LOADP) {
+        pf = load_frag_tr<T, kBlk>(bufs(Parity<P>{}).p + hp, 0, 16 * kg);
+        // Keep the read ahead of the next tile's loads: the compiler does
+        // not tell this buffer from the one they fill and would wait for them.
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (mb + 1 < cr.t1) dma_tile(mb + 1, bufs(Parity<1 - P>{}));
+      compute(hf, mb, bufs(Parity<P>{}), pf);
+    };
+    auto run = [&](auto hf) __attribute__((always_inline)) {
+      dma_tile(cr.t0, bufs(Parity<0>{}));
+      for (int mb = cr.t0; mb < cr.t1; mb += 2) {
+        step(hf, Parity<0>{}, mb);
+        if (mb + 1 < cr.t1) step(hf, Parity<1>{}, mb + 1);
+      }
+    };
+    if (half == 0)
+      run(Parity<0>{});
+    else
+      run(Parity<1>{});
+  }
+  if (cr.nch == 1) {
+    if (half == 0)
+      store_acc_rows<T, D>(at<T>(a.gk_out, b, h), a.gk_out.st, n, T_, acc, s);
+    else
+      store_acc_rows<T, D>(at<T>(a.gv_out, b, h), a.gv_out.st, n, T_, acc, 1.f);
+  } else {
+    float* base = a.ws_acc + part_index(a, bh, nblk, nb, ch) * 2 * kBlk * D;
+    store_acc_partial<D>(base + half * kBlk * D, cl, acc);
+  }
+}
+#endif
+
+#if TTT_GG_ROW8
+// ---------------------------------------------------------------------------
+// k_gg_row at D = 128 for 16-bit types without a window, bias or GdO, in
+// eight-wave workgroups at two waves per SIMD.  The four-wave kernel holds
+// per lane three stationary fragment sets (48 registers), the merged
+// dS*gK + Z1*K, Z2*K and P*K accumulators (96) and the score tiles of a
+// 64-key tile: more than 256 registers, so it runs one wave per SIMD.  Here
+// waves w and w + 4 (one SIMD) share the 16 query rows of row group w % 4 and
+// split every streamed key tile into its two 32-key halves (half = w / 4):
+// each forms the score tiles of its half only and sums its half's
+// contributions into its own accumulators and row sums; at the end the wave
+// of half 1 hands its sums to the wave of half 0 through LDS, which finishes
+// the rows.  No product is computed twice and the key tiles are fetched once
+// per workgroup.
+// ---------------------------------------------------------------------------
+template <typename T, bool LOADP>
+__global__ __launch_bounds__(kThreads8) void k_gg_row8(Params a) {
+  constexpr int D = 128;
+  typedef Elem<T> E;
+  typedef typename E::frag frag;
+  typedef Lds<T, D> L;
+  __shared__ __align__(16) T pK0[L::kRowElems];
+  __shared__ __align__(16) T pV0[L::kRowElems];
+  __shared__ __align__(16) T pgK0[L::kRowElems];
+  __shared__ __align__(16) T pgV0[L::kRowElems];
+  __shared__ __align__(16) T pK1[L::kRowElems];
+  __shared__ __align__(16) T pV1[L::kRowElems];
+  __shared__ __align__(16) T pgK1[L::kRowElems];
+  __shared__ __align__(16) T pgV1[L::kRowElems];
+  // The dO fragments of the block's rows (stationary, used by two products per
+  // tile), here rather than in registers: [row group][ks][lane].
+  __shared__ __align__(16) typename Elem<T>::frag sDo[4 * (D / 32) * 64];
+
+  const int T_ = a.T;
+  const int nblk = (T_ + kBlk - 1) / kBlk;
+  const Slot sl = grid_slot();
+  const Item it = launch_item<false>(a, sl.x, nblk);
+  if (it.blk < 0) return;
+  const int bi = it.blk, ch = it.ch;
+  const int bh = sl.y, b = bh / a.H, h = bh % a.H;
+  const int mb = a.causal ? (nblk - 1 - bi) : bi;
+  const Range rg = row_block_range(mb, nblk, T_, a.causal, 0, a.win_kind);
+  const Chunk cr = chunk_of(rg.lo, rg.hi, ch, a.chunk);
+  if (ch >= cr.nch) return;
+  const int tid = threadIdx.x, lane = tid & 63, c = lane & 15, g = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rgp = w & 3, half = w >> 2;
+  const int rl = 16 * rgp + c;
+  const int m = mb * kBlk + rl;
+  const bool row_ok = m < T_;
+  const RowMask<false> mk(a, mb, m);
+
+  const T* Q = at<const T>(a.q, b, h);
+  const T* K = at<const T>(a.k, b, h);
+  const T* V = at<const T>(a.v, b, h);
+  const T* dO = at<const T>(a.dout, b, h);
+  const T* gQ = at<const T>(a.gq, b, h);
+  const T* gK = at<const T>(a.gk, b, h);
+  const T* gV = at<const T>(a.gv, b, h);
+
+  frag qf[D / 32], gqf[D / 32];
+#pragma unroll
+  for (int ks = 0; ks < D / 32; ++ks) {
+    qf[ks] = scale_frag<T>(load_frag_row<T>(Q, a.q.st, m, T_, 32 * ks + 8 * g), a.scale);
+    gqf[ks] = scale_frag<T>(load_frag_row<T>(gQ, a.gq.st, m, T_, 32 * ks + 8 * g), a.scale);
+  }
+  // Half 0 stages dO (visible after the first step's barrier).
+  frag* const sdo = sDo + rgp * (D / 32) * 64 + lane;
+  if (half == 0) {
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) sdo[64 * ks] = load_frag_row<T>(dO, a.dout.st, m, T_, 32 * ks + 8 * g);
+  }
+  const int64_t ridx = (int64_t)bh * T_ + m;
+  const float Dm = row_ok ? a.rowsum_in[ridx] : 0.f;
+  const float lse2 = (!LOADP && row_ok) ? a.lse[ridx] * kLog2e : 0.f;
+  const T* Pm = LOADP ? at<const T>(a.p, b, h) + (int64_t)(row_ok ? m : 0) * a.p.st : nullptr;
+  const float s = a.scale;
+  const float kSl2 = kLog2e;  // raw score (in units of s) -> base 2
+
+  // a12 = dS*gK + Z1*K (the two products the combination needs only summed),
+  // a3 = Z2*K, a4 = P*K; row sums of Z1 and Z2 by MFMA against ones.
+  f32x4 a12[D / 16], a3[D / 16], a4[D / 16];
+#pragma unroll
+  for (int i = 0; i < D / 16; ++i) a12[i] = a3[i] = a4[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float e_acc = 0.f;
+  f32x4 xs4 = f32x4{0.f, 0.f, 0.f, 0.f}, ds4 = f32x4{0.f, 0.f, 0.f, 0.f};
+  frag ones;
+  {
+    const float one8[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+    ones = vals_frag<T>(one8);
+  }
+
+  // Key tile nb (its 32-key half HALF) from LDS tiles cK, cV, cgK, cgV; with
+  // LOADP, p already holds its probabilities.  The half is a compile-time
+  // constant so that every LDS address is a lane base plus an immediate (the
+  // LDS row permutation does not depend on bit 5 of the row).
+  auto tile_body = [&](auto hf, int nb, const T* cK, const T* cV, const T* cgK, const T* cgV, Tile& p)
+      __attribute__((always_inline)) {
+    constexpr int HALF = decltype(hf)::value;
+    constexpr int hk = 32 * HALF * L::kRowPitch;
+    const int nh = nb * kBlk + 32 * HALF;
+    Tile dp, gds, gp1;
+    if constexpr (!LOADP) {
+      p.zero();
+      mm_d_half<T, D>(p, 0, cK + hk, qf);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) p.set(0, j, fast_exp2(p.at(0, j) * kSl2 - lse2));
+    }
+    if (mk.tile(nb)) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) p.set(0, j, mk.masked(nh + stream_index(0, g, j)) ? 0.f : p.at(0, j));
+    }
+    dp.zero();
+    gds.zero();
+    gp1.zero();
+    {
+      // Read per tile: an opaque zero offset keeps the compiler from hoisting
+      // the loop-invariant reads back into registers for the whole loop.
+      int z = 0;
+      asm volatile("" : "+v"(z));
+      frag dof[D / 32];
+#pragma unroll
+      for (int ks = 0; ks < D / 32; ++ks) dof[ks] = sdo[64 * ks + z];
+      mm_d_half<T, D>(dp, 0, cV + hk, dof);
+      mm_d_half<T, D>(gp1, 0, cgV + hk, dof);
+    }
+    mm_d_half<T, D>(gds, 0, cgK + hk, qf);
+    mm_d_half<T, D>(gds, 0, cK + hk, gqf);
+    float vds[8], vz1[8], vz2[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float P = p.at(0, j);
+      const float gd = gds.at(0, j);
+      const float z2 = P * dp.at(0, j);
+      const float ds = z2 - P * Dm;  // P o (dP - D)
+      vds[j] = ds;
+      vz1[j] = P * gp1.at(0, j) + gd * ds;
+      vz2[j] = z2;
+      e_acc += gd * P;
+    }
+    const frag z1f = vals_frag<T>(vz1), z2f = vals_frag<T>(vz2);
+    xs4 = E::mma(xs4, ones, z1f);
+    ds4 = E::mma(ds4, ones, z2f);
+    mm_s_half<T, D>(a12, 0, cgK + hk, vals_frag<T>(vds));
+    mm_s3_half<T, D>(a12, z1f, a3, z2f, a4, tile_frag<T>(p, 0), 0, cK + hk);
+  };
+
+  const int64_t t0r = (int64_t)cr.t0 * kBlk;
+  const T* Kn = K + t0r * a.k.st;
+  const T* Vn = V + t0r * a.v.st;
+  const T* gKn = gK + t0r * a.gk.st;
+  const T* gVn = gV + t0r * a.gv.st;
+  const T* Pn = LOADP ? Pm + t0r + 32 * half + stream_index(0, g, 0) : nullptr;
+  const TileDma<T, D, 8> dd;
+  const int oK = dd.offset0(a.k.st), oV = dd.offset0(a.v.st), ogK = dd.offset0(a.gk.st), ogV = dd.offset0(a.gv.st);
+  frag pn;
+  auto dma_set = [&](int nb, T* k, T* v, T* gk, T* gv) __attribute__((always_inline)) {
+    const int n0 = nb * kBlk;
+    if (n0 + kBlk <= T_) {  // uniform: one test per tile for all four tiles and P
+      dd.load_full0(k, Kn, oK, a.k.st);
+      dd.load_full0(v, Vn, oV, a.v.st);
+      dd.load_full0(gk, gKn, ogK, a.gk.st);
+      dd.load_full0(gv, gVn, ogV, a.gv.st);
+      if constexpr (LOADP) pn = load_frag_g<T>(Pn);
+    } else {
+      dd.load_ragged0(k, Kn, a.k.st, T_ - n0, D);
+      dd.load_ragged0(v, Vn, a.v.st, T_ - n0, D);
+      dd.load_ragged0(gk, gKn, a.gk.st, T_ - n0, D);
+      dd.load_ragged0(gv, gVn, a.gv.st, T_ - n0, D);
+      if constexpr (LOADP) {
+        const int n = n0 + 32 * half + stream_index(0, g, 0);
+        pn = load_frag_g<T>(Pm + (n < T_ ? n : 0));
+      }
+      dma_wait();
+    }
+    Kn += kBlk * a.k.st;
+    Vn += kBlk * a.v.st;
+    gKn += kBlk * a.gk.st;
+    gVn += kBlk * a.gv.st;
+    if constexpr (LOADP) Pn += kBlk;
+  };
+  // Tile nb from set P while tile nb + 1 streams into set 1 - P.
+  auto step = [&](auto hf, auto par, int nb) __attribute__((always_inline)) {
+    constexpr int P = decltype(par)::value;
+    dma_wait();       // this wave's loads of tile nb (LDS tiles and P fragment)
+    __syncthreads();  // everyone's, and everyone is done with the other set
+    Tile p;
+    if constexpr (LOADP) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) p.set(0, j, E::f32(pn[j]));
+    }
+    // Keep the conversion ahead of the next tile's loads: sunk below them,
+    // it would wait for those loads (vmcnt) before the tile's work.
+    __builtin_amdgcn_sched_barrier(0);
+    if (nb + 1 < cr.t1) {
+      if constexpr (P == 0)
+        dma_set(nb + 1, pK1, pV1, pgK1, pgV1);
+      else
+        dma_set(nb + 1, pK0, pV0, pgK0, pgV0);
+    }
+    if constexpr (P == 0)
+      tile_body(hf, nb, pK0, pV0, pgK0, pgV0, p);
+    else
+      tile_body(hf, nb, pK1, pV1, pgK1, pgV1, p);
+  };
+  auto run = [&](auto hf) __attribute__((always_inline)) {
+    dma_set(cr.t0, pK0, pV0, pgK0, pgV0);
+    for (int nb = cr.t0; nb < cr.t1; nb += 2) {
+      step(hf, Parity<0>{}, nb);
+      if (nb + 1 < cr.t1) step(hf, Parity<1>{}, nb + 1);
+    }
+  };
+  if (half == 0)
+    run(Parity<0>{});
+  else
+    run(Parity<1>{});
+
+  // Pair sums through LDS (no loads are in flight after the last step): row
+  // group rgp uses two 16 KB tiles, [a12 | a3] and [a4 | E, X, D], as
+  // [slot][lane] 16-byte slots.
+  const float Ep = group_sum(e_acc);
+  __syncthreads();
+  f32x4* x0 = reinterpret_cast<f32x4*>(rgp == 0 ? pK0 : rgp == 1 ? pgK0 : rgp == 2 ? pK1 : pgK1);
+  f32x4* x1 = reinterpret_cast<f32x4*>(rgp == 0 ? pV0 : rgp == 1 ? pgV0 : rgp == 2 ? pV1 : pgV1);
+  if (half == 1) {
+#pragma unroll
+    for (int i = 0; i < D / 16; ++i) {
+      x0[i * 64 + lane] = a12[i];
+      x0[(8 + i) * 64 + lane] = a3[i];
+      x1[i * 64 + lane] = a4[i];
+    }
+    x1[8 * 64 + lane] = f32x4{Ep, xs4[0], ds4[0], 0.f};
+  }
+  __syncthreads();
+  if (half == 1) return;
+  const f32x4 sc = x1[8 * 64 + lane];
+  const float Ev = Ep + sc[0];
+  const float Xv = xs4[0] + sc[1];
+  const float Dv = ds4[0] + sc[2];
+#pragma unroll
+  for (int i = 0; i < D / 16; ++i) {
+    a12[i] += x0[i * 64 + lane];
+    a3[i] += x0[(8 + i) * 64 + lane];
+    a4[i] += x1[i * 64 + lane];
+  }
+  if (cr.nch == 1) {
+    const float Fv = Xv - Ev * Dv;
+    f32x4 gq[D / 16];
+#pragma unroll
+    for (int i = 0; i < D / 16; ++i) gq[i] = a12[i] - Ev * a3[i] - Fv * a4[i];
+    store_acc_rows<T, D>(at<T>(a.gq_out, b, h), a.gq_out.st, m, T_, gq, s);
+    if (row_ok && g == 0) {
+      a.e[ridx] = Ev;
+      a.f[ridx] = Fv;
+    }
+  } else {
+    const int64_t part = part_index(a, bh, nblk, mb, ch);
+    float* base = a.ws_acc + part * 3 * kBlk * D;
+    store_acc_partial<D>(base, rl, a12);
+    store_acc_partial<D>(base + kBlk * D, rl, a3);
+    store_acc_partial<D>(base + 2 * kBlk * D, rl, a4);
+    if (g == 0) {
+      float* scp = a.ws_sc + part * 3 * kBlk;
+      scp[rl] = Ev;
+      scp[kBlk + rl] = Xv;
+      scp[2 * kBlk + rl] = Dv;
+    }
+  }
+}
+#endif
+
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool XM>
 // False when the variant asked for is not in this object (ttt_launch.h
@@ -700,6 +1228,15 @@ static bool launch_gg_row_x(const Params& a, bool load_p, bool gdo, dim3 grid, h
       return true;
     }
   } else {
+#if TTT_GG_ROW8
+    if constexpr (D == 128 && sizeof(T) == 2 && !XM) {
+      if (load_p)
+        hipLaunchKernelGGL((k_gg_row8<T, true>), grid, dim3(kThreads8), 0, st, a);
+      else
+        hipLaunchKernelGGL((k_gg_row8<T, false>), grid, dim3(kThreads8), 0, st, a);
+      return true;
+    }
+#endif
     if constexpr ((TTT_GG_ROW_GDO & 1) != 0) {
       if (load_p)
         hipLaunchKernelGGL((k_gg_row<T, D, true, false, XM>), grid, dim3(kThreads), 0, st, a);
@@ -730,6 +1267,21 @@ static hipError_t launch_gg_col_t(int dtype, const Params& a, bool load_p, hipSt
   dim3 grid(nx + (fold ? nblk * CombineSlot<D>::kSub : 0), a.B * a.H);
   const Params& c = fold ? *rowc : a;
   const bool xm = extended_mask(a);
+#if TTT_GG_COL8
+  if constexpr (D == 128 && sizeof(T) == 2) {
+    if (!xm) {
+      {
+        const TimedLaunch tl(st, kTagGgCol);
+        if (load_p)
+          hipLaunchKernelGGL((k_gg_col8<T, true>), grid, dim3(kThreads8), 0, st, a, c, nx);
+        else
+          hipLaunchKernelGGL((k_gg_col8<T, false>), grid, dim3(kThreads8), 0, st, a, c, nx);
+      }
+      if (a.nchunk_max > 1) return launch_combine_sum(dtype, D, a, kOutGKGV, st);
+      return hipGetLastError();
+    }
+  }
+#endif
   {
     const TimedLaunch tl(st, kTagGgCol);
     if (load_p) {
@@ -754,6 +1306,10 @@ static int occupancy_gg_row_t(bool load_p, bool gdo) {
     if constexpr ((TTT_GG_ROW_GDO & 2) != 0)
       return load_p ? occupancy_of(k_gg_row<T, D, true, true, XM>) : occupancy_of(k_gg_row<T, D, false, true, XM>);
   } else {
+#if TTT_GG_ROW8
+    if constexpr (D == 128 && sizeof(T) == 2 && !XM)
+      return load_p ? occupancy_of(k_gg_row8<T, true>, kThreads8) : occupancy_of(k_gg_row8<T, false>, kThreads8);
+#endif
     if constexpr ((TTT_GG_ROW_GDO & 1) != 0)
       return load_p ? occupancy_of(k_gg_row<T, D, true, false, XM>) : occupancy_of(k_gg_row<T, D, false, false, XM>);
   }
@@ -762,6 +1318,10 @@ static int occupancy_gg_row_t(bool load_p, bool gdo) {
 
 template <typename T, int D, bool XM>
 static int occupancy_gg_col_t(bool load_p) {
+#if TTT_GG_COL8
+  if constexpr (D == 128 && sizeof(T) == 2 && !XM)
+    return load_p ? occupancy_of(k_gg_col8<T, true>, kThreads8) : occupancy_of(k_gg_col8<T, false>, kThreads8);
+#endif
   return load_p ? occupancy_of(k_gg_col<T, D, true, XM>) : occupancy_of(k_gg_col<T, D, false, XM>);
 }
 

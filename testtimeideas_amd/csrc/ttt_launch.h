@@ -39,12 +39,13 @@ enum : int { kFamFwdOnline = 0, kFamFwdP = 1, kFamDq = 2, kFamDkdv = 3, kFamGgRo
 constexpr int kFamNacc[] = {1, 1, 1, 2, 3, 5, 2, 1};
 constexpr int kFamNsc[] = {2, 2, 0, 0, 3, 3, 0, 2};
 
-// Workgroups of a kernel that one CU holds at once (HIP occupancy calculator
-// on the current device); 0 when it cannot be queried.
+// Workgroups of a kernel (of `threads` threads) that one CU holds at once
+// (HIP occupancy calculator on the current device); 0 when it cannot be
+// queried.
 template <typename K>
-inline int occupancy_of(K kernel) {
+inline int occupancy_of(K kernel, int threads = kThreads) {
   int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(kernel), kThreads, 0) !=
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(kernel), threads, 0) !=
       hipSuccess) {
     (void)hipGetLastError();
     return 0;

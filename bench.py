@@ -481,6 +481,8 @@ def main():
     ap.add_argument("--config", default="C3", choices=sorted(workloads.CONFIGS) + ["META_8K"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the T=16k point and forward-only metrics")
+    ap.add_argument("--forward-only", action="store_true",
+                    help="time only the O + LSE forward of --config (--steps calls) and print its line")
     ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay of the step")
     ap.add_argument("--autotune", action="store_true",
                     help="measured split per kernel family and shape (testtimeideas_amd.autotune), tuned in warmup")
@@ -512,6 +514,14 @@ def main():
                           "config": {"workload": r["config"]}, "meta": r}), flush=True)
         return
     cfg = workloads.CONFIGS[args.config]
+    if args.forward_only:
+        fm = fwd_mfma(cfg, dev, reps=args.steps)
+        print(json.dumps({"metric": "O+LSE forward us per call", "value": fm["us"], "unit": "us", "n_gpus": 1,
+                          "steps": args.steps, "warmup": 5, "higher_is_better": False, "scaling": "weak",
+                          "vs_baseline": None, "dtype": {"fp16": "f16", "bf16": "bf16", "fp32": "f32"}[cfg.dtype],
+                          "data": "synthetic", "config": {"workload": f"{cfg.name} O+LSE forward"}, "forward": fm}),
+              flush=True)
+        return
     x = workloads.make_inputs(cfg, seed=0, device=dev)
     step = make_step(cfg, x)
     # Backward passes run on the calling thread: the engine's default hand-off

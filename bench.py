@@ -180,36 +180,45 @@ def roofline_entry(cfg, ktimes, launch_ms=None, with_p=None):
     else:
         achieved = model["bytes"] / dur_s / 1e9
         peak, unit = workloads.PEAK_HBM_GBS, "GB/s"
-    return {"kernel": f"k_{kern}" if kernel_ms else name, "entry": name, "bound": model["bound"],
+    traffic, label = measured_traffic(name, cfg, kern if kernel_ms else None, with_label=True)
+    kname = (label.split("<")[0] if label else f"k_{kern}") if kernel_ms else name
+    return {"kernel": kname, "entry": name, "bound": model["bound"],
             "achieved": round(achieved, 2), "peak": peak, "unit": unit, "frac": round(achieved / peak, 4),
-            "traffic": measured_traffic(name, cfg, kern if kernel_ms else None),
+            "traffic": traffic,
             "avg_us": round(dur_s * 1e6, 2), "entry_us": round(ktimes[name] * 1e3, 2),
             "algorithmic_flops": model["flops"], "algorithmic_bytes": model["bytes"]}
 
 
-def measured_traffic(entry: str, cfg: workloads.Config, kernel=None):
+def measured_traffic(entry: str, cfg: workloads.Config, kernel=None, with_label: bool = False):
     """HBM bytes per launch from the committed rocprof PMC summary
     (FETCH_SIZE + WRITE_SIZE scaled by a plain-copy calibration): of the main
     kernel `kernel` alone as the step launches it (its fused form, with
-    combine workgroups appended, where there is one), or else summed over the
-    kernels the summary attributes to the entry point, its combine kernels
-    included; None without a summary."""
+    combine workgroups appended, where there is one; its eight-wave form
+    k_<kernel>8 where the step runs that), or else summed over the kernels the
+    summary attributes to the entry point, its combine kernels included; None
+    without a summary.  With `with_label`, (bytes, the summary's kernel label
+    or None)."""
+    def out(v, label=None):
+        return (v, label) if with_label else v
+
     path = os.path.join(ROOT, "profiles", f"pmc_traffic_{cfg.name}.json")
     if not os.path.exists(path):
-        return None
+        return out(None)
     with open(path) as f:
         data = json.load(f)["kernels"]
     if kernel is not None:
-        labels = [k for k in data if k.startswith(f"k_{kernel}<") and "@" not in k]
+        labels = [k for k in data if (k.startswith(f"k_{kernel}<") or k.startswith(f"k_{kernel}8<")) and "@" not in k]
         fused = [k for k in labels if "+" in k]
         pick = (fused or labels)[:1]
-        return round(data[pick[0]]["fetch_bytes"] + data[pick[0]]["write_bytes"]) if pick else None
+        if not pick:
+            return out(None)
+        return out(round(data[pick[0]]["fetch_bytes"] + data[pick[0]]["write_bytes"]), pick[0])
     total, found = 0.0, False
     for rec in data.values():
         if rec.get("entry") == entry:
             total += rec["fetch_bytes"] + rec["write_bytes"]
             found = True
-    return round(total) if found else None
+    return out(round(total) if found else None)
 
 
 def fwd_mfma(cfg: workloads.Config, dev, reps: int = 50) -> dict:

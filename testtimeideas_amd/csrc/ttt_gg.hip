@@ -102,6 +102,14 @@ namespace ttt {
 
 constexpr int kThreads8 = 2 * kThreads;  // the eight-wave kernels
 
+// Waves per SIMD of the eight-wave kernels (built at D = 128 only: at D = 64
+// two workgroups per CU would need 128 registers, and they spill 88-164 bytes
+// per lane at that cap).
+template <int D>
+struct Gg8Waves {
+  static constexpr int value = 2;
+};
+
 template <typename T, int D, bool COL>
 struct GgWaves {
   static constexpr int value = ((sizeof(T) == 2 || COL) && D == 64) ? 2 : 1;
@@ -711,9 +719,9 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, true>::value))) void k_gg_col(P
 // No product is computed twice, the streamed tiles are fetched once per
 // workgroup, and each wave holds one accumulator.
 // ---------------------------------------------------------------------------
-template <typename T, bool LOADP>
-__global__ __launch_bounds__(kThreads8) void k_gg_col8(Params a, Params rowc, int nx) {
-  constexpr int D = 128;
+template <typename T, int D, bool LOADP>
+__global__ __launch_bounds__(kThreads8) __attribute__((amdgpu_waves_per_eu(Gg8Waves<D>::value))) void k_gg_col8(
+    Params a, Params rowc, int nx) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
@@ -957,9 +965,9 @@ __global__ __launch_bounds__(kThreads8) void k_gg_col8(Params a, Params rowc, in
 // the rows.  No product is computed twice and the key tiles are fetched once
 // per workgroup.
 // ---------------------------------------------------------------------------
-template <typename T, bool LOADP>
-__global__ __launch_bounds__(kThreads8) void k_gg_row8(Params a) {
-  constexpr int D = 128;
+template <typename T, int D, bool LOADP>
+__global__ __launch_bounds__(kThreads8) __attribute__((amdgpu_waves_per_eu(Gg8Waves<D>::value))) void k_gg_row8(
+    Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
@@ -1170,21 +1178,21 @@ __global__ __launch_bounds__(kThreads8) void k_gg_row8(Params a) {
 #pragma unroll
     for (int i = 0; i < D / 16; ++i) {
       x0[i * 64 + lane] = a12[i];
-      x0[(8 + i) * 64 + lane] = a3[i];
+      x0[(D / 16 + i) * 64 + lane] = a3[i];
       x1[i * 64 + lane] = a4[i];
     }
-    x1[8 * 64 + lane] = f32x4{Ep, xs4[0], ds4[0], 0.f};
+    x1[(D / 16) * 64 + lane] = f32x4{Ep, xs4[0], ds4[0], 0.f};
   }
   __syncthreads();
   if (half == 1) return;
-  const f32x4 sc = x1[8 * 64 + lane];
+  const f32x4 sc = x1[(D / 16) * 64 + lane];
   const float Ev = Ep + sc[0];
   const float Xv = xs4[0] + sc[1];
   const float Dv = ds4[0] + sc[2];
 #pragma unroll
   for (int i = 0; i < D / 16; ++i) {
     a12[i] += x0[i * 64 + lane];
-    a3[i] += x0[(8 + i) * 64 + lane];
+    a3[i] += x0[(D / 16 + i) * 64 + lane];
     a4[i] += x1[i * 64 + lane];
   }
   if (cr.nch == 1) {
@@ -1229,11 +1237,11 @@ static bool launch_gg_row_x(const Params& a, bool load_p, bool gdo, dim3 grid, h
     }
   } else {
 #if TTT_GG_ROW8
-    if constexpr (D == 128 && sizeof(T) == 2 && !XM) {
+    if constexpr (sizeof(T) == 2 && !XM) {
       if (load_p)
-        hipLaunchKernelGGL((k_gg_row8<T, true>), grid, dim3(kThreads8), 0, st, a);
+        hipLaunchKernelGGL((k_gg_row8<T, D, true>), grid, dim3(kThreads8), 0, st, a);
       else
-        hipLaunchKernelGGL((k_gg_row8<T, false>), grid, dim3(kThreads8), 0, st, a);
+        hipLaunchKernelGGL((k_gg_row8<T, D, false>), grid, dim3(kThreads8), 0, st, a);
       return true;
     }
 #endif
@@ -1268,14 +1276,14 @@ static hipError_t launch_gg_col_t(int dtype, const Params& a, bool load_p, hipSt
   const Params& c = fold ? *rowc : a;
   const bool xm = extended_mask(a);
 #if TTT_GG_COL8
-  if constexpr (D == 128 && sizeof(T) == 2) {
+  if constexpr (sizeof(T) == 2) {
     if (!xm) {
       {
         const TimedLaunch tl(st, kTagGgCol);
         if (load_p)
-          hipLaunchKernelGGL((k_gg_col8<T, true>), grid, dim3(kThreads8), 0, st, a, c, nx);
+          hipLaunchKernelGGL((k_gg_col8<T, D, true>), grid, dim3(kThreads8), 0, st, a, c, nx);
         else
-          hipLaunchKernelGGL((k_gg_col8<T, false>), grid, dim3(kThreads8), 0, st, a, c, nx);
+          hipLaunchKernelGGL((k_gg_col8<T, D, false>), grid, dim3(kThreads8), 0, st, a, c, nx);
       }
       if (a.nchunk_max > 1) return launch_combine_sum(dtype, D, a, kOutGKGV, st);
       return hipGetLastError();
@@ -1307,8 +1315,8 @@ static int occupancy_gg_row_t(bool load_p, bool gdo) {
       return load_p ? occupancy_of(k_gg_row<T, D, true, true, XM>) : occupancy_of(k_gg_row<T, D, false, true, XM>);
   } else {
 #if TTT_GG_ROW8
-    if constexpr (D == 128 && sizeof(T) == 2 && !XM)
-      return load_p ? occupancy_of(k_gg_row8<T, true>, kThreads8) : occupancy_of(k_gg_row8<T, false>, kThreads8);
+    if constexpr (sizeof(T) == 2 && !XM)
+      return load_p ? occupancy_of(k_gg_row8<T, D, true>, kThreads8) : occupancy_of(k_gg_row8<T, D, false>, kThreads8);
 #endif
     if constexpr ((TTT_GG_ROW_GDO & 1) != 0)
       return load_p ? occupancy_of(k_gg_row<T, D, true, false, XM>) : occupancy_of(k_gg_row<T, D, false, false, XM>);
@@ -1319,8 +1327,8 @@ static int occupancy_gg_row_t(bool load_p, bool gdo) {
 template <typename T, int D, bool XM>
 static int occupancy_gg_col_t(bool load_p) {
 #if TTT_GG_COL8
-  if constexpr (D == 128 && sizeof(T) == 2 && !XM)
-    return load_p ? occupancy_of(k_gg_col8<T, true>, kThreads8) : occupancy_of(k_gg_col8<T, false>, kThreads8);
+  if constexpr (sizeof(T) == 2 && !XM)
+    return load_p ? occupancy_of(k_gg_col8<T, D, true>, kThreads8) : occupancy_of(k_gg_col8<T, D, false>, kThreads8);
 #endif
   return load_p ? occupancy_of(k_gg_col<T, D, true, XM>) : occupancy_of(k_gg_col<T, D, false, XM>);
 }

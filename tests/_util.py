@@ -31,6 +31,17 @@ ZERO_RMS = 1e-6
 ZERO_ABS_16 = 1e-3
 
 
+def check_f32_scaled(name, got, ref, abs_tol=MAX_ABS_32):
+    """fp32 max-abs error against abs_tol times the reference's largest
+    magnitude where that exceeds 1 (values of the helper Functions' VJPs reach
+    ~10, where fp32 rounding of their own dot products is ~1e-6 relative)."""
+    r = to_np(ref)
+    scale = max(1.0, float(np.max(np.abs(r)))) if r.size else 1.0
+    err = max_abs(got, ref)
+    assert err <= abs_tol * scale, f"{name}: max-abs {err:.3e} > {abs_tol:.1e} x {scale:.2f}"
+    return err
+
+
 def check(name, got, ref, dtype, rel_tol=REL_FRO_16, abs_tol=MAX_ABS_32):
     r = to_np(ref)
     if dtype == torch.float32:

@@ -954,16 +954,17 @@ __global__ __launch_bounds__(kThreads8) __attribute__((amdgpu_waves_per_eu(Gg8Wa
 // ---------------------------------------------------------------------------
 // k_gg_row at D = 128 for 16-bit types without a window, bias or GdO, in
 // eight-wave workgroups at two waves per SIMD.  The four-wave kernel holds
-// per lane three stationary fragment sets (48 registers), the merged
-// dS*gK + Z1*K, Z2*K and P*K accumulators (96) and the score tiles of a
-// 64-key tile: more than 256 registers, so it runs one wave per SIMD.  Here
-// waves w and w + 4 (one SIMD) share the 16 query rows of row group w % 4 and
-// split every streamed key tile into its two 32-key halves (half = w / 4):
-// each forms the score tiles of its half only and sums its half's
-// contributions into its own accumulators and row sums; at the end the wave
-// of half 1 hands its sums to the wave of half 0 through LDS, which finishes
-// the rows.  No product is computed twice and the key tiles are fetched once
-// per workgroup.
+// per lane three stationary fragment sets (48 registers), four accumulators
+// (128: dS*gK, Z1*K, Z2*K, P*K) and the score tiles of a 64-key tile: more
+// than 256 registers, so it runs one wave per SIMD.  Here waves w and w + 4
+// (one SIMD) share the 16 query rows of row group w % 4 and split every
+// streamed key tile into its two 32-key halves (half = w / 4): each forms the
+// score tiles of its half only and sums its half's contributions into its own
+// accumulators (dS*gK and Z1*K in one: the rows need only their sum) and row
+// sums; at the end the wave of half 1 hands its sums to the wave of half 0
+// through LDS, which finishes the rows.  dO's stationary fragments are read
+// from LDS per tile.  No product is computed twice and the key tiles are
+// fetched once per workgroup.
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool LOADP>
 __global__ __launch_bounds__(kThreads8) __attribute__((amdgpu_waves_per_eu(Gg8Waves<D>::value))) void k_gg_row8(

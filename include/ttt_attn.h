@@ -288,6 +288,10 @@ int ttt_attn_bwd_rowsum(const ttt_problem* pr, const ttt_view* p,
 /*
  * Double backward, row-block pass: computes the row statistics E and F
  * (stored for the column pass), GQ, and, when gdout != NULL, GdO.
+ * dq (may be NULL): the dQ that ttt_attn_bwd returned for the same q, k, v,
+ * dout, lse/p and rowsum.  Given (and gdout NULL), the pass reads it instead
+ * of forming one of its four products, dS*K (a third of its split partials
+ * fewer); GQ, E and F agree with the NULL form to rounding.
  * Replaces: the stubs triton_attn_bwd2_dq, backward_stubs.py:539-540, and the
  * torch double-backward of TritonDqDkFn / TritonRowSumFn / TritonDvFn,
  * backward_stubs.py:434-514 (corrected: full softmax-Jacobian terms).
@@ -295,11 +299,11 @@ int ttt_attn_bwd_rowsum(const ttt_problem* pr, const ttt_view* p,
 int ttt_attn_gg_row(const ttt_problem* pr, const ttt_view* q,
                     const ttt_view* k, const ttt_view* v,
                     const ttt_view* dout, const float* lse, const ttt_view* p,
-                    const float* rowsum, const ttt_view* gq,
-                    const ttt_view* gk, const ttt_view* gv,
-                    const ttt_view* gq_out, const ttt_view* gdout,
-                    float* e_out, float* f_out, void* workspace,
-                    int64_t workspace_bytes, void* stream);
+                    const float* rowsum, const ttt_view* dq,
+                    const ttt_view* gq, const ttt_view* gk,
+                    const ttt_view* gv, const ttt_view* gq_out,
+                    const ttt_view* gdout, float* e_out, float* f_out,
+                    void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Double backward, column-block pass: GK and GV, reading E and F from
@@ -317,7 +321,8 @@ int ttt_attn_gg_col(const ttt_problem* pr, const ttt_view* q,
                     int64_t workspace_bytes, void* stream);
 
 /*
- * Full double backward in one call: the work of ttt_attn_gg_row then
+ * Full double backward in one call: the work of ttt_attn_gg_row (with dq as
+ * there, NULL allowed) then
  * ttt_attn_gg_col on the same stream, with bitwise the same results.  e_buf
  * and f_buf are caller-owned fp32 [B*H*T] buffers.  When the row pass is
  * split, a small launch forms E and F, and the column launch also sums GQ
@@ -329,11 +334,12 @@ int ttt_attn_gg_col(const ttt_problem* pr, const ttt_view* q,
  */
 int ttt_attn_gg(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
                 const ttt_view* v, const ttt_view* dout, const float* lse,
-                const ttt_view* p, const float* rowsum, const ttt_view* gq,
-                const ttt_view* gk, const ttt_view* gv, const ttt_view* gq_out,
-                const ttt_view* gk_out, const ttt_view* gv_out,
-                const ttt_view* gdout, float* e_buf, float* f_buf,
-                void* workspace, int64_t workspace_bytes, void* stream);
+                const ttt_view* p, const float* rowsum, const ttt_view* dq,
+                const ttt_view* gq, const ttt_view* gk, const ttt_view* gv,
+                const ttt_view* gq_out, const ttt_view* gk_out,
+                const ttt_view* gv_out, const ttt_view* gdout, float* e_buf,
+                float* f_buf, void* workspace, int64_t workspace_bytes,
+                void* stream);
 
 /*
  * ttt_attn_gg with no device memory allocation: the same double backward,
@@ -357,10 +363,10 @@ int ttt_attn_gg(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
  */
 int ttt_attn_gg_noalloc(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
                         const ttt_view* v, const ttt_view* dout, const float* lse,
-                        const ttt_view* p, const float* rowsum, const ttt_view* gq,
-                        const ttt_view* gk, const ttt_view* gv, const ttt_view* gq_out,
-                        const ttt_view* gk_out, const ttt_view* gv_out,
-                        const ttt_view* gdout, void* stream);
+                        const ttt_view* p, const float* rowsum, const ttt_view* dq,
+                        const ttt_view* gq, const ttt_view* gk, const ttt_view* gv,
+                        const ttt_view* gq_out, const ttt_view* gk_out,
+                        const ttt_view* gv_out, const ttt_view* gdout, void* stream);
 
 #ifdef __cplusplus
 }

@@ -31,14 +31,19 @@ def _ref(xs, causal, scale):
 
 
 def _run(xs, causal, scale, save_p, want_gdo=True):
+    """Every entry point once; the double backward twice: as asked (the row
+    pass forms all its products) and in the dQ form (no GdO; the row pass
+    reads the first backward's dQ), whose results are the *_dq entries."""
     q, k, v, do, gq, gk, gv = (x.cuda() for x in xs)
     o, lse, p = _lib.fwd(q, k, v, causal, scale, save_p)
     dq, dk, dv, rowsum = _lib.bwd(q, k, v, o, do, lse, p, causal, scale)
     GQ, GK, GV, GdO = _lib.gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, causal, scale, want_gdo)
+    GQ2, GK2, GV2, _ = _lib.gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, causal, scale, False, dq=dq)
     if p is not None:  # the tiles the forward leaves unwritten, zeroed for the comparison
         _lib.fill_masked_p(p, causal)
     torch.cuda.synchronize()
-    return dict(o=o, lse=lse, p=p, dq=dq, dk=dk, dv=dv, rowsum=rowsum, gq=GQ, gk=GK, gv=GV, gdo=GdO)
+    return dict(o=o, lse=lse, p=p, dq=dq, dk=dk, dv=dv, rowsum=rowsum, gq=GQ, gk=GK, gv=GV, gdo=GdO,
+                gq_dq=GQ2, gk_dq=GK2, gv_dq=GV2)
 
 
 def _compare(out, ref, dtype, causal, t, names=("o", "dq", "dk", "dv", "gq", "gk", "gv", "gdo")):
@@ -47,6 +52,8 @@ def _compare(out, ref, dtype, causal, t, names=("o", "dq", "dk", "dv", "gq", "gk
         if out.get(n) is None:
             continue
         errs[n] = check(n, out[n], ref[n], dtype)
+        if out.get(n + "_dq") is not None:
+            errs[n + "_dq"] = check(n + "_dq", out[n + "_dq"], ref[n], dtype)
     # row statistics: LSE (natural log) and D
     errs["lse"] = check("lse", out["lse"], ref["lse"], torch.float32, abs_tol=2e-5 if dtype == torch.float32 else 2e-3)
     errs["rowsum"] = check("rowsum", out["rowsum"], ref["rowsum"], dtype)
@@ -136,7 +143,7 @@ def test_per_kernel_entry_points_match_fused():
     a = _run(xs, True, 0.125, True)
     with _lib.kernel_timing() as rec:
         b = _run(xs, True, 0.125, True)
-    for n in ("o", "dq", "dk", "dv", "gq", "gk", "gv", "gdo", "rowsum", "lse"):
+    for n in ("o", "dq", "dk", "dv", "gq", "gk", "gv", "gdo", "rowsum", "lse", "gq_dq", "gk_dq", "gv_dq"):
         assert torch.equal(a[n], b[n]), n
     assert set(rec) >= {"ttt_attn_fwd", "ttt_attn_bwd_dq", "ttt_attn_bwd_dkdv", "ttt_attn_gg_row",
                         "ttt_attn_gg_col"}
@@ -195,28 +202,32 @@ def test_fused_backward_entry(b, h, t, d, dtype, save_p, chunk, win):
     (1, 2, 700, 64, "fp16", True, True, 2, (_lib.WINDOW_SLIDING, 200)),
     (1, 1, 640, 64, "bf16", False, False, 3, (_lib.WINDOW_LOCAL, 128)),
 ])
-def test_fused_double_backward_entry(b, h, t, d, dtype, save_p, gdo, chunk, win):
+@pytest.mark.parametrize("use_dq", [False, True])
+def test_fused_double_backward_entry(b, h, t, d, dtype, save_p, gdo, chunk, win, use_dq):
     """ttt_attn_gg, whose column launch also finishes the row pass's split
-    blocks, gives bitwise the results of ttt_attn_gg_row + ttt_attn_gg_col."""
+    blocks, gives bitwise the results of ttt_attn_gg_row + ttt_attn_gg_col,
+    with and without the first backward's dQ (ignored with GdO)."""
     import ctypes
     dt = DT[dtype]
     m = _mask(win)
     q, k, v, do, gq, gk, gv = (x.cuda() for x in _inputs(b, h, t, d, dt, seed=t + d + 1))
-    print(f"[case] fused gg b={b} h={h} t={t} d={d} {dtype} save_p={save_p} gdo={gdo} chunk={chunk} win={win}",
-          flush=True)
+    print(f"[case] fused gg b={b} h={h} t={t} d={d} {dtype} save_p={save_p} gdo={gdo} chunk={chunk} win={win} "
+          f"dq={use_dq}", flush=True)
     o, lse, p = _lib.fwd(q, k, v, m, 0.125, save_p)
-    _, _, _, rs = _lib.bwd(q, k, v, o, do, lse, p, m, 0.125)
+    dq, _, _, rs = _lib.bwd(q, k, v, o, do, lse, p, m, 0.125)
+    if not use_dq:
+        dq = None
     with _lib.split_chunk(chunk), _lib.kernel_timing():  # timing: the row and column entry points
-        ref = _lib.gg(q, k, v, do, lse, p, rs, gq, gk, gv, m, 0.125, gdo)
+        ref = _lib.gg(q, k, v, do, lse, p, rs, gq, gk, gv, m, 0.125, gdo, dq=dq)
     pr = _lib._problem(q, m, 0.125, chunk)
     out = [torch.empty_like(x) for x in (q, k, v)] + [torch.empty_like(do) if gdo else None]
     e = torch.empty(b, h, t, dtype=torch.float32, device=q.device)
     f = torch.empty_like(e)
     wp, wn, _buf = _lib._workspace(pr, _lib.ENTRY_GG, q.device, gdo)
     _lib._call("ttt_attn_gg", ctypes.byref(pr), _lib._view(q), _lib._view(k), _lib._view(v), _lib._view(do),
-               _lib._fptr(lse), _lib._view(p), rs.data_ptr(), _lib._view(gq), _lib._view(gk), _lib._view(gv),
-               _lib._view(out[0]), _lib._view(out[1]), _lib._view(out[2]), _lib._view(out[3]), e.data_ptr(),
-               f.data_ptr(), wp, wn, _lib._stream())
+               _lib._fptr(lse), _lib._view(p), rs.data_ptr(), _lib._view(dq), _lib._view(gq), _lib._view(gk),
+               _lib._view(gv), _lib._view(out[0]), _lib._view(out[1]), _lib._view(out[2]), _lib._view(out[3]),
+               e.data_ptr(), f.data_ptr(), wp, wn, _lib._stream())
     torch.cuda.synchronize()
     for n, x, y in zip(("gq", "gk", "gv", "gdo"), out, ref):
         if y is not None:
@@ -229,7 +240,7 @@ def test_deterministic():
     print("[case] determinism", flush=True)
     a = _run(xs, True, 0.125, True)
     b = _run(xs, True, 0.125, True)
-    for n in ("o", "dq", "dk", "dv", "gq", "gk", "gv", "gdo", "lse", "rowsum"):
+    for n in ("o", "dq", "dk", "dv", "gq", "gk", "gv", "gdo", "lse", "rowsum", "gq_dq", "gk_dq", "gv_dq"):
         assert torch.equal(a[n], b[n]), n
     assert torch.equal(a["p"], b["p"])
 
@@ -328,7 +339,8 @@ def test_slices_divisible_by_eight(b, h, save_p, chunk):
 @pytest.mark.parametrize("save_p", [True, False])
 def test_launch_timing_counts_and_leaves_results_unchanged(save_p):
     """Per-kernel timing (ttt_kernel_timing) brackets every main-kernel
-    launch of the fused step with events: one launch per family per step,
+    launch of the fused step with events: one launch per family per step
+    (the double backward's two per step: _run takes it in both forms),
     positive durations, each shorter than the steps' wall time, and results
     bitwise those of an untimed step."""
     import time
@@ -346,9 +358,9 @@ def test_launch_timing_counts_and_leaves_results_unchanged(save_p):
     fams = ("fwd_stats", "fwd_p") if save_p else ("fwd_online",)
     for name in fams + ("bwd_dq", "bwd_dkdv", "gg_row", "gg_col"):
         ms, n = times[name]
-        assert n == steps and 0.0 < ms < wall_ms, (name, ms, n, wall_ms)
+        assert n == (2 if name.startswith("gg") else 1) * steps and 0.0 < ms < wall_ms, (name, ms, n, wall_ms)
     assert set(times) == set(fams + ("bwd_dq", "bwd_dkdv", "gg_row", "gg_col"))
-    for key in ("o", "lse", "dq", "dk", "dv", "gq", "gk", "gv", "gdo"):
+    for key in ("o", "lse", "dq", "dk", "dv", "gq", "gk", "gv", "gdo", "gq_dq", "gk_dq", "gv_dq"):
         assert torch.equal(out[key], ref[key]), key
     with _lib.launch_timing() as read:  # a new record each time, nothing timed yet
         assert read() == {}

@@ -32,6 +32,16 @@ def test_library_exports_every_declared_symbol():
     assert lib.ttt_version() >= 200
 
 
+def test_ctypes_signatures_match_header():
+    """Each ctypes argument list of _lib has as many parameters as the
+    header's declaration of that entry point."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    for name, args in _lib._SIGS.items():
+        m = re.search(r"\b" + name + r"\s*\(([^)]*)\)\s*;", text)
+        assert m, name
+        assert len(m.group(1).split(",")) == len(args), name
+
+
 def test_torch_binding_loads():
     """The torch binding of the fused entry points is built next to the
     library and exposes them (no call: there is no GPU here)."""
@@ -414,12 +424,17 @@ def test_one_launch_of_each_pass_per_gradgrad_step(monkeypatch):
         t = q.shape[2]
         return torch.zeros_like(q), torch.zeros(q.shape[:3]), torch.zeros(q.shape[:3] + (t,)) if want_p else None
 
+    made = {}
+
     def bwd(q, k, v, o, do, lse, p, causal, scale):
         calls["bwd"] += 1
-        return torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v), torch.zeros(q.shape[:3])
+        made["dq"] = torch.zeros_like(q)
+        return made["dq"], torch.zeros_like(k), torch.zeros_like(v), torch.zeros(q.shape[:3])
 
-    def gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, causal, scale, want_gdo):
+    def gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, causal, scale, want_gdo, dq=None):
         calls["gg"] += 1
+        # the double backward reads the first backward's dQ
+        assert dq is not None and dq.data_ptr() == made["dq"].data_ptr() and dq.shape == made["dq"].shape
         return torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v), None
 
     monkeypatch.setattr(_lib, "fwd", fwd)
@@ -462,8 +477,8 @@ def test_noalloc_rejects_too_many_rows_without_gpu():
     and says so before touching the device."""
     lib = _lib.load()
     pr = _prob(batch=64, seqlen=32769)
-    rc = lib.ttt_attn_gg_noalloc(ctypes.byref(pr), _v(), _v(), _v(), _v(), 0x20000, None, 0x20000, _v(), _v(), _v(),
-                                 _v(), _v(), _v(), None, None)
+    rc = lib.ttt_attn_gg_noalloc(ctypes.byref(pr), _v(), _v(), _v(), _v(), 0x20000, None, 0x20000, None, _v(), _v(),
+                                 _v(), _v(), _v(), _v(), None, None)
     assert rc == 1
     assert b"B*H*T" in lib.ttt_last_error()
 
@@ -494,4 +509,4 @@ def test_block_rows_choice():
     assert _fwd_rc(_prob(block_rows=96)) == 1 and b"block_rows" in lib.ttt_last_error()
     assert _fwd_rc(_prob(block_rows=128, dtype=2)) == 2 and b"block_rows" in lib.ttt_last_error()
     assert _fwd_rc(_prob(block_rows=128, window=16)) == 2
-    assert lib.ttt_version() >= 300
+    assert lib.ttt_version() >= 400

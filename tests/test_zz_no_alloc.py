@@ -26,11 +26,13 @@ def _inputs(b, h, t, d, dtype, seed):
 
 
 def _both(xs, causal, scale, save_p, want_gdo):
+    """Without GdO both take the first backward's dQ (the row pass's dQ form)."""
     q, k, v, do, rq, rk, rv = xs
     o, lse, p = _lib.fwd(q, k, v, causal, scale, save_p)
-    _, _, _, rowsum = _lib.bwd(q, k, v, o, do, lse, p, causal, scale)
-    ref = _lib.gg(q, k, v, do, lse, p, rowsum, rq, rk, rv, causal, scale, want_gdo)
-    got = _lib.gg_noalloc(q, k, v, do, lse, p, rowsum, rq, rk, rv, causal, scale, want_gdo)
+    dq, _, _, rowsum = _lib.bwd(q, k, v, o, do, lse, p, causal, scale)
+    dq = None if want_gdo else dq
+    ref = _lib.gg(q, k, v, do, lse, p, rowsum, rq, rk, rv, causal, scale, want_gdo, dq=dq)
+    got = _lib.gg_noalloc(q, k, v, do, lse, p, rowsum, rq, rk, rv, causal, scale, want_gdo, dq=dq)
     torch.cuda.synchronize()
     return ref, got
 

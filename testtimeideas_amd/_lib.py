@@ -101,14 +101,14 @@ _SIGS = {
     "ttt_attn_bwd": [_P(_Problem), _VP, _VP, _VP, _VP, _VP, _FP, _VP, _FP, _VP, _VP, _VP] + _WS + _ST,
     "ttt_attn_bwd_rowsum": [_P(_Problem), _VP, _VP, _VP, _FP] + _ST,
     "ttt_attn_fill_masked_p": [_P(_Problem), _VP] + _ST,
-    "ttt_attn_gg_row": [_P(_Problem), _VP, _VP, _VP, _VP, _FP, _VP, _FP, _VP, _VP, _VP, _VP, _VP, _FP, _FP]
-                       + _WS + _ST,
+    "ttt_attn_gg_row": [_P(_Problem), _VP, _VP, _VP, _VP, _FP, _VP, _FP, _VP, _VP, _VP, _VP, _VP, _VP, _FP,
+                        _FP] + _WS + _ST,
     "ttt_attn_gg_col": [_P(_Problem), _VP, _VP, _VP, _VP, _FP, _VP, _FP, _FP, _FP, _VP, _VP, _VP, _VP, _VP]
                        + _WS + _ST,
-    "ttt_attn_gg": [_P(_Problem), _VP, _VP, _VP, _VP, _FP, _VP, _FP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _FP,
-                    _FP] + _WS + _ST,
-    "ttt_attn_gg_noalloc": [_P(_Problem), _VP, _VP, _VP, _VP, _FP, _VP, _FP, _VP, _VP, _VP, _VP, _VP, _VP, _VP]
-                           + _ST,
+    "ttt_attn_gg": [_P(_Problem), _VP, _VP, _VP, _VP, _FP, _VP, _FP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
+                    _FP, _FP] + _WS + _ST,
+    "ttt_attn_gg_noalloc": [_P(_Problem), _VP, _VP, _VP, _VP, _FP, _VP, _FP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
+                            _VP] + _ST,
 }
 
 # ttt_entry codes (include/ttt_attn.h)
@@ -609,24 +609,31 @@ def rowsum_from_p(p, do, v, mask):
     return rs
 
 
-def gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, mask, scale: float, want_gdo: bool):
-    """Double backward: (GQ, GK, GV, GdO or None).  Reference stubs
-    backward_stubs.py:539-548; torch version :434-514 (corrected)."""
+def gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, mask, scale: float, want_gdo: bool, dq=None):
+    """Double backward: (GQ, GK, GV, GdO or None).  `dq`: the first
+    backward's dQ for the same inputs (``bwd``'s first output), or None; given,
+    the row pass reads it instead of forming one of its products (GQ agrees
+    to rounding).  Reference stubs backward_stubs.py:539-548; torch version
+    :434-514 (corrected)."""
     if q.numel() == 0:
         return (_empty_like_out(q), _empty_like_out(k), _empty_like_out(v),
                 _empty_like_out(do) if want_gdo else None)
     m = as_mask(mask)
     lp = p is not None
+    if dq is not None:
+        check_inputs(q, dq)
+        if not _kernel_ok(dq):
+            dq = dq.contiguous()
 
     def run(cr, cc):
-        return ext().gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, m.causal, float(scale), bool(want_gdo), cr, cc,
-                        int(m.window), int(m.window_kind), m.bias)
+        return ext().gg(q, k, v, do, lse, p, rowsum, dq, gq, gk, gv, m.causal, float(scale), bool(want_gdo), cr,
+                        cc, int(m.window), int(m.window_kind), m.bias)
 
     cr = _split_for(ENTRY_GG_ROW, q, m, scale, lp, want_gdo, lambda c: run(c, 0))
     cc = _split_for(ENTRY_GG_COL, q, m, scale, lp, False, lambda c: run(cr, c))
     if _timing is None:
         if cr == 0 and cc == 0:
-            return tuple(ext().gg_fused(q, k, v, do, lse, p, rowsum, gq, gk, gv, m.causal, float(scale),
+            return tuple(ext().gg_fused(q, k, v, do, lse, p, rowsum, dq, gq, gk, gv, m.causal, float(scale),
                                         bool(want_gdo), int(m.window), int(m.window_kind), m.bias))
         return tuple(run(cr, cc))
     gq_out = _empty_like_out(q)
@@ -641,8 +648,8 @@ def gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, mask, scale: float, want_gdo: bo
     prc = _problem(q, mask, scale, cc)
     wp, wn, _wbuf = _workspace(prr, ENTRY_GG_ROW, q.device, want_gdo)
     _timed("ttt_attn_gg_row", ctypes.byref(prr), _view(q), _view(k), _view(v), _view(do), lse_p, _view(p),
-           rowsum.data_ptr(), _view(gq), _view(gk), _view(gv), _view(gq_out), _view(gdo), e.data_ptr(),
-           f.data_ptr(), wp, wn, st)
+           rowsum.data_ptr(), _view(dq), _view(gq), _view(gk), _view(gv), _view(gq_out), _view(gdo),
+           e.data_ptr(), f.data_ptr(), wp, wn, st)
     wp, wn, _wbuf2 = _workspace(prc, ENTRY_GG_COL, q.device)
     _timed("ttt_attn_gg_col", ctypes.byref(prc), _view(q), _view(k), _view(v), _view(do), lse_p, _view(p),
            rowsum.data_ptr(), e.data_ptr(), f.data_ptr(), _view(gq), _view(gk), _view(gv), _view(gk_out),
@@ -650,10 +657,10 @@ def gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, mask, scale: float, want_gdo: bo
     return gq_out, gk_out, gv_out, gdo
 
 
-def gg_noalloc(q, k, v, do, lse, p, rowsum, gq, gk, gv, mask, scale: float, want_gdo: bool):
+def gg_noalloc(q, k, v, do, lse, p, rowsum, gq, gk, gv, mask, scale: float, want_gdo: bool, dq=None):
     """``gg`` through ttt_attn_gg_noalloc: the library's static device scratch
     instead of a workspace and E/F buffers (outputs are still allocated
-    here).  No counterpart in the reference."""
+    here); `dq` as in ``gg``.  No counterpart in the reference."""
     gq_out = _empty_like_out(q)
     gk_out = _empty_like_out(k)
     gv_out = _empty_like_out(v)
@@ -662,7 +669,7 @@ def gg_noalloc(q, k, v, do, lse, p, rowsum, gq, gk, gv, mask, scale: float, want
         return gq_out, gk_out, gv_out, gdo
     prob = _problem(q, mask, scale)
     _timed("ttt_attn_gg_noalloc", ctypes.byref(prob), _view(q), _view(k), _view(v), _view(do), _fptr(lse),
-           _view(p), rowsum.data_ptr(), _view(gq), _view(gk), _view(gv), _view(gq_out), _view(gk_out),
+           _view(p), rowsum.data_ptr(), _view(dq), _view(gq), _view(gk), _view(gv), _view(gq_out), _view(gk_out),
            _view(gv_out), _view(gdo), _stream())
     return gq_out, gk_out, gv_out, gdo
 

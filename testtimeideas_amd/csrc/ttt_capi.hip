@@ -541,7 +541,7 @@ void timing_mark(hipStream_t st, int tag, bool end) {
 
 extern "C" {
 
-int ttt_version(void) { return 300; }
+int ttt_version(void) { return 400; }
 
 int ttt_kernel_timing(int32_t capacity) {
   TimingPool& t = g_timing;
@@ -778,7 +778,8 @@ int ttt_attn_bwd_rowsum(const ttt_problem* pr, const ttt_view* p, const ttt_view
 // bytes (cap < 0: no limit).
 static int prep_gg_row(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
                        const ttt_view* dout, const float* lse, const ttt_view* p, const float* rowsum,
-                       const ttt_view* gq, const ttt_view* gk, const ttt_view* gv, const ttt_view* gq_out,
+                       const ttt_view* dq, const ttt_view* gq, const ttt_view* gk, const ttt_view* gv,
+                       const ttt_view* gq_out,
                        const ttt_view* gdout, float* e_out, float* f_out, void* workspace, int64_t workspace_bytes,
                        int64_t cap, ttt::Params* out) {
   TRY(check_problem(pr));
@@ -796,6 +797,9 @@ static int prep_gg_row(const ttt_problem* pr, const ttt_view* q, const ttt_view*
   if (!lp && !lse) return fail(TTT_ERR_INVALID_ARGUMENT, "lse: null pointer (required without p)");
   const bool gdo = gdout && gdout->data;
   if (gdo) TRY(take_view(pr, gdout, "gdout", &a.gdout));
+  // the first backward's dQ: read by the row pass without GdO (the kernels
+  // and combines take a.dq.p set as the dQ form)
+  if (dq && dq->data && !gdo) TRY(take_view(pr, dq, "dq", &a.dq));
   if (!rowsum || !e_out || !f_out) return fail(TTT_ERR_INVALID_ARGUMENT, "rowsum/e_out/f_out: null pointer");
   TRY(check_stats({lse, rowsum, e_out, f_out}));
   a.lse = const_cast<float*>(lse);
@@ -809,11 +813,11 @@ static int prep_gg_row(const ttt_problem* pr, const ttt_view* q, const ttt_view*
 
 static int gg_row_impl(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
                        const ttt_view* dout, const float* lse, const ttt_view* p, const float* rowsum,
-                       const ttt_view* gq, const ttt_view* gk, const ttt_view* gv, const ttt_view* gq_out,
-                       const ttt_view* gdout, float* e_out, float* f_out, void* workspace, int64_t workspace_bytes,
-                       void* stream, int64_t cap) {
+                       const ttt_view* dq, const ttt_view* gq, const ttt_view* gk, const ttt_view* gv,
+                       const ttt_view* gq_out, const ttt_view* gdout, float* e_out, float* f_out, void* workspace,
+                       int64_t workspace_bytes, void* stream, int64_t cap) {
   ttt::Params a;
-  TRY(prep_gg_row(pr, q, k, v, dout, lse, p, rowsum, gq, gk, gv, gq_out, gdout, e_out, f_out, workspace,
+  TRY(prep_gg_row(pr, q, k, v, dout, lse, p, rowsum, dq, gq, gk, gv, gq_out, gdout, e_out, f_out, workspace,
                   workspace_bytes, cap, &a));
   return launched(ttt::launch_gg_row(pr->dtype, (int)pr->head_dim, a, has_p(p), a.gdout.p != nullptr,
                                      (hipStream_t)stream),
@@ -864,10 +868,10 @@ static int gg_col_impl(const ttt_problem* pr, const ttt_view* q, const ttt_view*
 
 int ttt_attn_gg_row(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
                     const ttt_view* dout, const float* lse, const ttt_view* p, const float* rowsum,
-                    const ttt_view* gq, const ttt_view* gk, const ttt_view* gv, const ttt_view* gq_out,
-                    const ttt_view* gdout, float* e_out, float* f_out, void* workspace, int64_t workspace_bytes,
-                    void* stream) {
-  return gg_row_impl(pr, q, k, v, dout, lse, p, rowsum, gq, gk, gv, gq_out, gdout, e_out, f_out, workspace,
+                    const ttt_view* dq, const ttt_view* gq, const ttt_view* gk, const ttt_view* gv,
+                    const ttt_view* gq_out, const ttt_view* gdout, float* e_out, float* f_out, void* workspace,
+                    int64_t workspace_bytes, void* stream) {
+  return gg_row_impl(pr, q, k, v, dout, lse, p, rowsum, dq, gq, gk, gv, gq_out, gdout, e_out, f_out, workspace,
                      workspace_bytes, stream, -1);
 }
 
@@ -882,9 +886,9 @@ int ttt_attn_gg_col(const ttt_problem* pr, const ttt_view* q, const ttt_view* k,
 
 int ttt_attn_gg(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
                 const ttt_view* dout, const float* lse, const ttt_view* p, const float* rowsum,
-                const ttt_view* gq, const ttt_view* gk, const ttt_view* gv, const ttt_view* gq_out,
-                const ttt_view* gk_out, const ttt_view* gv_out, const ttt_view* gdout, float* e_buf,
-                float* f_buf, void* workspace, int64_t workspace_bytes, void* stream) {
+                const ttt_view* dq, const ttt_view* gq, const ttt_view* gk, const ttt_view* gv,
+                const ttt_view* gq_out, const ttt_view* gk_out, const ttt_view* gv_out, const ttt_view* gdout,
+                float* e_buf, float* f_buf, void* workspace, int64_t workspace_bytes, void* stream) {
   // The row pass's partials go in the first part of the workspace and the
   // column pass's after them: the column launch sums the row pass's split
   // blocks (GQ, GdO) in workgroups appended to its grid, after a small launch
@@ -896,8 +900,8 @@ int ttt_attn_gg(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, con
   const int64_t row_bytes = family_bytes(pr, choose_split(pr, fam, lp), fam);
   const int64_t ws_bytes = workspace ? workspace_bytes : 0;
   ttt::Params ar, ac;
-  TRY(prep_gg_row(pr, q, k, v, dout, lse, p, rowsum, gq, gk, gv, gq_out, gdout, e_buf, f_buf, workspace, ws_bytes,
-                  -1, &ar));
+  TRY(prep_gg_row(pr, q, k, v, dout, lse, p, rowsum, dq, gq, gk, gv, gq_out, gdout, e_buf, f_buf, workspace,
+                  ws_bytes, -1, &ar));
   if (ws_bytes < row_bytes)  // prep_gg_row has checked this; kept for the pointer arithmetic below
     return fail(TTT_ERR_WORKSPACE, "workspace of %lld bytes too small", (long long)ws_bytes);
   void* ws_c = row_bytes > 0 ? static_cast<void*>(static_cast<char*>(workspace) + row_bytes) : workspace;
@@ -910,8 +914,9 @@ int ttt_attn_gg(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, con
 
 int ttt_attn_gg_noalloc(const ttt_problem* pr, const ttt_view* q, const ttt_view* k, const ttt_view* v,
                         const ttt_view* dout, const float* lse, const ttt_view* p, const float* rowsum,
-                        const ttt_view* gq, const ttt_view* gk, const ttt_view* gv, const ttt_view* gq_out,
-                        const ttt_view* gk_out, const ttt_view* gv_out, const ttt_view* gdout, void* stream) {
+                        const ttt_view* dq, const ttt_view* gq, const ttt_view* gk, const ttt_view* gv,
+                        const ttt_view* gq_out, const ttt_view* gk_out, const ttt_view* gv_out,
+                        const ttt_view* gdout, void* stream) {
   TRY(check_problem(pr));
   const int64_t nstat = pr->batch * pr->heads * pr->seqlen;
   const int64_t one = (nstat * (int64_t)sizeof(float) + 255) / 256 * 256;  // E, then F, 256-byte aligned
@@ -927,7 +932,7 @@ int ttt_attn_gg_noalloc(const ttt_problem* pr, const ttt_view* q, const ttt_view
   float* f = reinterpret_cast<float*>(static_cast<char*>(base) + one);
   void* ws = static_cast<char*>(base) + 2 * one;
   const int64_t ws_bytes = kNoAllocScratchBytes - 2 * one;
-  TRY(gg_row_impl(pr, q, k, v, dout, lse, p, rowsum, gq, gk, gv, gq_out, gdout, e, f, ws, ws_bytes, stream,
+  TRY(gg_row_impl(pr, q, k, v, dout, lse, p, rowsum, dq, gq, gk, gv, gq_out, gdout, e, f, ws, ws_bytes, stream,
                   ws_bytes));
   return gg_col_impl(pr, q, k, v, dout, lse, p, rowsum, e, f, gq, gk, gv, gk_out, gv_out, ws, ws_bytes, stream,
                      ws_bytes);

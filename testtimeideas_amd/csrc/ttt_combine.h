@@ -139,6 +139,9 @@ __device__ __forceinline__ void combine_sum_block(const Params& a, int which, in
 // sums (written when write_ef), then GQ (and GdO).
 // Accumulators: 0..2 = dS*gK + Z1*K, Z2*K, P*K; 3..4 = P*gV + (P o gdS)*V, P*V.
 // Scalars: 0 = E, 1 = rowsum(Z1), 2 = rowsum(Z2).
+// The dQ form (a.dq.p set, no GdO): accumulators 0..1 = dS*gK + Z1*K, P*K;
+// scalar 2 = X summed in fp32 (Xf); GQ = s*(acc0 - X acc1) - E dQ and
+// F = Xf - E D.
 template <typename T, int D, bool GDO>
 __device__ __forceinline__ void combine_gg_row_block(const Params& a, int bx, int by, bool write_ef) {
   constexpr int NACC = GDO ? 5 : 3;
@@ -152,6 +155,22 @@ __device__ __forceinline__ void combine_gg_row_block(const Params& a, int bx, in
   const int row = cs.blk * kBlk + r;
   if (row >= T_) return;
   const int64_t p0 = part_index(a, bh, nblk, cs.blk, 0);
+  if constexpr (!GDO) {
+    if (a.dq.p) {
+      float sc[3];
+      sum_scalars<3>(sc, a.ws_sc, p0, nch, r);
+      const float ev = sc[0], gv = sc[1];
+      f32x4 t[2];
+      sum_parts<D, 2>(t, a.ws_acc, p0, nch, 2, 0, r, cs.d0);
+      const f32x4 dq = load4<T>(at<const T>(a.dq, b, h) + (int64_t)row * a.dq.st + cs.d0);
+      store_slot<T>(a.gq_out, b, h, row, cs.d0, (t[0] - gv * t[1]) * a.scale - ev * dq);
+      if (write_ef && cs.d0 == 0) {
+        a.e[(int64_t)bh * T_ + row] = ev;
+        a.f[(int64_t)bh * T_ + row] = sc[2] - ev * a.rowsum_in[(int64_t)bh * T_ + row];
+      }
+      return;
+    }
+  }
   float sc[3];
   sum_scalars<3>(sc, a.ws_sc, p0, nch, r);
   const float ev = sc[0], xv = sc[1], dv = sc[2];

@@ -112,7 +112,8 @@ __global__ __launch_bounds__(kThreads) void k_combine_gg_ef(Params a) {
   sum_scalars<3>(sc, a.ws_sc, part_index(a, bh, nblk, blk, 0), nch, r);
   const float ev = sc[0], xv = sc[1], dv = sc[2];
   a.e[(int64_t)bh * T_ + row] = ev;
-  a.f[(int64_t)bh * T_ + row] = xv - ev * dv;
+  // the dQ form: dv = X summed in fp32, F = dv - E D
+  a.f[(int64_t)bh * T_ + row] = a.dq.p ? dv - ev * a.rowsum_in[(int64_t)bh * T_ + row] : xv - ev * dv;
 }
 
 // ---------------------------------------------------------------------------

@@ -511,6 +511,21 @@ __device__ __forceinline__ void store4(T* p, f32x4 v) {
   }
 }
 
+// Load four consecutive elements as fp32.
+template <typename T>
+__device__ __forceinline__ f32x4 load4(const T* p) {
+  if constexpr (sizeof(T) == 2) {
+    typedef T t4 __attribute__((ext_vector_type(4)));
+    const t4 f = *reinterpret_cast<const t4*>(p);
+    f32x4 v;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = Elem<T>::f32(f[j]);
+    return v;
+  } else {
+    return *reinterpret_cast<const f32x4*>(p);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Score-tile container: 64 streamed x 16 stationary values per wave, held as
 // four MFMA accumulators.  at(kb, j) is the value at streamed index
@@ -943,6 +958,24 @@ __device__ __forceinline__ void mm_s_half(f32x4* acc, int kb, const T* X, typena
   for (int ds = 0; ds < DSN; ++ds) acc[ds] = Elem<T>::mma(acc[ds], x[ds], y);
 }
 
+// mm_s_half for two products over the same half tile (acc_n += y_n . X),
+// reading each fragment of X once.
+template <typename T, int D>
+__device__ __forceinline__ void mm_s2_half(f32x4* acc0, typename Elem<T>::frag y0, f32x4* acc1,
+                                           typename Elem<T>::frag y1, int kb, const T* X) {
+  typedef typename Elem<T>::frag frag;
+  constexpr int DSN = D / 16;
+  frag x[DSN];
+#pragma unroll
+  for (int ds = 0; ds < DSN; ++ds) x[ds] = load_frag_tr<T, D>(X, 32 * kb, 16 * ds);
+  if constexpr (sizeof(T) == 2) __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int ds = 0; ds < DSN; ++ds) {
+    acc0[ds] = Elem<T>::mma(acc0[ds], x[ds], y0);
+    acc1[ds] = Elem<T>::mma(acc1[ds], x[ds], y1);
+  }
+}
+
 // mm_s_half for three products over the same half tile (acc_n += y_n . X),
 // reading each fragment of X once.
 template <typename T, int D>
@@ -992,6 +1025,16 @@ __device__ __forceinline__ void store_acc_rows(T* base, int64_t ld, int row, int
   T* rp = base + (int64_t)row * ld + 4 * g;
 #pragma unroll
   for (int ds = 0; ds < D / 16; ++ds) store4<T>(rp + 16 * ds, acc[ds] * mul);
+}
+
+// The elements store_acc_rows would write (this lane: row `row`, columns
+// 16*ds + 4g .. +3), read as fp32; zero past nrows.
+template <typename T, int D>
+__device__ __forceinline__ void load_acc_rows(const T* base, int64_t ld, int row, int nrows, f32x4* out) {
+  const int g = (threadIdx.x & 63) >> 4;
+  const T* rp = base + (int64_t)(row < nrows ? row : 0) * ld + 4 * g;
+#pragma unroll
+  for (int ds = 0; ds < D / 16; ++ds) out[ds] = row < nrows ? load4<T>(rp + 16 * ds) : f32x4{0.f, 0.f, 0.f, 0.f};
 }
 
 // Offset (floats) of element (row r, column d) in one 64 x D block of fp32

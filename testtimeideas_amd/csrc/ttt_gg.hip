@@ -21,6 +21,18 @@
 // P*gV + (P o gdS)*V and P*V) and the three
 // row sums, and k_combine_gg_row applies the same formulas to the totals.
 //
+// Given the first backward's dQ = s*(dS*K) (the dQ form, without GdO), the
+// Z2*K product drops out: Z2 = dS + D o P exactly (D = rowsum(dO o O) of the
+// first backward, the D in dS), so
+//   gS*K = Z1*K - E o (dS*K) - G o (P*K),  G = F + E D,
+//   GQ = s*(dS*gK + Z1*K - G o (P*K)) - E o dQ,
+// and with rowsum(P) = 1 and rowsum(dS) = 0 (both exact in exact arithmetic,
+// to rounding here), G = X = rowsum(Z1) and F = X - E D.  For GQ, X is summed
+// from the rounded Z1 values the product Z1*K consumes (16-bit types: by MFMA
+// against ones), so that the row's gS sums to zero to rounding; F, which the
+// column pass sets against its own fp32 gP, takes X summed in fp32.  Chunks
+// write dS*gK + Z1*K and P*K and the row sums E, X and the fp32 X.
+//
 // k_gg_col (stationary key rows, streamed query tiles) reads D, E, F per
 // streamed row and forms dS, gdP, gS tile by tile for GK and GV.
 //
@@ -116,13 +128,16 @@ struct GgWaves {
 };
 
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool LOADP, bool GDO, bool XM>
+template <typename T, int D, bool LOADP, bool GDO, bool XM, bool DQ>
 __global__ __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, false>::value))) void k_gg_row(Params a) {
   typedef Elem<T> E;
   typedef typename E::frag frag;
   typedef Lds<T, D> L;
-  constexpr int NACC = GDO ? 5 : 3;  // split partials: dS*gK + Z1*K, Z2*K, P*K (+ P*gV + (P o gdS)*V, P*V)
+  static_assert(!(DQ && GDO), "the dQ form has no GdO variant");
+  // split partials: dS*gK + Z1*K, Z2*K, P*K (+ P*gV + (P o gdS)*V, P*V), the
+  // dQ form without Z2*K; row sums E, X and rowsum(Z2) (dQ form: X in fp32)
+  constexpr int NACC = DQ ? 2 : GDO ? 5 : 3;
   // 16-bit types stream tiles straight into LDS (TileDma), into two buffer
   // sets in distinct arrays with a compile-time role per loop step (kPar), so
   // that the current tile's LDS reads need not wait for the next tile's loads;
@@ -186,16 +201,18 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, false>::value))) void k_gg_row(
   }
   const int64_t ridx = (int64_t)bh * T_ + m;
   const float Dm = row_ok ? a.rowsum_in[ridx] : 0.f;
+  const f32x4 mDm4 = f32x4{-Dm, -Dm, -Dm, -Dm};
   const float lse2 = (!LOADP && row_ok) ? a.lse[ridx] * kLog2e : 0.f;
   const T* Pm = LOADP ? at<const T>(a.p, b, h) + (int64_t)(row_ok ? m : 0) * a.p.st : nullptr;
   const float s = a.scale;
   const float kSl2 = kLog2e;  // raw score (in units of s) -> base 2
 
-  f32x4 a1[D / 16], a2[D / 16], a3[D / 16], a4[D / 16];
+  f32x4 a1[D / 16], a2[D / 16], a3[DQ ? 1 : D / 16], a4[D / 16];
   f32x4 b1[GDO ? D / 16 : 1], b2[GDO ? D / 16 : 1], b3[GDO ? D / 16 : 1];
 #pragma unroll
   for (int i = 0; i < D / 16; ++i) {
-    a1[i] = a2[i] = a3[i] = a4[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    a1[i] = a2[i] = a4[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (!DQ) a3[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     if constexpr (GDO) b1[i] = b2[i] = b3[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   float e_acc = 0.f, x_acc = 0.f, d_acc = 0.f;
@@ -279,7 +296,13 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, false>::value))) void k_gg_row(
         for (int j = 0; j < 8; ++j)
           p.set(kb, j, mk.masked(n0 + stream_index(kb, g, j)) ? 0.f : p.at(kb, j));
     }
-    dp.zero();
+    // The dQ form needs dP only as dP - D: the MFMAs start from -D.
+    if constexpr (DQ) {
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) dp.q[q4] = mDm4;
+    } else {
+      dp.zero();
+    }
     gds.zero();
     gp1.zero();
     mm_d<T, D>(dp, cV, dof);
@@ -296,14 +319,15 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, false>::value))) void k_gg_row(
         const float P = p.at(kb, j);
         const float gd = gds.at(kb, j);
         const float dpv = dp.at(kb, j);
-        const float z2 = P * dpv;
-        const float ds = z2 - P * Dm;  // P o (dP - D)
-        const float z1 = P * gp1.at(kb, j) + gd * ds;
+        const float z2 = DQ ? 0.f : P * dpv;
+        const float ds = DQ ? P * dpv : z2 - P * Dm;  // P o (dP - D) (dQ form: dpv = dP - D)
+        float z1 = P * gp1.at(kb, j) + gd * ds;
+        // dQ form: z1 in fp32 for X and packed for the product; opaque, so
+        // that the pack is a conversion of this value, not a second FMA
+        if constexpr (DQ && kMfmaSums) asm volatile("" : "+v"(z1));
         e_acc += gd * P;
-        if constexpr (!kMfmaSums) {
-          x_acc += z1;
-          d_acc += z2;
-        }
+        if constexpr (!kMfmaSums || DQ) x_acc += z1;  // dQ form: X in fp32, for F
+        if constexpr (!kMfmaSums && !DQ) d_acc += z2;
         vds[j] = ds;
         vz1[j] = z1;
         vz2[j] = z2;
@@ -311,16 +335,19 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, false>::value))) void k_gg_row(
       }
       dsf[kb] = vals_frag<T>(vds);
       z1f[kb] = vals_frag<T>(vz1);
-      z2f[kb] = vals_frag<T>(vz2);
+      if constexpr (!DQ) z2f[kb] = vals_frag<T>(vz2);
       if constexpr (kMfmaSums) {
         xs4 = E::mma(xs4, ones, z1f[kb]);
-        ds4 = E::mma(ds4, ones, z2f[kb]);
+        if constexpr (!DQ) ds4 = E::mma(ds4, ones, z2f[kb]);
       }
       pf[kb] = tile_frag<T>(p, kb);
       if constexpr (GDO) z4f[kb] = vals_frag<T>(vz4);
     }
     mm_s<T, D>(a1, cgK, dsf);
-    mm_s3<T, D>(a2, z1f, a3, z2f, a4, pf, cK);
+    if constexpr (DQ)
+      mm_s2<T, D>(a2, z1f, a4, pf, cK);
+    else
+      mm_s3<T, D>(a2, z1f, a3, z2f, a4, pf, cK);
     if constexpr (GDO) {
       mm_s<T, D>(b1, cgV, pf);
       mm_s2<T, D>(b2, z4f, b3, pf, cV);
@@ -423,13 +450,23 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, false>::value))) void k_gg_row(
   }
   const float Ev = group_sum(e_acc);
   const float Xv = kMfmaSums ? xs4[0] : group_sum(x_acc);
-  const float Dv = kMfmaSums ? ds4[0] : group_sum(d_acc);
+  // rowsum(Z2); the dQ form: X summed in fp32
+  const float Dv = DQ ? (kMfmaSums ? group_sum(x_acc) : Xv) : kMfmaSums ? ds4[0] : group_sum(d_acc);
   if (cr.nch == 1) {
-    const float Fv = Xv - Ev * Dv;
+    const float Gv = Xv;  // the dQ form's G
+    const float Fv = DQ ? Dv - Ev * Dm : Xv - Ev * Dv;
     f32x4 gq[D / 16];
+    if constexpr (DQ) {
+      f32x4 dq[D / 16];
+      load_acc_rows<T, D>(at<const T>(a.dq, b, h), a.dq.st, m, T_, dq);
 #pragma unroll
-    for (int i = 0; i < D / 16; ++i) gq[i] = a1[i] + a2[i] - Ev * a3[i] - Fv * a4[i];
-    store_acc_rows<T, D>(at<T>(a.gq_out, b, h), a.gq_out.st, m, T_, gq, s);
+      for (int i = 0; i < D / 16; ++i) gq[i] = (a1[i] + a2[i] - Gv * a4[i]) * s - Ev * dq[i];
+      store_acc_rows<T, D>(at<T>(a.gq_out, b, h), a.gq_out.st, m, T_, gq, 1.f);
+    } else {
+#pragma unroll
+      for (int i = 0; i < D / 16; ++i) gq[i] = a1[i] + a2[i] - Ev * a3[i] - Fv * a4[i];
+      store_acc_rows<T, D>(at<T>(a.gq_out, b, h), a.gq_out.st, m, T_, gq, s);
+    }
     if constexpr (GDO) {
       f32x4 go[D / 16];
 #pragma unroll
@@ -448,8 +485,12 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, false>::value))) void k_gg_row(
 #pragma unroll
     for (int i = 0; i < D / 16; ++i) a1[i] += a2[i];
     store_acc_partial<D>(base, rl, a1);
-    store_acc_partial<D>(base + kBlk * D, rl, a3);
-    store_acc_partial<D>(base + 2 * kBlk * D, rl, a4);
+    if constexpr (DQ) {
+      store_acc_partial<D>(base + kBlk * D, rl, a4);
+    } else {
+      store_acc_partial<D>(base + kBlk * D, rl, a3);
+      store_acc_partial<D>(base + 2 * kBlk * D, rl, a4);
+    }
     if constexpr (GDO) {
 #pragma unroll
       for (int i = 0; i < D / 16; ++i) b1[i] += b2[i];
@@ -964,9 +1005,9 @@ __global__ __launch_bounds__(kThreads8) __attribute__((amdgpu_waves_per_eu(Gg8Wa
 // sums; at the end the wave of half 1 hands its sums to the wave of half 0
 // through LDS, which finishes the rows.  dO's stationary fragments are read
 // from LDS per tile.  No product is computed twice and the key tiles are
-// fetched once per workgroup.
+// fetched once per workgroup.  The dQ form (DQ) drops Z2*K as k_gg_row does.
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool LOADP>
+template <typename T, int D, bool LOADP, bool DQ>
 __global__ __launch_bounds__(kThreads8) __attribute__((amdgpu_waves_per_eu(Gg8Waves<D>::value))) void k_gg_row8(
     Params a) {
   typedef Elem<T> E;
@@ -1025,17 +1066,23 @@ __global__ __launch_bounds__(kThreads8) __attribute__((amdgpu_waves_per_eu(Gg8Wa
   }
   const int64_t ridx = (int64_t)bh * T_ + m;
   const float Dm = row_ok ? a.rowsum_in[ridx] : 0.f;
+  const f32x4 mDm4 = f32x4{-Dm, -Dm, -Dm, -Dm};
   const float lse2 = (!LOADP && row_ok) ? a.lse[ridx] * kLog2e : 0.f;
   const T* Pm = LOADP ? at<const T>(a.p, b, h) + (int64_t)(row_ok ? m : 0) * a.p.st : nullptr;
   const float s = a.scale;
   const float kSl2 = kLog2e;  // raw score (in units of s) -> base 2
 
   // a12 = dS*gK + Z1*K (the two products the combination needs only summed),
-  // a3 = Z2*K, a4 = P*K; row sums of Z1 and Z2 by MFMA against ones.
-  f32x4 a12[D / 16], a3[D / 16], a4[D / 16];
+  // a3 = Z2*K (not in the dQ form), a4 = P*K; row sums of Z1 and Z2 by MFMA
+  // against ones.
+  constexpr int NACC = DQ ? 2 : 3;  // split partials: a12, (a3,) a4; row sums E, X, rowsum(Z2) (dQ form: fp32 X)
+  f32x4 a12[D / 16], a3[DQ ? 1 : D / 16], a4[D / 16];
 #pragma unroll
-  for (int i = 0; i < D / 16; ++i) a12[i] = a3[i] = a4[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float e_acc = 0.f;
+  for (int i = 0; i < D / 16; ++i) {
+    a12[i] = a4[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (!DQ) a3[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  float e_acc = 0.f, x_acc = 0.f;  // x_acc: X in fp32 (dQ form)
   f32x4 xs4 = f32x4{0.f, 0.f, 0.f, 0.f}, ds4 = f32x4{0.f, 0.f, 0.f, 0.f};
   frag ones;
   {
@@ -1063,7 +1110,13 @@ __global__ __launch_bounds__(kThreads8) __attribute__((amdgpu_waves_per_eu(Gg8Wa
 #pragma unroll
       for (int j = 0; j < 8; ++j) p.set(0, j, mk.masked(nh + stream_index(0, g, j)) ? 0.f : p.at(0, j));
     }
-    dp.zero();
+    // The dQ form needs dP only as dP - D: the MFMAs start from -D.
+    if constexpr (DQ) {
+      dp.q[0] = mDm4;
+      dp.q[1] = mDm4;
+    } else {
+      dp.zero();
+    }
     gds.zero();
     gp1.zero();
     {
@@ -1084,18 +1137,27 @@ __global__ __launch_bounds__(kThreads8) __attribute__((amdgpu_waves_per_eu(Gg8Wa
     for (int j = 0; j < 8; ++j) {
       const float P = p.at(0, j);
       const float gd = gds.at(0, j);
-      const float z2 = P * dp.at(0, j);
-      const float ds = z2 - P * Dm;  // P o (dP - D)
+      const float z2 = DQ ? 0.f : P * dp.at(0, j);
+      const float ds = DQ ? P * dp.at(0, j) : z2 - P * Dm;  // P o (dP - D) (dQ form: dp = dP - D)
       vds[j] = ds;
       vz1[j] = P * gp1.at(0, j) + gd * ds;
       vz2[j] = z2;
       e_acc += gd * P;
+      if constexpr (DQ) {
+        asm volatile("" : "+v"(vz1[j]));  // as in k_gg_row: one FMA for both uses
+        x_acc += vz1[j];
+      }
     }
-    const frag z1f = vals_frag<T>(vz1), z2f = vals_frag<T>(vz2);
+    const frag z1f = vals_frag<T>(vz1);
     xs4 = E::mma(xs4, ones, z1f);
-    ds4 = E::mma(ds4, ones, z2f);
     mm_s_half<T, D>(a12, 0, cgK + hk, vals_frag<T>(vds));
-    mm_s3_half<T, D>(a12, z1f, a3, z2f, a4, tile_frag<T>(p, 0), 0, cK + hk);
+    if constexpr (DQ) {
+      mm_s2_half<T, D>(a12, z1f, a4, tile_frag<T>(p, 0), 0, cK + hk);
+    } else {
+      const frag z2f = vals_frag<T>(vz2);
+      ds4 = E::mma(ds4, ones, z2f);
+      mm_s3_half<T, D>(a12, z1f, a3, z2f, a4, tile_frag<T>(p, 0), 0, cK + hk);
+    }
   };
 
   const int64_t t0r = (int64_t)cr.t0 * kBlk;
@@ -1172,6 +1234,7 @@ __global__ __launch_bounds__(kThreads8) __attribute__((amdgpu_waves_per_eu(Gg8Wa
   // group rgp uses two 16 KB tiles, [a12 | a3] and [a4 | E, X, D], as
   // [slot][lane] 16-byte slots.
   const float Ep = group_sum(e_acc);
+  if constexpr (DQ) ds4[0] = group_sum(x_acc);  // the dQ form's third row sum: X in fp32
   __syncthreads();
   f32x4* x0 = reinterpret_cast<f32x4*>(rgp == 0 ? pK0 : rgp == 1 ? pgK0 : rgp == 2 ? pK1 : pgK1);
   f32x4* x1 = reinterpret_cast<f32x4*>(rgp == 0 ? pV0 : rgp == 1 ? pgV0 : rgp == 2 ? pV1 : pgV1);
@@ -1179,7 +1242,7 @@ __global__ __launch_bounds__(kThreads8) __attribute__((amdgpu_waves_per_eu(Gg8Wa
 #pragma unroll
     for (int i = 0; i < D / 16; ++i) {
       x0[i * 64 + lane] = a12[i];
-      x0[(D / 16 + i) * 64 + lane] = a3[i];
+      if constexpr (!DQ) x0[(D / 16 + i) * 64 + lane] = a3[i];
       x1[i * 64 + lane] = a4[i];
     }
     x1[(D / 16) * 64 + lane] = f32x4{Ep, xs4[0], ds4[0], 0.f};
@@ -1189,29 +1252,38 @@ __global__ __launch_bounds__(kThreads8) __attribute__((amdgpu_waves_per_eu(Gg8Wa
   const f32x4 sc = x1[(D / 16) * 64 + lane];
   const float Ev = Ep + sc[0];
   const float Xv = xs4[0] + sc[1];
-  const float Dv = ds4[0] + sc[2];
+  const float Dv = ds4[0] + sc[2];  // rowsum(Z2); the dQ form: X in fp32
 #pragma unroll
   for (int i = 0; i < D / 16; ++i) {
     a12[i] += x0[i * 64 + lane];
-    a3[i] += x0[(D / 16 + i) * 64 + lane];
+    if constexpr (!DQ) a3[i] += x0[(D / 16 + i) * 64 + lane];
     a4[i] += x1[i * 64 + lane];
   }
   if (cr.nch == 1) {
-    const float Fv = Xv - Ev * Dv;
+    const float Gv = Xv;  // the dQ form's G
+    const float Fv = DQ ? Dv - Ev * Dm : Xv - Ev * Dv;
     f32x4 gq[D / 16];
+    if constexpr (DQ) {
+      f32x4 dq[D / 16];
+      load_acc_rows<T, D>(at<const T>(a.dq, b, h), a.dq.st, m, T_, dq);
 #pragma unroll
-    for (int i = 0; i < D / 16; ++i) gq[i] = a12[i] - Ev * a3[i] - Fv * a4[i];
-    store_acc_rows<T, D>(at<T>(a.gq_out, b, h), a.gq_out.st, m, T_, gq, s);
+      for (int i = 0; i < D / 16; ++i) gq[i] = (a12[i] - Gv * a4[i]) * s - Ev * dq[i];
+      store_acc_rows<T, D>(at<T>(a.gq_out, b, h), a.gq_out.st, m, T_, gq, 1.f);
+    } else {
+#pragma unroll
+      for (int i = 0; i < D / 16; ++i) gq[i] = a12[i] - Ev * a3[i] - Fv * a4[i];
+      store_acc_rows<T, D>(at<T>(a.gq_out, b, h), a.gq_out.st, m, T_, gq, s);
+    }
     if (row_ok && g == 0) {
       a.e[ridx] = Ev;
       a.f[ridx] = Fv;
     }
   } else {
     const int64_t part = part_index(a, bh, nblk, mb, ch);
-    float* base = a.ws_acc + part * 3 * kBlk * D;
+    float* base = a.ws_acc + part * NACC * kBlk * D;
     store_acc_partial<D>(base, rl, a12);
-    store_acc_partial<D>(base + kBlk * D, rl, a3);
-    store_acc_partial<D>(base + 2 * kBlk * D, rl, a4);
+    if constexpr (!DQ) store_acc_partial<D>(base + kBlk * D, rl, a3);
+    store_acc_partial<D>(base + (NACC - 1) * kBlk * D, rl, a4);
     if (g == 0) {
       float* scp = a.ws_sc + part * 3 * kBlk;
       scp[rl] = Ev;
@@ -1225,32 +1297,48 @@ __global__ __launch_bounds__(kThreads8) __attribute__((amdgpu_waves_per_eu(Gg8Wa
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool XM>
 // False when the variant asked for is not in this object (ttt_launch.h
-// routes each variant to the object that has it).
+// routes each variant to the object that has it).  Without GdO, a given dQ
+// (a.dq.p) selects the dQ form.
 static bool launch_gg_row_x(const Params& a, bool load_p, bool gdo, dim3 grid, hipStream_t st) {
   const TimedLaunch tl(st, kTagGgRow);
   if (gdo) {
     if constexpr ((TTT_GG_ROW_GDO & 2) != 0) {
       if (load_p)
-        hipLaunchKernelGGL((k_gg_row<T, D, true, true, XM>), grid, dim3(kThreads), 0, st, a);
+        hipLaunchKernelGGL((k_gg_row<T, D, true, true, XM, false>), grid, dim3(kThreads), 0, st, a);
       else
-        hipLaunchKernelGGL((k_gg_row<T, D, false, true, XM>), grid, dim3(kThreads), 0, st, a);
+        hipLaunchKernelGGL((k_gg_row<T, D, false, true, XM, false>), grid, dim3(kThreads), 0, st, a);
       return true;
     }
   } else {
+    const bool dq = a.dq.p != nullptr;
 #if TTT_GG_ROW8
     if constexpr (sizeof(T) == 2 && !XM) {
-      if (load_p)
-        hipLaunchKernelGGL((k_gg_row8<T, D, true>), grid, dim3(kThreads8), 0, st, a);
-      else
-        hipLaunchKernelGGL((k_gg_row8<T, D, false>), grid, dim3(kThreads8), 0, st, a);
+      if (dq) {
+        if (load_p)
+          hipLaunchKernelGGL((k_gg_row8<T, D, true, true>), grid, dim3(kThreads8), 0, st, a);
+        else
+          hipLaunchKernelGGL((k_gg_row8<T, D, false, true>), grid, dim3(kThreads8), 0, st, a);
+      } else {
+        if (load_p)
+          hipLaunchKernelGGL((k_gg_row8<T, D, true, false>), grid, dim3(kThreads8), 0, st, a);
+        else
+          hipLaunchKernelGGL((k_gg_row8<T, D, false, false>), grid, dim3(kThreads8), 0, st, a);
+      }
       return true;
     }
 #endif
     if constexpr ((TTT_GG_ROW_GDO & 1) != 0) {
-      if (load_p)
-        hipLaunchKernelGGL((k_gg_row<T, D, true, false, XM>), grid, dim3(kThreads), 0, st, a);
-      else
-        hipLaunchKernelGGL((k_gg_row<T, D, false, false, XM>), grid, dim3(kThreads), 0, st, a);
+      if (dq) {
+        if (load_p)
+          hipLaunchKernelGGL((k_gg_row<T, D, true, false, XM, true>), grid, dim3(kThreads), 0, st, a);
+        else
+          hipLaunchKernelGGL((k_gg_row<T, D, false, false, XM, true>), grid, dim3(kThreads), 0, st, a);
+      } else {
+        if (load_p)
+          hipLaunchKernelGGL((k_gg_row<T, D, true, false, XM, false>), grid, dim3(kThreads), 0, st, a);
+        else
+          hipLaunchKernelGGL((k_gg_row<T, D, false, false, XM, false>), grid, dim3(kThreads), 0, st, a);
+      }
       return true;
     }
   }
@@ -1309,18 +1397,25 @@ static hipError_t launch_gg_col_t(int dtype, const Params& a, bool load_p, hipSt
   return hipGetLastError();
 }
 
+// Workgroups per CU of the row kernel.  The split is chosen from the form
+// without dQ, so that a workspace sized before the call fits either form; the
+// dQ form runs at least as many (the same waves-per-SIMD target and LDS,
+// fewer registers).
 template <typename T, int D, bool XM>
 static int occupancy_gg_row_t(bool load_p, bool gdo) {
   if (gdo) {
     if constexpr ((TTT_GG_ROW_GDO & 2) != 0)
-      return load_p ? occupancy_of(k_gg_row<T, D, true, true, XM>) : occupancy_of(k_gg_row<T, D, false, true, XM>);
+      return load_p ? occupancy_of(k_gg_row<T, D, true, true, XM, false>)
+                    : occupancy_of(k_gg_row<T, D, false, true, XM, false>);
   } else {
 #if TTT_GG_ROW8
     if constexpr (sizeof(T) == 2 && !XM)
-      return load_p ? occupancy_of(k_gg_row8<T, D, true>, kThreads8) : occupancy_of(k_gg_row8<T, D, false>, kThreads8);
+      return load_p ? occupancy_of(k_gg_row8<T, D, true, false>, kThreads8)
+                    : occupancy_of(k_gg_row8<T, D, false, false>, kThreads8);
 #endif
     if constexpr ((TTT_GG_ROW_GDO & 1) != 0)
-      return load_p ? occupancy_of(k_gg_row<T, D, true, false, XM>) : occupancy_of(k_gg_row<T, D, false, false, XM>);
+      return load_p ? occupancy_of(k_gg_row<T, D, true, false, XM, false>)
+                    : occupancy_of(k_gg_row<T, D, false, false, XM, false>);
   }
   return 0;
 }

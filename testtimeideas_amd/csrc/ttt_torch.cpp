@@ -182,10 +182,11 @@ std::vector<at::Tensor> bwd_fused(const at::Tensor& q, const at::Tensor& k, cons
   return {dq, dk, dv, rowsum};
 }
 
-// Double backward: (GQ, GK, GV, GdO or None).
+// Double backward: (GQ, GK, GV, GdO or None).  dq: the first backward's dQ,
+// or None (ttt_attn_gg_row).
 std::vector<at::Tensor> gg(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const at::Tensor& dout,
                            const at::Tensor& lse, const c10::optional<at::Tensor>& p, const at::Tensor& rowsum,
-                           const at::Tensor& gq, const at::Tensor& gk, const at::Tensor& gv, bool causal, double scale,
+                           const c10::optional<at::Tensor>& dq, const at::Tensor& gq, const at::Tensor& gk, const at::Tensor& gv, bool causal, double scale,
                            bool want_gdo, int64_t split_row, int64_t split_col, int64_t window, int64_t window_kind,
                            const c10::optional<at::Tensor>& bias) {
   const ttt_problem pr = problem_of(q, causal, scale, split_row, window, window_kind, bias);
@@ -203,11 +204,13 @@ std::vector<at::Tensor> gg(const at::Tensor& q, const at::Tensor& k, const at::T
   const ttt_view vgq = view_of(gq), vgk = view_of(gk), vgv = view_of(gv);
   const ttt_view ogq = view_of(gq_out), ogk = view_of(gk_out), ogv = view_of(gv_out);
   const ttt_view ogdo = want_gdo ? view_of(gdo) : none_view();
+  const bool ldq = dq && dq->defined();
+  const ttt_view vdq = ldq ? view_of(*dq) : none_view();
   void* st = stream_of(q);
   const float* rs = rowsum.data_ptr<float>();
-  check(ttt_attn_gg_row(&pr, &vq, &vk, &vv, &vdo, lse.data_ptr<float>(), lp ? &vp : nullptr, rs, &vgq, &vgk, &vgv,
-                        &ogq, want_gdo ? &ogdo : nullptr, e.data_ptr<float>(), f.data_ptr<float>(), ptr_or_null(ws),
-                        wsb, st),
+  check(ttt_attn_gg_row(&pr, &vq, &vk, &vv, &vdo, lse.data_ptr<float>(), lp ? &vp : nullptr, rs,
+                        ldq ? &vdq : nullptr, &vgq, &vgk, &vgv, &ogq, want_gdo ? &ogdo : nullptr,
+                        e.data_ptr<float>(), f.data_ptr<float>(), ptr_or_null(ws), wsb, st),
         "ttt_attn_gg_row");
   check(ttt_attn_gg_col(&pc, &vq, &vk, &vv, &vdo, lse.data_ptr<float>(), lp ? &vp : nullptr, rs,
                         e.data_ptr<float>(), f.data_ptr<float>(), &vgq, &vgk, &vgv, &ogk, &ogv, ptr_or_null(ws), wsb,
@@ -220,7 +223,8 @@ std::vector<at::Tensor> gg(const at::Tensor& q, const at::Tensor& k, const at::T
 // the column launch then also finishes the row pass's split blocks.
 std::vector<at::Tensor> gg_fused(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
                                  const at::Tensor& dout, const at::Tensor& lse, const c10::optional<at::Tensor>& p,
-                                 const at::Tensor& rowsum, const at::Tensor& gq, const at::Tensor& gk,
+                                 const at::Tensor& rowsum, const c10::optional<at::Tensor>& dq,
+                                 const at::Tensor& gq, const at::Tensor& gk,
                                  const at::Tensor& gv, bool causal, double scale, bool want_gdo, int64_t window,
                                  int64_t window_kind, const c10::optional<at::Tensor>& bias) {
   const ttt_problem pr = problem_of(q, causal, scale, 0, window, window_kind, bias);
@@ -237,9 +241,11 @@ std::vector<at::Tensor> gg_fused(const at::Tensor& q, const at::Tensor& k, const
   const ttt_view vgq = view_of(gq), vgk = view_of(gk), vgv = view_of(gv);
   const ttt_view ogq = view_of(gq_out), ogk = view_of(gk_out), ogv = view_of(gv_out);
   const ttt_view ogdo = want_gdo ? view_of(gdo) : none_view();
+  const bool ldq = dq && dq->defined();
+  const ttt_view vdq = ldq ? view_of(*dq) : none_view();
   check(ttt_attn_gg(&pr, &vq, &vk, &vv, &vdo, lse.data_ptr<float>(), lp ? &vp : nullptr, rowsum.data_ptr<float>(),
-                    &vgq, &vgk, &vgv, &ogq, &ogk, &ogv, want_gdo ? &ogdo : nullptr, e.data_ptr<float>(),
-                    f.data_ptr<float>(), ptr_or_null(ws), wsb, stream_of(q)),
+                    ldq ? &vdq : nullptr, &vgq, &vgk, &vgv, &ogq, &ogk, &ogv, want_gdo ? &ogdo : nullptr,
+                    e.data_ptr<float>(), f.data_ptr<float>(), ptr_or_null(ws), wsb, stream_of(q)),
         "ttt_attn_gg");
   return {gq_out, gk_out, gv_out, gdo};
 }

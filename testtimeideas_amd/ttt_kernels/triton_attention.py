@@ -86,13 +86,14 @@ def mode_kind(bwd_mode: str) -> str:
 
 class _AttnBwdFn(torch.autograd.Function):
     """First backward as a function of (q, k, v, dO); its backward is the
-    double backward."""
+    double backward.  The kernel-layout dQ is kept for it: the row pass of the
+    double backward reads dQ = s*(dS*K) instead of forming that product."""
 
     @staticmethod
     def forward(ctx, q, k, v, do, qp, kp, vp, op, lse, p, mask, scale, lay):
         dop = lay.q(do)
         dq, dk, dv, rowsum = _lib.bwd(qp, kp, vp, op, dop, lse, p, mask, scale)
-        ctx.save_for_backward(qp, kp, vp, dop, lse, p, rowsum)
+        ctx.save_for_backward(qp, kp, vp, dop, lse, p, rowsum, dq)
         ctx.mask = mask
         ctx.scale = scale
         ctx.lay = lay
@@ -101,12 +102,13 @@ class _AttnBwdFn(torch.autograd.Function):
     @staticmethod
     @once_differentiable
     def backward(ctx, gdq, gdk, gdv):
-        qp, kp, vp, dop, lse, p, rowsum = ctx.saved_tensors
+        qp, kp, vp, dop, lse, p, rowsum, dq = ctx.saved_tensors
         lay = ctx.lay
         g1 = lay.q(gdq.to(qp.dtype))
         g2, g3 = (lay.k(g.to(qp.dtype)) for g in (gdk, gdv))
         want_gdo = ctx.needs_input_grad[3]
-        gq, gk, gv, gdo = _lib.gg(qp, kp, vp, dop, lse, p, rowsum, g1, g2, g3, ctx.mask, ctx.scale, want_gdo)
+        gq, gk, gv, gdo = _lib.gg(qp, kp, vp, dop, lse, p, rowsum, g1, g2, g3, ctx.mask, ctx.scale, want_gdo,
+                                  dq=dq)
         need = ctx.needs_input_grad
         return (lay.uq(gq) if need[0] else None,
                 lay.uk(gk) if need[1] else None,

@@ -154,10 +154,10 @@ _KERNEL = {
     # dK,dV from P: dV, dP, dK; P read; q, v, do read, dk, dv written; D read
     "ttt_attn_bwd_dkdv/p": (6, 1, 5, 1),
     "ttt_attn_bwd_dkdv": (8, 0, 6, 2),
-    # grad-grad row pass: dP, gdS (2), gP1, dS gK, gS K; P read; q,k,v,do,gq,gk,gv read, GQ written;
-    # D read, E and F written
-    "ttt_attn_gg_row/p": (12, 1, 8, 3),
-    "ttt_attn_gg_row": (14, 0, 8, 4),
+    # grad-grad row pass: dP, gdS (2), gP1, dS gK, gS K; P read; q,k,v,do,gq,gk,gv and the first
+    # backward's dQ read (the dQ form, which the autograd path runs), GQ written; D read, E and F written
+    "ttt_attn_gg_row/p": (12, 1, 9, 3),
+    "ttt_attn_gg_row": (14, 0, 9, 4),
     # grad-grad column pass: dP, gdS (2), gP1, dS^T gQ, gS^T Q, gdP^T dO; P read;
     # 7 inputs, GK and GV written; D, E, F read
     "ttt_attn_gg_col/p": (14, 1, 9, 3),

@@ -584,17 +584,18 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, true>::value))) void k_gg_col(P
   const float s = a.scale;
   const float kSl2 = kLog2e;  // raw score (in units of s) -> base 2
 
+  // Stationary fragments negated (K and gK also scaled by s): the products
+  // that start from the staged row statistics come out as D - dP, E - gdS
+  // and G - gP1 (G = F + E D), and the scores of the recomputed P as -s q.k.
   frag kf[D / 32], gkf[D / 32], vf[D / 32], gvf[D / 32];
 #pragma unroll
   for (int ks = 0; ks < D / 32; ++ks) {
-    kf[ks] = load_frag_row<T>(K, a.k.st, n, T_, 32 * ks + 8 * g);
-    gkf[ks] = load_frag_row<T>(gK, a.gk.st, n, T_, 32 * ks + 8 * g);
-    {
-      kf[ks] = scale_frag<T>(kf[ks], a.scale);
-      gkf[ks] = scale_frag<T>(gkf[ks], a.scale);
-    }
-    vf[ks] = load_frag_row<T>(V, a.v.st, n, T_, 32 * ks + 8 * g);
-    gvf[ks] = load_frag_row<T>(gV, a.gv.st, n, T_, 32 * ks + 8 * g);
+    kf[ks] = scale_frag<T>(load_frag_row<T>(K, a.k.st, n, T_, 32 * ks + 8 * g), -a.scale);
+    gkf[ks] = scale_frag<T>(load_frag_row<T>(gK, a.gk.st, n, T_, 32 * ks + 8 * g), -a.scale);
+    vf[ks] = scale_frag<T>(load_frag_row<T>(V, a.v.st, n, T_, 32 * ks + 8 * g), -1.f);
+    gvf[ks] = scale_frag<T>(load_frag_row<T>(gV, a.gv.st, n, T_, 32 * ks + 8 * g), -1.f);
+    // kept as computed (left to itself the compiler redoes a negation per tile)
+    asm volatile("" : "+v"(kf[ks]), "+v"(gkf[ks]), "+v"(vf[ks]), "+v"(gvf[ks]));
   }
 
   f32x4 acc_gk[D / 16], acc_gv[D / 16];
@@ -614,8 +615,8 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, true>::value))) void k_gg_col(P
       }
     } else {
       p.zero();
-      mm_d<T, D>(p, cb.q, kf);
-      recompute_p_col<T, XM>(p, a, bcol, m0, cb.st, 3, kSl2);
+      mm_d<T, D>(p, cb.q, kf);  // -s q.k
+      recompute_p_col<T, XM>(p, a, bcol, m0, cb.st, 3, -kSl2);
     }
     if (mk.tile(mb)) {
 #pragma unroll
@@ -624,31 +625,40 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, true>::value))) void k_gg_col(P
         for (int j = 0; j < 8; ++j)
           p.set(kb, j, mk.masked(m0 + stream_index(kb, g, j)) ? 0.f : p.at(kb, j));
     }
-    dp.zero();
-    gds.zero();
-    gp1.zero();
     // The streamed tile in two halves: products over d for half kb, its
-    // elementwise terms, then its contributions to GK and GV.
+    // elementwise terms, then its contributions to GK and GV.  The products
+    // start from the streamed rows' D, E and G, so that (stationary fragments
+    // negated) nd = D - dP = -(dP - D), ng = E - gdS and ngp = G - gP1; then
+    //   -dS = P nd,  -gdP = P ng,  -gS = P (gP - F)(-1) = P (ngp - ng nd),
+    // since gP - F = gP1 + (gdS - E)(dP - D) - G.  GK and GV accumulate with
+    // the sign flipped, which the stores undo.
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      mm_d2_half<T, D>(dp, gp1, kb, cb.dout, vf, gvf);
-      mm_d_half<T, D>(gds, kb, cb.gq, kf);
-      mm_d_half<T, D>(gds, kb, cb.q, gkf);
       float d8[8], e8[8], f8[8];
       stat_read8(d8, cb.st, 0, kb);
       stat_read8(e8, cb.st, 1, kb);
       stat_read8(f8, cb.st, 2, kb);
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        dp.q[2 * kb + h2] = f32x4{d8[4 * h2], d8[4 * h2 + 1], d8[4 * h2 + 2], d8[4 * h2 + 3]};
+        gds.q[2 * kb + h2] = f32x4{e8[4 * h2], e8[4 * h2 + 1], e8[4 * h2 + 2], e8[4 * h2 + 3]};
+        f32x4 g4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) g4[i] = f8[4 * h2 + i] + e8[4 * h2 + i] * d8[4 * h2 + i];
+        gp1.q[2 * kb + h2] = g4;
+      }
+      mm_d2_half<T, D>(dp, gp1, kb, cb.dout, vf, gvf);
+      mm_d_half<T, D>(gds, kb, cb.gq, kf);
+      mm_d_half<T, D>(gds, kb, cb.q, gkf);
       float vds[8], vgs[8], vgdp[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float P = p.at(kb, j);
-        const float dpv = dp.at(kb, j);
-        const float gd = gds.at(kb, j);
-        const float dmd = dpv - d8[j];
-        const float gp = gp1.at(kb, j) + gd * dmd - e8[j] * dpv;
-        vds[j] = P * dmd;
-        vgdp[j] = P * (gd - e8[j]);
-        vgs[j] = P * (gp - f8[j]);
+        const float nd = dp.at(kb, j);
+        const float ng = gds.at(kb, j);
+        vds[j] = P * nd;
+        vgdp[j] = P * ng;
+        vgs[j] = P * (gp1.at(kb, j) - ng * nd);
       }
       mm_s_half<T, D>(acc_gk, kb, cb.gq, vals_frag<T>(vds));
       mm_s_half<T, D>(acc_gk, kb, cb.q, vals_frag<T>(vgs));
@@ -733,10 +743,16 @@ __attribute__((amdgpu_waves_per_eu(GgWaves<T, D, true>::value))) void k_gg_col(P
       compute(mb, bufs(Parity<0>{}));
     }
   }
+  // the accumulators hold -GK/s and -GV
   if (cr.nch == 1) {
-    store_acc_rows<T, D>(at<T>(a.gk_out, b, h), a.gk_out.st, n, T_, acc_gk, s);
-    store_acc_rows<T, D>(at<T>(a.gv_out, b, h), a.gv_out.st, n, T_, acc_gv, 1.f);
+    store_acc_rows<T, D>(at<T>(a.gk_out, b, h), a.gk_out.st, n, T_, acc_gk, -s);
+    store_acc_rows<T, D>(at<T>(a.gv_out, b, h), a.gv_out.st, n, T_, acc_gv, -1.f);
   } else {
+#pragma unroll
+    for (int i = 0; i < D / 16; ++i) {
+      acc_gk[i] = -acc_gk[i];
+      acc_gv[i] = -acc_gv[i];
+    }
     float* base = a.ws_acc + part_index(a, bh, nblk, nb, ch) * 2 * kBlk * D;
     store_acc_partial<D>(base, cl, acc_gk);
     store_acc_partial<D>(base + kBlk * D, cl, acc_gv);
@@ -835,13 +851,15 @@ __global__ __launch_bounds__(kThreads8) __attribute__((amdgpu_waves_per_eu(Gg8Wa
   const float s = a.scale;
   const float kSl2 = kLog2e;  // raw score (in units of s) -> base 2
 
+  // Stationary fragments negated, as in k_gg_col.
   frag kf[D / 32], gkf[D / 32], vf[D / 32], gvf[D / 32];
 #pragma unroll
   for (int ks = 0; ks < D / 32; ++ks) {
-    kf[ks] = scale_frag<T>(load_frag_row<T>(K, a.k.st, n, T_, 32 * ks + 8 * g), s);
-    gkf[ks] = scale_frag<T>(load_frag_row<T>(gK, a.gk.st, n, T_, 32 * ks + 8 * g), s);
-    vf[ks] = load_frag_row<T>(V, a.v.st, n, T_, 32 * ks + 8 * g);
-    gvf[ks] = load_frag_row<T>(gV, a.gv.st, n, T_, 32 * ks + 8 * g);
+    kf[ks] = scale_frag<T>(load_frag_row<T>(K, a.k.st, n, T_, 32 * ks + 8 * g), -s);
+    gkf[ks] = scale_frag<T>(load_frag_row<T>(gK, a.gk.st, n, T_, 32 * ks + 8 * g), -s);
+    vf[ks] = scale_frag<T>(load_frag_row<T>(V, a.v.st, n, T_, 32 * ks + 8 * g), -1.f);
+    gvf[ks] = scale_frag<T>(load_frag_row<T>(gV, a.gv.st, n, T_, 32 * ks + 8 * g), -1.f);
+    asm volatile("" : "+v"(kf[ks]), "+v"(gkf[ks]), "+v"(vf[ks]), "+v"(gvf[ks]));  // as in k_gg_col
   }
 
   f32x4 acc[D / 16];  // GK (half 0) or GV (half 1)
@@ -871,33 +889,39 @@ __global__ __launch_bounds__(kThreads8) __attribute__((amdgpu_waves_per_eu(Gg8Wa
       float l2[8];
       stat_read8(l2, st, 3, 0);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) p.set(0, j, fast_exp2(p.at(0, j) * kSl2 - l2[j] * kLog2e));
+      for (int j = 0; j < 8; ++j) p.set(0, j, fast_exp2(p.at(0, j) * -kSl2 - l2[j] * kLog2e));  // scores -s q.k
     }
     if (mk.tile(mb)) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) p.set(0, j, mk.masked(m0 + stream_index(0, g, j)) ? 0.f : p.at(0, j));
     }
-    dp.zero();
-    gds.zero();
-    gp1.zero();
-    mm_d2_half<T, D>(dp, gp1, 0, cb.dout + hq, vf, gvf);
-    mm_d_half<T, D>(gds, 0, cb.gq + hq, kf);
-    mm_d_half<T, D>(gds, 0, cb.q + hq, gkf);
+    // The products start from the rows' D, E and G = F + E D, as in k_gg_col:
+    // nd = D - dP, ng = E - gdS, ngp = G - gP1, and -dS, -gdP, -gS below.
     float d8[8], e8[8], f8[8];
     stat_read8(d8, st, 0, 0);
     stat_read8(e8, st, 1, 0);
     stat_read8(f8, st, 2, 0);
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      dp.q[h2] = f32x4{d8[4 * h2], d8[4 * h2 + 1], d8[4 * h2 + 2], d8[4 * h2 + 3]};
+      gds.q[h2] = f32x4{e8[4 * h2], e8[4 * h2 + 1], e8[4 * h2 + 2], e8[4 * h2 + 3]};
+      f32x4 g4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) g4[i] = f8[4 * h2 + i] + e8[4 * h2 + i] * d8[4 * h2 + i];
+      gp1.q[h2] = g4;
+    }
+    mm_d2_half<T, D>(dp, gp1, 0, cb.dout + hq, vf, gvf);
+    mm_d_half<T, D>(gds, 0, cb.gq + hq, kf);
+    mm_d_half<T, D>(gds, 0, cb.q + hq, gkf);
     float vds[8], vgs[8], vgdp[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float P = p.at(0, j);
-      const float dpv = dp.at(0, j);
-      const float gd = gds.at(0, j);
-      const float dmd = dpv - d8[j];
-      const float gp = gp1.at(0, j) + gd * dmd - e8[j] * dpv;
-      vds[j] = P * dmd;
-      vgdp[j] = P * (gd - e8[j]);
-      vgs[j] = P * (gp - f8[j]);
+      const float nd = dp.at(0, j);
+      const float ng = gds.at(0, j);
+      vds[j] = P * nd;
+      vgdp[j] = P * ng;
+      vgs[j] = P * (gp1.at(0, j) - ng * nd);
     }
     if constexpr (HALF == 0) {
       xk[128] = vals_frag<T>(vgdp);
@@ -979,12 +1003,15 @@ __global__ __launch_bounds__(kThreads8) __attribute__((amdgpu_waves_per_eu(Gg8Wa
     else
       run(Parity<1>{});
   }
+  // acc holds -GK/s (half 0) or -GV (half 1)
   if (cr.nch == 1) {
     if (half == 0)
-      store_acc_rows<T, D>(at<T>(a.gk_out, b, h), a.gk_out.st, n, T_, acc, s);
+      store_acc_rows<T, D>(at<T>(a.gk_out, b, h), a.gk_out.st, n, T_, acc, -s);
     else
-      store_acc_rows<T, D>(at<T>(a.gv_out, b, h), a.gv_out.st, n, T_, acc, 1.f);
+      store_acc_rows<T, D>(at<T>(a.gv_out, b, h), a.gv_out.st, n, T_, acc, -1.f);
   } else {
+#pragma unroll
+    for (int i = 0; i < D / 16; ++i) acc[i] = -acc[i];
     float* base = a.ws_acc + part_index(a, bh, nblk, nb, ch) * 2 * kBlk * D;
     store_acc_partial<D>(base + half * kBlk * D, cl, acc);
   }

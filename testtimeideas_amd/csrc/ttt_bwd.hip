@@ -18,6 +18,9 @@
 // bias when there is one (saved P already holds it).  XM instantiates the
 // window/bias code.
 // The next tile's loads are issued before the current tile's math.
+// dP - D comes out of the MFMAs: in k_bwd_dq they start from -D (the
+// stationary row's), in k_bwd_dkdv from the streamed rows' D with the
+// stationary V fragments negated (then D - dP, and dK is stored negated back).
 //
 // Reference semantics: ttt_kernels/triton_attention.py:364-378 (save_p torch
 // backward), :416-420 (recompute); ttt_kernels/backward_stubs.py:124-425.
@@ -154,6 +157,7 @@ __attribute__((amdgpu_waves_per_eu(DqWaves<T, D, LOADP>::value))) void k_bwd_dq(
     Dm = row_dot_do_o<T, D>(dof, at<const T>(a.o, b, h), a.o.st, m, T_);
     if (a.rowsum_out && ch == 0 && row_ok && g == 0) a.rowsum_out[ridx] = Dm;
   }
+  const f32x4 mDm4 = f32x4{-Dm, -Dm, -Dm, -Dm};  // dP's MFMAs start from -D: they give dP - D
   const float lse2 = (!LOADP && row_ok) ? a.lse[ridx] * kLog2e : 0.f;
   const T* Pm = LOADP ? at<const T>(a.p, b, h) + (int64_t)(row_ok ? m : 0) * a.p.st : nullptr;
 
@@ -265,14 +269,15 @@ __attribute__((amdgpu_waves_per_eu(DqWaves<T, D, LOADP>::value))) void k_bwd_dq(
           p.set(kb, j, mk.masked(n0 + stream_index(kb, g, j)) ? 0.f : p.at(kb, j));
     }
     Tile dp;
-    dp.zero();
-    mm_d<T, D>(dp, cV, dof);
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) dp.q[q4] = mDm4;
+    mm_d<T, D>(dp, cV, dof);  // dP - D
     frag dsf[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       float v[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = p.at(kb, j) * (dp.at(kb, j) - Dm);
+      for (int j = 0; j < 8; ++j) v[j] = p.at(kb, j) * dp.at(kb, j);
       dsf[kb] = vals_frag<T>(v);
     }
     mm_s<T, D>(acc, cK, dsf);
@@ -403,7 +408,12 @@ __attribute__((amdgpu_waves_per_eu(DkdvWaves<T, D, LOADP, DV_ONLY>::value))) voi
   frag vf[D / 32], kf[D / 32];
 #pragma unroll
   for (int ks = 0; ks < D / 32; ++ks) {
-    if constexpr (!DV_ONLY) vf[ks] = load_frag_row<T>(V, a.v.st, n, T_, 32 * ks + 8 * g);
+    // negated: dP's MFMAs start from the streamed rows' D and give D - dP;
+    // kept as computed (left to itself the compiler redoes the negation per tile)
+    if constexpr (!DV_ONLY) {
+      vf[ks] = scale_frag<T>(load_frag_row<T>(V, a.v.st, n, T_, 32 * ks + 8 * g), -1.f);
+      asm volatile("" : "+v"(vf[ks]));
+    }
     if constexpr (!LOADP) kf[ks] = load_frag_row<T>(K, a.k.st, n, T_, 32 * ks + 8 * g);
   }
 
@@ -531,18 +541,23 @@ __attribute__((amdgpu_waves_per_eu(DkdvWaves<T, D, LOADP, DV_ONLY>::value))) voi
     mm_s<T, D>(acc_dv, cdO, pf);
     if constexpr (!DV_ONLY) {
       Tile dp;
-      dp.zero();
-      mm_d<T, D>(dp, cdO, vf);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        float d8[8];
+        stat_read8(d8, cS, kSD, kb);
+        dp.q[2 * kb] = f32x4{d8[0], d8[1], d8[2], d8[3]};
+        dp.q[2 * kb + 1] = f32x4{d8[4], d8[5], d8[6], d8[7]};
+      }
+      mm_d<T, D>(dp, cdO, vf);  // D - dP
       frag dsf[2];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        float d8[8], v[8];
-        stat_read8(d8, cS, kSD, kb);
+        float v[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = p.at(kb, j) * (dp.at(kb, j) - d8[j]);
+        for (int j = 0; j < 8; ++j) v[j] = p.at(kb, j) * dp.at(kb, j);  // -dS
         dsf[kb] = vals_frag<T>(v);
       }
-      mm_s<T, D>(acc_dk, cQ, dsf);
+      mm_s<T, D>(acc_dk, cQ, dsf);  // -dK / s
     }
   };
   if constexpr (kDma) {
@@ -555,11 +570,15 @@ __attribute__((amdgpu_waves_per_eu(DkdvWaves<T, D, LOADP, DV_ONLY>::value))) voi
   }
   if (cr.nch == 1) {
     store_acc_rows<T, D>(at<T>(a.dv, b, h), a.dv.st, n, T_, acc_dv, 1.f);
-    if constexpr (!DV_ONLY) store_acc_rows<T, D>(at<T>(a.dk, b, h), a.dk.st, n, T_, acc_dk, a.scale);
+    if constexpr (!DV_ONLY) store_acc_rows<T, D>(at<T>(a.dk, b, h), a.dk.st, n, T_, acc_dk, -a.scale);
   } else {
     float* base = a.ws_acc + part_index(a, bh, nblk, nb, ch) * 2 * kBlk * D;
     store_acc_partial<D>(base, cl, acc_dv);
-    if constexpr (!DV_ONLY) store_acc_partial<D>(base + kBlk * D, cl, acc_dk);
+    if constexpr (!DV_ONLY) {
+#pragma unroll
+      for (int i = 0; i < D / 16; ++i) acc_dk[i] = -acc_dk[i];
+      store_acc_partial<D>(base + kBlk * D, cl, acc_dk);
+    }
   }
 }
 

@@ -798,6 +798,46 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_stats(Pa
 
 // ---------------------------------------------------------------------------
 
+// Row LSE (base 2) of the P pass's row m = 64 mb + rl from the statistics
+// pass: the final LSE, or, when the pass was split into nch chunks, merged
+// from the chunks' partial max and sum (and then written, by the lanes of
+// `write`, as the natural-log LSE).  The statistics of up to kBatch chunks
+// are loaded together (chunk indices past the last repeat it), then merged
+// in chunk order: loaded one at a time, each waited for the last, and the
+// prologue of the longest blocks took several microseconds (b1 h1 T8192: 12
+// chunks).
+__device__ __forceinline__ float p_pass_lse2(const Params& a, int bh, int nblk, int mb, int rl, int nch,
+                                             bool write) {
+  const int T_ = a.T, m = mb * kBlk + rl;
+  const int64_t ridx = (int64_t)bh * T_ + m;
+  if (nch == 1) return (m < T_) ? a.lse[ridx] * kLog2e : 0.f;
+  constexpr int kBatch = 8;
+  const float* sc0 = a.ws_sc + part_index(a, bh, nblk, mb, 0) * 2 * kBlk + rl;
+  float mm = -INFINITY, ll = 0.f;
+  for (int k0 = 0; k0 < nch; k0 += kBatch) {
+    float mk[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) mk[u] = sc0[(int64_t)min(k0 + u, nch - 1) * 2 * kBlk];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) mm = fmaxf(mm, mk[u]);  // repeats of the last chunk leave the max
+  }
+  for (int k0 = 0; k0 < nch; k0 += kBatch) {
+    float mk[kBatch], lk[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int64_t k = min(k0 + u, nch - 1);
+      mk[u] = sc0[k * 2 * kBlk];
+      lk[u] = sc0[k * 2 * kBlk + kBlk];
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      if (k0 + u < nch) ll += lk[u] * fast_exp2(mk[u] - mm);
+  }
+  const float lse2 = mm + __log2f(ll);
+  if (write && m < T_) a.lse[ridx] = lse2 * kLn2;
+  return lse2;
+}
+
 template <typename T, int D, bool XM>
 __global__ __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_p(Params a) {
@@ -829,42 +869,8 @@ __attribute__((amdgpu_waves_per_eu(FwdPWaves<T, D>::value))) void k_fwd_p(Params
   const int m = mb * kBlk + rl;
   const RowMask<XM> mk(a, mb, m);
   const T* brow = (XM && a.bias.p) ? at<const T>(a.bias, b, h) + (int64_t)(m < T_ ? m : 0) * a.bias.st : nullptr;
-  const int64_t ridx = (int64_t)bh * T_ + m;
 
-  // Row LSE (base 2) from the statistics pass.
-  float lse2;
-  if (cr.nch == 1) {
-    lse2 = (m < T_) ? a.lse[ridx] * kLog2e : 0.f;
-  } else {
-    // The statistics of up to kBatch chunks are loaded together (chunk
-    // indices past the last repeat it), then merged in chunk order: loaded
-    // one at a time, each waited for the last, and the prologue of the
-    // longest blocks took several microseconds (b1 h1 T8192: 12 chunks).
-    constexpr int kBatch = 8;
-    const float* sc0 = a.ws_sc + part_index(a, bh, nblk, mb, 0) * 2 * kBlk + rl;
-    float mm = -INFINITY, ll = 0.f;
-    for (int k0 = 0; k0 < cr.nch; k0 += kBatch) {
-      float mk[kBatch];
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) mk[u] = sc0[(int64_t)min(k0 + u, cr.nch - 1) * 2 * kBlk];
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) mm = fmaxf(mm, mk[u]);  // repeats of the last chunk leave the max
-    }
-    for (int k0 = 0; k0 < cr.nch; k0 += kBatch) {
-      float mk[kBatch], lk[kBatch];
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const int64_t k = min(k0 + u, cr.nch - 1);
-        mk[u] = sc0[k * 2 * kBlk];
-        lk[u] = sc0[k * 2 * kBlk + kBlk];
-      }
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u)
-        if (k0 + u < cr.nch) ll += lk[u] * fast_exp2(mk[u] - mm);
-    }
-    lse2 = mm + __log2f(ll);
-    if (ch == 0 && g == 0 && m < T_) a.lse[ridx] = lse2 * kLn2;
-  }
+  const float lse2 = p_pass_lse2(a, bh, nblk, mb, rl, cr.nch, ch == 0 && g == 0);
 
   const T* Q = at<const T>(a.q, b, h);
   const T* K = at<const T>(a.k, b, h);

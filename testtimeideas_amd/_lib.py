@@ -247,6 +247,12 @@ def _kernel_ok(t: torch.Tensor) -> bool:
     """The C ABI takes `t` as it is: unit last stride, a positive T stride (an
     operand expanded along T has stride 0 there and is copied), 16-byte
     aligned base and strides."""
+    st = t.stride()
+    if len(st) == 4 and st[3] == 1:
+        # the common case in one pass: [B,H,T,D] with row-major strides
+        b, h, n, d = t.shape
+        if st[2] == d and st[1] == n * d and st[0] == h * n * d and d > 0:
+            return (d * t.element_size()) % 16 == 0 and t.data_ptr() % 16 == 0
     if t.stride(-1) != 1 and t.size(-1) > 1:
         return False
     if t.stride(2) <= 0:
@@ -494,12 +500,21 @@ def _empty_like_out(x: torch.Tensor) -> torch.Tensor:
 # Tensor-level entry points (inputs already padded and validated).  `mask` is
 # a Mask, or a bool for a plain causal flag.
 # ---------------------------------------------------------------------------
+def _library_choice() -> bool:
+    """Every launch takes the library's own split: nothing forced, no tuning,
+    no per-kernel timing (the entry points then call the binding directly)."""
+    return not _split_chunk and not _block_rows and _timing is None and not autotune.enabled()
+
+
 def fwd(q, k, v, mask, scale: float, want_p: bool):
     """Forward: O, LSE and (save_p) P.  Reference: TritonAttentionFn.forward,
     ttt_kernels/triton_attention.py:261-337 (P path :51-59, :270-273)."""
     if q.numel() == 0:
         return _empty_like_out(q), _stats(q), alloc_p(q) if want_p else None
     m = as_mask(mask)
+    if _library_choice():
+        return tuple(ext().fwd(q, k, v, m.causal, float(scale), bool(want_p), 0, int(m.window), int(m.window_kind),
+                               m.bias, 0))
     ent = ENTRY_FWD_P if want_p else ENTRY_FWD
 
     def run(c, rows=0):
@@ -530,6 +545,9 @@ def bwd(q, k, v, o, do, lse, p, mask, scale: float):
         return _empty_like_out(q), _empty_like_out(k), _empty_like_out(v), _stats(q)
     m = as_mask(mask)
     lp = p is not None
+    if _library_choice():
+        return tuple(ext().bwd_fused(q, k, v, o, do, lse, p, m.causal, float(scale), int(m.window),
+                                     int(m.window_kind), m.bias))
 
     def run(cq, ck):
         return ext().bwd(q, k, v, o, do, lse, p, m.causal, float(scale), cq, ck, int(m.window), int(m.window_kind),
@@ -621,9 +639,14 @@ def gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, mask, scale: float, want_gdo: bo
     m = as_mask(mask)
     lp = p is not None
     if dq is not None:
-        check_inputs(q, dq)
+        if dq.shape != q.shape or dq.dtype != q.dtype or dq.device != q.device:
+            raise ValueError(f"dq: expected the shape, dtype and device of q {tuple(q.shape)}, got "
+                             f"{tuple(dq.shape)} {dq.dtype} {dq.device}")
         if not _kernel_ok(dq):
             dq = dq.contiguous()
+    if _library_choice():
+        return tuple(ext().gg_fused(q, k, v, do, lse, p, rowsum, dq, gq, gk, gv, m.causal, float(scale),
+                                    bool(want_gdo), int(m.window), int(m.window_kind), m.bias))
 
     def run(cr, cc):
         return ext().gg(q, k, v, do, lse, p, rowsum, dq, gq, gk, gv, m.causal, float(scale), bool(want_gdo), cr,

@@ -56,22 +56,41 @@ class Layout:
         self.dpad = _lib.padded_head_dim(d)
         self.qpad = qpad
         self.kpad = kpad
+        # operands go to the kernels as they are (when their strides allow)
+        self.plain = self.dpad == d and qpad == 0 and kpad == 0
 
     def q(self, t: torch.Tensor) -> torch.Tensor:
+        if self.plain and _lib._kernel_ok(t):
+            return t
         return _lib.prep_rows(t, self.dpad, self.qpad, 0)
 
     def k(self, t: torch.Tensor) -> torch.Tensor:
+        if self.plain and _lib._kernel_ok(t):
+            return t
         return _lib.prep_rows(t, self.dpad, 0, self.kpad)
 
     def uq(self, t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
-        if t is None or (self.qpad == 0 and t.size(-1) == self.d):
+        if t is None or self.plain or (self.qpad == 0 and t.size(-1) == self.d):
             return t
         return t[..., self.qpad:, :self.d]
 
     def uk(self, t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
-        if t is None or (self.kpad == 0 and t.size(-1) == self.d):
+        if t is None or self.plain or (self.kpad == 0 and t.size(-1) == self.d):
             return t
         return t[..., :t.size(-2) - self.kpad, :self.d]
+
+
+# Layouts without padding rows, one per head dim (immutable), and the two
+# plain causal masks: shared by every call instead of built per call.
+_PLAIN_LAYOUTS: dict = {}
+_CAUSAL_MASKS = (_lib.Mask(causal=False), _lib.Mask(causal=True))
+
+
+def plain_layout(d: int) -> Layout:
+    lay = _PLAIN_LAYOUTS.get(d)
+    if lay is None:
+        lay = _PLAIN_LAYOUTS[d] = Layout(d)
+    return lay
 
 
 def mode_kind(bwd_mode: str) -> str:
@@ -87,10 +106,17 @@ def mode_kind(bwd_mode: str) -> str:
 class _AttnBwdFn(torch.autograd.Function):
     """First backward as a function of (q, k, v, dO); its backward is the
     double backward.  The kernel-layout dQ is kept for it: the row pass of the
-    double backward reads dQ = s*(dS*K) instead of forming that product."""
+    double backward reads dQ = s*(dS*K) instead of forming that product.
+
+    `fwd` = (qp, kp, vp, op, lse, p, mask, scale, lay), the saved forward in
+    kernel layout, goes in as one plain object: autograd does not look inside
+    it, so no gradient flows into those tensors (the closed-form double
+    backward already covers every dependence on q, k, v, and O is an output
+    of the forward node)."""
 
     @staticmethod
-    def forward(ctx, q, k, v, do, qp, kp, vp, op, lse, p, mask, scale, lay):
+    def forward(ctx, q, k, v, do, fwd):
+        qp, kp, vp, op, lse, p, mask, scale, lay = fwd
         dop = lay.q(do)
         dq, dk, dv, rowsum = _lib.bwd(qp, kp, vp, op, dop, lse, p, mask, scale)
         ctx.save_for_backward(qp, kp, vp, dop, lse, p, rowsum, dq)
@@ -104,8 +130,10 @@ class _AttnBwdFn(torch.autograd.Function):
     def backward(ctx, gdq, gdk, gdv):
         qp, kp, vp, dop, lse, p, rowsum, dq = ctx.saved_tensors
         lay = ctx.lay
-        g1 = lay.q(gdq.to(qp.dtype))
-        g2, g3 = (lay.k(g.to(qp.dtype)) for g in (gdk, gdv))
+        dt = qp.dtype
+        g1 = lay.q(gdq if gdq.dtype == dt else gdq.to(dt))
+        g2 = lay.k(gdk if gdk.dtype == dt else gdk.to(dt))
+        g3 = lay.k(gdv if gdv.dtype == dt else gdv.to(dt))
         want_gdo = ctx.needs_input_grad[3]
         gq, gk, gv, gdo = _lib.gg(qp, kp, vp, dop, lse, p, rowsum, g1, g2, g3, ctx.mask, ctx.scale, want_gdo,
                                   dq=dq)
@@ -114,7 +142,7 @@ class _AttnBwdFn(torch.autograd.Function):
                 lay.uk(gk) if need[1] else None,
                 lay.uk(gv) if need[2] else None,
                 lay.uq(gdo) if want_gdo else None,
-                None, None, None, None, None, None, None, None, None)
+                None)
 
 
 class SavedProbs(tuple):
@@ -169,11 +197,8 @@ def attn_backward(ctx, grad_out: torch.Tensor):
     q, k, v, qp, kp, vp, op, lse, p = ctx.saved_tensors
     mask, scale, lay = ctx.mask, ctx.scale, ctx.lay
     if torch.is_grad_enabled():
-        # The kernel operands go in detached: the closed-form double backward
-        # already covers every dependence on q, k, v, so no gradient may flow
-        # into O (an output of this node) or into the saved inputs a second time.
-        return _AttnBwdFn.apply(q, k, v, grad_out, qp.detach(), kp.detach(), vp.detach(), op.detach(), lse, p,
-                                mask, scale, lay)
+        # O detached: the saved node holds no edge into the forward's graph
+        return _AttnBwdFn.apply(q, k, v, grad_out, (qp, kp, vp, op.detach(), lse, p, mask, scale, lay))
     dq, dk, dv, _ = _lib.bwd(qp, kp, vp, op, lay.q(grad_out), lse, p, mask, scale)
     return lay.uq(dq), lay.uk(dk), lay.uk(dv)
 
@@ -189,7 +214,7 @@ class TritonAttentionFn(torch.autograd.Function):
         if scale is None:
             scale = 1.0 / math.sqrt(q.size(-1))
         ctx.causal = causal
-        return attn_forward(ctx, q, k, v, _lib.Mask(causal=bool(causal)), scale, bwd_mode, Layout(q.size(-1)))
+        return attn_forward(ctx, q, k, v, _CAUSAL_MASKS[bool(causal)], scale, bwd_mode, plain_layout(q.size(-1)))
 
     @staticmethod
     def backward(ctx, grad_out: torch.Tensor):

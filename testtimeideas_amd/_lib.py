@@ -263,6 +263,15 @@ def _kernel_ok(t: torch.Tensor) -> bool:
     return all((s * eb) % 16 == 0 for s in t.stride()[:-1])
 
 
+def _ready(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+    """`t`, or a copy with fresh contiguous strides when the C ABI would not
+    take it as it is (the torch binding does the same in C++ for its own
+    calls; this is for the ctypes calls)."""
+    if t is None or _kernel_ok(t):
+        return t
+    return t.clone(memory_format=torch.contiguous_format)
+
+
 def prep(t: torch.Tensor, d_pad: int) -> torch.Tensor:
     """Return a [B,H,T,d_pad] tensor the kernels accept (copy only if needed)."""
     d = t.size(-1)
@@ -527,6 +536,7 @@ def fwd(q, k, v, mask, scale: float, want_p: bool):
         rows, c = _fwd_config(q, m, scale, lambda rc: run(rc[1], rc[0]))
     if _timing is None:
         return tuple(run(c, rows))
+    q, k, v = _ready(q), _ready(k), _ready(v)
     o = _empty_like_out(q)
     lse = _stats(q)
     p = alloc_p(q) if want_p else None
@@ -560,6 +570,7 @@ def bwd(q, k, v, o, do, lse, p, mask, scale: float):
             return tuple(ext().bwd_fused(q, k, v, o, do, lse, p, m.causal, float(scale), int(m.window),
                                          int(m.window_kind), m.bias))
         return tuple(run(cq, ck))
+    q, k, v, o, do = _ready(q), _ready(k), _ready(v), _ready(o), _ready(do)
     dq = _empty_like_out(q)
     dk = _empty_like_out(k)
     dv = _empty_like_out(v)
@@ -642,8 +653,6 @@ def gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, mask, scale: float, want_gdo: bo
         if dq.shape != q.shape or dq.dtype != q.dtype or dq.device != q.device:
             raise ValueError(f"dq: expected the shape, dtype and device of q {tuple(q.shape)}, got "
                              f"{tuple(dq.shape)} {dq.dtype} {dq.device}")
-        if not _kernel_ok(dq):
-            dq = dq.contiguous()
     if _library_choice():
         return tuple(ext().gg_fused(q, k, v, do, lse, p, rowsum, dq, gq, gk, gv, m.causal, float(scale),
                                     bool(want_gdo), int(m.window), int(m.window_kind), m.bias))
@@ -659,6 +668,7 @@ def gg(q, k, v, do, lse, p, rowsum, gq, gk, gv, mask, scale: float, want_gdo: bo
             return tuple(ext().gg_fused(q, k, v, do, lse, p, rowsum, dq, gq, gk, gv, m.causal, float(scale),
                                         bool(want_gdo), int(m.window), int(m.window_kind), m.bias))
         return tuple(run(cr, cc))
+    q, k, v, do, dq, gq, gk, gv = (_ready(t) for t in (q, k, v, do, dq, gq, gk, gv))
     gq_out = _empty_like_out(q)
     gk_out = _empty_like_out(k)
     gv_out = _empty_like_out(v)

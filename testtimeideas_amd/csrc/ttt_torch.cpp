@@ -7,10 +7,11 @@
 // The ctypes binding (testtimeideas_amd/_lib.py) spends tens of microseconds
 // of Python per call building views, problems and outputs; the autograd path
 // of one grad-grad step makes three such calls.  This module does the same
-// work in C++: it takes kernel-ready tensors (head dim padded, strides
-// checked by the Python layer), allocates outputs, statistics and the
-// workspace with torch's caching allocator on the tensors' device, and calls
-// the C entry points on torch's current HIP stream.  A nonzero status raises
+// work in C++: it takes tensors with the head dim already padded (by the
+// Python layer), copies any whose strides the C ABI does not take (ready),
+// allocates outputs, statistics and the workspace with torch's caching
+// allocator on the tensors' device, and calls the C entry points on torch's
+// current HIP stream.  A nonzero status raises
 // RuntimeError with the library's message.  No kernel runs here and nothing
 // falls back: the C ABI is the only compute path.
 #include <torch/extension.h>
@@ -42,6 +43,22 @@ ttt_view view_of(const at::Tensor& t) {
   v.stride_h = t.stride(1);
   v.stride_t = t.stride(2);
   return v;
+}
+
+// `t` itself when the C ABI takes it as it is (unit last stride, a positive
+// T stride, 16-byte aligned base and B/H/T strides), else a contiguous copy
+// (fresh strides, so a size-1 dimension's stride is positive too).
+at::Tensor ready(const at::Tensor& t) {
+  const int64_t eb = t.element_size();
+  const bool ok = (t.stride(3) == 1 || t.size(3) <= 1) && t.stride(2) > 0 &&
+                  reinterpret_cast<uintptr_t>(t.data_ptr()) % 16 == 0 && (t.stride(0) * eb) % 16 == 0 &&
+                  (t.stride(1) * eb) % 16 == 0 && (t.stride(2) * eb) % 16 == 0;
+  return ok ? t : at::empty(t.sizes(), t.options()).copy_(t);
+}
+
+c10::optional<at::Tensor> ready(const c10::optional<at::Tensor>& t) {
+  if (!t || !t->defined()) return t;
+  return ready(*t);
 }
 
 ttt_view none_view() {
@@ -114,9 +131,10 @@ void* stream_of(const at::Tensor& x) {
 }
 
 // Forward: (O, LSE, P or None).  Replaces TritonAttentionFn.forward's launches.
-std::vector<at::Tensor> fwd(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, bool causal, double scale,
-                            bool want_p, int64_t split_chunk, int64_t window, int64_t window_kind,
+std::vector<at::Tensor> fwd(const at::Tensor& q_, const at::Tensor& k_, const at::Tensor& v_, bool causal,
+                            double scale, bool want_p, int64_t split_chunk, int64_t window, int64_t window_kind,
                             const c10::optional<at::Tensor>& bias, int64_t block_rows) {
+  const at::Tensor q = ready(q_), k = ready(k_), v = ready(v_);
   const ttt_problem pr = problem_of(q, causal, scale, split_chunk, window, window_kind, bias, block_rows);
   at::Tensor o = at::empty(q.sizes(), q.options());
   at::Tensor lse = stats_of(q);
@@ -132,10 +150,11 @@ std::vector<at::Tensor> fwd(const at::Tensor& q, const at::Tensor& k, const at::
 }
 
 // First backward: (dQ, dK, dV, D).  split_dq, split_dkdv: each family's split.
-std::vector<at::Tensor> bwd(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const at::Tensor& o,
-                            const at::Tensor& dout, const at::Tensor& lse, const c10::optional<at::Tensor>& p,
+std::vector<at::Tensor> bwd(const at::Tensor& q_, const at::Tensor& k_, const at::Tensor& v_, const at::Tensor& o_,
+                            const at::Tensor& dout_, const at::Tensor& lse, const c10::optional<at::Tensor>& p,
                             bool causal, double scale, int64_t split_dq, int64_t split_dkdv, int64_t window,
                             int64_t window_kind, const c10::optional<at::Tensor>& bias) {
+  const at::Tensor q = ready(q_), k = ready(k_), v = ready(v_), o = ready(o_), dout = ready(dout_);
   const ttt_problem pq = problem_of(q, causal, scale, split_dq, window, window_kind, bias);
   const ttt_problem pk = problem_of(q, causal, scale, split_dkdv, window, window_kind, bias);
   at::Tensor dq = at::empty(q.sizes(), q.options());
@@ -161,10 +180,11 @@ std::vector<at::Tensor> bwd(const at::Tensor& q, const at::Tensor& k, const at::
 
 // The same through ttt_attn_bwd when both families take the library's split:
 // the dK/dV launch then also finishes dQ's split blocks.
-std::vector<at::Tensor> bwd_fused(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
-                                  const at::Tensor& o, const at::Tensor& dout, const at::Tensor& lse,
+std::vector<at::Tensor> bwd_fused(const at::Tensor& q_, const at::Tensor& k_, const at::Tensor& v_,
+                                  const at::Tensor& o_, const at::Tensor& dout_, const at::Tensor& lse,
                                   const c10::optional<at::Tensor>& p, bool causal, double scale, int64_t window,
                                   int64_t window_kind, const c10::optional<at::Tensor>& bias) {
+  const at::Tensor q = ready(q_), k = ready(k_), v = ready(v_), o = ready(o_), dout = ready(dout_);
   const ttt_problem pr = problem_of(q, causal, scale, 0, window, window_kind, bias);
   at::Tensor dq = at::empty(q.sizes(), q.options());
   at::Tensor dk = at::empty(k.sizes(), k.options());
@@ -184,11 +204,15 @@ std::vector<at::Tensor> bwd_fused(const at::Tensor& q, const at::Tensor& k, cons
 
 // Double backward: (GQ, GK, GV, GdO or None).  dq: the first backward's dQ,
 // or None (ttt_attn_gg_row).
-std::vector<at::Tensor> gg(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const at::Tensor& dout,
+std::vector<at::Tensor> gg(const at::Tensor& q_, const at::Tensor& k_, const at::Tensor& v_, const at::Tensor& dout_,
                            const at::Tensor& lse, const c10::optional<at::Tensor>& p, const at::Tensor& rowsum,
-                           const c10::optional<at::Tensor>& dq, const at::Tensor& gq, const at::Tensor& gk, const at::Tensor& gv, bool causal, double scale,
-                           bool want_gdo, int64_t split_row, int64_t split_col, int64_t window, int64_t window_kind,
+                           const c10::optional<at::Tensor>& dq_, const at::Tensor& gq_, const at::Tensor& gk_,
+                           const at::Tensor& gv_, bool causal, double scale, bool want_gdo, int64_t split_row,
+                           int64_t split_col, int64_t window, int64_t window_kind,
                            const c10::optional<at::Tensor>& bias) {
+  const at::Tensor q = ready(q_), k = ready(k_), v = ready(v_), dout = ready(dout_);
+  const at::Tensor gq = ready(gq_), gk = ready(gk_), gv = ready(gv_);
+  const c10::optional<at::Tensor> dq = ready(dq_);
   const ttt_problem pr = problem_of(q, causal, scale, split_row, window, window_kind, bias);
   const ttt_problem pc = problem_of(q, causal, scale, split_col, window, window_kind, bias);
   at::Tensor gq_out = at::empty(q.sizes(), q.options());
@@ -221,12 +245,15 @@ std::vector<at::Tensor> gg(const at::Tensor& q, const at::Tensor& k, const at::T
 
 // The same through ttt_attn_gg when both passes take the library's split:
 // the column launch then also finishes the row pass's split blocks.
-std::vector<at::Tensor> gg_fused(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
-                                 const at::Tensor& dout, const at::Tensor& lse, const c10::optional<at::Tensor>& p,
-                                 const at::Tensor& rowsum, const c10::optional<at::Tensor>& dq,
-                                 const at::Tensor& gq, const at::Tensor& gk,
-                                 const at::Tensor& gv, bool causal, double scale, bool want_gdo, int64_t window,
-                                 int64_t window_kind, const c10::optional<at::Tensor>& bias) {
+std::vector<at::Tensor> gg_fused(const at::Tensor& q_, const at::Tensor& k_, const at::Tensor& v_,
+                                 const at::Tensor& dout_, const at::Tensor& lse, const c10::optional<at::Tensor>& p,
+                                 const at::Tensor& rowsum, const c10::optional<at::Tensor>& dq_,
+                                 const at::Tensor& gq_, const at::Tensor& gk_, const at::Tensor& gv_, bool causal,
+                                 double scale, bool want_gdo, int64_t window, int64_t window_kind,
+                                 const c10::optional<at::Tensor>& bias) {
+  const at::Tensor q = ready(q_), k = ready(k_), v = ready(v_), dout = ready(dout_);
+  const at::Tensor gq = ready(gq_), gk = ready(gk_), gv = ready(gv_);
+  const c10::optional<at::Tensor> dq = ready(dq_);
   const ttt_problem pr = problem_of(q, causal, scale, 0, window, window_kind, bias);
   at::Tensor gq_out = at::empty(q.sizes(), q.options());
   at::Tensor gk_out = at::empty(k.sizes(), k.options());

@@ -59,13 +59,15 @@ class Layout:
         # operands go to the kernels as they are (when their strides allow)
         self.plain = self.dpad == d and qpad == 0 and kpad == 0
 
+    # A plain layout hands operands over as they are: the binding copies one
+    # whose strides the kernels do not take.
     def q(self, t: torch.Tensor) -> torch.Tensor:
-        if self.plain and _lib._kernel_ok(t):
+        if self.plain:
             return t
         return _lib.prep_rows(t, self.dpad, self.qpad, 0)
 
     def k(self, t: torch.Tensor) -> torch.Tensor:
-        if self.plain and _lib._kernel_ok(t):
+        if self.plain:
             return t
         return _lib.prep_rows(t, self.dpad, 0, self.kpad)
 

@@ -70,6 +70,7 @@ constexpr int64_t kDeferRounds = 4;        // P pass: rounds of workgroups from 
 // dQ +15 % with the hint).
 constexpr int64_t kPStreamBytes = 128ll << 20;
 constexpr int64_t kMaxSimWorkgroups = 16;  // x slots: larger grids are not considered
+constexpr int kDkdvPerCu = 2;  // saved-P dK/dV workgroups per CU the split simulation assumes at most
 constexpr int kFallbackCus = 256;
 constexpr int kFallbackPerCu = 2;
 // Chunks shorter than this are not worth a combine pass.
@@ -188,6 +189,13 @@ int64_t family_slots(const ttt_problem* pr, int fam, bool load_p) {
       default: n = ttt::occupancy_gg_col(dt, D, load_p, xm); break;
     }
     if (n <= 0) n = kFallbackPerCu;
+    // The saved-P dK/dV kernels run about two workgroups per CU where the
+    // occupancy calculator allows three (counters: 1.9-2.0 waves per SIMD at
+    // b1 h1 T8192/16384 d64), and their splits fitted to two measured faster
+    // (b1 h1 d64 fp16 causal steps, same box: T8192 -1.9 %, T16384 -0.3 %; the
+    // recompute variant, +1.5 % at T8192 with the cap, keeps three, and so
+    // does D = 128, where nothing was fitted).
+    if (fam == ttt::kFamDkdv && load_p && D == 64 && n > kDkdvPerCu) n = kDkdvPerCu;
     per_cu[dev][fam][dt][ds][lp][xm].store(n, std::memory_order_relaxed);
   }
   return std::max<int64_t>(1, (int64_t)cus * n * kSlotFill / 100);

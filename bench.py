@@ -320,16 +320,10 @@ def c2_bench(dev, steps: int, warmup: int) -> dict:
             "reference_h100_fwd_ms": REFERENCE_C2_FWD_H100_MS}
 
 
-def c5_bench(dev, steps: int, warmup: int) -> dict:
-    """C5 (b4 h16 T8192 d128 bf16 causal, q, k, v x 0.5): the full step."""
-    cfg = workloads.CONFIGS["C5"]
-    x = workloads.make_inputs(cfg, seed=0, device=dev)
-    step = make_step(cfg, x)
-    ms = time_steps(step, steps, warmup)
-    roof = workloads.roofline_us(cfg)
-    kt = kernel_times(step, 3)
-    lt = launch_times(step, 3)
-    # the same step with every kernel family's configuration measured per shape (the first step tunes)
+def autotuned(step, steps: int):
+    """(ms per step, choices) of the same step with every kernel family's
+    configuration measured per shape (testtimeideas_amd.autotune; the first
+    step tunes, untimed).  Tuning is left as it was found."""
     was = autotune.enabled()
     autotune.enable(True)
     try:
@@ -340,6 +334,19 @@ def c5_bench(dev, steps: int, warmup: int) -> dict:
     finally:
         autotune.enable(was)
         autotune.clear()
+    return tuned_ms, tuned
+
+
+def c5_bench(dev, steps: int, warmup: int) -> dict:
+    """C5 (b4 h16 T8192 d128 bf16 causal, q, k, v x 0.5): the full step."""
+    cfg = workloads.CONFIGS["C5"]
+    x = workloads.make_inputs(cfg, seed=0, device=dev)
+    step = make_step(cfg, x)
+    ms = time_steps(step, steps, warmup)
+    roof = workloads.roofline_us(cfg)
+    kt = kernel_times(step, 3)
+    lt = launch_times(step, 3)
+    tuned_ms, tuned = autotuned(step, steps)
     return {"ms": round(ms, 3), "autotuned_ms": round(tuned_ms, 3), "autotuned_choices": tuned,
             "tflops": round(roof["flops"] / (ms * 1e-3) / 1e12, 1),
             "step_roofline_us": round(roof["roofline_us"], 1),
@@ -544,6 +551,8 @@ def main():
     launch_ms = launch_times(step, args.steps)
     graph_ms = graph_steps(cfg, x, args.steps, args.warmup) if not args.no_graph else None
     roof = workloads.roofline_us(cfg)
+    # beside the library's own splits (value): the same step with them measured per shape
+    tuned_ms, tuned_choices = (None, None) if args.autotune else autotuned(step, args.steps)
 
     out = {
         "metric": METRIC,
@@ -570,6 +579,8 @@ def main():
         "step_roofline_us": round(roof["roofline_us"], 2),
         "step_roofline_frac": round(roof["roofline_us"] * 1e-3 / ms, 5),
         "graph_ms_per_step": None if graph_ms is None else round(graph_ms, 4),
+        "autotuned_ms_per_step": None if tuned_ms is None else round(tuned_ms, 4),
+        "autotuned_choices": tuned_choices,
         "scalar_loss_ms_per_step": None if ms_scalar is None else round(ms_scalar, 4),
         "kernel_us": {k: round(v * 1e3, 2) for k, v in sorted(ktimes.items())},
         "kernel_sum_us": round(sum(ktimes.values()) * 1e3, 2),

@@ -269,11 +269,13 @@ double simulate_launch(const std::vector<int64_t>& len, int64_t c, int64_t bh, i
 // Tiles per workgroup (see above).  Chunks are at least kMinChunk tiles, and a
 // split must beat no split by kSplitTiles.  Cached per shape.
 // kind: 0 row blocks, 1 column blocks, 2 row-block pairs (len in their units).
-int64_t best_chunk(const ttt_problem* pr, const std::vector<int64_t>& len, int kind, int64_t bh, int64_t slots) {
+// cfloor: no chunk below it is considered (0: none).
+int64_t best_chunk(const ttt_problem* pr, const std::vector<int64_t>& len, int kind, int64_t bh, int64_t slots,
+                   int64_t cfloor = 0) {
   static std::mutex mu;
-  static std::map<std::tuple<int64_t, int, int, int, int, int64_t, int64_t, int>, int64_t> cache;
+  static std::map<std::tuple<int64_t, int, int, int, int, int64_t, int64_t, int, int64_t>, int64_t> cache;
   const auto key = std::make_tuple((int64_t)pr->seqlen, pr->causal, eff_window(pr), pr->window_kind, kind,
-                                   bh, slots, pr->bias.data ? 1 : 0);
+                                   bh, slots, pr->bias.data ? 1 : 0, cfloor);
   // plain causal launches run their chunks longest first (causal_item)
   const bool longest_first = pr->causal && !has_xm(pr);
   {
@@ -289,7 +291,7 @@ int64_t best_chunk(const ttt_problem* pr, const std::vector<int64_t>& len, int k
     best = simulate_launch(len, lmax, bh, slots, longest_first, &used) + kWgCostTiles * used;
   }
   // candidates: every length up to 64 tiles, then steps of ~3%
-  const int64_t cmin = kind == 2 ? kMinPairChunk : kMinChunk;
+  const int64_t cmin = std::max<int64_t>(kind == 2 ? kMinPairChunk : kMinChunk, cfloor);
   for (int64_t c = std::min<int64_t>(cmin, lmax); c < lmax; c = c < 64 ? c + 1 : c + std::max<int64_t>(1, c / 32)) {
     if (bh * slice_workgroups(len, c) > kMaxSimWorkgroups * slots) continue;
     int64_t used = 0;
@@ -355,7 +357,12 @@ Split choose_split(const ttt_problem* pr, int fam, bool load_p) {
     // Blocks of unequal length (causal or windowed) are simulated up to
     // kSimBlocks times the slots; equal blocks stop splitting at the slots.
     const int64_t fill = (pr->causal ? kSimBlocks : 1) * slots;
-    c = bh * s.nblk >= fill ? lmax : best_chunk(pr, len, col, bh, slots);
+    // The P pass merges the statistics pass's chunks in batches of
+    // kLseMergeBatch loads before its first tile: chunks past one batch cost
+    // it another round trip (b1 h1 T8192 d64 causal, forward with P: 40.9 us
+    // at 12 chunks, 38.6 at 8; T16384: 104.7 us at 8, 128 at 11).
+    const int64_t cfloor = fam == ttt::kFamFwdP ? (lmax + ttt::kLseMergeBatch - 1) / ttt::kLseMergeBatch : 0;
+    c = bh * s.nblk >= fill ? lmax : best_chunk(pr, len, col, bh, slots, cfloor);
   }
   s.chunk = (int)std::min<int64_t>(c, lmax);
   s.nchunk_max = (int)((lmax + s.chunk - 1) / s.chunk);

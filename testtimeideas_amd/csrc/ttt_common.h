@@ -41,6 +41,9 @@ namespace ttt {
 
 constexpr int kThreads = 256;  // four wave64s per workgroup
 constexpr int kBlk = 64;       // stationary rows per workgroup == streamed tile rows
+// Statistics-pass chunks the P pass loads together when it merges them into
+// the LSE (p_pass_lse2); the split chooser keeps its chunks to one batch.
+constexpr int kLseMergeBatch = 8;
 
 constexpr float kLog2e = 1.4426950408889634f;  // 1/ln(2)
 constexpr float kLn2 = 0.6931471805599453f;    // ln(2)

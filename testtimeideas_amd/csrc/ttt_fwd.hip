@@ -811,7 +811,7 @@ __device__ __forceinline__ float p_pass_lse2(const Params& a, int bh, int nblk, 
   const int T_ = a.T, m = mb * kBlk + rl;
   const int64_t ridx = (int64_t)bh * T_ + m;
   if (nch == 1) return (m < T_) ? a.lse[ridx] * kLog2e : 0.f;
-  constexpr int kBatch = 8;
+  constexpr int kBatch = kLseMergeBatch;
   const float* sc0 = a.ws_sc + part_index(a, bh, nblk, mb, 0) * 2 * kBlk + rl;
   float mm = -INFINITY, ll = 0.f;
   for (int k0 = 0; k0 < nch; k0 += kBatch) {

@@ -551,8 +551,9 @@ def main():
     launch_ms = launch_times(step, args.steps)
     graph_ms = graph_steps(cfg, x, args.steps, args.warmup) if not args.no_graph else None
     roof = workloads.roofline_us(cfg)
-    # beside the library's own splits (value): the same step with them measured per shape
-    tuned_ms, tuned_choices = (None, None) if args.autotune else autotuned(step, args.steps)
+    # beside the library's own splits (value): the same step with them measured per shape (not in
+    # --no-extra runs, which the profiles use: tuning launches every candidate split)
+    tuned_ms, tuned_choices = (None, None) if args.autotune or args.no_extra else autotuned(step, args.steps)
 
     out = {
         "metric": METRIC,
